@@ -1,0 +1,297 @@
+"""Headline benchmark: batched ragged paged decode on one MI355X.
+
+    python bench.py [--gpus 1] [--steps 50] [--warmup 10]
+
+Workload (config 2 of the path's spec, `config.workload` in the JSON line):
+N = 128 sequences, lengths from the reference generator (bench_throughput.cu:50-57,
+seed 12345: sum 83,212, max 2,022), H = 8 query = KV heads, D = 64, BLOCK = 16,
+fp16 K/V in a shared pool sized to actual use, blocks handed out by the
+free-list in a seeded random order, q/K/V ~ N(0,1), fp32 accumulation.
+A step is one decode pass over the whole batch (one kernel launch).
+Inputs are resident in HBM; the timed loop rotates over --rotate pool copies
+(4 x 172 MB > the 256 MB Infinity Cache) so every step streams from HBM.
+
+value = algorithmic bytes per step / mean kernel time (GB/s); algorithmic bytes
+= sum_i L_i * Hkv * D * 2 (K,V) * 2 B + q + out + block tables + lengths/offsets.
+The output is checked against the CPU oracle before timing.
+
+Extras in the same line: config 3 (long-context split-K, Qwen2.5-0.5B attention
+shape) and config 4 (256-request continuous vs static batching trace, 24 layers
+of append + GQA decode per step), each measured the same way.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "paged decode KV GB/s (% of HBM peak) @N=128 ragged; continuous tokens/s"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def build_c2(lens, Hq, Hkv, D, B, rotate, seed):
+    from kvcache_amd import KVC_F16
+    from kvcache_amd.device import DeviceBuffer, fill_normal
+    from kvcache_amd.engine import BlockAllocator
+    from kvcache_amd.workloads import build_tables
+
+    nb = int(sum((int(x) + B - 1) // B for x in lens))
+    alloc = BlockAllocator(nb)           # pool sized to actual use
+    alloc.shuffle(seed)                  # blocks come out in a seeded random physical order
+    table, tab_off = build_tables(lens, B, alloc)
+    N = len(lens)
+    elems = nb * Hkv * B * D
+    pools = []
+    for r in range(rotate):
+        k, v = DeviceBuffer(elems * 2), DeviceBuffer(elems * 2)
+        fill_normal(k, elems, KVC_F16, seed * 1000 + 2 * r + 1)
+        fill_normal(v, elems, KVC_F16, seed * 1000 + 2 * r + 2)
+        pools.append((k, v))
+    q = DeviceBuffer(N * Hq * D * 2)
+    fill_normal(q, N * Hq * D, KVC_F16, seed * 1000 + 999)
+    meta = dict(table=DeviceBuffer.from_numpy(table), tab_off=DeviceBuffer.from_numpy(tab_off),
+                lens=DeviceBuffer.from_numpy(np.asarray(lens, np.int32)), out=DeviceBuffer(N * Hq * D * 2))
+    return dict(nb=nb, table=table, tab_off=tab_off, pools=pools, q=q, **meta)
+
+
+def alg_bytes(lens, Hq, Hkv, D, B, esz=2):
+    kv = int(np.sum(lens, dtype=np.int64)) * Hkv * D * 2 * esz
+    n = len(lens)
+    other = 2 * n * Hq * D * esz + 4 * int(sum((int(x) + B - 1) // B for x in lens)) + 4 * (2 * n + 1)
+    return kv, kv + other
+
+
+def time_decode(W, lens, Hq, Hkv, D, B, split, steps, warmup, stream=None):
+    """Runs warmup + steps launches (rotating pools) and returns per-launch times (ms)."""
+    from kvcache_amd import KVC_F16, ops
+    from kvcache_amd.device import Event, synchronize
+
+    cap = int(max(lens))
+    N = len(lens)
+    scale = 1.0 / np.sqrt(D)
+
+    def launch(i):
+        k, v = W["pools"][i % len(W["pools"])]
+        ops.launch_batched_paged(W["q"], k, v, W["table"], W["tab_off"], W["lens"], W["out"], N, Hq, D, B, cap,
+                                 scale, Hkv=Hkv, dtype=KVC_F16, split=split, stream=stream)
+
+    for i in range(warmup):
+        launch(i)
+    synchronize()
+    evs = [Event() for _ in range(steps + 1)]
+    evs[0].record(stream)
+    for i in range(steps):
+        launch(i)
+        evs[i + 1].record(stream)
+    synchronize()
+    per = np.array([evs[i].elapsed_ms(evs[i + 1]) for i in range(steps)])
+    total = evs[0].elapsed_ms(evs[-1])
+    return per, total
+
+
+def check_c2(W, lens, Hq, Hkv, D, B, split):
+    """One launch on pool copy 0, compared with the CPU oracle (max abs <= 2e-3)."""
+    import oracle
+    from kvcache_amd import KVC_F16, ops
+    from kvcache_amd.device import synchronize
+
+    N = len(lens)
+    k, v = W["pools"][0]
+    ops.launch_batched_paged(W["q"], k, v, W["table"], W["tab_off"], W["lens"], W["out"], N, Hq, D, B,
+                             int(max(lens)), 1.0 / np.sqrt(D), Hkv=Hkv, dtype=KVC_F16, split=split)
+    synchronize()
+    shape = (W["nb"], Hkv, B, D)
+    kp, vp = k.to_numpy(np.float16, shape), v.to_numpy(np.float16, shape)
+    q = W["q"].to_numpy(np.float16, (N, Hq, D))
+    got = W["out"].to_numpy(np.float16, (N, Hq, D)).astype(np.float64)
+    ref = oracle.batched_paged(q, kp, vp, W["table"], W["tab_off"], lens, Hkv, B, 1.0 / np.sqrt(D),
+                               nthreads=min(os.cpu_count() or 1, 16))
+    return float(np.abs(got - ref).max()), (q, kp, vp)
+
+
+def cpu_baseline(host_data, W, lens, Hkv, B, D, budget_s, kv_bytes):
+    """The oracle (C++ restatement, double accumulation) on the host cores: full
+    passes over the same workload repeated until ~budget_s of wall time."""
+    import oracle
+
+    q, kp, vp = host_data
+    threads = min(os.cpu_count() or 1, 16)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        oracle.batched_paged(q, kp, vp, W["table"], W["tab_off"], lens, Hkv, B, 1.0 / np.sqrt(D), nthreads=threads)
+        reps += 1
+        if time.perf_counter() - t0 >= budget_s or reps >= 2000:
+            break
+    dt = (time.perf_counter() - t0) / reps
+    t1 = time.perf_counter()
+    oracle.batched_paged(q, kp, vp, W["table"], W["tab_off"], lens, Hkv, B, 1.0 / np.sqrt(D), nthreads=1)
+    dt1 = time.perf_counter() - t1
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(kv_bytes / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{reps} full passes of the N=128 ragged batch (oracle/oracle.cpp, double accumulation over "
+                      f"the same fp16 pool), {threads} threads, {reps * dt:.1f} s",
+            "single_thread_GBps": round(kv_bytes / dt1 / 1e9, 3), "cpu_model": cpu_model,
+            "host_cpus": os.cpu_count()}
+
+
+def bench_c3(steps, warmup):
+    """Config 3: Hq 14 / Hkv 2, D 64, lengths {8192,16384,32768,32768}, 512-token splits."""
+    lens = np.array([8192, 16384, 32768, 32768], np.int32)
+    Hq, Hkv, D, B = 14, 2, 64, 16
+    W = build_c2(lens, Hq, Hkv, D, B, rotate=8, seed=3)   # 8 x 46 MB rotate past the Infinity Cache
+    per, _ = time_decode(W, lens, Hq, Hkv, D, B, 512, steps, warmup)
+    kv, total = alg_bytes(lens, Hq, Hkv, D, B)
+    t = float(np.mean(per))
+    return {"workload": "C3 long-context split-K 14q/2kv D64 ctx {8k,16k,32k,32k} fp16 split 512",
+            "us_per_step": round(t * 1e3, 2), "GBps": round(total / (t * 1e-3) / 1e9, 1),
+            "frac_hbm_peak": round(total / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "kv_bytes": kv}
+
+
+def bench_c4():
+    """Config 4: 256 requests, width 32, 2048 MB pool, 24 layers of write + GQA decode
+    per step (14q/2kv, D 64, fp16); continuous vs static, offline and Poisson 400/s."""
+    from kvcache_amd import KVC_F16
+    from kvcache_amd import workloads as Wl
+    from kvcache_amd.engine import Engine, EngineConfig, run_continuous, run_static
+
+    num_blocks = (2048 * 1024 * 1024) // (24 * 2 * 16 * 64 * 2 * 2)
+    cfg = EngineConfig(n_heads=14, n_kv_heads=2, head_dim=64, block_size=16, num_blocks=num_blocks, max_batch=32,
+                       n_layers=24, dtype=KVC_F16, kv_write=True, clock_mode=0)
+    eng = Engine(cfg)
+    out = {"workload": "C4 256 requests, width 32, 2048 MB pool, 24 layers write+decode, 14q/2kv D64 fp16",
+           "num_blocks": num_blocks}
+    for name, trace in (("offline", Wl.baseline_trace(256, 0.0, 11)), ("poisson400", Wl.baseline_trace(256, 400.0, 11)),
+                        ("ref_offline", Wl.ref_trace())):
+        p, g, a = trace
+        res = {}
+        for pol, fn in (("continuous", lambda: run_continuous(p, g, a, eng)),
+                        ("static", lambda: run_static(p, g, a, eng, 32))):
+            st = fn()
+            res[pol] = {"iters": st.iters, "tokens": st.tokens,
+                        "tokens_per_s": round(st.tokens / (st.wall_us * 1e-6), 1) if st.wall_us else 0.0,
+                        "host_tokens_per_s": round(st.tokens / (st.host_wall_us * 1e-6), 1),
+                        "slot_util": round(st.slot_util, 4), "avg_batch": round(st.avg_batch, 2),
+                        "peak_blocks": st.peak_blocks, "p50_ms": round(st.p50_latency_us / 1e3, 3),
+                        "p99_ms": round(st.p99_latency_us / 1e3, 3), "avg_ms": round(st.avg_latency_us / 1e3, 3),
+                        "gpu_ms": round(st.gpu_us / 1e3, 2), "makespan_ms": round(st.wall_us / 1e3, 2)}
+        out[name] = res
+    return out
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--split", type=int, default=0, help="decode split size in tokens (0 = automatic)")
+    ap.add_argument("--rotate", type=int, default=4, help="pool copies cycled by the timed loop")
+    ap.add_argument("--lengths", choices=["reference", "loguniform"], default="reference")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extras", action="store_true", help="skip configs 3 and 4")
+    ap.add_argument("--sweep", type=str, default="", help="comma list of split sizes to time (diagnostic)")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py: this build targets one GPU; --gpus {a.gpus} is not supported (collectives and sharding "
+              "are out of scope -- see DESIGN.md for how the path would shard)", file=sys.stderr)
+        return 2
+
+    from kvcache_amd import ops
+    from kvcache_amd.device import has_device
+    from kvcache_amd import workloads as Wl
+
+    if not has_device():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 1
+    lens = Wl.ref_lengths() if a.lengths == "reference" else Wl.loguniform_lengths(128, 16, 2048, 7)
+    N, Hq, Hkv, D, B = 128, 8, 8, 64, 16
+    split = a.split or ops.decode_auto_split(N, Hq, Hkv, D, B, int(lens.max()))
+    log(f"C2: N={N} sum_len={int(lens.sum())} max={int(lens.max())} split={split} rotate={a.rotate}")
+    W = build_c2(lens, Hq, Hkv, D, B, a.rotate, seed=12345)
+    err, host_data = check_c2(W, lens, Hq, Hkv, D, B, split)
+    log(f"parity vs oracle: max abs err {err:.3e} (bar 2e-3)")
+    if not err <= 2e-3:
+        print(json.dumps({"metric": METRIC, "error": f"parity failure: max abs err {err}"}))
+        return 1
+    kv, total = alg_bytes(lens, Hq, Hkv, D, B)
+
+    sweep = {}
+    for s in [int(x) for x in a.sweep.split(",") if x]:
+        per, _ = time_decode(W, lens, Hq, Hkv, D, B, s, 20, 5)
+        sweep[s] = round(float(np.mean(per)) * 1e3, 2)
+        log(f"sweep split={s}: {sweep[s]} us")
+
+    per, total_ms = time_decode(W, lens, Hq, Hkv, D, B, split, a.steps, a.warmup)
+    t_launch = float(np.mean(per))              # ms, mean of per-launch event intervals
+    ms_per_step = total_ms / a.steps
+    achieved = total / (t_launch * 1e-3) / 1e9
+    log(f"C2 cold: {t_launch * 1e3:.2f} us/launch (median {np.median(per) * 1e3:.2f}), {achieved:.1f} GB/s")
+    warm_per, _ = time_decode({**W, "pools": W["pools"][:1]}, lens, Hq, Hkv, D, B, split, a.steps, a.warmup)
+    warm = total / (float(np.mean(warm_per)) * 1e-3) / 1e9
+    log(f"C2 warm (one pool, Infinity-Cache resident): {np.mean(warm_per) * 1e3:.2f} us, {warm:.1f} GB/s")
+
+    extras = {}
+    if not a.no_extras:
+        del W["pools"]
+        try:
+            extras["c3"] = bench_c3(a.steps, a.warmup)
+            log(f"C3: {extras['c3']}")
+        except Exception as e:  # noqa: BLE001 -- extras never hide the headline
+            extras["c3"] = {"error": repr(e)}
+        try:
+            extras["c4"] = bench_c4()
+            log(f"C4: {json.dumps(extras['c4'])}")
+        except Exception as e:  # noqa: BLE001
+            extras["c4"] = {"error": repr(e)}
+
+    cpu = None
+    if not a.no_cpu_baseline:
+        cpu = cpu_baseline(host_data, W, lens, Hkv, B, D, a.cpu_seconds, kv)
+        log(f"CPU baseline: {cpu}")
+
+    line = {
+        "metric": METRIC, "value": round(achieved, 1), "unit": "GB/s", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": round(ms_per_step, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f16", "data": "synthetic",
+        "config": {"workload": "C2 batched ragged paged decode: N=128, reference lengths (seed 12345, sum 83212, "
+                               "max 2022), H=8 (MHA), D=64, BLOCK=16, fp16 KV, fp32 accumulate, shuffled free list",
+                   "lengths": a.lengths, "split_tokens": split, "rotating_pool_copies": a.rotate,
+                   "parallelism": "single GPU"},
+        "pct_hbm_peak": round(100 * achieved / HBM_PEAK_GBS, 2),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "split_kernel<_Float16,64,1,kPagedUniform> (fused LSE merge)",
+                     "algorithmic_bytes_per_launch": total, "kv_bytes_per_launch": kv,
+                     "mean_launch_us": round(t_launch * 1e3, 3)},
+        "warm_GBps": round(warm, 1),
+        "parity_max_abs_err": err,
+        "cpu_baseline": cpu,
+        "extras": extras,
+    }
+    if sweep:
+        line["split_sweep_us"] = sweep
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

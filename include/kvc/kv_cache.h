@@ -1,0 +1,82 @@
+// kv_cache.h -- reference-named kernel launchers over the C ABI (kvc_abi.h).
+//
+// Same names, argument order and layouts as the reference's
+// src/include/kv_cache.h:2-34 (fp32, MHA, null stream) and the fp16 GQA
+// launchers of src/include/qwen_kernels.h:15-37, so existing call sites compile
+// unchanged.  Differences a caller can see:
+//   * each launcher returns the kvc_status (0 = ok) instead of void; the last
+//     failure message is kvc_last_error();
+//   * launch_batched_paged and launch_batched_paged_flash run the same kernel
+//     (online fp32 softmax with split-K), so they agree bit for bit;
+//   * launch_flash_decode allocates nothing per call: its partials live in a
+//     grow-only library workspace (pass your own through kvc_flash_decode).
+// Optional trailing arguments select a stream (hipStream_t as void*).
+#pragma once
+#include <hip/hip_fp16.h>
+
+#include "../kvc_abi.h"
+
+inline int launch_append(const float* k_new, const float* v_new, float* k_cache, float* v_cache, int pos, int H,
+                         int D, int S, kvc_stream_t stream = nullptr) {
+    return kvc_append(k_new, v_new, k_cache, v_cache, pos, H, D, S, KVC_F32, stream);
+}
+
+inline int launch_decode(const float* q, const float* k_cache, const float* v_cache, float* out, int cur_len, int H,
+                         int D, int S, float scale, kvc_stream_t stream = nullptr) {
+    return kvc_decode(q, k_cache, v_cache, out, cur_len, H, D, S, scale, KVC_F32, stream);
+}
+
+inline int launch_paged(const float* q, const float* k_pool, const float* v_pool, const int* block_table, float* out,
+                        int cur_len, int H, int D, int BLOCK, float scale, kvc_stream_t stream = nullptr) {
+    return kvc_paged_decode(q, k_pool, v_pool, block_table, out, cur_len, H, D, BLOCK, scale, KVC_F32, stream);
+}
+
+inline int launch_batched_decode(const float* q, const float* k_cache, const float* v_cache, const int* cur_len,
+                                 float* out, int N, int H, int D, int MAXS, int cap, float scale,
+                                 kvc_stream_t stream = nullptr) {
+    return kvc_batched_decode(q, k_cache, v_cache, cur_len, out, N, H, H, D, MAXS, cap, scale, KVC_F32, nullptr, 0,
+                              stream);
+}
+
+inline int launch_batched_paged(const float* q, const float* k_pool, const float* v_pool, const int* table_all,
+                                const int* tab_off, const int* cur_len, float* out, int N, int H, int D, int BLOCK,
+                                int cap, float scale, kvc_stream_t stream = nullptr) {
+    return kvc_batched_paged_decode(q, k_pool, v_pool, table_all, tab_off, cur_len, out, N, H, H, D, BLOCK, cap, scale,
+                                    KVC_F32, nullptr, 0, stream);
+}
+
+inline int launch_batched_paged_flash(const float* q, const float* k_pool, const float* v_pool, const int* table_all,
+                                      const int* tab_off, const int* cur_len, float* out, int N, int H, int D,
+                                      int BLOCK, int cap, float scale, kvc_stream_t stream = nullptr) {
+    return launch_batched_paged(q, k_pool, v_pool, table_all, tab_off, cur_len, out, N, H, D, BLOCK, cap, scale,
+                                stream);
+}
+
+inline int launch_flash_decode(const float* q, const float* k_cache, const float* v_cache, float* out, int cur_len,
+                               int H, int D, int S, float scale, int num_splits, kvc_stream_t stream = nullptr) {
+    return kvc_flash_decode(q, k_cache, v_cache, out, cur_len, H, D, S, scale, num_splits, KVC_F32, nullptr, 0,
+                            stream);
+}
+
+// ---- fp16 / GQA family (qwen_kernels.h:15-37) --------------------------------
+inline int qk_write_kv(const half* k, const half* v, half* k_pool, half* v_pool, const int* block_table_dev,
+                       int start_pos, int L, int Hkv, int D, int BLOCK, kvc_stream_t stream = nullptr) {
+    return kvc_write_kv(k, v, k_pool, v_pool, block_table_dev, start_pos, L, Hkv, D, BLOCK, KVC_F16, stream);
+}
+
+inline int qk_batched_write_kv(const half* k, const half* v, half* k_pool, half* v_pool, const int* table_all,
+                               const int* tab_off, const int* wpos, int N, int Hkv, int D, int BLOCK,
+                               kvc_stream_t stream = nullptr) {
+    return kvc_batched_write_kv(k, v, k_pool, v_pool, table_all, tab_off, wpos, N, Hkv, D, BLOCK, KVC_F16, stream);
+}
+
+// The reference sizes nothing by the longest sequence here; the split-K plan
+// needs an upper bound, so `cap` (max cur_len) is an extra trailing argument
+// with a generous default.
+inline int qk_batched_paged_decode_attn(const half* q, half* out, const half* k_pool, const half* v_pool,
+                                        const int* table_all, const int* tab_off, const int* cur_len, int N, int Hq,
+                                        int Hkv, int D, int BLOCK, float scale, int cap = 32768,
+                                        kvc_stream_t stream = nullptr) {
+    return kvc_batched_paged_decode(q, k_pool, v_pool, table_all, tab_off, cur_len, out, N, Hq, Hkv, D, BLOCK, cap,
+                                    scale, KVC_F16, nullptr, 0, stream);
+}

@@ -1,0 +1,210 @@
+// model_runner.h -- executes one decode step of a running batch on the GPU.
+//
+// Drop-in for the reference's ModelRunner (src/include/model_runner.h:28-84):
+// same constructor (n_heads, head_dim, block_size, max_batch, max_pool_blocks)
+// and decode_step(batch, kvm) -> step time in us, with the same packing
+// (model_runner.h:61-69): block tables concatenated in batch order, offsets,
+// lengths clamped to >= 1.  What changes on MI355X:
+//   * the step's metadata {N, tab_off[N+1], len[N], wpos[N], slot[N], table_all}
+//     is packed into ONE pinned host buffer (a ring of them, so the host can
+//     run ahead of the GPU) and moved with ONE async copy (kvc_step_upload)
+//     instead of three blocking cudaMemcpy;
+//   * GQA (n_kv_heads < n_heads), fp16 KV and n_layers layer slices;
+//   * with kv_write the step follows the model path (qwen_serve.cu:130-160):
+//     per layer, the new token's K/V go to slot[r] (= phys*BLOCK + pos%BLOCK,
+//     precomputed here) and attention covers cur_len (which already includes it);
+//   * every packed step is folded into an FNV-1a digest so the schedule can be
+//     compared bit for bit with an independent restatement;
+//   * the clock is either measured (events around the step's kernels, as the
+//     reference) or a deterministic cost model c0 + c1*N + c2*sum(len).
+// Query/key/value inputs are synthetic N(0,1) buffers filled once on the device.
+#pragma once
+#include <algorithm>
+#include <cstdint>
+#include <cstring>
+#include <vector>
+
+#include "../kvc_abi.h"
+#include "kv_cache_manager.h"
+#include "sequence.h"
+
+struct RunnerOptions {
+    int n_kv_heads = 0;      // 0: = n_heads (MHA)
+    int n_layers = 1;
+    int dtype = KVC_F32;
+    bool kv_write = false;
+    int clock_mode = 0;      // 0 measured, 1 virtual
+    double c0 = 0, c1 = 0, c2 = 0;
+    bool device = true;
+    int split_tokens = 0;    // 0: automatic
+    uint64_t seed = 0x6b76636163686531ull;
+};
+
+struct ModelRunner {
+    static constexpr int kRing = 4;
+    int n_heads, head_dim, block_size, max_batch, max_pool_blocks;
+    float scale;
+    RunnerOptions opt;
+    int n_kv_heads;
+
+    void *dq = nullptr, *dk = nullptr, *dv = nullptr, *dout = nullptr;
+    int* d_meta = nullptr;
+    int* h_meta[kRing] = {};
+    void* h_ev[kRing] = {};
+    bool h_ev_used[kRing] = {};
+    int ring = 0;
+    void *ev0 = nullptr, *ev1 = nullptr;
+    kvc_stream_t stream = nullptr;
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
+
+    std::vector<int> h_tab, h_off, h_len, h_wpos, h_slot;
+    uint64_t digest = 1469598103934665603ull;
+    long long last_sum_len = 0;
+    int last_cap = 0;
+
+    ModelRunner(int n_heads_, int head_dim_, int block_size_, int max_batch_, int max_pool_blocks_,
+                const RunnerOptions& o = RunnerOptions())
+        : n_heads(n_heads_), head_dim(head_dim_), block_size(block_size_), max_batch(max_batch_),
+          max_pool_blocks(max_pool_blocks_), scale(1.0f / __builtin_sqrtf((float)head_dim_)), opt(o),
+          n_kv_heads(o.n_kv_heads > 0 ? o.n_kv_heads : n_heads_) {
+        if (n_heads <= 0 || head_dim <= 0 || block_size <= 0 || max_batch <= 0 || max_pool_blocks <= 0)
+            throw kvc::Error(KVC_ERR_ARG, "ModelRunner: sizes must be positive");
+        if (n_heads % n_kv_heads) throw kvc::Error(KVC_ERR_ARG, "ModelRunner: n_heads % n_kv_heads != 0");
+        if (opt.n_layers <= 0) opt.n_layers = 1;
+        h_tab.reserve(max_pool_blocks);
+        h_off.reserve(max_batch + 1);
+        h_len.reserve(max_batch);
+        if (!opt.device) return;
+        const size_t es = kvc::dtype_size(opt.dtype);
+        const size_t nq = (size_t)opt.n_layers * max_batch * n_heads * head_dim;
+        const size_t nkv = (size_t)opt.n_layers * max_batch * n_kv_heads * head_dim;
+        kvc::check(kvc_stream_create(&stream), "ModelRunner stream");
+        kvc::check(kvc_malloc(&dq, nq * es), "ModelRunner q");
+        kvc::check(kvc_malloc(&dk, nkv * es), "ModelRunner k");
+        kvc::check(kvc_malloc(&dv, nkv * es), "ModelRunner v");
+        kvc::check(kvc_malloc(&dout, (size_t)max_batch * n_heads * head_dim * es), "ModelRunner out");
+        kvc::check(kvc_malloc((void**)&d_meta, meta_ints() * sizeof(int)), "ModelRunner meta");
+        for (int i = 0; i < kRing; ++i) {
+            kvc::check(kvc_host_alloc((void**)&h_meta[i], meta_ints() * sizeof(int)), "ModelRunner pinned meta");
+            kvc::check(kvc_event_create(&h_ev[i]), "ModelRunner event");
+        }
+        kvc::check(kvc_event_create(&ev0), "ModelRunner event");
+        kvc::check(kvc_event_create(&ev1), "ModelRunner event");
+        kvc::check(kvc_fill_normal(dq, nq, opt.dtype, opt.seed, 1.0f, stream), "ModelRunner fill q");
+        kvc::check(kvc_fill_normal(dk, nkv, opt.dtype, opt.seed + 1, 1.0f, stream), "ModelRunner fill k");
+        kvc::check(kvc_fill_normal(dv, nkv, opt.dtype, opt.seed + 2, 1.0f, stream), "ModelRunner fill v");
+        kvc::check(kvc_stream_synchronize(stream), "ModelRunner init");
+    }
+    ~ModelRunner() {
+        if (stream) kvc_stream_synchronize(stream);
+        kvc_free(dq); kvc_free(dk); kvc_free(dv); kvc_free(dout); kvc_free(d_meta); kvc_free(ws);
+        for (int i = 0; i < kRing; ++i) { kvc_host_free(h_meta[i]); kvc_event_destroy(h_ev[i]); }
+        kvc_event_destroy(ev0); kvc_event_destroy(ev1);
+        kvc_stream_destroy(stream);
+    }
+    ModelRunner(const ModelRunner&) = delete;
+    ModelRunner& operator=(const ModelRunner&) = delete;
+
+    size_t meta_ints() const { return 1 + (size_t)(max_batch + 1) + 3 * (size_t)max_batch + max_pool_blocks; }
+    void reset_digest() { digest = 1469598103934665603ull; }
+    void fold(int32_t x) {
+        const uint32_t u = (uint32_t)x;
+        for (int i = 0; i < 4; ++i) { digest ^= (u >> (8 * i)) & 0xffu; digest *= 1099511628211ull; }
+    }
+    // Synthetic per-layer inputs ([n_layers][max_batch][H][D]).
+    void* q_layer(int l) const { return (char*)dq + (size_t)l * max_batch * n_heads * head_dim * kvc::dtype_size(opt.dtype); }
+    void* k_layer(int l) const { return (char*)dk + (size_t)l * max_batch * n_kv_heads * head_dim * kvc::dtype_size(opt.dtype); }
+    void* v_layer(int l) const { return (char*)dv + (size_t)l * max_batch * n_kv_heads * head_dim * kvc::dtype_size(opt.dtype); }
+
+    // One decode step over `batch`.  wpos (kv_write only): per sequence the position
+    // its new K/V are written to this step, or -1 for a slot that only idles.
+    double decode_step(const std::vector<Sequence*>& batch, KVCacheManager& kvm, const int* wpos = nullptr) {
+        const int n = (int)batch.size();
+        if (n == 0) return 0.0;
+        if (n > max_batch) throw kvc::Error(KVC_ERR_ARG, "decode_step: batch larger than max_batch");
+        h_tab.clear(); h_off.clear(); h_len.clear(); h_wpos.clear(); h_slot.clear();
+        int cap = 1;
+        long long sum_len = 0;
+        for (int r = 0; r < n; ++r) {
+            const Sequence* s = batch[r];
+            h_off.push_back((int)h_tab.size());
+            h_tab.insert(h_tab.end(), s->block_table.begin(), s->block_table.end());
+            const int L = s->cur_len > 0 ? s->cur_len : 1;
+            h_len.push_back(L);
+            cap = std::max(cap, L);
+            sum_len += L;
+            if (opt.kv_write) {
+                const int p = wpos ? wpos[r] : -1;
+                h_wpos.push_back(p);
+                h_slot.push_back(p >= 0 ? s->block_table[p / block_size] * block_size + p % block_size : -1);
+            }
+        }
+        h_off.push_back((int)h_tab.size());
+        if ((int)h_tab.size() > max_pool_blocks) throw kvc::Error(KVC_ERR_ARG, "decode_step: tables exceed max_pool_blocks");
+        fold(n);
+        for (int x : h_off) fold(x);
+        for (int x : h_len) fold(x);
+        if (opt.kv_write) for (int x : h_wpos) fold(x);
+        for (int x : h_tab) fold(x);
+        last_sum_len = sum_len;
+        last_cap = cap;
+        const double virt = opt.c0 + opt.c1 * (double)n + opt.c2 * (double)sum_len;
+        if (!opt.device) return virt;
+        if (!kvm.has_device()) throw kvc::Error(KVC_ERR_STATE, "decode_step: KV manager has no device pools");
+
+        // pack: [N | off N+1 | len N | wpos N | slot N | tab T]
+        if (h_ev_used[ring]) kvc::check(kvc_event_synchronize(h_ev[ring]), "meta ring wait");
+        int* h = h_meta[ring];
+        size_t o = 0;
+        h[o++] = n;
+        std::memcpy(h + o, h_off.data(), h_off.size() * sizeof(int)); o += h_off.size();
+        std::memcpy(h + o, h_len.data(), n * sizeof(int)); o += n;
+        if (opt.kv_write) {
+            std::memcpy(h + o, h_wpos.data(), n * sizeof(int));
+            std::memcpy(h + o + n, h_slot.data(), n * sizeof(int));
+        }
+        o += 2 * (size_t)n;
+        std::memcpy(h + o, h_tab.data(), h_tab.size() * sizeof(int)); o += h_tab.size();
+        kvc::check(kvc_step_upload(d_meta, h, o * sizeof(int), stream), "step upload");
+        kvc::check(kvc_event_record(h_ev[ring], stream), "meta ring record");
+        h_ev_used[ring] = true;
+        ring = (ring + 1) % kRing;
+        const int* d_off = d_meta + 1;
+        const int* d_len = d_off + n + 1;
+        const int* d_slot = d_len + 2 * n;
+        const int* d_tab = d_len + 3 * n;
+
+        const size_t need = kvc_decode_workspace_size(n, n_heads, n_kv_heads, head_dim, block_size, cap,
+                                                      opt.split_tokens, opt.dtype);
+        if (need > ws_bytes) {
+            kvc::check(kvc_stream_synchronize(stream), "workspace growth");
+            kvc_free(ws);
+            ws = nullptr;
+            ws_bytes = 0;
+            const size_t sz = std::max(need * 2, (size_t)1 << 20);
+            kvc::check(kvc_malloc(&ws, sz), "decode workspace");
+            ws_bytes = sz;
+        }
+        kvc::check(kvc_event_record(ev0, stream), "event");
+        for (int l = 0; l < opt.n_layers; ++l) {
+            if (opt.kv_write)
+                kvc::check(kvc_write_kv_slots(k_layer(l), v_layer(l), kvm.k_layer(l), kvm.v_layer(l), d_slot, n,
+                                              n_kv_heads, head_dim, block_size, opt.dtype, stream),
+                           "write_kv");
+            kvc::check(kvc_batched_paged_decode_split(q_layer(l), kvm.k_layer(l), kvm.v_layer(l), d_tab, d_off, d_len,
+                                                      dout, n, n_heads, n_kv_heads, head_dim, block_size, cap, scale,
+                                                      opt.dtype, opt.split_tokens, ws, ws_bytes, stream),
+                       "paged decode");
+        }
+        kvc::check(kvc_event_record(ev1, stream), "event");
+        if (opt.clock_mode != 0) return virt;
+        float ms = 0.f;
+        kvc::check(kvc_event_elapsed_ms(&ms, ev0, ev1), "event elapsed");
+        return (double)ms * 1e3;
+    }
+
+    void synchronize() {
+        if (stream) kvc::check(kvc_stream_synchronize(stream), "ModelRunner sync");
+    }
+};

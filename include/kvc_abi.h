@@ -1,0 +1,239 @@
+/* kvc_abi.h -- C ABI of the MI355X (gfx950) paged-decode library libkvcache_amd.so.
+ *
+ * Drop-in boundary for the decode hot path of kimxinw/kvcache.  Every kernel
+ * entry point mirrors one reference launcher (argument order kept, cited as
+ * reference file:line) and extends it with:
+ *   - an element type `dtype` (KVC_F32 as the reference, or KVC_F16),
+ *   - separate query / KV head counts (Hq, Hkv) for grouped-query attention,
+ *   - an explicit HIP stream (`stream` is a hipStream_t; NULL = null stream),
+ *   - caller-provided workspace for split-K partials (NULL = a grow-only buffer
+ *     owned by the library, allocated on first need),
+ *   - an int status instead of void: 0 = KVC_OK, otherwise a KVC_ERR_* code,
+ *     with a readable message from kvc_last_error().
+ * No function throws across this boundary.  All launches are asynchronous on
+ * `stream`; every pointer argument named *_pool, *_cache, q, out, k, v, table*
+ * or *len* is a device pointer unless stated otherwise.
+ *
+ * Layouts (elements of dtype):
+ *   contiguous cache [H(kv), S, D] (single sequence) or [N, Hkv, MAXS, D];
+ *   paged pool       [num_blocks, Hkv, BLOCK, D]  (reference kv_cache_manager.h:30);
+ *   q / out          [N, Hq, D];
+ *   table_all        concatenated block tables, sequence s starts at tab_off[s].
+ */
+#ifndef KVC_ABI_H
+#define KVC_ABI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* kvc_stream_t; /* a hipStream_t */
+
+enum kvc_status {
+    KVC_OK = 0,
+    KVC_ERR_ARG = 1,         /* bad shape / null pointer / out-of-range argument */
+    KVC_ERR_UNSUPPORTED = 2, /* shape the kernels do not implement (e.g. head_dim) */
+    KVC_ERR_HIP = 3,         /* a HIP runtime call failed */
+    KVC_ERR_NOMEM = 4,       /* device or pinned allocation failed / pool exhausted */
+    KVC_ERR_WORKSPACE = 5,   /* caller workspace smaller than required */
+    KVC_ERR_STATE = 6        /* call not valid in the object's current state */
+};
+enum kvc_dtype { KVC_F32 = 0, KVC_F16 = 1 };
+
+/* ---- library ---------------------------------------------------------- */
+int         kvc_version(void);                 /* 100*major + minor */
+const char* kvc_status_string(int status);
+const char* kvc_last_error(void);               /* last failure on this host thread */
+int         kvc_device_count(int* count);
+/* Tuning knobs (process-wide): "fused_merge" (1: the last-arriving chunk of a
+ * sequence merges the split partials inside the decode kernel; 0: a separate merge
+ * kernel), "target_units" (automatic split: waves to aim for), "min_chunk_bytes"
+ * (automatic split: least K+V bytes per wave). */
+int         kvc_set_tuning(const char* key, int value);
+int         kvc_get_tuning(const char* key, int* value);
+
+/* ---- device memory / stream / event plumbing (thin HIP wrappers) ------- */
+int kvc_malloc(void** dptr, size_t bytes);
+int kvc_free(void* dptr);
+int kvc_host_alloc(void** hptr, size_t bytes);  /* pinned host memory */
+int kvc_host_free(void* hptr);
+int kvc_memcpy_h2d(void* dst, const void* src, size_t bytes, kvc_stream_t stream);
+int kvc_memcpy_d2h(void* dst, const void* src, size_t bytes, kvc_stream_t stream);
+int kvc_memcpy_d2d(void* dst, const void* src, size_t bytes, kvc_stream_t stream);
+int kvc_memset(void* dst, int value, size_t bytes, kvc_stream_t stream);
+int kvc_stream_create(kvc_stream_t* stream);    /* default priority */
+int kvc_stream_destroy(kvc_stream_t stream);
+int kvc_stream_synchronize(kvc_stream_t stream);
+int kvc_device_synchronize(void);
+int kvc_event_create(void** ev);
+int kvc_event_destroy(void* ev);
+int kvc_event_record(void* ev, kvc_stream_t stream);
+int kvc_event_synchronize(void* ev);
+int kvc_event_elapsed_ms(float* ms, void* start, void* stop); /* synchronizes on stop */
+
+/* One packed per-step upload: copies `bytes` from (preferably pinned) host
+ * memory to the device with a single async copy on `stream`.  Replaces the
+ * three blocking cudaMemcpy of model_runner.h:70-72. */
+int kvc_step_upload(void* dst_device, const void* src_host, size_t bytes, kvc_stream_t stream);
+
+/* Deterministic N(0, stddev^2) fill of n elements of dtype (synthetic K/V/q). */
+int kvc_fill_normal(void* dst, size_t n, int dtype, uint64_t seed, float stddev, kvc_stream_t stream);
+
+/* ---- K/V append ------------------------------------------------------- */
+/* launch_append (kv_cache.h:2-4, kv_cache.cu:5-19): k_new/v_new [H,D] -> cache[h,pos,:] of [H,S,D]. */
+int kvc_append(const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+               int pos, int H, int D, int S, int dtype, kvc_stream_t stream);
+
+/* qk_write_kv (qwen_kernels.h:15-16, qwen_kernels.cu:111-126): L tokens k/v [L,Hkv,D]
+ * into the paged pool at positions start_pos..start_pos+L-1 of one block table. */
+int kvc_write_kv(const void* k, const void* v, void* k_pool, void* v_pool,
+                 const int* block_table, int start_pos, int L, int Hkv, int D, int BLOCK,
+                 int dtype, kvc_stream_t stream);
+
+/* qk_batched_write_kv (qwen_kernels.h:30-32, qwen_kernels.cu:270-290): one token per
+ * sequence, k/v [N,Hkv,D] -> pool at position wpos[r] of table table_all+tab_off[r].
+ * Rows with wpos[r] < 0 are skipped. */
+int kvc_batched_write_kv(const void* k, const void* v, void* k_pool, void* v_pool,
+                         const int* table_all, const int* tab_off, const int* wpos,
+                         int N, int Hkv, int D, int BLOCK, int dtype, kvc_stream_t stream);
+
+/* Slot-mapped write (no reference counterpart; the scheduler precomputes
+ * slot = phys*BLOCK + pos%BLOCK per row): k/v [rows,Hkv,D] -> pool; slot < 0 skips. */
+int kvc_write_kv_slots(const void* k, const void* v, void* k_pool, void* v_pool,
+                       const int* slot_map, int rows, int Hkv, int D, int BLOCK,
+                       int dtype, kvc_stream_t stream);
+
+/* ---- decode attention --------------------------------------------------- */
+/* launch_decode (kv_cache.h:5-6, decode_attn.cu:5-52): one sequence, contiguous [H,S,D]. */
+int kvc_decode(const void* q, const void* k_cache, const void* v_cache, void* out,
+               int cur_len, int H, int D, int S, float scale, int dtype, kvc_stream_t stream);
+
+/* launch_paged (kv_cache.h:9-11, paged.cu:7-62): one sequence, pool [NB,H,BLOCK,D].
+ * Bit-identical to kvc_decode on the same logical data. */
+int kvc_paged_decode(const void* q, const void* k_pool, const void* v_pool,
+                     const int* block_table, void* out, int cur_len,
+                     int H, int D, int BLOCK, float scale, int dtype, kvc_stream_t stream);
+
+/* launch_batched_decode (kv_cache.h:15-17, batched.cu:49-88,132-138): caches
+ * [N,Hkv,MAXS,D], lengths cur_len[N] (device), cap = max length (host). */
+int kvc_batched_decode(const void* q, const void* k_cache, const void* v_cache,
+                       const int* cur_len, void* out, int N, int Hq, int Hkv, int D,
+                       int MAXS, int cap, float scale, int dtype,
+                       void* workspace, size_t workspace_bytes, kvc_stream_t stream);
+
+/* launch_batched_paged / launch_batched_paged_flash (kv_cache.h:20-27,
+ * batched.cu:97-147,157-207) and qk_batched_paged_decode_attn (qwen_kernels.h:35-37,
+ * qwen_kernels.cu:293-335): one query per sequence over its pages [0,cur_len[s]).
+ * Bit-identical to kvc_batched_decode on the same logical data. */
+int kvc_batched_paged_decode(const void* q, const void* k_pool, const void* v_pool,
+                             const int* table_all, const int* tab_off, const int* cur_len,
+                             void* out, int N, int Hq, int Hkv, int D, int BLOCK, int cap,
+                             float scale, int dtype,
+                             void* workspace, size_t workspace_bytes, kvc_stream_t stream);
+
+/* Same as kvc_batched_paged_decode with an explicit split size: each sequence is
+ * cut into chunks of split_tokens tokens (a multiple of BLOCK; 0 = automatic),
+ * chunks run in parallel and are merged by log-sum-exp.  Long-context split-K
+ * (flash_decode.cu:103-126 generalised to paged, batched, GQA). */
+int kvc_batched_paged_decode_split(const void* q, const void* k_pool, const void* v_pool,
+                                   const int* table_all, const int* tab_off, const int* cur_len,
+                                   void* out, int N, int Hq, int Hkv, int D, int BLOCK, int cap,
+                                   float scale, int dtype, int split_tokens,
+                                   void* workspace, size_t workspace_bytes, kvc_stream_t stream);
+
+/* kvc_batched_decode with an explicit split size (any positive token count). */
+int kvc_batched_decode_split(const void* q, const void* k_cache, const void* v_cache,
+                             const int* cur_len, void* out, int N, int Hq, int Hkv, int D,
+                             int MAXS, int cap, float scale, int dtype, int split_tokens,
+                             void* workspace, size_t workspace_bytes, kvc_stream_t stream);
+
+/* Workspace (bytes) needed by the batched calls for a batch of N sequences whose
+ * longest is cap tokens, with split_tokens as given (0 = the automatic choice).
+ * BLOCK = 0 for the contiguous calls. */
+size_t kvc_decode_workspace_size(int N, int Hq, int Hkv, int D, int BLOCK, int cap, int split_tokens, int dtype);
+/* The split size the automatic choice picks for this shape (BLOCK = 0: contiguous). */
+int kvc_decode_auto_split(int N, int Hq, int Hkv, int D, int BLOCK, int cap, int dtype);
+
+/* launch_flash_decode (kv_cache.h:32-34, flash_decode.cu:103-126): one sequence,
+ * contiguous [H,S,D], num_splits clamped to [1, cur_len]; split j covers
+ * [j*ceil(L/ns), ...) and the partials are merged by log-sum-exp.  Unlike the
+ * reference it allocates nothing: partials go to `workspace`. */
+int kvc_flash_decode(const void* q, const void* k_cache, const void* v_cache, void* out,
+                     int cur_len, int H, int D, int S, float scale, int num_splits, int dtype,
+                     void* workspace, size_t workspace_bytes, kvc_stream_t stream);
+size_t kvc_flash_decode_workspace_size(int H, int D, int num_splits);
+
+/* ---- block free-list (block_alloc.h:10-43), host only ------------------- */
+typedef struct kvc_block_allocator kvc_block_allocator;
+int  kvc_block_allocator_create(int total_blocks, kvc_block_allocator** out);
+void kvc_block_allocator_destroy(kvc_block_allocator* a);
+int  kvc_block_allocator_alloc(kvc_block_allocator* a);   /* block id, or -1 when empty */
+void kvc_block_allocator_free(kvc_block_allocator* a, const int* blocks, int n);
+void kvc_block_allocator_reset(kvc_block_allocator* a);
+int  kvc_block_allocator_free_count(const kvc_block_allocator* a);
+int  kvc_block_allocator_used_count(const kvc_block_allocator* a);
+/* Permute the current free list with a seeded Fisher-Yates shuffle so later
+ * allocations come out in a random physical order (fragmented pool workloads). */
+void kvc_block_allocator_shuffle(kvc_block_allocator* a, uint64_t seed);
+int  kvc_blocks_needed(int seq_len, int block);           /* block_alloc.h:41-43 */
+
+/* ---- serving loop: Engine (engine.h) and static baseline (scheduler.h) --- */
+typedef struct kvc_engine_config {
+    int n_heads;       /* query heads (EngineConfig.n_heads, engine.h:25) */
+    int n_kv_heads;    /* KV heads; 0 = n_heads (MHA, as the reference) */
+    int head_dim;
+    int block_size;
+    int num_blocks;    /* pool blocks per layer slice */
+    int max_batch;
+    int n_layers;      /* KV layer slices [n_layers, num_blocks, Hkv, BLOCK, D]; 0 = 1 */
+    int dtype;         /* KVC_F32 (reference) or KVC_F16 */
+    int kv_write;      /* 0: reference step (attend over cur_len, grow after, engine.h:132-137);
+                          1: per layer write K/V at cur_len then attend over cur_len+1
+                             (qwen_serve.cu:130-160) */
+    int clock_mode;    /* 0: clock advances by the measured GPU step time (engine.h:132-133);
+                          1: virtual clock, step cost = c0 + c1*N + c2*sum(len) us */
+    double virt_c0, virt_c1, virt_c2;
+    int device;        /* 1: own device pools and launch kernels; 0: scheduling only (no GPU) */
+    int split_tokens;  /* decode split size; 0 = automatic */
+    uint64_t seed;     /* seed of the synthetic q/k/v fill */
+} kvc_engine_config;
+
+typedef struct kvc_engine_stats {     /* EngineStats (engine.h:33-45) + p50 + digest */
+    int iters;
+    long long tokens;
+    double gpu_us;          /* sum of step times (measured or virtual) */
+    double wall_us;         /* scheduler clock at the end = makespan */
+    long long slot_steps;
+    long long useful_steps;
+    int peak_blocks;
+    int finished;
+    double avg_latency_us;
+    double p50_latency_us;
+    double p99_latency_us;
+    uint64_t step_digest;   /* FNV-1a 64 over every step's packed metadata */
+    double host_wall_us;    /* real elapsed time of the whole run on the host clock */
+} kvc_engine_stats;
+
+typedef struct kvc_request { int id; double arrival_us; int prompt_len; int gen_len; } kvc_request;
+
+typedef struct kvc_engine kvc_engine;
+int  kvc_engine_create(const kvc_engine_config* cfg, kvc_engine** out);
+void kvc_engine_destroy(kvc_engine* e);
+int  kvc_engine_reset(kvc_engine* e);
+/* Requests must be added in non-decreasing arrival order (engine.h:87). */
+int  kvc_engine_add_request(kvc_engine* e, int prompt_len, int max_new_tokens, double arrival_us);
+/* One iteration; *more = 0 once every request has finished.  Returns KVC_ERR_STATE if the
+ * head of the queue can never be admitted (its worst case exceeds the pool). */
+int  kvc_engine_step(kvc_engine* e, int* more);
+int  kvc_engine_run(kvc_engine* e, kvc_engine_stats* out);
+int  kvc_engine_stats_get(const kvc_engine* e, kvc_engine_stats* out);
+/* run_static (scheduler.h:33-89) over the engine's pool and runner. */
+int  kvc_run_static(kvc_engine* e, const kvc_request* reqs, int n, int max_batch, kvc_engine_stats* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* KVC_ABI_H */

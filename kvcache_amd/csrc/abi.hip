@@ -1,0 +1,502 @@
+// abi.hip -- the extern "C" boundary of libkvcache_amd.so (declared in include/kvc_abi.h).
+//
+// Validates shapes, plans each decode launch (query heads per wave, split size,
+// addressing mode, workspace carve-up) and forwards to the kernels in decode.hip
+// and append.hip.  Nothing here throws across the boundary; every entry point
+// returns a kvc_status and records a message for kvc_last_error().
+#include "internal.hpp"
+#include "kvc_abi.h"
+
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+namespace kvc {
+
+namespace {
+thread_local std::string g_last_error;
+}
+
+int set_error(int status, const std::string& msg) {
+    g_last_error = msg;
+    return status;
+}
+
+Tuning& tuning() {
+    static Tuning t;
+    return t;
+}
+
+int hip_check(hipError_t e, const char* what) {
+    if (e == hipSuccess) return KVC_OK;
+    return set_error(KVC_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+namespace {
+
+constexpr size_t kAlign = 256;
+inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+inline int esize(int dtype) { return dtype == KVC_F16 ? 2 : 4; }
+inline bool dtype_ok(int dtype) { return dtype == KVC_F16 || dtype == KVC_F32; }
+inline bool d_ok(int D) { return D == 32 || D == 64 || D == 128 || D == 256; }
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Query heads one wave serves from the same K/V registers (a divisor of the GQA group).
+inline bool g_instantiated(int D, int G) {
+    if (D == 64 || D == 128) return G == 1 || G == 2 || G == 4 || G == 7 || G == 8;
+    return G == 1;
+}
+int choose_g(int group, int D) {
+    static const int cands[] = {8, 7, 4, 2, 1};
+    for (int c : cands)
+        if (group % c == 0 && g_instantiated(D, c)) return c;
+    return 1;
+}
+// Tokens covered by one wave-wide 16-byte load.
+inline int tokens_per_wave_load(int D, int dtype) { return 64 / (D * esize(dtype) / 16); }
+
+int auto_split(int N, int Hq, int Hkv, int D, int BLOCK, int cap, int dtype) {
+    const int group = Hq / Hkv;
+    const int nsub = group / choose_g(group, D);
+    const long long per_chunk_units = (long long)N * Hkv * nsub;
+    // Enough waves to keep every SIMD of the 256 CUs streaming, but never less
+    // than min_chunk_bytes of K+V per wave so the partial traffic stays small.
+    const long long target_units = std::max(1, tuning().target_units);
+    long long ch = per_chunk_units > 0 ? ((long long)std::max(cap, 1) * per_chunk_units + target_units - 1) / target_units : 1;
+    const long long min_ch = std::max<long long>(16, tuning().min_chunk_bytes / (2LL * D * esize(dtype)));
+    ch = std::max(ch, min_ch);
+    long long p2 = 1;
+    while (p2 < ch) p2 <<= 1;
+    ch = p2;
+    if (BLOCK > 0 && ch % BLOCK) ch = (ch + BLOCK - 1) / BLOCK * BLOCK;
+    if (ch > (1 << 24)) ch = 1 << 24;
+    return (int)ch;
+}
+
+struct Plan {
+    int G = 1, nsub = 1, mode = kContiguous, chunk = 1, max_chunks = 1;
+    size_t acc_bytes = 0, ml_bytes = 0, ws_bytes = 0;
+};
+
+// Workspace: [part_acc | part_ml | arrival counters (one u64 per seq x KV head x subgroup)].
+void size_workspace(Plan& pl, int N, int Hq, int Hkv, int D) {
+    if (pl.max_chunks <= 1) return;
+    const size_t recs = (size_t)N * pl.max_chunks * Hq;
+    pl.acc_bytes = align_up(recs * D * sizeof(float), kAlign);
+    pl.ml_bytes = align_up(recs * 2 * sizeof(float), kAlign);
+    pl.ws_bytes = pl.acc_bytes + pl.ml_bytes + align_up((size_t)N * Hkv * pl.nsub * sizeof(uint64_t), kAlign);
+}
+
+Plan plan_batched(int N, int Hq, int Hkv, int D, int BLOCK, int cap, int dtype, int split, bool paged) {
+    Plan pl;
+    const int group = Hq / Hkv;
+    pl.G = choose_g(group, D);
+    pl.nsub = group / pl.G;
+    pl.chunk = split > 0 ? split : auto_split(N, Hq, Hkv, D, paged ? BLOCK : 0, cap, dtype);
+    pl.max_chunks = std::max(1, (std::max(cap, 0) + pl.chunk - 1) / pl.chunk);
+    const int tpw = tokens_per_wave_load(D, dtype);
+    if (paged) pl.mode = (BLOCK % tpw == 0 && pl.chunk % BLOCK == 0) ? kPagedUniform : kPagedPerLane;
+    size_workspace(pl, N, Hq, Hkv, D);
+    return pl;
+}
+
+// Call tag for the fused-merge arrival counters; never 0 (0 is the reset value).
+std::atomic<unsigned> g_epoch{0x9e3779b9u};
+unsigned next_epoch() {
+    unsigned e = g_epoch.fetch_add(1u, std::memory_order_relaxed) + 1u;
+    return e ? e : g_epoch.fetch_add(1u, std::memory_order_relaxed) + 1u;
+}
+
+// Library-owned grow-only workspace per device (used when the caller passes none).
+std::mutex g_ws_mu;
+std::vector<std::pair<void*, size_t>> g_ws;
+
+int default_workspace(size_t bytes, void** out) {
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    int dev = 0;
+    int rc = hip_check(hipGetDevice(&dev), "hipGetDevice");
+    if (rc) return rc;
+    if ((int)g_ws.size() <= dev) g_ws.resize(dev + 1, {nullptr, 0});
+    auto& slot = g_ws[dev];
+    if (slot.second < bytes) {
+        if (slot.first) {
+            // queued kernels may still read the old buffer
+            rc = hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize (workspace growth)");
+            if (rc) return rc;
+            (void)hipFree(slot.first);
+            slot = {nullptr, 0};
+        }
+        const size_t sz = align_up(std::max(bytes, (size_t)1 << 20), (size_t)1 << 20);
+        void* p = nullptr;
+        if (hipMalloc(&p, sz) != hipSuccess) return set_error(KVC_ERR_NOMEM, "workspace allocation failed");
+        slot = {p, sz};
+    }
+    *out = slot.first;
+    return KVC_OK;
+}
+
+int resolve_workspace(const Plan& pl, void* ws, size_t ws_bytes, DecodeParams& p) {
+    if (pl.max_chunks <= 1) return KVC_OK;
+    if (!ws) {
+        int rc = default_workspace(pl.ws_bytes, &ws);
+        if (rc) return rc;
+    } else if (ws_bytes < pl.ws_bytes) {
+        return set_error(KVC_ERR_WORKSPACE, "workspace too small: need " + std::to_string(pl.ws_bytes) +
+                                                " bytes, got " + std::to_string(ws_bytes));
+    } else if (((uintptr_t)ws & 15u) != 0) {
+        return set_error(KVC_ERR_ARG, "workspace must be 16-byte aligned");
+    }
+    p.part_acc = static_cast<float*>(ws);
+    p.part_ml = reinterpret_cast<float*>(static_cast<char*>(ws) + pl.acc_bytes);
+    p.counters = tuning().fused_merge
+                     ? reinterpret_cast<unsigned long long*>(static_cast<char*>(ws) + pl.acc_bytes + pl.ml_bytes)
+                     : nullptr;
+    p.epoch = next_epoch();
+    return KVC_OK;
+}
+
+int check_common(int N, int Hq, int Hkv, int D, int dtype, const void* q, const void* k, const void* v,
+                 const void* out) {
+    if (!dtype_ok(dtype)) return set_error(KVC_ERR_ARG, "dtype must be KVC_F32 (0) or KVC_F16 (1)");
+    if (N < 0 || Hq <= 0 || Hkv <= 0) return set_error(KVC_ERR_ARG, "N must be >= 0 and head counts > 0");
+    if (Hq % Hkv) return set_error(KVC_ERR_ARG, "Hq must be a multiple of Hkv");
+    if (!d_ok(D)) return set_error(KVC_ERR_UNSUPPORTED, "head_dim must be 32, 64, 128 or 256");
+    if (N == 0) return KVC_OK;
+    if (!q || !k || !v || !out) return set_error(KVC_ERR_ARG, "null q/k/v/out pointer");
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
+        return set_error(KVC_ERR_ARG, "q, k, v and out must be 16-byte aligned");
+    return KVC_OK;
+}
+
+int run_batched(const void* q, const void* k, const void* v, const int* table_all, const int* tab_off,
+                const int* cur_len, int fixed_len, void* out, int N, int Hq, int Hkv, int D, int BLOCK,
+                long long seq_stride, long long head_stride, int cap, float scale, int dtype, int split,
+                bool paged, void* ws, size_t ws_bytes, hipStream_t st) {
+    int rc = check_common(N, Hq, Hkv, D, dtype, q, k, v, out);
+    if (rc || N == 0) return rc;
+    if (paged && (BLOCK <= 0 || !table_all)) return set_error(KVC_ERR_ARG, "paged decode needs BLOCK > 0 and a block table");
+    if (cap < 0) return set_error(KVC_ERR_ARG, "cap must be >= 0");
+    if (split < 0) return set_error(KVC_ERR_ARG, "split_tokens must be >= 0");
+    if (paged && split > 0 && split % BLOCK) return set_error(KVC_ERR_ARG, "split_tokens must be a multiple of BLOCK");
+    if (!std::isfinite(scale)) return set_error(KVC_ERR_ARG, "scale must be finite");
+    const Plan pl = plan_batched(N, Hq, Hkv, D, BLOCK, cap, dtype, split, paged);
+    DecodeLaunch L{};
+    DecodeParams& p = L.p;
+    p.q = q; p.k = k; p.v = v; p.out = out;
+    p.table_all = table_all; p.tab_off = tab_off; p.cur_len = cur_len; p.fixed_len = fixed_len;
+    p.seq_stride = seq_stride; p.head_stride = head_stride;
+    p.N = N; p.Hq = Hq; p.Hkv = Hkv; p.block = paged ? BLOCK : 1;
+    p.group = Hq / Hkv; p.nsub = pl.nsub;
+    p.chunk_tokens = pl.chunk; p.num_splits = 0; p.max_chunks = pl.max_chunks;
+    p.scale_log2 = scale * 1.4426950408889634f;
+    rc = resolve_workspace(pl, ws, ws_bytes, p);
+    if (rc) return rc;
+    L.dtype = dtype; L.D = D; L.G = pl.G; L.mode = pl.mode; L.need_merge = pl.max_chunks > 1;
+    return launch_decode(L, st);
+}
+
+template <class F>
+int guarded(F&& f) {
+    try {
+        return f();
+    } catch (const std::exception& e) {
+        return set_error(KVC_ERR_ARG, std::string("internal error: ") + e.what());
+    } catch (...) {
+        return set_error(KVC_ERR_ARG, "internal error");
+    }
+}
+
+inline hipStream_t S(kvc_stream_t s) { return static_cast<hipStream_t>(s); }
+
+}  // namespace
+}  // namespace kvc
+
+using namespace kvc;
+
+extern "C" {
+
+int kvc_version(void) { return 100; }
+
+const char* kvc_status_string(int s) {
+    switch (s) {
+        case KVC_OK: return "ok";
+        case KVC_ERR_ARG: return "invalid argument";
+        case KVC_ERR_UNSUPPORTED: return "unsupported shape";
+        case KVC_ERR_HIP: return "HIP runtime error";
+        case KVC_ERR_NOMEM: return "out of memory";
+        case KVC_ERR_WORKSPACE: return "workspace too small";
+        case KVC_ERR_STATE: return "invalid state";
+        default: return "unknown status";
+    }
+}
+
+const char* kvc_last_error(void) { return g_last_error.c_str(); }
+
+int kvc_device_count(int* count) {
+    if (!count) return set_error(KVC_ERR_ARG, "null count");
+    *count = 0;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return KVC_OK;  // no device: count 0
+    *count = n;
+    return KVC_OK;
+}
+
+int kvc_malloc(void** dptr, size_t bytes) {
+    if (!dptr) return set_error(KVC_ERR_ARG, "null out pointer");
+    *dptr = nullptr;
+    if (bytes == 0) return KVC_OK;
+    if (hipMalloc(dptr, bytes) != hipSuccess) {
+        *dptr = nullptr;
+        return set_error(KVC_ERR_NOMEM, "hipMalloc of " + std::to_string(bytes) + " bytes failed");
+    }
+    return KVC_OK;
+}
+int kvc_free(void* dptr) { return dptr ? hip_check(hipFree(dptr), "hipFree") : KVC_OK; }
+int kvc_host_alloc(void** hptr, size_t bytes) {
+    if (!hptr) return set_error(KVC_ERR_ARG, "null out pointer");
+    *hptr = nullptr;
+    if (bytes == 0) return KVC_OK;
+    if (hipHostMalloc(hptr, bytes, hipHostMallocDefault) != hipSuccess) {
+        *hptr = nullptr;
+        return set_error(KVC_ERR_NOMEM, "hipHostMalloc failed");
+    }
+    return KVC_OK;
+}
+int kvc_host_free(void* hptr) { return hptr ? hip_check(hipHostFree(hptr), "hipHostFree") : KVC_OK; }
+int kvc_memcpy_h2d(void* dst, const void* src, size_t bytes, kvc_stream_t st) {
+    if (!bytes) return KVC_OK;
+    return hip_check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, S(st)), "hipMemcpyAsync H2D");
+}
+int kvc_memcpy_d2h(void* dst, const void* src, size_t bytes, kvc_stream_t st) {
+    if (!bytes) return KVC_OK;
+    int rc = hip_check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, S(st)), "hipMemcpyAsync D2H");
+    return rc ? rc : hip_check(hipStreamSynchronize(S(st)), "hipStreamSynchronize");
+}
+int kvc_memcpy_d2d(void* dst, const void* src, size_t bytes, kvc_stream_t st) {
+    if (!bytes) return KVC_OK;
+    return hip_check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, S(st)), "hipMemcpyAsync D2D");
+}
+int kvc_memset(void* dst, int value, size_t bytes, kvc_stream_t st) {
+    if (!bytes) return KVC_OK;
+    return hip_check(hipMemsetAsync(dst, value, bytes, S(st)), "hipMemsetAsync");
+}
+int kvc_stream_create(kvc_stream_t* st) {
+    if (!st) return set_error(KVC_ERR_ARG, "null out pointer");
+    hipStream_t s = nullptr;
+    int rc = hip_check(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreate");
+    *st = s;
+    return rc;
+}
+int kvc_stream_destroy(kvc_stream_t st) { return st ? hip_check(hipStreamDestroy(S(st)), "hipStreamDestroy") : KVC_OK; }
+int kvc_stream_synchronize(kvc_stream_t st) { return hip_check(hipStreamSynchronize(S(st)), "hipStreamSynchronize"); }
+int kvc_device_synchronize(void) { return hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize"); }
+int kvc_event_create(void** ev) {
+    if (!ev) return set_error(KVC_ERR_ARG, "null out pointer");
+    hipEvent_t e = nullptr;
+    int rc = hip_check(hipEventCreate(&e), "hipEventCreate");
+    *ev = e;
+    return rc;
+}
+int kvc_event_destroy(void* ev) { return ev ? hip_check(hipEventDestroy((hipEvent_t)ev), "hipEventDestroy") : KVC_OK; }
+int kvc_event_record(void* ev, kvc_stream_t st) { return hip_check(hipEventRecord((hipEvent_t)ev, S(st)), "hipEventRecord"); }
+int kvc_event_synchronize(void* ev) { return hip_check(hipEventSynchronize((hipEvent_t)ev), "hipEventSynchronize"); }
+int kvc_event_elapsed_ms(float* ms, void* a, void* b) {
+    if (!ms) return set_error(KVC_ERR_ARG, "null out pointer");
+    int rc = hip_check(hipEventSynchronize((hipEvent_t)b), "hipEventSynchronize");
+    if (rc) return rc;
+    return hip_check(hipEventElapsedTime(ms, (hipEvent_t)a, (hipEvent_t)b), "hipEventElapsedTime");
+}
+
+int kvc_step_upload(void* dst, const void* src, size_t bytes, kvc_stream_t st) {
+    if (!bytes) return KVC_OK;
+    if (!dst || !src) return set_error(KVC_ERR_ARG, "null upload pointer");
+    return hip_check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, S(st)), "step upload");
+}
+
+int kvc_fill_normal(void* dst, size_t n, int dtype, uint64_t seed, float stddev, kvc_stream_t st) {
+    if (!dtype_ok(dtype)) return set_error(KVC_ERR_ARG, "bad dtype");
+    if (n && !dst) return set_error(KVC_ERR_ARG, "null fill pointer");
+    return launch_fill_normal(dst, n, dtype, seed, stddev, S(st));
+}
+
+// ---- K/V writes ------------------------------------------------------------
+static int write_common(int dtype, int heads, int D, const void* k, const void* v, void* kd, void* vd) {
+    if (!dtype_ok(dtype)) return set_error(KVC_ERR_ARG, "bad dtype");
+    if (heads <= 0 || D <= 0) return set_error(KVC_ERR_ARG, "heads and D must be > 0");
+    if (!k || !v || !kd || !vd) return set_error(KVC_ERR_ARG, "null K/V pointer");
+    return KVC_OK;
+}
+
+int kvc_append(const void* k_new, const void* v_new, void* k_cache, void* v_cache, int pos, int H, int D,
+               int S_, int dtype, kvc_stream_t st) {
+    return guarded([&]() -> int {
+        int rc = write_common(dtype, H, D, k_new, v_new, k_cache, v_cache);
+        if (rc) return rc;
+        if (pos < 0 || pos >= S_) return set_error(KVC_ERR_ARG, "pos must be in [0, S)");
+        WriteParams p{k_new, v_new, k_cache, v_cache, nullptr, nullptr, nullptr, 1, H, D, 1, pos, S_, kWriteAppend};
+        return launch_write(p, dtype, S(st));
+    });
+}
+
+int kvc_write_kv(const void* k, const void* v, void* k_pool, void* v_pool, const int* block_table, int start_pos,
+                 int L, int Hkv, int D, int BLOCK, int dtype, kvc_stream_t st) {
+    return guarded([&]() -> int {
+        int rc = write_common(dtype, Hkv, D, k, v, k_pool, v_pool);
+        if (rc) return rc;
+        if (L < 0 || start_pos < 0 || BLOCK <= 0) return set_error(KVC_ERR_ARG, "bad L / start_pos / BLOCK");
+        if (L > 0 && !block_table) return set_error(KVC_ERR_ARG, "null block table");
+        WriteParams p{k, v, k_pool, v_pool, block_table, nullptr, nullptr, L, Hkv, D, BLOCK, start_pos, 0, kWriteTable};
+        return launch_write(p, dtype, S(st));
+    });
+}
+
+int kvc_batched_write_kv(const void* k, const void* v, void* k_pool, void* v_pool, const int* table_all,
+                         const int* tab_off, const int* wpos, int N, int Hkv, int D, int BLOCK, int dtype,
+                         kvc_stream_t st) {
+    return guarded([&]() -> int {
+        int rc = write_common(dtype, Hkv, D, k, v, k_pool, v_pool);
+        if (rc) return rc;
+        if (N < 0 || BLOCK <= 0) return set_error(KVC_ERR_ARG, "bad N / BLOCK");
+        if (N > 0 && (!table_all || !tab_off || !wpos)) return set_error(KVC_ERR_ARG, "null table / offsets / wpos");
+        WriteParams p{k, v, k_pool, v_pool, table_all, tab_off, wpos, N, Hkv, D, BLOCK, 0, 0, kWriteBatched};
+        return launch_write(p, dtype, S(st));
+    });
+}
+
+int kvc_write_kv_slots(const void* k, const void* v, void* k_pool, void* v_pool, const int* slot_map, int rows,
+                       int Hkv, int D, int BLOCK, int dtype, kvc_stream_t st) {
+    return guarded([&]() -> int {
+        int rc = write_common(dtype, Hkv, D, k, v, k_pool, v_pool);
+        if (rc) return rc;
+        if (rows < 0 || BLOCK <= 0) return set_error(KVC_ERR_ARG, "bad rows / BLOCK");
+        if (rows > 0 && !slot_map) return set_error(KVC_ERR_ARG, "null slot map");
+        WriteParams p{k, v, k_pool, v_pool, nullptr, nullptr, slot_map, rows, Hkv, D, BLOCK, 0, 0, kWriteSlots};
+        return launch_write(p, dtype, S(st));
+    });
+}
+
+// ---- decode ------------------------------------------------------------------
+int kvc_decode(const void* q, const void* k_cache, const void* v_cache, void* out, int cur_len, int H, int D,
+               int S_, float scale, int dtype, kvc_stream_t st) {
+    return guarded([&]() -> int {
+        if (S_ < 0 || cur_len > S_) return set_error(KVC_ERR_ARG, "cur_len must be <= S");
+        return run_batched(q, k_cache, v_cache, nullptr, nullptr, nullptr, cur_len, out, 1, H, H, D, 0, 0,
+                           (long long)S_ * D, std::max(cur_len, 0), scale, dtype, 0, false, nullptr, 0, S(st));
+    });
+}
+
+int kvc_paged_decode(const void* q, const void* k_pool, const void* v_pool, const int* block_table, void* out,
+                     int cur_len, int H, int D, int BLOCK, float scale, int dtype, kvc_stream_t st) {
+    return guarded([&]() -> int {
+        return run_batched(q, k_pool, v_pool, block_table, nullptr, nullptr, cur_len, out, 1, H, H, D, BLOCK, 0, 0,
+                           std::max(cur_len, 0), scale, dtype, 0, true, nullptr, 0, S(st));
+    });
+}
+
+int kvc_batched_decode(const void* q, const void* k_cache, const void* v_cache, const int* cur_len, void* out, int N,
+                       int Hq, int Hkv, int D, int MAXS, int cap, float scale, int dtype, void* ws, size_t ws_bytes,
+                       kvc_stream_t st) {
+    return kvc_batched_decode_split(q, k_cache, v_cache, cur_len, out, N, Hq, Hkv, D, MAXS, cap, scale, dtype, 0, ws,
+                                    ws_bytes, st);
+}
+
+int kvc_batched_decode_split(const void* q, const void* k_cache, const void* v_cache, const int* cur_len, void* out,
+                             int N, int Hq, int Hkv, int D, int MAXS, int cap, float scale, int dtype, int split,
+                             void* ws, size_t ws_bytes, kvc_stream_t st) {
+    return guarded([&]() -> int {
+        if (MAXS < 0 || cap > MAXS) return set_error(KVC_ERR_ARG, "cap must be <= MAXS");
+        if (N > 0 && !cur_len) return set_error(KVC_ERR_ARG, "null cur_len");
+        return run_batched(q, k_cache, v_cache, nullptr, nullptr, cur_len, 0, out, N, Hq, Hkv, D, 0,
+                           (long long)Hkv * MAXS * D, (long long)MAXS * D, cap, scale, dtype, split, false, ws,
+                           ws_bytes, S(st));
+    });
+}
+
+int kvc_batched_paged_decode(const void* q, const void* k_pool, const void* v_pool, const int* table_all,
+                             const int* tab_off, const int* cur_len, void* out, int N, int Hq, int Hkv, int D,
+                             int BLOCK, int cap, float scale, int dtype, void* ws, size_t ws_bytes, kvc_stream_t st) {
+    return kvc_batched_paged_decode_split(q, k_pool, v_pool, table_all, tab_off, cur_len, out, N, Hq, Hkv, D, BLOCK,
+                                          cap, scale, dtype, 0, ws, ws_bytes, st);
+}
+
+int kvc_batched_paged_decode_split(const void* q, const void* k_pool, const void* v_pool, const int* table_all,
+                                   const int* tab_off, const int* cur_len, void* out, int N, int Hq, int Hkv, int D,
+                                   int BLOCK, int cap, float scale, int dtype, int split, void* ws, size_t ws_bytes,
+                                   kvc_stream_t st) {
+    return guarded([&]() -> int {
+        if (N > 0 && (!tab_off || !cur_len)) return set_error(KVC_ERR_ARG, "null tab_off / cur_len");
+        return run_batched(q, k_pool, v_pool, table_all, tab_off, cur_len, 0, out, N, Hq, Hkv, D, BLOCK, 0, 0, cap,
+                           scale, dtype, split, true, ws, ws_bytes, S(st));
+    });
+}
+
+size_t kvc_decode_workspace_size(int N, int Hq, int Hkv, int D, int BLOCK, int cap, int split, int dtype) {
+    if (N <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || !d_ok(D) || cap < 0 || split < 0 || !dtype_ok(dtype)) return 0;
+    return plan_batched(N, Hq, Hkv, D, BLOCK, cap, dtype, split, BLOCK > 0).ws_bytes;
+}
+
+int kvc_decode_auto_split(int N, int Hq, int Hkv, int D, int BLOCK, int cap, int dtype) {
+    if (N <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || !d_ok(D) || cap < 0 || !dtype_ok(dtype)) return 0;
+    return auto_split(N, Hq, Hkv, D, BLOCK, cap, dtype);
+}
+
+size_t kvc_flash_decode_workspace_size(int H, int D, int num_splits) {
+    if (H <= 0 || !d_ok(D) || num_splits <= 1) return 0;
+    Plan pl;
+    pl.max_chunks = num_splits;
+    size_workspace(pl, 1, H, H, D);
+    return pl.ws_bytes;
+}
+
+int kvc_set_tuning(const char* key, int value) {
+    if (!key) return set_error(KVC_ERR_ARG, "null key");
+    const std::string k(key);
+    if (k == "fused_merge") tuning().fused_merge = value ? 1 : 0;
+    else if (k == "target_units" && value > 0) tuning().target_units = value;
+    else if (k == "min_chunk_bytes" && value > 0) tuning().min_chunk_bytes = value;
+    else return set_error(KVC_ERR_ARG, "unknown tuning key or bad value: " + k);
+    return KVC_OK;
+}
+
+int kvc_get_tuning(const char* key, int* value) {
+    if (!key || !value) return set_error(KVC_ERR_ARG, "null argument");
+    const std::string k(key);
+    if (k == "fused_merge") *value = tuning().fused_merge;
+    else if (k == "target_units") *value = tuning().target_units;
+    else if (k == "min_chunk_bytes") *value = tuning().min_chunk_bytes;
+    else return set_error(KVC_ERR_ARG, "unknown tuning key: " + k);
+    return KVC_OK;
+}
+
+int kvc_flash_decode(const void* q, const void* k_cache, const void* v_cache, void* out, int cur_len, int H, int D,
+                     int S_, float scale, int num_splits, int dtype, void* ws, size_t ws_bytes, kvc_stream_t st) {
+    return guarded([&]() -> int {
+        int rc = check_common(1, H, H, D, dtype, q, k_cache, v_cache, out);
+        if (rc) return rc;
+        if (S_ < 0 || cur_len > S_) return set_error(KVC_ERR_ARG, "cur_len must be <= S");
+        if (!std::isfinite(scale)) return set_error(KVC_ERR_ARG, "scale must be finite");
+        int ns = std::max(1, num_splits);          // flash_decode.cu:106-107
+        ns = std::max(1, std::min(ns, cur_len));
+        Plan pl;
+        pl.max_chunks = ns;
+        size_workspace(pl, 1, H, H, D);
+        DecodeLaunch L{};
+        DecodeParams& p = L.p;
+        p.q = q; p.k = k_cache; p.v = v_cache; p.out = out;
+        p.fixed_len = std::max(cur_len, 0);
+        p.seq_stride = 0; p.head_stride = (long long)S_ * D;
+        p.N = 1; p.Hq = H; p.Hkv = H; p.block = 1; p.group = 1; p.nsub = 1;
+        p.chunk_tokens = 0; p.num_splits = ns; p.max_chunks = ns;
+        p.scale_log2 = scale * 1.4426950408889634f;
+        rc = resolve_workspace(pl, ws, ws_bytes, p);
+        if (rc) return rc;
+        L.dtype = dtype; L.D = D; L.G = 1; L.mode = kContiguous; L.need_merge = ns > 1;
+        return launch_decode(L, S(st));
+    });
+}
+
+}  // extern "C"

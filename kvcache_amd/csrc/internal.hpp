@@ -1,0 +1,85 @@
+// internal.hpp -- declarations shared by the translation units of libkvcache_amd.so.
+// Not installed; the public surface is include/kvc_abi.h (C) and include/kvc/*.h (C++).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "status.hpp"
+
+namespace kvc {
+
+// Checks a HIP return code; on failure records it and returns KVC_ERR_HIP.
+int hip_check(hipError_t e, const char* what);
+
+// ---------------------------------------------------------------------------
+// Decode launch description (host side).  One "unit" = (sequence s, KV head hk,
+// query-head subgroup sub, chunk c); each unit is one wave64.
+// ---------------------------------------------------------------------------
+enum DecodeMode { kContiguous = 0, kPagedUniform = 1, kPagedPerLane = 2 };
+
+struct DecodeParams {
+    const void* q;
+    const void* k;
+    const void* v;
+    void* out;
+    const int* table_all;     // paged only
+    const int* tab_off;       // paged only (nullptr: single table starting at table_all)
+    const int* cur_len;       // device lengths (nullptr: use fixed_len)
+    float* part_acc;          // [N*max_chunks*Hq, D] fp32 partial accumulators
+    float* part_ml;           // [N*max_chunks*Hq, 2] (running max in log2 units, running sum)
+    unsigned long long* counters;  // [N*Hkv*nsub] arrival counters (fused merge), or nullptr
+    long long seq_stride;     // contiguous: elements between sequences
+    long long head_stride;    // contiguous: elements between KV heads
+    int N, Hq, Hkv, block;
+    int group;                // Hq / Hkv
+    int nsub;                 // query-head subgroups per KV head (group / G)
+    int chunk_tokens;         // >0: fixed chunk size (tokens); else num_splits mode
+    int num_splits;           // >0: chunk = ceil(L / num_splits) per sequence
+    int max_chunks;           // chunks per sequence covered by the grid
+    int fixed_len;            // length used when cur_len == nullptr
+    float scale_log2;         // softmax scale * log2(e)
+    unsigned epoch;           // per-call tag of the arrival counters
+};
+
+struct DecodeLaunch {
+    DecodeParams p;
+    int dtype;   // KVC_F32 / KVC_F16
+    int D;
+    int G;       // query heads per unit
+    int mode;    // DecodeMode
+    bool need_merge;
+};
+
+// Launches the split kernel and, when needed and not fused, the merge kernel.
+int launch_decode(const DecodeLaunch& L, hipStream_t stream);
+
+// Tuning knobs (kvc_set_tuning).
+struct Tuning {
+    int fused_merge = 1;        // last-arriving chunk merges (single kernel) instead of a merge kernel
+    int target_units = 4096;    // automatic split: waves to aim for
+    int min_chunk_bytes = 32768;// automatic split: least K+V bytes per wave
+};
+Tuning& tuning();
+
+// ---------------------------------------------------------------------------
+// K/V row writes.
+// ---------------------------------------------------------------------------
+enum WriteMode { kWriteAppend = 0, kWriteTable = 1, kWriteBatched = 2, kWriteSlots = 3 };
+struct WriteParams {
+    const void* k;
+    const void* v;
+    void* kd;
+    void* vd;
+    const int* table;    // kWriteTable: block table; kWriteBatched: table_all
+    const int* tab_off;  // kWriteBatched
+    const int* idx;      // kWriteBatched: wpos[rows]; kWriteSlots: slot_map[rows]
+    int rows, heads, D, block, start_pos, S, mode;
+};
+int launch_write(const WriteParams& p, int dtype, hipStream_t stream);
+
+// Deterministic N(0,1) fill (Box-Muller over a counter hash), fp32 or fp16.
+int launch_fill_normal(void* dst, size_t n, int dtype, uint64_t seed, float stddev, hipStream_t stream);
+
+}  // namespace kvc

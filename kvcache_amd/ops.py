@@ -1,0 +1,113 @@
+"""Python mirror of the reference's kernel launchers (src/include/kv_cache.h:2-34,
+src/include/qwen_kernels.h:15-37), over the C ABI.
+
+Same names and argument order as the reference; every pointer argument may be a
+DeviceBuffer or a raw device address (int).  Extra keyword arguments carry what
+the MI355X boundary adds: dtype (KVC_F32 default, as the reference), Hkv for
+GQA, split size, workspace and stream.  Failures raise KvcError (the reference
+printed and exited).  Parity tests call these exactly as the reference's
+drivers call the CUDA launchers.
+"""
+from __future__ import annotations
+
+from ._native import KVC_F16, KVC_F32, check, lib
+from .device import DeviceBuffer
+
+__all__ = [
+    "launch_append", "launch_decode", "launch_paged", "launch_batched_decode", "launch_batched_paged",
+    "launch_batched_paged_flash", "launch_flash_decode", "qk_write_kv", "qk_batched_write_kv",
+    "qk_batched_paged_decode_attn", "write_kv_slots", "decode_workspace_size", "decode_auto_split",
+    "flash_decode_workspace_size", "KVC_F16", "KVC_F32",
+]
+
+
+def _p(x):
+    if x is None:
+        return None
+    if isinstance(x, DeviceBuffer):
+        return x.ptr
+    return int(x)
+
+
+def _ws(workspace):
+    if workspace is None:
+        return None, 0
+    if isinstance(workspace, DeviceBuffer):
+        return workspace.ptr, workspace.nbytes
+    ptr, nbytes = workspace
+    return int(ptr), int(nbytes)
+
+
+def launch_append(k_new, v_new, k_cache, v_cache, pos, H, D, S, *, dtype=KVC_F32, stream=None):
+    check(lib().kvc_append(_p(k_new), _p(v_new), _p(k_cache), _p(v_cache), pos, H, D, S, dtype, stream))
+
+
+def launch_decode(q, k_cache, v_cache, out, cur_len, H, D, S, scale, *, dtype=KVC_F32, stream=None):
+    check(lib().kvc_decode(_p(q), _p(k_cache), _p(v_cache), _p(out), cur_len, H, D, S, scale, dtype, stream))
+
+
+def launch_paged(q, k_pool, v_pool, block_table, out, cur_len, H, D, BLOCK, scale, *, dtype=KVC_F32, stream=None):
+    check(lib().kvc_paged_decode(_p(q), _p(k_pool), _p(v_pool), _p(block_table), _p(out), cur_len, H, D, BLOCK,
+                                 scale, dtype, stream))
+
+
+def launch_batched_decode(q, k_cache, v_cache, cur_len, out, N, H, D, MAXS, cap, scale, *, Hkv=None,
+                          dtype=KVC_F32, split=0, workspace=None, stream=None):
+    ws, wsb = _ws(workspace)
+    check(lib().kvc_batched_decode_split(_p(q), _p(k_cache), _p(v_cache), _p(cur_len), _p(out), N, H,
+                                         Hkv or H, D, MAXS, cap, scale, dtype, split, ws, wsb, stream))
+
+
+def launch_batched_paged(q, k_pool, v_pool, table_all, tab_off, cur_len, out, N, H, D, BLOCK, cap, scale, *,
+                         Hkv=None, dtype=KVC_F32, split=0, workspace=None, stream=None):
+    ws, wsb = _ws(workspace)
+    check(lib().kvc_batched_paged_decode_split(_p(q), _p(k_pool), _p(v_pool), _p(table_all), _p(tab_off),
+                                               _p(cur_len), _p(out), N, H, Hkv or H, D, BLOCK, cap, scale, dtype,
+                                               split, ws, wsb, stream))
+
+
+# Same kernel as launch_batched_paged (online softmax is the only implementation).
+launch_batched_paged_flash = launch_batched_paged
+
+
+def launch_flash_decode(q, k_cache, v_cache, out, cur_len, H, D, S, scale, num_splits, *, dtype=KVC_F32,
+                        workspace=None, stream=None):
+    ws, wsb = _ws(workspace)
+    check(lib().kvc_flash_decode(_p(q), _p(k_cache), _p(v_cache), _p(out), cur_len, H, D, S, scale, num_splits,
+                                 dtype, ws, wsb, stream))
+
+
+def qk_write_kv(k, v, k_pool, v_pool, block_table_dev, start_pos, L, Hkv, D, BLOCK, *, dtype=KVC_F16, stream=None):
+    check(lib().kvc_write_kv(_p(k), _p(v), _p(k_pool), _p(v_pool), _p(block_table_dev), start_pos, L, Hkv, D, BLOCK,
+                             dtype, stream))
+
+
+def qk_batched_write_kv(k, v, k_pool, v_pool, table_all, tab_off, wpos, N, Hkv, D, BLOCK, *, dtype=KVC_F16,
+                        stream=None):
+    check(lib().kvc_batched_write_kv(_p(k), _p(v), _p(k_pool), _p(v_pool), _p(table_all), _p(tab_off), _p(wpos), N,
+                                     Hkv, D, BLOCK, dtype, stream))
+
+
+def qk_batched_paged_decode_attn(q, out, k_pool, v_pool, table_all, tab_off, cur_len, N, Hq, Hkv, D, BLOCK, scale,
+                                 *, cap, dtype=KVC_F16, split=0, workspace=None, stream=None):
+    ws, wsb = _ws(workspace)
+    check(lib().kvc_batched_paged_decode_split(_p(q), _p(k_pool), _p(v_pool), _p(table_all), _p(tab_off),
+                                               _p(cur_len), _p(out), N, Hq, Hkv, D, BLOCK, cap, scale, dtype, split,
+                                               ws, wsb, stream))
+
+
+def write_kv_slots(k, v, k_pool, v_pool, slot_map, rows, Hkv, D, BLOCK, *, dtype=KVC_F16, stream=None):
+    check(lib().kvc_write_kv_slots(_p(k), _p(v), _p(k_pool), _p(v_pool), _p(slot_map), rows, Hkv, D, BLOCK, dtype,
+                                   stream))
+
+
+def decode_workspace_size(N, Hq, Hkv, D, BLOCK, cap, split=0, dtype=KVC_F16) -> int:
+    return int(lib().kvc_decode_workspace_size(N, Hq, Hkv, D, BLOCK, cap, split, dtype))
+
+
+def decode_auto_split(N, Hq, Hkv, D, BLOCK, cap, dtype=KVC_F16) -> int:
+    return int(lib().kvc_decode_auto_split(N, Hq, Hkv, D, BLOCK, cap, dtype))
+
+
+def flash_decode_workspace_size(H, D, num_splits) -> int:
+    return int(lib().kvc_flash_decode_workspace_size(H, D, num_splits))

@@ -1,0 +1,90 @@
+"""The C ABI library loads, exports every symbol include/kvc_abi.h declares, and
+rejects bad shapes with a status (no GPU needed: validation precedes any HIP call)."""
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+
+from kvcache_amd import _native as N
+from kvcache_amd import ops
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "kvc_abi.h"
+
+
+def declared_functions() -> set[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return set(re.findall(r"^\s*(?:const\s+)?[\w\s\*]+?\b(kvc_\w+)\s*\(", text, flags=re.M))
+
+
+def test_header_declares_functions():
+    names = declared_functions()
+    assert len(names) > 40 and "kvc_batched_paged_decode" in names and "kvc_engine_run" in names
+
+
+def test_library_exports_every_declared_symbol():
+    L = N.lib()
+    missing = [n for n in sorted(declared_functions()) if not hasattr(L, n)]
+    assert not missing, missing
+
+
+def test_python_bindings_cover_header():
+    assert declared_functions() == set(N.exported_names())
+
+
+def test_version_and_status_strings():
+    L = N.lib()
+    assert L.kvc_version() >= 100
+    assert L.kvc_status_string(N.KVC_ERR_WORKSPACE) == b"workspace too small"
+
+
+def _fake(n=16):
+    return 0x10000  # 16-byte aligned non-null address; never dereferenced on the error paths below
+
+
+@pytest.mark.parametrize("D,status", [(48, N.KVC_ERR_UNSUPPORTED), (512, N.KVC_ERR_UNSUPPORTED)])
+def test_unsupported_head_dim(D, status):
+    p = _fake()
+    with pytest.raises(N.KvcError) as e:
+        ops.launch_batched_paged(p, p, p, p, p, p, p, 4, 8, D, 16, 100, 0.1, dtype=N.KVC_F16)
+    assert e.value.status == status and "head_dim" in str(e.value)
+
+
+def test_bad_arguments_rejected():
+    p = _fake()
+    with pytest.raises(N.KvcError) as e:  # Hq not a multiple of Hkv
+        ops.launch_batched_paged(p, p, p, p, p, p, p, 4, 7, 64, 16, 100, 0.1, Hkv=2, dtype=N.KVC_F16)
+    assert e.value.status == N.KVC_ERR_ARG
+    with pytest.raises(N.KvcError) as e:  # misaligned q
+        ops.launch_batched_paged(p + 2, p, p, p, p, p, p, 4, 8, 64, 16, 100, 0.1, dtype=N.KVC_F16)
+    assert e.value.status == N.KVC_ERR_ARG and "aligned" in str(e.value)
+    with pytest.raises(N.KvcError) as e:  # split not a multiple of BLOCK
+        ops.launch_batched_paged(p, p, p, p, p, p, p, 4, 8, 64, 16, 100, 0.1, dtype=N.KVC_F16, split=24)
+    assert e.value.status == N.KVC_ERR_ARG
+    with pytest.raises(N.KvcError) as e:  # caller workspace too small
+        ops.launch_batched_paged(p, p, p, p, p, p, p, 4, 8, 64, 16, 5000, 0.1, dtype=N.KVC_F16, split=128,
+                                 workspace=(p, 64))
+    assert e.value.status == N.KVC_ERR_WORKSPACE
+    with pytest.raises(N.KvcError) as e:
+        ops.launch_decode(p, p, p, p, 10, 8, 64, 5, 0.1)  # cur_len > S
+    assert e.value.status == N.KVC_ERR_ARG
+    with pytest.raises(N.KvcError) as e:
+        ops.launch_append(p, p, p, p, 7, 8, 64, 7)  # pos >= S
+    assert e.value.status == N.KVC_ERR_ARG
+
+
+def test_empty_batch_is_a_noop():
+    ops.launch_batched_paged(None, None, None, None, None, None, None, 0, 8, 64, 16, 0, 0.1, dtype=N.KVC_F16)
+
+
+def test_workspace_size_and_auto_split():
+    # ragged C2 shape: auto split is a power of two, multiple of BLOCK, and sizes the partials
+    sp = ops.decode_auto_split(128, 8, 8, 64, 16, 2022)
+    assert sp >= 16 and sp % 16 == 0 and (sp & (sp - 1)) == 0
+    ws = ops.decode_workspace_size(128, 8, 8, 64, 16, 2022)
+    chunks = -(-2022 // sp)
+    assert ws >= 128 * chunks * 8 * (64 + 2) * 4
+    assert ops.decode_workspace_size(4, 14, 2, 64, 16, 32768, 512) >= 4 * 64 * 14 * 66 * 4
+    assert ops.decode_workspace_size(4, 8, 8, 64, 16, 100, 128) == 0  # single chunk: no partials
+    assert ops.flash_decode_workspace_size(8, 64, 1) == 0
+    assert ops.flash_decode_workspace_size(8, 64, 7) >= 8 * 7 * 66 * 4

@@ -1,0 +1,61 @@
+"""The C++ Engine / run_static driving real kernels on the GPU.
+
+With the deterministic clock every decision and every uploaded per-step table
+must equal the oracle's (digest), exactly as in the host-only run; with the
+measured clock the accounting invariants of demo_engine.cu:40-41 must hold.
+"""
+import numpy as np
+import pytest
+
+from kvcache_amd import KVC_F16, KVC_F32
+from kvcache_amd import workloads as W
+from kvcache_amd.engine import Engine, EngineConfig, run_continuous, run_static
+
+from _helpers import say
+
+pytestmark = pytest.mark.gpu
+COST = (20.0, 1.5, 0.01)
+
+
+def _same(ours, ref):
+    assert (ours.iters, ours.tokens, ours.slot_steps, ours.useful_steps, ours.peak_blocks, ours.finished) == (
+        ref.iters, ref.tokens, ref.slot_steps, ref.useful_steps, ref.peak_blocks, ref.finished)
+    assert ours.wall_us == ref.wall_us and ours.p99_latency_us == ref.p99_latency_us
+    assert ours.step_digest == ref.digest
+
+
+@pytest.mark.parametrize("kv_write", [False, True])
+def test_engine_on_gpu_matches_oracle_schedule(orc, kv_write):
+    say(f"engine gpu virtual clock kv_write={kv_write}")
+    p, g, a = W.ref_trace(nreq=64, rate=400.0)
+    cfg = EngineConfig(n_heads=8, head_dim=64, block_size=16, num_blocks=4096, max_batch=32, kv_write=kv_write,
+                       clock_mode=1, virt_c0=COST[0], virt_c1=COST[1], virt_c2=COST[2], dtype=KVC_F32)
+    eng = Engine(cfg)
+    rc, ref = orc.sim_engine(p, g, a, 16, 4096, 32, kv_write, COST)
+    _same(run_continuous(p, g, a, eng), ref)
+    rc, ref_s, _ = orc.sim_static(p, g, a, 16, 4096, 32, kv_write, COST)
+    _same(run_static(p, g, a, eng, 32), ref_s)
+
+
+def test_config4_shape_24_layers_gqa_fp16(orc):
+    # 14 q / 2 kv heads, D 64, 24 layers of write + decode per step, pool of 2048 MB
+    say("engine config-4 shape, 24 layers")
+    num_blocks = (2048 * 1024 * 1024) // (24 * 2 * 16 * 64 * 2 * 2)
+    p, g, a = W.baseline_trace(48, 0.0, 11)
+    cfg = EngineConfig(n_heads=14, n_kv_heads=2, head_dim=64, block_size=16, num_blocks=num_blocks, max_batch=32,
+                       n_layers=24, dtype=KVC_F16, kv_write=True, clock_mode=1, virt_c0=COST[0],
+                       virt_c1=COST[1], virt_c2=COST[2])
+    eng = Engine(cfg)
+    rc, ref = orc.sim_engine(p, g, a, 16, num_blocks, 32, True, COST)
+    _same(run_continuous(p, g, a, eng), ref)
+
+
+def test_measured_clock_invariants(orc):
+    say("engine measured clock")
+    p, g = orc.demo_trace(256, 123)
+    eng = Engine(EngineConfig(n_heads=8, head_dim=64, block_size=16, num_blocks=512, max_batch=32))
+    st = run_continuous(p, g, np.zeros(256), eng)
+    assert st.tokens == g.sum() and st.finished == 256 and st.peak_blocks <= 512
+    assert st.gpu_us > 0 and st.wall_us == pytest.approx(st.gpu_us)
+    ss = run_static(p, g, np.zeros(256), eng, 32)
+    assert ss.tokens == g.sum() and ss.finished == 256 and ss.iters >= st.iters

@@ -1,0 +1,176 @@
+"""The product's host logic (C++ BlockAllocator / Engine / run_static behind the
+C ABI, and the Python workload generators) against the oracle -- bit-exact, on
+the CPU.  The Engine runs in scheduling-only mode (device = 0, virtual clock):
+no GPU, same decisions, same packed per-step metadata (digest)."""
+import numpy as np
+import pytest
+
+from kvcache_amd import KVC_F16, KVC_F32
+from kvcache_amd import workloads as W
+from kvcache_amd._native import KVC_ERR_STATE, KvcError
+from kvcache_amd.engine import BlockAllocator, Engine, EngineConfig, blocks_needed, run_continuous, run_static
+
+
+def test_workload_generators_match_oracle(orc):
+    np.testing.assert_array_equal(W.ref_lengths(), orc.ref_lengths())
+    np.testing.assert_array_equal(W.ref_lengths(64, 4096, 99), orc.ref_lengths(64, 4096, 99))
+    for rate in (0.0, 400.0):
+        for a, b in zip(W.ref_trace(rate=rate), orc.ref_trace(rate=rate)):
+            np.testing.assert_array_equal(a, b)
+    s = np.arange(4)[:, None, None, None]
+    h = np.arange(3)[None, :, None, None]
+    pos = np.arange(5)[None, None, :, None]
+    d = np.arange(8)[None, None, None, :]
+    vec = W.hval(s, h, pos, d, 2)
+    ref = np.vectorize(lambda a, b, c, e: orc.hval(int(a), int(b), int(c), int(e), 2))(s, h, pos, d)
+    np.testing.assert_array_equal(vec, ref.astype(np.float32))
+
+
+def test_baseline_generators_are_seeded_and_shaped():
+    a = W.loguniform_lengths(128, 16, 2048, 7)
+    assert np.array_equal(a, W.loguniform_lengths(128, 16, 2048, 7)) and a.min() >= 16 and a.max() <= 2048
+    p, g, arr = W.baseline_trace(256, 400.0, 11)
+    assert p.min() >= 1 and p.max() <= 256 and g.min() >= 1 and g.max() <= 512 and np.all(np.diff(arr) > 0)
+    assert 100 < g.mean() < 260
+
+
+def _script(seed, n=300):
+    r = np.random.default_rng(seed)
+    ops, args = [], []
+    for _ in range(n):
+        x = r.random()
+        if x < 0.6:
+            ops.append(0); args.append(0)
+        elif x < 0.95:
+            ops.append(-1); args.append(int(r.integers(1, 6)))
+        else:
+            ops.append(-2); args.append(0)
+    return ops, args
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_block_allocator_matches_oracle_and_reference(orc, seed):
+    ops, args = _script(seed)
+    a = BlockAllocator(16)
+    held, out = [], []
+    for o, k in zip(ops, args):
+        if o == 0:
+            b = a.alloc(); out.append(b)
+            if b >= 0:
+                held.append(b)
+        elif o == -1:
+            fr, held = held[:k], held[k:]
+            a.free_blocks(fr); out.append(a.free_count())
+        else:
+            a.reset(); held = []; out.append(a.free_count())
+    assert out == orc.alloc_script(16, ops, args).tolist()
+    if orc.ref_driver_available():
+        text = "16\n" + "".join("A\n" if o == 0 else (f"F {k}\n" if o == -1 else "R\n") for o, k in zip(ops, args))
+        assert out == orc.run_ref_alloc_driver(text)
+
+
+def test_allocator_basics_and_shuffle():
+    a = BlockAllocator(8)
+    assert [a.alloc() for _ in range(3)] == [0, 1, 2] and a.used_count() == 3
+    a.free_blocks([1, 0])
+    assert a.alloc() == 0 and a.alloc() == 1
+    b = BlockAllocator(1000)
+    b.shuffle(5)
+    got = [b.alloc() for _ in range(1000)]
+    assert sorted(got) == list(range(1000)) and got != list(range(1000)) and b.alloc() == -1
+    assert blocks_needed(17, 16) == 2 and blocks_needed(0, 16) == 0
+
+
+COST = (20.0, 1.5, 0.01)
+
+
+def _cfg(block, num_blocks, width, kv_write, **kw):
+    return EngineConfig(n_heads=8, head_dim=64, block_size=block, num_blocks=num_blocks, max_batch=width,
+                        kv_write=kv_write, clock_mode=1, virt_c0=COST[0], virt_c1=COST[1], virt_c2=COST[2],
+                        device=False, **kw)
+
+
+def _same(ours, ref):
+    assert ours.iters == ref.iters
+    assert ours.tokens == ref.tokens
+    assert ours.slot_steps == ref.slot_steps and ours.useful_steps == ref.useful_steps
+    assert ours.peak_blocks == ref.peak_blocks and ours.finished == ref.finished
+    assert ours.gpu_us == ref.gpu_us and ours.wall_us == ref.wall_us
+    assert ours.avg_latency_us == ref.avg_latency_us
+    assert ours.p50_latency_us == ref.p50_latency_us and ours.p99_latency_us == ref.p99_latency_us
+    assert ours.step_digest == ref.digest
+
+
+TRACES = {
+    "ref_offline": lambda: W.ref_trace(),
+    "ref_poisson400": lambda: W.ref_trace(rate=400.0),
+    "baseline_offline": lambda: W.baseline_trace(256, 0.0, 11),
+    "baseline_poisson400": lambda: W.baseline_trace(256, 400.0, 11),
+}
+
+
+@pytest.mark.parametrize("trace", sorted(TRACES))
+@pytest.mark.parametrize("kv_write", [False, True])
+def test_engine_and_static_match_oracle(orc, trace, kv_write):
+    p, g, a = TRACES[trace]()
+    for num_blocks in (32768, 600):  # roomy pool, and one where the reservation binds
+        eng = Engine(_cfg(16, num_blocks, 32, kv_write))
+        rc, ref = orc.sim_engine(p, g, a, 16, num_blocks, 32, kv_write, COST)
+        assert rc == 0
+        _same(run_continuous(p, g, a, eng), ref)
+        rc, ref_s, _ = orc.sim_static(p, g, a, 16, num_blocks, 32, kv_write, COST)
+        _same(run_static(p, g, a, eng, 32), ref_s)
+
+
+def test_engine_reference_known_answers():
+    p, g, a = W.ref_trace()
+    eng = Engine(_cfg(16, 32768, 32, False))
+    st = run_static(p, g, a, eng, 32)
+    assert st.iters == 3898 and st.tokens == 48523 and round(100 * st.slot_util, 1) == 38.9
+    co = run_continuous(p, g, a, eng)
+    assert co.iters == 1801 and co.slot_util == 1.0
+
+
+def test_engine_demo_invariants(orc):
+    p, g = orc.demo_trace(256, 123)
+    eng = Engine(_cfg(16, 512, 32, False))
+    st = run_continuous(p, g, np.zeros(256), eng)
+    assert st.tokens == g.sum() and st.finished == 256 and st.peak_blocks <= 512
+
+
+def test_engine_step_api_and_reset():
+    eng = Engine(_cfg(16, 100, 4, False))
+    for i in range(6):
+        eng.add_request(10, 3)
+    steps = 0
+    while eng.step():
+        steps += 1
+    st = eng.stats()
+    assert st.finished == 6 and st.tokens == 18
+    eng.reset()
+    assert eng.stats().iters == 0
+
+
+def test_never_admissible_request_raises():
+    eng = Engine(_cfg(16, 5, 4, False))
+    eng.add_request(50, 50)
+    with pytest.raises(KvcError) as e:
+        eng.run()
+    assert e.value.status == KVC_ERR_STATE
+
+
+def test_out_of_order_arrivals_rejected():
+    eng = Engine(_cfg(16, 100, 4, False))
+    eng.add_request(5, 5, 100.0)
+    with pytest.raises(KvcError):
+        eng.add_request(5, 5, 50.0)
+
+
+@pytest.mark.parametrize("dtype", [KVC_F32, KVC_F16])
+def test_gqa_layers_config_is_accepted_host_only(dtype):
+    cfg = _cfg(16, 10922, 32, True, n_kv_heads=2, n_layers=24, dtype=dtype)
+    cfg.n_heads = 14
+    eng = Engine(cfg)
+    p, g, a = W.ref_trace(nreq=64)
+    st = run_continuous(p, g, a, eng)
+    assert st.tokens == g.sum()

@@ -1,0 +1,205 @@
+"""Pins the oracle's workload generators and scheduling restatement.
+
+Known answers come from the reference README (tests/golden/known_answers.json),
+from its test programs (test_kv_manager.cu, demo_engine.cu) and from closed
+forms of the policies (batch width 1 -> sequential, width >= n -> one wave).
+The allocator is also compared with the reference's own block_alloc.h compiled
+by oracle/Makefile (oracle/_ref) when the reference tree is present.
+"""
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+GOLDEN = json.loads((Path(__file__).parent / "golden" / "known_answers.json").read_text())["published"]
+
+
+def pub(key):
+    return GOLDEN[key]["value"]
+
+
+# ---- workload generators -------------------------------------------------------
+def test_ragged_lengths_known_answers(orc):
+    L = orc.ref_lengths(128, 2048, 12345)
+    assert L.sum() == 83212 and L.max() == 2022 and L.min() >= 16
+    assert round(L.mean()) == pub("ragged_batch_mean_len")
+    H, D, B, LMAX, MB = 8, 64, 16, 2048, 1048576.0
+    blocks = sum((int(x) + B - 1) // B for x in L)
+    assert blocks == 5259
+    reserved = 128 * H * LMAX * D * 4 * 2 / MB           # bench_throughput.cu:75
+    used = L.sum() * H * D * 4 * 2 / MB                  # :76
+    paged = (blocks * H * B * D * 4 * 2 + blocks * 4) / MB   # :77-78
+    assert round(reserved) == pub("ragged_batch_reserved_mb_contiguous")
+    assert round(used) == pub("ragged_batch_used_mb_contiguous")
+    assert round(paged) == pub("ragged_batch_mb_paged")
+    assert round(100 * used / reserved, 1) == pub("ragged_batch_util_pct_contiguous")
+    budget = 4096 * MB                                    # :135-139
+    per_seq_paged = ((int(L.mean()) + B - 1) // B) * H * B * D * 4 * 2
+    assert int(budget / (H * LMAX * D * 4 * 2)) == pub("budget_4096mb_max_seqs_contiguous")
+    assert int(budget / per_seq_paged) == pub("budget_4096mb_max_seqs_paged")
+
+
+def test_continuous_trace_known_answers(orc):
+    p, g, a = orc.ref_trace(256, 256, 512, 0.0, 2024)
+    assert g.sum() == 48523 and abs(g.sum() - pub("offline_generated_tokens_approx")) < 100
+    assert np.all(a == 0) and 16 <= p.min() and p.max() < 256 and 8 <= g.min() and g.max() < 512
+    # online trace draws u after rp, rg (bench_continuous.cu:46), so lengths differ from offline
+    p2, g2, a2 = orc.ref_trace(256, 256, 512, 400.0, 2024)
+    assert np.all(np.diff(a2) > 0) and not np.array_equal(p2, p)
+    assert abs(a2[-1] / 1e6 - 256 / 400) < 0.25      # ~256 arrivals at 400/s
+
+
+def test_hval_and_shuffle(orc):
+    from kvcache_amd import workloads as W
+    for args in [(0, 0, 0, 0, 1), (5, 3, 100, 63, 2), (127, 7, 2021, 0, 3)]:
+        assert orc.hval(*args) == W.hval(*args)
+        assert -1.0 <= orc.hval(*args) < 1.0
+    perm = orc.shuffle_perm(64, 42)
+    assert sorted(perm.tolist()) == list(range(64)) and perm.tolist() != list(range(64))
+    np.testing.assert_array_equal(perm, W.shuffle_perm(64, 42))
+
+
+# ---- allocator / manager ---------------------------------------------------------
+def test_kv_manager_known_answers(orc):
+    # test_kv_manager.cu:13-55: 8 blocks x 4 tokens, Hkv 2, D 8
+    k = orc.Kvm(8, 4, 2, 8)
+    assert k.free_blocks() == 8
+    assert k.allocate_prompt(0, 5) and len(k.table(0)) == 2 and k.cur_len(0) == 5
+    assert k.free_blocks() == 6 and k.slack(0) == 3
+    for _ in range(3):
+        k.append_token(0)
+    assert len(k.table(0)) == 2 and k.slack(0) == 0
+    k.append_token(0)
+    assert len(k.table(0)) == 3 and k.cur_len(0) == 9 and k.free_blocks() == 5
+    assert k.allocate_prompt(1, 20) and k.free_blocks() == 0
+    assert not k.allocate_prompt(2, 1) and k.table(2) == []
+    assert not k.append_token(1)
+    k.free(0)
+    assert k.table(0) == [] and k.free_blocks() == 3
+    assert k.append_token(1)
+    # test_kv_manager.cu:53-55 expects (((3*2+1)*4+2)*8) = 240
+    assert k.slot_offset(3, 1, 2) == 240
+    # fresh pool hands out 0,1,2,...; A took 0,1 then 2; B took 3..7; A's free pushes
+    # 0,1,2 so B's growth pops 2 (LIFO, block_alloc.h:16,25,31)
+    assert k.table(1) == [3, 4, 5, 6, 7, 2]
+
+
+def _random_script(seed, total=16, n=200):
+    r = np.random.default_rng(seed)
+    ops, args = [], []
+    for _ in range(n):
+        x = r.random()
+        if x < 0.6:
+            ops.append(0); args.append(0)
+        elif x < 0.95:
+            ops.append(-1); args.append(int(r.integers(1, 6)))
+        else:
+            ops.append(-2); args.append(0)
+    return ops, args
+
+
+def _script_text(total, ops, args):
+    lines = [str(total)]
+    for o, a in zip(ops, args):
+        lines.append("A" if o == 0 else (f"F {a}" if o == -1 else "R"))
+    return "\n".join(lines) + "\n"
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2, 3])
+def test_alloc_oracle_matches_reference_code(orc, seed):
+    if not orc.ref_driver_available():
+        pytest.skip("oracle/_ref not built (reference tree absent)")
+    ops, args = _random_script(seed)
+    ours = orc.alloc_script(16, ops, args).tolist()
+    ref = orc.run_ref_alloc_driver(_script_text(16, ops, args))
+    assert ours == ref
+
+
+def test_blocks_needed_and_done_against_reference_code(orc):
+    if not orc.ref_driver_available():
+        pytest.skip("oracle/_ref not built (reference tree absent)")
+    cases = [(l, b) for l in (0, 1, 15, 16, 17, 31, 32, 33, 1000) for b in (1, 4, 16)]
+    out = orc.run_ref_alloc_driver("1\n" + "".join(f"N {l} {b}\n" for l, b in cases))
+    assert out == [(l + b - 1) // b for l, b in cases]
+    out = orc.run_ref_alloc_driver("1\nD 5 9 4\nD 5 8 4\nD 0 0 0\n")
+    assert out == [1, 0, 1]
+
+
+# ---- scheduling ------------------------------------------------------------------
+POOL = 32768  # bench_continuous.cu:33-34: 2048 MB / (8*16*64*2*4 B)
+
+
+def test_static_offline_known_answers(orc):
+    p, g, a = orc.ref_trace()
+    rc, st, order = orc.sim_static(p, g, a, 16, POOL, 32)
+    assert rc == 0 and st.iters == pub("offline_static_iters")
+    assert round(100 * st.useful_steps / st.slot_steps, 1) == pub("offline_static_slot_util_pct")
+    assert st.tokens == 48523 and st.finished == 256
+    assert order[:3].tolist() == [176, 161, 162]     # libstdc++ introsort permutation of equal keys
+
+
+def test_continuous_offline_known_answers(orc):
+    p, g, a = orc.ref_trace()
+    rc, st = orc.sim_engine(p, g, a, 16, POOL, 32)
+    assert rc == 0 and st.iters == 1801 and st.tokens == 48523 and st.useful_steps == st.slot_steps
+    # README.md:96's 1701 is the Engine fed in run_static's std::sort order
+    _, _, order = orc.sim_static(p, g, a, 16, POOL, 32)
+    rc, st2 = orc.sim_engine(p[order], g[order], a[order], 16, POOL, 32)
+    assert st2.iters == pub("offline_continuous_iters_readme")
+    assert 100 * st2.useful_steps / st2.slot_steps == pub("offline_continuous_slot_util_pct")
+
+
+@pytest.mark.parametrize("kv_write", [False, True])
+def test_policy_closed_forms(orc, kv_write):
+    r = np.random.default_rng(3)
+    n = 40
+    p = r.integers(1, 60, n).astype(np.int32)
+    g = r.integers(1, 50, n).astype(np.int32)
+    a = np.zeros(n)
+    # width 1: strictly sequential; latency of request k = sum of gen[0..k] steps of cost 1
+    rc, st = orc.sim_engine(p, g, a, 16, 10000, 1, kv_write)
+    assert st.iters == g.sum() and st.tokens == g.sum()
+    lat = np.sort(np.cumsum(g).astype(np.float64))
+    assert st.avg_latency_us == pytest.approx(lat.mean(), abs=1e-9)
+    assert st.p99_latency_us == lat[min(int(n * 0.99), n - 1)]
+    assert st.p50_latency_us == lat[min(int(n * 0.5), n - 1)]
+    rc, ss, _ = orc.sim_static(p, g, a, 16, 10000, 1, kv_write)
+    assert ss.iters == g.sum() and ss.tokens == g.sum()
+    # width >= n: one wave of max(gen) steps for both policies
+    rc, st = orc.sim_engine(p, g, a, 16, 10000, n, kv_write)
+    assert st.iters == g.max()
+    rc, ss, _ = orc.sim_static(p, g, a, 16, 10000, n, kv_write)
+    assert ss.iters == g.max() and ss.slot_steps == n * g.max() and ss.useful_steps == g.sum()
+    # one wave: after step t the sequences with gen >= t hold ceil((prompt + t)/16) blocks;
+    # a sequence that finished at step t' < t was retired at the start of step t'+1
+    peak = max(sum((int(pi) + t + 15) // 16 for pi, gi in zip(p, g) if gi >= t) for t in range(1, g.max() + 1))
+    assert st.peak_blocks == peak
+
+
+def test_isolated_poisson_arrivals(orc):
+    # arrivals far apart: every request runs alone, latency = gen * c0
+    n = 20
+    p = np.full(n, 10, np.int32)
+    g = np.arange(1, n + 1, dtype=np.int32)
+    a = np.arange(n) * 1e6
+    rc, st = orc.sim_engine(p, g, a, 16, 1000, 8, False, (5.0, 0.0, 0.0))
+    lat = np.sort(g * 5.0)
+    assert st.avg_latency_us == pytest.approx(lat.mean()) and st.iters == g.sum()
+    assert st.wall_us == pytest.approx(a[-1] + g[-1] * 5.0)
+
+
+def test_demo_engine_invariants(orc):
+    # demo_engine.cu:14-42: 8 heads, D 64, BLOCK 16, 512 blocks, width 32, srand(123)
+    p, g = orc.demo_trace(256, 123)
+    assert 8 <= p.min() and p.max() <= 127 and 16 <= g.min() and g.max() <= 215
+    rc, st = orc.sim_engine(p, g, np.zeros(256), 16, 512, 32)
+    assert rc == 0 and st.tokens == g.sum() and st.finished == 256 and st.peak_blocks <= 512
+
+
+def test_never_admissible_request_is_reported(orc):
+    # worst case ceil((prompt+gen)/16) = 7 blocks > pool of 5: the reference Engine would spin forever
+    rc, st = orc.sim_engine([50], [50], [0.0], 16, 5, 4)
+    assert rc == 1
+    rc, st, _ = orc.sim_static([50], [50], [0.0], 16, 5, 4)
+    assert rc == 1 and st.finished == 0
