@@ -41,7 +41,12 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def build_c2(lens, Hq, Hkv, D, B, rotate, seed):
+def set_tuning(key: str, value: int) -> None:
+    from kvcache_amd._native import check, lib
+    check(lib().kvc_set_tuning(key.encode(), int(value)))
+
+
+def build_c2(lens, Hq, Hkv, D, B, rotate, seed, shuffle=True):
     from kvcache_amd import KVC_F16
     from kvcache_amd.device import DeviceBuffer, fill_normal
     from kvcache_amd.engine import BlockAllocator
@@ -49,7 +54,8 @@ def build_c2(lens, Hq, Hkv, D, B, rotate, seed):
 
     nb = int(sum((int(x) + B - 1) // B for x in lens))
     alloc = BlockAllocator(nb)           # pool sized to actual use
-    alloc.shuffle(seed)                  # blocks come out in a seeded random physical order
+    if shuffle:
+        alloc.shuffle(seed)              # blocks come out in a seeded random physical order
     table, tab_off = build_tables(lens, B, alloc)
     N = len(lens)
     elems = nb * Hkv * B * D
@@ -63,7 +69,7 @@ def build_c2(lens, Hq, Hkv, D, B, rotate, seed):
     fill_normal(q, N * Hq * D, KVC_F16, seed * 1000 + 999)
     meta = dict(table=DeviceBuffer.from_numpy(table), tab_off=DeviceBuffer.from_numpy(tab_off),
                 lens=DeviceBuffer.from_numpy(np.asarray(lens, np.int32)), out=DeviceBuffer(N * Hq * D * 2))
-    return dict(nb=nb, table=table, tab_off=tab_off, pools=pools, q=q, **meta)
+    return dict(nb=nb, table_host=table, tab_off_host=tab_off, pools=pools, q=q, **meta)
 
 
 def alg_bytes(lens, Hq, Hkv, D, B, esz=2):
@@ -73,8 +79,10 @@ def alg_bytes(lens, Hq, Hkv, D, B, esz=2):
     return kv, kv + other
 
 
-def time_decode(W, lens, Hq, Hkv, D, B, split, steps, warmup, stream=None):
-    """Runs warmup + steps launches (rotating pools) and returns per-launch times (ms)."""
+def time_decode(W, lens, Hq, Hkv, D, B, split, steps, warmup, stream=None, per_launch=False):
+    """Runs warmup + steps back-to-back launches (rotating pools).  Returns (mean ms per
+    launch over the timed region bracketed by one event pair, per-launch event
+    intervals when per_launch -- those markers add inter-kernel gaps)."""
     from kvcache_amd import KVC_F16, ops
     from kvcache_amd.device import Event, synchronize
 
@@ -90,15 +98,51 @@ def time_decode(W, lens, Hq, Hkv, D, B, split, steps, warmup, stream=None):
     for i in range(warmup):
         launch(i)
     synchronize()
-    evs = [Event() for _ in range(steps + 1)]
-    evs[0].record(stream)
+    if per_launch:
+        evs = [Event() for _ in range(steps + 1)]
+        evs[0].record(stream)
+        for i in range(steps):
+            launch(i)
+            evs[i + 1].record(stream)
+        synchronize()
+        return evs[0].elapsed_ms(evs[-1]) / steps, np.array([evs[i].elapsed_ms(evs[i + 1]) for i in range(steps)])
+    e0, e1 = Event(), Event()
+    e0.record(stream)
     for i in range(steps):
         launch(i)
-        evs[i + 1].record(stream)
+    e1.record(stream)
     synchronize()
-    per = np.array([evs[i].elapsed_ms(evs[i + 1]) for i in range(steps)])
-    total = evs[0].elapsed_ms(evs[-1])
-    return per, total
+    return e0.elapsed_ms(e1) / steps, None
+
+
+def time_planned(W, lens, Hq, Hkv, D, B, steps, warmup, target=0, rotate=None):
+    """The planned path: the host plan (built once from the host lengths, as the
+    scheduler does every step) is resident on the device; launches back to back."""
+    from kvcache_amd import KVC_F16, ops
+    from kvcache_amd.device import DeviceBuffer, Event, synchronize
+
+    work, nu, nr = ops.decode_plan(lens, Hq, Hkv, D, B, tab_off=W["tab_off_host"], dtype=KVC_F16,
+                                   target_tokens=target)
+    wdev = DeviceBuffer.from_numpy(work)
+    ws = DeviceBuffer(max(ops.planned_workspace_size(Hq, Hkv, D, nr), 256))
+    pools = W["pools"] if rotate is None else W["pools"][:rotate]
+    N = len(lens)
+
+    def launch(i):
+        k, v = pools[i % len(pools)]
+        ops.launch_batched_paged_planned(W["q"], k, v, W["table"], len(W["table_host"]), W["out"], N, Hq, Hkv, D,
+                                         B, 1.0 / np.sqrt(D), wdev, nu, nr, dtype=KVC_F16, workspace=ws)
+
+    for i in range(warmup):
+        launch(i)
+    synchronize()
+    e0, e1 = Event(), Event()
+    e0.record()
+    for i in range(steps):
+        launch(i)
+    e1.record()
+    synchronize()
+    return e0.elapsed_ms(e1) / steps, nu, nr, launch
 
 
 def check_c2(W, lens, Hq, Hkv, D, B, split):
@@ -116,9 +160,22 @@ def check_c2(W, lens, Hq, Hkv, D, B, split):
     kp, vp = k.to_numpy(np.float16, shape), v.to_numpy(np.float16, shape)
     q = W["q"].to_numpy(np.float16, (N, Hq, D))
     got = W["out"].to_numpy(np.float16, (N, Hq, D)).astype(np.float64)
-    ref = oracle.batched_paged(q, kp, vp, W["table"], W["tab_off"], lens, Hkv, B, 1.0 / np.sqrt(D),
+    ref = oracle.batched_paged(q, kp, vp, W["table_host"], W["tab_off_host"], lens, Hkv, B, 1.0 / np.sqrt(D),
                                nthreads=min(os.cpu_count() or 1, 16))
     return float(np.abs(got - ref).max()), (q, kp, vp)
+
+
+def check_planned(W, launch, lens, Hq, Hkv, D, B, host_data):
+    """The planned path's output on pool copy 0 against the oracle's."""
+    import oracle
+    from kvcache_amd.device import synchronize
+    launch(0)
+    synchronize()
+    q, kp, vp = host_data
+    got = W["out"].to_numpy(np.float16, (len(lens), Hq, D)).astype(np.float64)
+    ref = oracle.batched_paged(q, kp, vp, W["table_host"], W["tab_off_host"], lens, Hkv, B, 1.0 / np.sqrt(D),
+                               nthreads=min(os.cpu_count() or 1, 16))
+    return float(np.abs(got - ref).max())
 
 
 def cpu_baseline(host_data, W, lens, Hkv, B, D, budget_s, kv_bytes):
@@ -130,13 +187,14 @@ def cpu_baseline(host_data, W, lens, Hkv, B, D, budget_s, kv_bytes):
     threads = min(os.cpu_count() or 1, 16)
     reps, t0 = 0, time.perf_counter()
     while True:
-        oracle.batched_paged(q, kp, vp, W["table"], W["tab_off"], lens, Hkv, B, 1.0 / np.sqrt(D), nthreads=threads)
+        oracle.batched_paged(q, kp, vp, W["table_host"], W["tab_off_host"], lens, Hkv, B, 1.0 / np.sqrt(D),
+                             nthreads=threads)
         reps += 1
         if time.perf_counter() - t0 >= budget_s or reps >= 2000:
             break
     dt = (time.perf_counter() - t0) / reps
     t1 = time.perf_counter()
-    oracle.batched_paged(q, kp, vp, W["table"], W["tab_off"], lens, Hkv, B, 1.0 / np.sqrt(D), nthreads=1)
+    oracle.batched_paged(q, kp, vp, W["table_host"], W["tab_off_host"], lens, Hkv, B, 1.0 / np.sqrt(D), nthreads=1)
     dt1 = time.perf_counter() - t1
     cpu_model = ""
     try:
@@ -158,9 +216,8 @@ def bench_c3(steps, warmup):
     lens = np.array([8192, 16384, 32768, 32768], np.int32)
     Hq, Hkv, D, B = 14, 2, 64, 16
     W = build_c2(lens, Hq, Hkv, D, B, rotate=8, seed=3)   # 8 x 46 MB rotate past the Infinity Cache
-    per, _ = time_decode(W, lens, Hq, Hkv, D, B, 512, steps, warmup)
+    t, _ = time_decode(W, lens, Hq, Hkv, D, B, 512, steps, warmup)
     kv, total = alg_bytes(lens, Hq, Hkv, D, B)
-    t = float(np.mean(per))
     return {"workload": "C3 long-context split-K 14q/2kv D64 ctx {8k,16k,32k,32k} fp16 split 512",
             "us_per_step": round(t * 1e3, 2), "GBps": round(total / (t * 1e-3) / 1e9, 1),
             "frac_hbm_peak": round(total / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "kv_bytes": kv}
@@ -197,6 +254,25 @@ def bench_c4():
     return out
 
 
+def copy_calibration(mib: int) -> int:
+    """A plain copy of known size: under rocprofv3 --pmc its FETCH_SIZE / WRITE_SIZE per
+    dispatch against mib MiB gives the scale factor applied to the decode counters."""
+    from kvcache_amd._native import check, lib
+    from kvcache_amd.device import DeviceBuffer, Event, synchronize
+    n = mib << 20
+    a, b = DeviceBuffer(n), DeviceBuffer(n)
+    a.zero(); b.zero()
+    synchronize()
+    e0, e1 = Event(), Event()
+    e0.record()
+    for _ in range(10):
+        check(lib().kvc_memcpy_d2d(b.ptr, a.ptr, n, None))
+    e1.record()
+    ms = e0.elapsed_ms(e1) / 10
+    print(json.dumps({"copy_MiB": mib, "ms_per_copy": round(ms, 4), "GBps_read_plus_write": round(2 * n / ms / 1e6, 1)}))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -204,11 +280,22 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--split", type=int, default=0, help="decode split size in tokens (0 = automatic)")
     ap.add_argument("--rotate", type=int, default=4, help="pool copies cycled by the timed loop")
-    ap.add_argument("--lengths", choices=["reference", "loguniform"], default="reference")
+    ap.add_argument("--lengths", choices=["reference", "loguniform", "uniform"], default="reference",
+                    help="reference generator, log-uniform variant, or every sequence at the reference mean")
+    ap.add_argument("--no-shuffle", action="store_true", help="hand out pool blocks in order (diagnostic)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="skip configs 3 and 4")
-    ap.add_argument("--sweep", type=str, default="", help="comma list of split sizes to time (diagnostic)")
+    ap.add_argument("--sweep", type=str, default="",
+                    help="comma list of split[:waves_per_block[:fused_merge]] to time (diagnostic)")
+    ap.add_argument("--wpb", type=int, default=0, help="waves per workgroup (0 automatic, 4, 8)")
+    ap.add_argument("--batch", type=int, default=4, help="wave-loads per batch (2, 4, 8)")
+    ap.add_argument("--plan-target", type=int, default=0, help="planned path: tokens per unit (0 automatic)")
+    ap.add_argument("--plan-sweep", type=str, default="", help="comma list of planned targets to time")
+    ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
+                    help="only run 10 device-to-device copies of MIB MiB (HBM counter calibration) and exit")
+    ap.add_argument("--fused", type=int, default=-1,
+                    help="merge mode: -1 automatic, 0 merge kernel, 1 fused with fences, 2 fused coherent")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build targets one GPU; --gpus {a.gpus} is not supported (collectives and sharding "
@@ -222,11 +309,21 @@ def main() -> int:
     if not has_device():
         print("bench.py: no GPU visible", file=sys.stderr)
         return 1
-    lens = Wl.ref_lengths() if a.lengths == "reference" else Wl.loguniform_lengths(128, 16, 2048, 7)
+    set_tuning("waves_per_block", a.wpb)
+    set_tuning("fused_merge", a.fused)
+    set_tuning("batch", a.batch)
+    if a.copy_calib:
+        return copy_calibration(a.copy_calib)
+    if a.lengths == "reference":
+        lens = Wl.ref_lengths()
+    elif a.lengths == "loguniform":
+        lens = Wl.loguniform_lengths(128, 16, 2048, 7)
+    else:
+        lens = np.full(128, int(round(Wl.ref_lengths().mean())), np.int32)
     N, Hq, Hkv, D, B = 128, 8, 8, 64, 16
     split = a.split or ops.decode_auto_split(N, Hq, Hkv, D, B, int(lens.max()))
     log(f"C2: N={N} sum_len={int(lens.sum())} max={int(lens.max())} split={split} rotate={a.rotate}")
-    W = build_c2(lens, Hq, Hkv, D, B, a.rotate, seed=12345)
+    W = build_c2(lens, Hq, Hkv, D, B, a.rotate, seed=12345, shuffle=not a.no_shuffle)
     err, host_data = check_c2(W, lens, Hq, Hkv, D, B, split)
     log(f"parity vs oracle: max abs err {err:.3e} (bar 2e-3)")
     if not err <= 2e-3:
@@ -235,19 +332,39 @@ def main() -> int:
     kv, total = alg_bytes(lens, Hq, Hkv, D, B)
 
     sweep = {}
-    for s in [int(x) for x in a.sweep.split(",") if x]:
-        per, _ = time_decode(W, lens, Hq, Hkv, D, B, s, 20, 5)
-        sweep[s] = round(float(np.mean(per)) * 1e3, 2)
-        log(f"sweep split={s}: {sweep[s]} us")
+    knobs = [("waves_per_block", 0), ("fused_merge", -1), ("batch", 4), ("last_chunk_first", 1)]
+    for spec in [x for x in a.sweep.split(",") if x]:
+        # split[:waves_per_block[:fused_merge[:batch[:last_chunk_first]]]]
+        parts = [int(v) for v in spec.split(":")]
+        for (key, dflt), val in zip(knobs, parts[1:] + [None] * len(knobs)):
+            set_tuning(key, dflt if val is None else val)
+        t, _ = time_decode(W, lens, Hq, Hkv, D, B, parts[0], 30, 5)
+        sweep[spec] = round(t * 1e3, 2)
+        log(f"sweep split:wpb:merge:batch:order={spec}: {sweep[spec]} us")
+    set_tuning("waves_per_block", a.wpb)
+    set_tuning("fused_merge", a.fused)
+    set_tuning("batch", a.batch)
+    set_tuning("last_chunk_first", 1)
 
-    per, total_ms = time_decode(W, lens, Hq, Hkv, D, B, split, a.steps, a.warmup)
-    t_launch = float(np.mean(per))              # ms, mean of per-launch event intervals
-    ms_per_step = total_ms / a.steps
+    t_raw, _ = time_decode(W, lens, Hq, Hkv, D, B, split, a.steps, a.warmup)   # ms per launch
+    raw = total / (t_raw * 1e-3) / 1e9
+    log(f"C2 cold, device-lengths path (split {split}): {t_raw * 1e3:.2f} us/launch, {raw:.1f} GB/s")
+    for tgt in [int(x) for x in a.plan_sweep.split(",") if x]:
+        tp, nu, nr, _ = time_planned(W, lens, Hq, Hkv, D, B, 30, 5, target=tgt)
+        sweep[f"plan{tgt}"] = round(tp * 1e3, 2)
+        log(f"sweep planned target={tgt}: {tp * 1e3:.2f} us ({nu} units, {nr} records)")
+    t_launch, n_units, n_records, launch = time_planned(W, lens, Hq, Hkv, D, B, a.steps, a.warmup, target=a.plan_target)
+    err_planned = check_planned(W, launch, lens, Hq, Hkv, D, B, host_data)
+    log(f"planned parity vs oracle: max abs err {err_planned:.3e}")
+    if not err_planned <= 2e-3:
+        print(json.dumps({"metric": METRIC, "error": f"planned parity failure: max abs err {err_planned}"}))
+        return 1
+    ms_per_step = t_launch
     achieved = total / (t_launch * 1e-3) / 1e9
-    log(f"C2 cold: {t_launch * 1e3:.2f} us/launch (median {np.median(per) * 1e3:.2f}), {achieved:.1f} GB/s")
-    warm_per, _ = time_decode({**W, "pools": W["pools"][:1]}, lens, Hq, Hkv, D, B, split, a.steps, a.warmup)
-    warm = total / (float(np.mean(warm_per)) * 1e-3) / 1e9
-    log(f"C2 warm (one pool, Infinity-Cache resident): {np.mean(warm_per) * 1e3:.2f} us, {warm:.1f} GB/s")
+    log(f"C2 cold, planned path ({n_units} units): {t_launch * 1e3:.2f} us/launch, {achieved:.1f} GB/s")
+    t_warm, _, _, _ = time_planned(W, lens, Hq, Hkv, D, B, a.steps, a.warmup, target=a.plan_target, rotate=1)
+    warm = total / (t_warm * 1e-3) / 1e9
+    log(f"C2 warm (one pool, Infinity-Cache resident): {t_warm * 1e3:.2f} us, {warm:.1f} GB/s")
 
     extras = {}
     if not a.no_extras:
@@ -274,12 +391,13 @@ def main() -> int:
         "vs_baseline": None, "dtype": "f16", "data": "synthetic",
         "config": {"workload": "C2 batched ragged paged decode: N=128, reference lengths (seed 12345, sum 83212, "
                                "max 2022), H=8 (MHA), D=64, BLOCK=16, fp16 KV, fp32 accumulate, shuffled free list",
-                   "lengths": a.lengths, "split_tokens": split, "rotating_pool_copies": a.rotate,
-                   "parallelism": "single GPU"},
+                   "lengths": a.lengths, "path": "planned (host plan resident, one kernel per step)",
+                   "planned_units": n_units, "rotating_pool_copies": a.rotate, "parallelism": "single GPU"},
+        "device_lengths_path": {"split_tokens": split, "us_per_step": round(t_raw * 1e3, 3), "GBps": round(raw, 1)},
         "pct_hbm_peak": round(100 * achieved / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "split_kernel<_Float16,64,1,kPagedUniform> (fused LSE merge)",
+                     "kernel": "split_kernel<_Float16,64,1,kPagedUniform,4,4> (planned paged decode, fused LSE merge)",
                      "algorithmic_bytes_per_launch": total, "kv_bytes_per_launch": kv,
                      "mean_launch_us": round(t_launch * 1e3, 3)},
         "warm_GBps": round(warm, 1),

@@ -48,10 +48,15 @@ int         kvc_version(void);                 /* 100*major + minor */
 const char* kvc_status_string(int status);
 const char* kvc_last_error(void);               /* last failure on this host thread */
 int         kvc_device_count(int* count);
-/* Tuning knobs (process-wide): "fused_merge" (1: the last-arriving chunk of a
- * sequence merges the split partials inside the decode kernel; 0: a separate merge
- * kernel), "target_units" (automatic split: waves to aim for), "min_chunk_bytes"
- * (automatic split: least K+V bytes per wave). */
+/* Tuning knobs (process-wide): "fused_merge" (how split partials are merged:
+ * -1 automatic, 0 a separate merge kernel, 1 the last-arriving chunk merges
+ * behind agent-scope fences, 2 the last-arriving chunk merges partials written
+ * and read with coherent atomic accesses), "target_units" (automatic split:
+ * workgroups to aim for),
+ * "min_chunk_bytes" (automatic split: least K+V bytes per workgroup),
+ * "waves_per_block" (0 automatic, 4 or 8 waves cooperating on one chunk),
+ * "batch" (2, 4 or 8 wave-loads per double-buffered batch when a wave serves at
+ * most two query heads), "last_chunk_first" (1: dispatch later chunks first). */
 int         kvc_set_tuning(const char* key, int value);
 int         kvc_get_tuning(const char* key, int* value);
 
@@ -156,6 +161,27 @@ int kvc_batched_decode_split(const void* q, const void* k_cache, const void* v_c
 size_t kvc_decode_workspace_size(int N, int Hq, int Hkv, int D, int BLOCK, int cap, int split_tokens, int dtype);
 /* The split size the automatic choice picks for this shape (BLOCK = 0: contiguous). */
 int kvc_decode_auto_split(int N, int Hq, int Hkv, int D, int BLOCK, int cap, int dtype);
+
+/* Planned decode for host-known lengths (the serving path: the scheduler knows
+ * every length when it builds the step).  kvc_decode_plan cuts each sequence into
+ * near-equal block-aligned chunks sized so the batch fills the GPU about once and
+ * writes the units, longest first, as 8 ints each {s, kv_head_slot | chunk << 16,
+ * j0, j1, chunks, record group, counter, table index of the chunk's first block}
+ * into `work` (host memory; work == NULL only reports *n_units / *n_records).
+ * host_tab_off (N+1, may be NULL: tables packed in sequence order) locates each
+ * sequence's table in table_all.  target_tokens = 0 picks the chunk size.  The
+ * caller copies the work list to the device (e.g. inside its per-step upload) and
+ * runs kvc_batched_paged_decode_planned with the same shape and tables; every
+ * block-id read is bounded by table_len (ints in table_all).  Partials of split
+ * sequences are merged by the last chunk to finish, inside the same kernel. */
+int kvc_decode_plan(const int* host_lens, const int* host_tab_off, int N, int Hq, int Hkv, int D, int BLOCK,
+                    int dtype, int target_tokens, int* work, int capacity, int* n_units, int* n_records);
+size_t kvc_decode_planned_workspace_size(int Hq, int Hkv, int D, int n_records);
+int kvc_batched_paged_decode_planned(const void* q, const void* k_pool, const void* v_pool,
+                                     const int* table_all, int table_len, void* out,
+                                     int N, int Hq, int Hkv, int D, int BLOCK, float scale,
+                                     int dtype, const int* work, int n_units, int n_records,
+                                     void* workspace, size_t workspace_bytes, kvc_stream_t stream);
 
 /* launch_flash_decode (kv_cache.h:32-34, flash_decode.cu:103-126): one sequence,
  * contiguous [H,S,D], num_splits clamped to [1, cur_len]; split j covers

@@ -8,6 +8,7 @@
 #include "kvc_abi.h"
 
 #include <algorithm>
+#include <climits>
 #include <atomic>
 #include <cmath>
 #include <cstring>
@@ -63,8 +64,8 @@ int auto_split(int N, int Hq, int Hkv, int D, int BLOCK, int cap, int dtype) {
     const int group = Hq / Hkv;
     const int nsub = group / choose_g(group, D);
     const long long per_chunk_units = (long long)N * Hkv * nsub;
-    // Enough waves to keep every SIMD of the 256 CUs streaming, but never less
-    // than min_chunk_bytes of K+V per wave so the partial traffic stays small.
+    // Enough workgroups to keep all 256 CUs streaming, but never less than
+    // min_chunk_bytes of K+V per workgroup so the partial traffic stays small.
     const long long target_units = std::max(1, tuning().target_units);
     long long ch = per_chunk_units > 0 ? ((long long)std::max(cap, 1) * per_chunk_units + target_units - 1) / target_units : 1;
     const long long min_ch = std::max<long long>(16, tuning().min_chunk_bytes / (2LL * D * esize(dtype)));
@@ -78,9 +79,25 @@ int auto_split(int N, int Hq, int Hkv, int D, int BLOCK, int cap, int dtype) {
 }
 
 struct Plan {
-    int G = 1, nsub = 1, mode = kContiguous, chunk = 1, max_chunks = 1;
+    int G = 1, nsub = 1, mode = kContiguous, chunk = 1, max_chunks = 1, wpb = 4, lpb_shift = 0;
+    bool chunk_blocks_ok = true;  // the per-lane path stages at most 4096 block ids per chunk
     size_t acc_bytes = 0, ml_bytes = 0, ws_bytes = 0;
 };
+
+inline int ilog2_exact(int x) {  // log2 of a power of two, else -1
+    if (x <= 0 || (x & (x - 1))) return -1;
+    int r = 0;
+    while ((1 << r) < x) ++r;
+    return r;
+}
+
+// Waves per workgroup: 8 when the grid is small (long contexts, few sequences),
+// so each chunk still streams with many loads in flight; 4 otherwise.
+int choose_wpb(long long units) {
+    const int t = tuning().waves_per_block;
+    if (t == 4 || t == 8) return t;
+    return units < 1024 ? 8 : 4;
+}
 
 // Workspace: [part_acc | part_ml | arrival counters (one u64 per seq x KV head x subgroup)].
 void size_workspace(Plan& pl, int N, int Hq, int Hkv, int D) {
@@ -99,7 +116,18 @@ Plan plan_batched(int N, int Hq, int Hkv, int D, int BLOCK, int cap, int dtype, 
     pl.chunk = split > 0 ? split : auto_split(N, Hq, Hkv, D, paged ? BLOCK : 0, cap, dtype);
     pl.max_chunks = std::max(1, (std::max(cap, 0) + pl.chunk - 1) / pl.chunk);
     const int tpw = tokens_per_wave_load(D, dtype);
-    if (paged) pl.mode = (BLOCK % tpw == 0 && pl.chunk % BLOCK == 0) ? kPagedUniform : kPagedPerLane;
+    if (paged) {
+        // scalar block ids need whole wave-loads per block (a power of two of them)
+        // and at most 64 blocks per chunk (one table entry per lane)
+        const int lpb = BLOCK % tpw == 0 ? ilog2_exact(BLOCK / tpw) : -1;
+        const bool uniform = lpb >= 0 && pl.chunk % BLOCK == 0 && pl.chunk / BLOCK <= 64;
+        pl.mode = uniform ? kPagedUniform : kPagedPerLane;
+        pl.lpb_shift = uniform ? lpb : 0;
+        // per-lane path: block ids of a chunk are staged in LDS (at most 4096)
+        const int span = (pl.chunk + BLOCK - 1) / BLOCK + (pl.chunk % BLOCK ? 1 : 0);
+        pl.chunk_blocks_ok = uniform || span <= 4096;
+    }
+    pl.wpb = choose_wpb((long long)pl.max_chunks * N * Hkv * pl.nsub);
     size_workspace(pl, N, Hq, Hkv, D);
     return pl;
 }
@@ -152,10 +180,10 @@ int resolve_workspace(const Plan& pl, void* ws, size_t ws_bytes, DecodeParams& p
     }
     p.part_acc = static_cast<float*>(ws);
     p.part_ml = reinterpret_cast<float*>(static_cast<char*>(ws) + pl.acc_bytes);
-    p.counters = tuning().fused_merge
-                     ? reinterpret_cast<unsigned long long*>(static_cast<char*>(ws) + pl.acc_bytes + pl.ml_bytes)
-                     : nullptr;
+    p.counters = reinterpret_cast<unsigned long long*>(static_cast<char*>(ws) + pl.acc_bytes + pl.ml_bytes);
     p.epoch = next_epoch();
+    const int t = tuning().fused_merge;
+    p.merge_mode = t >= 0 ? t : (pl.max_chunks <= 8 ? kMergeAtomic : kMergeKernel);
     return KVC_OK;
 }
 
@@ -184,10 +212,12 @@ int run_batched(const void* q, const void* k, const void* v, const int* table_al
     if (paged && split > 0 && split % BLOCK) return set_error(KVC_ERR_ARG, "split_tokens must be a multiple of BLOCK");
     if (!std::isfinite(scale)) return set_error(KVC_ERR_ARG, "scale must be finite");
     const Plan pl = plan_batched(N, Hq, Hkv, D, BLOCK, cap, dtype, split, paged);
+    if (!pl.chunk_blocks_ok)
+        return set_error(KVC_ERR_UNSUPPORTED, "split_tokens spans more than 4096 blocks of this block size");
     DecodeLaunch L{};
     DecodeParams& p = L.p;
     p.q = q; p.k = k; p.v = v; p.out = out;
-    p.table_all = table_all; p.tab_off = tab_off; p.cur_len = cur_len; p.fixed_len = fixed_len;
+    p.table_all = table_all; p.tab_off = tab_off; p.cur_len = cur_len; p.fixed_len = fixed_len; p.cap = cap;
     p.seq_stride = seq_stride; p.head_stride = head_stride;
     p.N = N; p.Hq = Hq; p.Hkv = Hkv; p.block = paged ? BLOCK : 1;
     p.group = Hq / Hkv; p.nsub = pl.nsub;
@@ -195,8 +225,108 @@ int run_batched(const void* q, const void* k, const void* v, const int* table_al
     p.scale_log2 = scale * 1.4426950408889634f;
     rc = resolve_workspace(pl, ws, ws_bytes, p);
     if (rc) return rc;
-    L.dtype = dtype; L.D = D; L.G = pl.G; L.mode = pl.mode; L.need_merge = pl.max_chunks > 1;
+    p.lpb_shift = pl.lpb_shift;
+    p.last_chunk_first = tuning().last_chunk_first;
+    L.dtype = dtype; L.D = D; L.G = pl.G; L.mode = pl.mode; L.wpb = pl.wpb; L.batch = tuning().batch;
+    L.need_merge = pl.max_chunks > 1;
     return launch_decode(L, st);
+}
+
+// ---- planned decode (host-known lengths) ----------------------------------
+// A unit = {s, hk*nsub + sub, j0, j1, c, nc, record group, counter}.  Every
+// sequence is cut into nc near-equal chunks (multiples of BLOCK, at most 64
+// blocks so the uniform paged path applies) sized so the whole batch fills the
+// resident workgroup slots about once; units are sorted longest first so the
+// hardware dispatcher fills the machine greedily (longest-processing-time order).
+constexpr int kPlanInts = 8;
+
+struct PlanShape {
+    int G, nsub, hks, tpw, wpb, min_chunk, max_chunk;
+    bool uniform;
+};
+
+PlanShape plan_shape(int Hq, int Hkv, int D, int BLOCK, int dtype) {
+    PlanShape ps{};
+    const int group = Hq / Hkv;
+    ps.G = choose_g(group, D);
+    ps.nsub = group / ps.G;
+    ps.hks = Hkv * ps.nsub;
+    ps.tpw = tokens_per_wave_load(D, dtype);
+    const int lpb = BLOCK % ps.tpw == 0 ? ilog2_exact(BLOCK / ps.tpw) : -1;
+    ps.uniform = lpb >= 0;
+    ps.wpb = 4;
+    // each wave should stream at least two batches of 4 wave-loads
+    ps.min_chunk = ((ps.wpb * ps.tpw * 8 + BLOCK - 1) / BLOCK) * BLOCK;
+    ps.max_chunk = ps.uniform ? 64 * BLOCK : std::max(BLOCK, 4095 * BLOCK);
+    return ps;
+}
+
+int make_plan(const int* lens, const int* tab_off, int N, int Hq, int Hkv, int D, int BLOCK, int dtype, int target,
+              int* work, int capacity, int* n_units, int* n_records) {
+    const PlanShape ps = plan_shape(Hq, Hkv, D, BLOCK, dtype);
+    if (ps.hks > 0xFFFF) return set_error(KVC_ERR_UNSUPPORTED, "too many KV heads for the plan encoding");
+    long long total = 0;
+    for (int i = 0; i < N; ++i) total += std::max(lens[i], 1);
+    total *= ps.hks;
+    if (target <= 0) {
+        // resident workgroups: ~7 per CU for one or two heads per wave, ~3 for larger groups
+        const long long slots = 256LL * (ps.G <= 2 ? 7 : 3);
+        target = (int)std::min<long long>((total + slots - 1) / slots, INT_MAX / 2);
+    }
+    int T = std::max(target, ps.min_chunk);
+    T = (T + BLOCK - 1) / BLOCK * BLOCK;
+    T = std::min(T, ps.max_chunk);
+    struct U { int len, s, hks, j0, j1, c, nc, rec, ctr, tab; };
+    std::vector<U> units;
+    int rec = 0, ctr = 0;
+    long long off = 0;  // table start of sequence i when tab_off is not given: tables packed in order
+    for (int i = 0; i < N; ++i) {
+        const int L = std::max(lens[i], 0);
+        const long long t0 = tab_off ? tab_off[i] : off;
+        off += (L + BLOCK - 1) / BLOCK;
+        if (t0 > INT_MAX - (L + BLOCK - 1) / BLOCK) return set_error(KVC_ERR_ARG, "block tables too long");
+        int nc = 1, chunk = std::max(L, 1);
+        if (L > ps.max_chunk || L > T + T / 2) {
+            nc = std::max(2, (L + T / 2) / T);                      // nearest whole number of chunks
+            nc = std::max(nc, (L + ps.max_chunk - 1) / ps.max_chunk);
+            chunk = (L + nc - 1) / nc;
+            chunk = (chunk + BLOCK - 1) / BLOCK * BLOCK;            // block-aligned chunk starts
+            nc = (L + chunk - 1) / chunk;
+        }
+        if (nc > 0x7FFF) return set_error(KVC_ERR_UNSUPPORTED, "too many chunks per sequence for the plan encoding");
+        for (int h = 0; h < ps.hks; ++h) {
+            const int r = nc > 1 ? rec : -1, k = nc > 1 ? ctr : -1;
+            for (int c = 0; c < nc; ++c) {
+                const int j0 = std::min(c * chunk, L), j1 = std::min(j0 + chunk, L);
+                units.push_back(U{j1 - j0, i, h, j0, j1, c, nc, r, k, (int)t0 + j0 / BLOCK});
+            }
+            if (nc > 1) { rec += nc; ++ctr; }
+        }
+    }
+    std::stable_sort(units.begin(), units.end(), [](const U& a, const U& b) { return a.len > b.len; });
+    *n_units = (int)units.size();
+    *n_records = rec;
+    if (!work) return KVC_OK;  // size query
+    if (capacity < (int)units.size())
+        return set_error(KVC_ERR_WORKSPACE, "plan capacity " + std::to_string(capacity) + " < " +
+                                                std::to_string(units.size()) + " units");
+    for (size_t u = 0; u < units.size(); ++u) {
+        int* w = work + u * kPlanInts;
+        w[0] = units[u].s; w[1] = units[u].hks | (units[u].c << 16); w[2] = units[u].j0; w[3] = units[u].j1;
+        w[4] = units[u].nc; w[5] = units[u].rec; w[6] = units[u].ctr; w[7] = units[u].tab;
+    }
+    return KVC_OK;
+}
+
+size_t planned_workspace(int Hq, int Hkv, int D, int n_records) {
+    if (n_records <= 0) return 0;
+    Plan pl;
+    const int group = Hq / Hkv;
+    pl.G = choose_g(group, D);
+    const size_t recs = (size_t)n_records * pl.G;
+    pl.acc_bytes = align_up(recs * D * sizeof(float), kAlign);
+    pl.ml_bytes = align_up(recs * 2 * sizeof(float), kAlign);
+    return pl.acc_bytes + pl.ml_bytes + align_up((size_t)n_records * sizeof(uint64_t), kAlign);
 }
 
 template <class F>
@@ -434,6 +564,74 @@ int kvc_batched_paged_decode_split(const void* q, const void* k_pool, const void
     });
 }
 
+int kvc_decode_plan(const int* host_lens, const int* host_tab_off, int N, int Hq, int Hkv, int D, int BLOCK,
+                    int dtype, int target_tokens, int* work, int capacity, int* n_units, int* n_records) {
+    return guarded([&]() -> int {
+        if (!n_units || !n_records) return set_error(KVC_ERR_ARG, "null output pointer");
+        if (N < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || BLOCK <= 0) return set_error(KVC_ERR_ARG, "bad shape");
+        if (!d_ok(D)) return set_error(KVC_ERR_UNSUPPORTED, "head_dim must be 32, 64, 128 or 256");
+        if (!dtype_ok(dtype)) return set_error(KVC_ERR_ARG, "bad dtype");
+        if (N > 0 && !host_lens) return set_error(KVC_ERR_ARG, "null lengths");
+        return make_plan(host_lens, host_tab_off, N, Hq, Hkv, D, BLOCK, dtype, target_tokens, work, capacity, n_units,
+                         n_records);
+    });
+}
+
+size_t kvc_decode_planned_workspace_size(int Hq, int Hkv, int D, int n_records) {
+    if (Hq <= 0 || Hkv <= 0 || Hq % Hkv || !d_ok(D) || n_records < 0) return 0;
+    return planned_workspace(Hq, Hkv, D, n_records);
+}
+
+int kvc_batched_paged_decode_planned(const void* q, const void* k_pool, const void* v_pool, const int* table_all,
+                                     int table_len, void* out, int N, int Hq, int Hkv, int D, int BLOCK,
+                                     float scale, int dtype, const int* work, int n_units, int n_records, void* ws,
+                                     size_t ws_bytes, kvc_stream_t st) {
+    return guarded([&]() -> int {
+        int rc = check_common(N, Hq, Hkv, D, dtype, q, k_pool, v_pool, out);
+        if (rc || N == 0 || n_units == 0) return rc;
+        if (BLOCK <= 0 || !table_all || table_len <= 0 || !work || n_units < 0 || n_records < 0)
+            return set_error(KVC_ERR_ARG, "planned decode needs BLOCK > 0, a block table and a work list");
+        if (!std::isfinite(scale)) return set_error(KVC_ERR_ARG, "scale must be finite");
+        const PlanShape ps = plan_shape(Hq, Hkv, D, BLOCK, dtype);
+        DecodeLaunch L{};
+        DecodeParams& p = L.p;
+        p.q = q; p.k = k_pool; p.v = v_pool; p.out = out;
+        p.table_all = table_all; p.table_len = table_len;
+        p.N = N; p.Hq = Hq; p.Hkv = Hkv; p.block = BLOCK;
+        p.group = Hq / Hkv; p.nsub = ps.nsub;
+        p.chunk_tokens = 1; p.max_chunks = 1; p.cap = INT_MAX;
+        p.scale_log2 = scale * 1.4426950408889634f;
+        p.work = work;
+        p.lpb_shift = ps.uniform ? ilog2_exact(BLOCK / ps.tpw) : 0;
+        if (n_records > 0) {
+            const size_t need = planned_workspace(Hq, Hkv, D, n_records);
+            if (!ws) {
+                rc = default_workspace(need, &ws);
+                if (rc) return rc;
+            } else if (ws_bytes < need) {
+                return set_error(KVC_ERR_WORKSPACE, "workspace too small: need " + std::to_string(need) +
+                                                        " bytes, got " + std::to_string(ws_bytes));
+            } else if (((uintptr_t)ws & 15u) != 0) {
+                return set_error(KVC_ERR_ARG, "workspace must be 16-byte aligned");
+            }
+            const size_t recs = (size_t)n_records * ps.G;
+            const size_t acc = align_up(recs * D * sizeof(float), kAlign), ml = align_up(recs * 2 * sizeof(float), kAlign);
+            p.part_acc = static_cast<float*>(ws);
+            p.part_ml = reinterpret_cast<float*>(static_cast<char*>(ws) + acc);
+            p.counters = reinterpret_cast<unsigned long long*>(static_cast<char*>(ws) + acc + ml);
+        }
+        p.epoch = next_epoch();
+        p.merge_mode = tuning().fused_merge == kMergeFence ? kMergeFence : kMergeAtomic;  // planned: always fused
+        // the grid is the unit list; chunk_range is not used on this path
+        L.dtype = dtype; L.D = D; L.G = ps.G; L.mode = ps.uniform ? kPagedUniform : kPagedPerLane;
+        L.wpb = tuning().waves_per_block ? tuning().waves_per_block : ps.wpb;
+        L.batch = tuning().batch;
+        L.need_merge = false;
+        L.units = n_units;
+        return launch_decode(L, S(st));
+    });
+}
+
 size_t kvc_decode_workspace_size(int N, int Hq, int Hkv, int D, int BLOCK, int cap, int split, int dtype) {
     if (N <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || !d_ok(D) || cap < 0 || split < 0 || !dtype_ok(dtype)) return 0;
     return plan_batched(N, Hq, Hkv, D, BLOCK, cap, dtype, split, BLOCK > 0).ws_bytes;
@@ -455,9 +653,12 @@ size_t kvc_flash_decode_workspace_size(int H, int D, int num_splits) {
 int kvc_set_tuning(const char* key, int value) {
     if (!key) return set_error(KVC_ERR_ARG, "null key");
     const std::string k(key);
-    if (k == "fused_merge") tuning().fused_merge = value ? 1 : 0;
+    if (k == "fused_merge" && value >= -1 && value <= 2) tuning().fused_merge = value;
     else if (k == "target_units" && value > 0) tuning().target_units = value;
     else if (k == "min_chunk_bytes" && value > 0) tuning().min_chunk_bytes = value;
+    else if (k == "waves_per_block" && (value == 0 || value == 4 || value == 8)) tuning().waves_per_block = value;
+    else if (k == "batch" && (value == 2 || value == 4 || value == 8)) tuning().batch = value;
+    else if (k == "last_chunk_first" && (value == 0 || value == 1)) tuning().last_chunk_first = value;
     else return set_error(KVC_ERR_ARG, "unknown tuning key or bad value: " + k);
     return KVC_OK;
 }
@@ -468,6 +669,9 @@ int kvc_get_tuning(const char* key, int* value) {
     if (k == "fused_merge") *value = tuning().fused_merge;
     else if (k == "target_units") *value = tuning().target_units;
     else if (k == "min_chunk_bytes") *value = tuning().min_chunk_bytes;
+    else if (k == "waves_per_block") *value = tuning().waves_per_block;
+    else if (k == "batch") *value = tuning().batch;
+    else if (k == "last_chunk_first") *value = tuning().last_chunk_first;
     else return set_error(KVC_ERR_ARG, "unknown tuning key: " + k);
     return KVC_OK;
 }
@@ -488,13 +692,17 @@ int kvc_flash_decode(const void* q, const void* k_cache, const void* v_cache, vo
         DecodeParams& p = L.p;
         p.q = q; p.k = k_cache; p.v = v_cache; p.out = out;
         p.fixed_len = std::max(cur_len, 0);
+        p.cap = p.fixed_len;
         p.seq_stride = 0; p.head_stride = (long long)S_ * D;
         p.N = 1; p.Hq = H; p.Hkv = H; p.block = 1; p.group = 1; p.nsub = 1;
         p.chunk_tokens = 0; p.num_splits = ns; p.max_chunks = ns;
         p.scale_log2 = scale * 1.4426950408889634f;
         rc = resolve_workspace(pl, ws, ws_bytes, p);
         if (rc) return rc;
-        L.dtype = dtype; L.D = D; L.G = 1; L.mode = kContiguous; L.need_merge = ns > 1;
+        p.last_chunk_first = tuning().last_chunk_first;
+        L.dtype = dtype; L.D = D; L.G = 1; L.mode = kContiguous; L.wpb = choose_wpb((long long)ns * H);
+        L.batch = tuning().batch;
+        L.need_merge = ns > 1;
         return launch_decode(L, S(st));
     });
 }

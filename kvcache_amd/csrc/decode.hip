@@ -42,8 +42,6 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kWave = 64;
-constexpr int kWavesPerBlock = 4;
-constexpr int kThreads = kWave * kWavesPerBlock;
 
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {
@@ -123,7 +121,7 @@ __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirs
 // unit has no chunk (beyond the sequence's chunk count).
 __device__ __forceinline__ bool chunk_range(const DecodeParams& p, int s, int c, int& nc, int& j0, int& j1) {
     int L = p.cur_len ? p.cur_len[s] : p.fixed_len;
-    L = L > 0 ? L : 0;
+    L = min(max(L, 0), p.cap);  // a length above the stated cap never reads past the caches
     if (p.num_splits > 0) {
         nc = p.num_splits;
         const int ch = (L + nc - 1) / nc;
@@ -139,30 +137,36 @@ __device__ __forceinline__ bool chunk_range(const DecodeParams& p, int s, int c,
     return c < nc;
 }
 
-// Log-sum-exp merge of the nc chunk partials of (sequence s, query head hq):
+// Log-sum-exp merge of the nc chunk partials of one query head: chunk c's
+// record is rec0 + c*cstride (acc at record*D, (m, l) at record*2):
 //   M = max_c m_c,  out = sum_c 2^(m_c-M) acc_c / sum_c 2^(m_c-M) l_c.
-// One wave; lane d owns output dims d, d+64, ...
-template <typename T, int D>
-__device__ __forceinline__ void merge_head(const DecodeParams& p, int s, int hq, int nc, int lane) {
+// One wave; lane d owns output dims d, d+64, ...  COHERENT reads the partials
+// with agent-scope atomic loads (partials written by other XCDs bypass stale
+// L2 lines); otherwise plain loads after an acquire fence.
+template <typename T, int D, bool COHERENT>
+__device__ __forceinline__ void merge_head(const DecodeParams& p, size_t rec0, size_t cstride, int nc, T* ob,
+                                           int lane) {
     constexpr int DPL = (D + kWave - 1) / kWave;
-    const size_t rec0 = (size_t)s * p.max_chunks * p.Hq + hq;
+    auto ld = [](const float* a) {
+        if constexpr (COHERENT) return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else return *a;
+    };
     float M = -FLT_MAX;
-    for (int c = 0; c < nc; ++c) M = fmaxf(M, p.part_ml[(rec0 + (size_t)c * p.Hq) * 2]);
+    for (int c = 0; c < nc; ++c) M = fmaxf(M, ld(p.part_ml + (rec0 + (size_t)c * cstride) * 2));
     float l = 0.f, acc[DPL];
 #pragma unroll
     for (int j = 0; j < DPL; ++j) acc[j] = 0.f;
     for (int c = 0; c < nc; ++c) {
-        const size_t rec = rec0 + (size_t)c * p.Hq;
-        const float w = fast_exp2(p.part_ml[rec * 2] - M);
-        l = __builtin_fmaf(w, p.part_ml[rec * 2 + 1], l);
+        const size_t rec = rec0 + (size_t)c * cstride;
+        const float w = fast_exp2(ld(p.part_ml + rec * 2) - M);
+        l = __builtin_fmaf(w, ld(p.part_ml + rec * 2 + 1), l);
 #pragma unroll
         for (int j = 0; j < DPL; ++j) {
             const int d = lane + j * kWave;
-            if (d < D) acc[j] = __builtin_fmaf(w, p.part_acc[rec * D + d], acc[j]);
+            if (d < D) acc[j] = __builtin_fmaf(w, ld(p.part_acc + rec * D + d), acc[j]);
         }
     }
     const float inv = l > 0.f ? 1.0f / l : 0.f;
-    T* ob = static_cast<T*>(p.out) + ((size_t)s * p.Hq + hq) * D;
 #pragma unroll
     for (int j = 0; j < DPL; ++j) {
         const int d = lane + j * kWave;
@@ -185,28 +189,89 @@ __device__ __forceinline__ unsigned arrive(unsigned long long* ctr, unsigned epo
     }
 }
 
-template <typename T, int D, int G, int MODE>
-__global__ __launch_bounds__(kThreads) void split_kernel(DecodeParams p) {
+// K/V registers of U wave-loads: the double-buffered unit of the inner loop.
+template <int U>
+struct Batch {
+    u32x4 k[U], v[U];
+    int k0;  // this wave's index of the batch's first wave-load
+};
+
+// Buffer descriptor over `bytes` bytes at `base` (raw, unswizzled, 32-bit data
+// format).  Loads whose offset is >= bytes return 0 and touch no memory.
+constexpr int kBufferWord3 = 0x00020000;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, kBufferWord3);
+}
+__device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, int voffset) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, voffset, 0, 0);
+}
+
+// Largest chunk, in blocks, the per-lane paged path stages in LDS.
+constexpr int kMaxChunkBlocks = 4096;
+
+// One workgroup of WPB waves per unit (sequence s, KV head hk, head subgroup,
+// chunk c).  The chunk's wave-loads (TPW tokens each) are dealt round-robin to
+// the waves; every wave keeps two batches of U wave-loads in flight (ping-pong)
+// and its own online-softmax state per token slot.  Loads carry no control flow:
+// contiguous and uniform-paged tiles are read with buffer loads whose descriptor
+// covers exactly the tile's valid rows (rows past the chunk read as 0 and cost
+// no memory traffic), so the compiler can count outstanding loads exactly and
+// the next batch streams while the current one is consumed.  At the end the
+// token slots are merged with lane shuffles, the waves through LDS, and wave 0
+// writes either the normalised output (single-chunk sequence) or the chunk
+// partial, optionally followed by the fused cross-chunk merge.
+template <typename T, int D, int G, int MODE, int WPB, int U>
+__global__ __launch_bounds__(WPB * kWave) void split_kernel(DecodeParams p) {
     using Tr = Traits<T>;
     constexpr int EPL = Tr::EPL;
     constexpr int LPT = D / EPL;      // lanes per K/V row
     constexpr int TPW = kWave / LPT;  // rows (tokens) per wave-wide load
-    constexpr int U = G <= 2 ? 4 : 2; // wave-loads in flight per iteration
+    constexpr int ROW = D * (int)sizeof(T);  // bytes per K/V row
     static_assert(LPT >= 1 && LPT <= kWave && D % EPL == 0, "unsupported head_dim");
+    __shared__ float s_acc[WPB][G][D];
+    __shared__ float s_m[WPB][G], s_l[WPB][G];
+    __shared__ int s_tab[MODE == kPagedPerLane ? kMaxChunkBlocks : 1];
 
     const int lane = threadIdx.x & (kWave - 1);
+    const int wave = uniform(threadIdx.x >> 6);
     const int tslot = lane / LPT;
     const int dl = lane % LPT;
 
-    int unit = uniform(blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6));
-    const int sub = unit % p.nsub;  unit /= p.nsub;
-    const int hk = unit % p.Hkv;    unit /= p.Hkv;
-    const int s = unit % p.N;
-    const int c = unit / p.N;
-    if (c >= p.max_chunks) return;
-    int nc, j0, j1;
-    if (!chunk_range(p, s, c, nc, j0, j1)) return;
+    int s, hk, sub, c, nc, j0, j1;
+    size_t rec0, cstride, ctr_idx;  // partial record of (this chunk, head 0); stride between chunks; counter
+    int tab_start = 0;  // planned: index into table_all of the chunk's first block
+    if (p.work != nullptr) {
+        // planned unit {s, hks | c << 16, j0, j1, nc, record group, counter, table start}
+        const int* w = p.work + (size_t)blockIdx.x * 8;
+        s = w[0];
+        const int hks = w[1] & 0xFFFF;
+        c = w[1] >> 16;
+        hk = hks / p.nsub;
+        sub = hks % p.nsub;
+        j0 = max(w[2], 0);
+        j1 = max(w[3], j0);
+        nc = max(w[4], 1);
+        rec0 = (size_t)(w[5] > 0 ? w[5] : 0) * G + (size_t)c * G;
+        cstride = G;
+        ctr_idx = w[6] > 0 ? w[6] : 0;
+        tab_start = w[7];
+    } else {
+        int unit = blockIdx.x;
+        sub = unit % p.nsub;  unit /= p.nsub;
+        hk = unit % p.Hkv;    unit /= p.Hkv;
+        s = unit % p.N;
+        // chunk index is the slowest-varying; with last_chunk_first the later chunks
+        // (which only long sequences have, and which are full-size) dispatch first
+        c = p.last_chunk_first ? p.max_chunks - 1 - unit / p.N : unit / p.N;
+        if (c >= p.max_chunks) return;
+        if (!chunk_range(p, s, c, nc, j0, j1)) return;
+        rec0 = ((size_t)s * p.max_chunks + c) * p.Hq + hk * p.group + sub * G;
+        cstride = p.Hq;
+        ctr_idx = ((size_t)s * p.Hkv + hk) * p.nsub + sub;
+    }
     const int hq0 = hk * p.group + sub * G;
+    const int nwl = (j1 - j0 + TPW - 1) / TPW;                          // wave-loads in the chunk
+    const int kmax = wave < nwl ? (nwl - wave + WPB - 1) / WPB : 0;     // this wave's share
 
     u32x4 qv[G];
     {
@@ -214,7 +279,6 @@ __global__ __launch_bounds__(kThreads) void split_kernel(DecodeParams p) {
 #pragma unroll
         for (int g = 0; g < G; ++g) qv[g] = *reinterpret_cast<const u32x4*>(qb + (size_t)g * D);
     }
-
     float m[G], l[G], acc[G][EPL];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
@@ -224,100 +288,120 @@ __global__ __launch_bounds__(kThreads) void split_kernel(DecodeParams p) {
         for (int e = 0; e < EPL; ++e) acc[g][e] = 0.f;
     }
 
-    const T* kb = static_cast<const T*>(p.k);
-    const T* vb = static_cast<const T*>(p.v);
-    const int lane_off = tslot * D + dl * EPL;
-    size_t cbase = 0;
-    const int* table = nullptr;
+    const char* kb = static_cast<const char*>(p.k);
+    const char* vb = static_cast<const char*>(p.v);
+    size_t cbase = 0;         // contiguous: byte offset of (s, hk, token 0)
+    int tbl = 0;              // uniform paged: block ids of the chunk, one per lane
+    const int b0 = j0 / p.block;
     if constexpr (MODE == kContiguous) {
-        cbase = (size_t)s * p.seq_stride + (size_t)hk * p.head_stride;
+        cbase = ((size_t)s * p.seq_stride + (size_t)hk * p.head_stride) * sizeof(T);
     } else {
-        table = p.table_all + (p.tab_off ? p.tab_off[s] : 0);
+        // blocks the chunk touches (0 for an empty chunk); the planner keeps this
+        // within kMaxChunkBlocks, the min() only guards the LDS staging
+        const int nblk = min(j1 > j0 ? (j1 - 1) / p.block - b0 + 1 : 0, kMaxChunkBlocks);
+        // The block ids are read through a descriptor: on the planned path the
+        // descriptor spans table_all (table_len ints), so any plan reads inside it;
+        // otherwise it spans this chunk's nblk entries.
+        const int first = p.work ? tab_start : (p.tab_off ? p.tab_off[s] : 0) + b0;
+        const __amdgpu_buffer_rsrc_t trs =
+            p.work ? tile_rsrc(p.table_all, p.table_len * 4) : tile_rsrc(p.table_all + first, nblk * 4);
+        const int tb = p.work ? first * 4 : 0;  // byte offset of the chunk's first entry
+        if constexpr (MODE == kPagedUniform) {
+            // unconditional: lanes past the chunk's blocks read a neighbour's id or 0 and
+            // are never selected by the readlane below
+            tbl = (int)__builtin_amdgcn_raw_buffer_load_b32(trs, tb + lane * 4, 0, 0);
+        } else {
+            for (int b = threadIdx.x; b < nblk; b += WPB * kWave)
+                s_tab[b] = (int)__builtin_amdgcn_raw_buffer_load_b32(trs, tb + b * 4, 0, 0);
+            __syncthreads();
+        }
     }
 
-    // kPagedUniform: block-table window of 64 entries held one per lane.
-    int win = 0, tbl = 0, cur_b = 0, cur_in = 0, nblk = 0;
-    if constexpr (MODE == kPagedUniform) {
-        cur_b = j0 / p.block;
-        cur_in = j0 - cur_b * p.block;
-        nblk = (j1 + p.block - 1) / p.block;
-        win = cur_b;
-        if (win + lane < nblk) tbl = table[win + lane];
-    }
-
-    for (int base = j0; base < j1; base += U * TPW) {
-        u32x4 kr[U], vr[U];
-        bool valid[U];
+    auto issue = [&](int k0, Batch<U>& b) {
+        b.k0 = k0;
 #pragma unroll
-        for (int i = 0; i < U; ++i) {
-            const int t0 = base + i * TPW;
-            const int tt = t0 + tslot;
-            valid[i] = tt < j1;
-            size_t off = 0;
-            if constexpr (MODE == kContiguous) {
-                off = cbase + (size_t)t0 * D + lane_off;
-            } else if constexpr (MODE == kPagedUniform) {
-                int phys = 0;
-                if (t0 < j1) {
-                    if (cur_b - win >= kWave) {
-                        win += kWave;
-                        tbl = (win + lane < nblk) ? table[win + lane] : 0;
-                    }
-                    phys = __builtin_amdgcn_readlane(tbl, cur_b - win);
-                }
-                off = ((size_t)(phys * p.Hkv + hk) * p.block + cur_in) * D + lane_off;
-                cur_in += TPW;
-                if (cur_in >= p.block) { cur_in -= p.block; ++cur_b; }
+        for (int u = 0; u < U; ++u) {
+            const int i = wave + WPB * (k0 + u);   // wave-load index within the chunk
+            const int t0 = j0 + i * TPW;
+            if constexpr (MODE == kPagedPerLane) {
+                int tt = t0 + tslot;
+                const bool ok = tt < j1;
+                tt = ok ? tt : j0;                     // a valid row; the value is discarded below
+                const int bb = tt / p.block;
+                const int phys = s_tab[bb - b0];
+                const size_t off = ((size_t)(phys * p.Hkv + hk) * p.block + (tt - bb * p.block)) * ROW + dl * 16;
+                const u32x4 kk = *reinterpret_cast<const u32x4*>(kb + off);
+                const u32x4 vv = *reinterpret_cast<const u32x4*>(vb + off);
+                b.k[u] = kk;
+                b.v[u] = ok ? vv : u32x4{0, 0, 0, 0};
             } else {
-                int phys = 0, in = 0;
-                if (valid[i]) {
-                    const int b = tt / p.block;
-                    in = tt - b * p.block;
-                    phys = table[b];
+                // valid rows of this wave-load (kept scalar: the descriptor must live in SGPRs)
+                const int rows = uniform(min(max(j1 - t0, 0), TPW));
+                size_t tile;
+                if constexpr (MODE == kContiguous) {
+                    tile = cbase + (size_t)max(t0, 0) * ROW;
+                } else {
+                    const int rel = i >> p.lpb_shift;           // block of the chunk
+                    const int phys = __builtin_amdgcn_readlane(tbl, min(rel, kWave - 1));
+                    const int in = (i & ((1 << p.lpb_shift) - 1)) * TPW;
+                    tile = ((size_t)(phys * p.Hkv + hk) * p.block + in) * ROW;
                 }
-                off = ((size_t)(phys * p.Hkv + hk) * p.block + in) * D + dl * EPL;
-            }
-            kr[i] = u32x4{0, 0, 0, 0};
-            vr[i] = u32x4{0, 0, 0, 0};
-            if (valid[i]) {
-                kr[i] = *reinterpret_cast<const u32x4*>(kb + off);
-                vr[i] = *reinterpret_cast<const u32x4*>(vb + off);
+                b.k[u] = buffer_load16(tile_rsrc(kb + tile, rows * ROW), lane * 16);
+                b.v[u] = buffer_load16(tile_rsrc(vb + tile, rows * ROW), lane * 16);
             }
         }
+    };
 
+    auto consume = [&](const Batch<U>& b) {
+        bool valid[U];
         float vf[U][EPL];
 #pragma unroll
-        for (int i = 0; i < U; ++i) Tr::to_float(vr[i], vf[i]);
-
+        for (int u = 0; u < U; ++u) {
+            valid[u] = j0 + (wave + WPB * (b.k0 + u)) * TPW + tslot < j1;
+            Tr::to_float(b.v[u], vf[u]);
+        }
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             float sc[U];
             float mx = m[g];
 #pragma unroll
-            for (int i = 0; i < U; ++i) {
-                sc[i] = group_sum<LPT>(Tr::dot(qv[g], kr[i])) * p.scale_log2;
-                mx = valid[i] ? fmaxf(mx, sc[i]) : mx;
+            for (int u = 0; u < U; ++u) {
+                sc[u] = group_sum<LPT>(Tr::dot(qv[g], b.k[u])) * p.scale_log2;
+                mx = valid[u] ? fmaxf(mx, sc[u]) : mx;
             }
             const float corr = fast_exp2(m[g] - mx);
-            float pi[U], ps = 0.f;
+            float pu[U], ps = 0.f;
 #pragma unroll
-            for (int i = 0; i < U; ++i) {
-                pi[i] = valid[i] ? fast_exp2(sc[i] - mx) : 0.f;
-                ps += pi[i];
+            for (int u = 0; u < U; ++u) {
+                pu[u] = valid[u] ? fast_exp2(sc[u] - mx) : 0.f;
+                ps += pu[u];
             }
             l[g] = __builtin_fmaf(l[g], corr, ps);
 #pragma unroll
             for (int e = 0; e < EPL; ++e) {
                 float a = acc[g][e] * corr;
 #pragma unroll
-                for (int i = 0; i < U; ++i) a = __builtin_fmaf(pi[i], vf[i][e], a);
+                for (int u = 0; u < U; ++u) a = __builtin_fmaf(pu[u], vf[u][e], a);
                 acc[g][e] = a;
             }
             m[g] = mx;
         }
+    };
+
+    if (kmax > 0) {
+        Batch<U> A, B;
+        issue(0, A);
+        for (int k = 0;; k += 2 * U) {
+            issue(k + U, B);          // past the end it reads nothing (zero-size tiles)
+            consume(A);
+            if (k + U >= kmax) break;
+            issue(k + 2 * U, A);
+            consume(B);
+            if (k + 2 * U >= kmax) break;
+        }
     }
 
-    // Merge the TPW token slots (lanes that differ in bits >= log2(LPT)).
+    // Merge the TPW token slots of the wave (lanes that differ in bits >= log2(LPT)).
 #pragma unroll
     for (int msk = LPT; msk < kWave; msk <<= 1) {
 #pragma unroll
@@ -331,94 +415,205 @@ __global__ __launch_bounds__(kThreads) void split_kernel(DecodeParams p) {
             m[g] = mx;
         }
     }
-
-    if (nc == 1) {
-        if (tslot == 0) {
-            T* ob = static_cast<T*>(p.out) + ((size_t)s * p.Hq + hq0) * D + dl * EPL;
+    if (tslot == 0) {
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const float inv = l[g] > 0.f ? 1.0f / l[g] : 0.f;
-                float o[EPL];
+        for (int g = 0; g < G; ++g)
 #pragma unroll
-                for (int e = 0; e < EPL; ++e) o[e] = acc[g][e] * inv;
-                *reinterpret_cast<u32x4*>(ob + (size_t)g * D) = Tr::from_float(o);
-            }
-        }
-    } else {
-        const size_t rec0 = ((size_t)s * p.max_chunks + c) * p.Hq + hq0;
+            for (int e = 0; e < EPL; ++e) s_acc[wave][g][dl * EPL + e] = acc[g][e];
+    }
+    if (lane == 0) {
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-            if (tslot == 0) {
-                float* pa = p.part_acc + (rec0 + g) * D + dl * EPL;
+            s_m[wave][g] = m[g];
+            s_l[wave][g] = l[g];
+        }
+    }
+    __syncthreads();
+    if (wave != 0) return;
+
+    // Wave 0 merges the WPB wave partials: lane handles (g, d) = divmod(idx, D).
+    T* ob = static_cast<T*>(p.out) + ((size_t)s * p.Hq + hq0) * D;
+    for (int idx = lane; idx < G * D; idx += kWave) {
+        const int g = idx / D, d = idx % D;
+        float M = -FLT_MAX;
 #pragma unroll
-                for (int e = 0; e < EPL; e += 4)
-                    *reinterpret_cast<f32x4*>(pa + e) = f32x4{acc[g][e], acc[g][e + 1], acc[g][e + 2], acc[g][e + 3]};
+        for (int w = 0; w < WPB; ++w) M = fmaxf(M, s_m[w][g]);
+        float lt = 0.f, at = 0.f;
+#pragma unroll
+        for (int w = 0; w < WPB; ++w) {
+            const float wt = fast_exp2(s_m[w][g] - M);
+            lt = __builtin_fmaf(wt, s_l[w][g], lt);
+            at = __builtin_fmaf(wt, s_acc[w][g][d], at);
+        }
+        if (nc == 1) {
+            ob[(size_t)g * D + d] = (T)(lt > 0.f ? at * (1.0f / lt) : 0.f);
+        } else if (p.merge_mode == kMergeAtomic) {
+            __hip_atomic_store(p.part_acc + (rec0 + g) * D + d, at, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (d == 0) {
+                __hip_atomic_store(p.part_ml + (rec0 + g) * 2, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(p.part_ml + (rec0 + g) * 2 + 1, lt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
-            if (lane == 0) {
-                p.part_ml[(rec0 + g) * 2] = m[g];
-                p.part_ml[(rec0 + g) * 2 + 1] = l[g];
+        } else {
+            p.part_acc[(rec0 + g) * D + d] = at;
+            if (d == 0) {
+                p.part_ml[(rec0 + g) * 2] = M;
+                p.part_ml[(rec0 + g) * 2 + 1] = lt;
             }
         }
-        if (p.counters == nullptr) return;  // a separate merge kernel follows
-        // Fused merge: publish the partials, count arrivals; the last chunk merges.
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        unsigned long long* ctr = p.counters + ((size_t)s * p.Hkv + hk) * p.nsub + sub;
-        unsigned before = 0;
-        if (lane == 0) before = arrive(ctr, p.epoch);
-        before = (unsigned)uniform((int)before);
-        if (before != (unsigned)(nc - 1)) return;
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-        for (int g = 0; g < G; ++g) merge_head<T, D>(p, s, hq0 + g, nc, lane);
-        if (lane == 0) __hip_atomic_store(ctr, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    if (nc == 1 || p.merge_mode == kMergeKernel) return;  // single chunk, or a merge kernel follows
+    // Fused merge: publish the partials, count arrivals; the last chunk merges.
+    if (p.merge_mode == kMergeAtomic) {
+        // the partial stores were coherent; wait until this wave's stores completed
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_waitcnt(0);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    } else {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    }
+    unsigned long long* ctr = p.counters + ctr_idx;
+    unsigned before = 0;
+    if (lane == 0) before = arrive(ctr, p.epoch);
+    before = (unsigned)uniform((int)before);
+    if (before != (unsigned)(nc - 1)) return;
+    const size_t first = rec0 - (size_t)c * cstride;  // record of chunk 0, head 0
+    if (p.merge_mode == kMergeAtomic) {
+        for (int g = 0; g < G; ++g) merge_head<T, D, true>(p, first + g, cstride, nc, ob + (size_t)g * D, lane);
+    } else {
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        for (int g = 0; g < G; ++g) merge_head<T, D, false>(p, first + g, cstride, nc, ob + (size_t)g * D, lane);
+    }
+    if (lane == 0) __hip_atomic_store(ctr, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Standalone log-sum-exp merge: one 512-thread workgroup per (sequence, query
+// head).  All chunk maxima are loaded at once and reduced; then MG = 512/D chunk
+// groups x D dims accumulate 2^(m_c-M) * (acc_c, l_c) with independent loads
+// (unrolled), and the groups are summed through LDS.  Sequences with a single
+// chunk were finished by the split kernel and exit at once.
+constexpr int kMergeThreads = 512;
+
 template <typename T, int D>
-__global__ __launch_bounds__(kThreads) void merge_kernel(DecodeParams p) {
-    const int lane = threadIdx.x & (kWave - 1);
-    const int w = uniform(blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6));
-    if (w >= p.N * p.Hq) return;
-    const int s = w / p.Hq, hq = w % p.Hq;
+__global__ __launch_bounds__(kMergeThreads) void merge_kernel(DecodeParams p) {
+    constexpr int MG = kMergeThreads / D;  // chunk groups
+    __shared__ float s_red[kMergeThreads / kWave];
+    __shared__ float s_acc[MG][D];
+    __shared__ float s_l[MG];
+    const int t = threadIdx.x;
+    const int lane = t & (kWave - 1), wave = t >> 6;
+    const int s = blockIdx.x / p.Hq, hq = blockIdx.x % p.Hq;
     int nc, j0, j1;
     chunk_range(p, s, 0, nc, j0, j1);
     if (nc <= 1) return;
-    merge_head<T, D>(p, s, hq, nc, lane);
+    const size_t rec0 = (size_t)s * p.max_chunks * p.Hq + hq;
+    const size_t cstride = (size_t)p.Hq;  // records between consecutive chunks
+
+    float mx = -FLT_MAX;
+    for (int c = t; c < nc; c += kMergeThreads) mx = fmaxf(mx, p.part_ml[(rec0 + c * cstride) * 2]);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, shfl_xor(mx, o));
+    if (lane == 0) s_red[wave] = mx;
+    __syncthreads();
+    float M = s_red[0];
+#pragma unroll
+    for (int w = 1; w < kMergeThreads / kWave; ++w) M = fmaxf(M, s_red[w]);
+
+    const int cg = t / D, d = t % D;
+    float at = 0.f, lt = 0.f;
+    int c = cg;
+    for (; c + 3 * MG < nc; c += 4 * MG) {
+        float w4[4], a4[4], l4[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const size_t rec = rec0 + (size_t)(c + u * MG) * cstride;
+            w4[u] = p.part_ml[rec * 2];
+            l4[u] = p.part_ml[rec * 2 + 1];
+            a4[u] = p.part_acc[rec * D + d];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const float w = fast_exp2(w4[u] - M);
+            lt = __builtin_fmaf(w, l4[u], lt);
+            at = __builtin_fmaf(w, a4[u], at);
+        }
+    }
+    for (; c < nc; c += MG) {
+        const size_t rec = rec0 + (size_t)c * cstride;
+        const float w = fast_exp2(p.part_ml[rec * 2] - M);
+        lt = __builtin_fmaf(w, p.part_ml[rec * 2 + 1], lt);
+        at = __builtin_fmaf(w, p.part_acc[rec * D + d], at);
+    }
+    s_acc[cg][d] = at;
+    if (d == 0) s_l[cg] = lt;
+    __syncthreads();
+    if (t < D) {
+        float a = 0.f, l = 0.f;
+#pragma unroll
+        for (int g = 0; g < MG; ++g) {
+            a += s_acc[g][t];
+            l += s_l[g];
+        }
+        static_cast<T*>(p.out)[((size_t)s * p.Hq + hq) * D + t] = (T)(l > 0.f ? a * (1.0f / l) : 0.f);
+    }
 }
 
-template <typename T, int D, int G>
+template <typename T, int D, int G, int WPB, int U>
 int launch_split_mode(const DecodeLaunch& L, dim3 grid, hipStream_t st) {
+    const dim3 block(WPB * kWave);
     switch (L.mode) {
-        case kContiguous:   hipLaunchKernelGGL((split_kernel<T, D, G, kContiguous>), grid, dim3(kThreads), 0, st, L.p); break;
-        case kPagedUniform: hipLaunchKernelGGL((split_kernel<T, D, G, kPagedUniform>), grid, dim3(kThreads), 0, st, L.p); break;
-        case kPagedPerLane: hipLaunchKernelGGL((split_kernel<T, D, G, kPagedPerLane>), grid, dim3(kThreads), 0, st, L.p); break;
+        case kContiguous:   hipLaunchKernelGGL((split_kernel<T, D, G, kContiguous, WPB, U>), grid, block, 0, st, L.p); break;
+        case kPagedUniform: hipLaunchKernelGGL((split_kernel<T, D, G, kPagedUniform, WPB, U>), grid, block, 0, st, L.p); break;
+        case kPagedPerLane: hipLaunchKernelGGL((split_kernel<T, D, G, kPagedPerLane, WPB, U>), grid, block, 0, st, L.p); break;
         default: return set_error(KVC_ERR_ARG, "unknown decode mode");
     }
     return KVC_OK;
+}
+
+// Wave-loads per double-buffered batch: 4 for one or two query heads per wave
+// (2 and 8 selectable for D 64/128), 2 for larger head groups (register budget).
+template <typename T, int D, int G, int WPB>
+int launch_split_u(const DecodeLaunch& L, dim3 grid, hipStream_t st) {
+    if constexpr (G <= 2) {
+        if constexpr (D == 64 || D == 128) {
+            if (L.batch == 2) return launch_split_mode<T, D, G, WPB, 2>(L, grid, st);
+            if (L.batch == 8) return launch_split_mode<T, D, G, WPB, 8>(L, grid, st);
+        }
+        return launch_split_mode<T, D, G, WPB, 4>(L, grid, st);
+    } else {
+        return launch_split_mode<T, D, G, WPB, 2>(L, grid, st);
+    }
+}
+
+template <typename T, int D, int G>
+int launch_split_wpb(const DecodeLaunch& L, dim3 grid, hipStream_t st) {
+    if (L.wpb == 8) return launch_split_u<T, D, G, 8>(L, grid, st);
+    if (L.wpb == 4) return launch_split_u<T, D, G, 4>(L, grid, st);
+    return set_error(KVC_ERR_ARG, "waves per block must be 4 or 8");
 }
 
 template <typename T, int D>
 int launch_split_g(const DecodeLaunch& L, dim3 grid, hipStream_t st) {
     if constexpr (D == 64 || D == 128) {
         switch (L.G) {
-            case 1: return launch_split_mode<T, D, 1>(L, grid, st);
-            case 2: return launch_split_mode<T, D, 2>(L, grid, st);
-            case 4: return launch_split_mode<T, D, 4>(L, grid, st);
-            case 7: return launch_split_mode<T, D, 7>(L, grid, st);
-            case 8: return launch_split_mode<T, D, 8>(L, grid, st);
+            case 1: return launch_split_wpb<T, D, 1>(L, grid, st);
+            case 2: return launch_split_wpb<T, D, 2>(L, grid, st);
+            case 4: return launch_split_wpb<T, D, 4>(L, grid, st);
+            case 7: return launch_split_wpb<T, D, 7>(L, grid, st);
+            case 8: return launch_split_wpb<T, D, 8>(L, grid, st);
             default: break;
         }
     } else {
-        if (L.G == 1) return launch_split_mode<T, D, 1>(L, grid, st);
+        if (L.G == 1) return launch_split_wpb<T, D, 1>(L, grid, st);
     }
     return set_error(KVC_ERR_UNSUPPORTED, "query heads per unit not instantiated");
 }
 
 template <typename T>
 int launch_typed(const DecodeLaunch& L, hipStream_t st) {
-    const long long units = (long long)L.p.max_chunks * L.p.N * L.p.Hkv * L.p.nsub;
+    const long long units = L.p.work ? (long long)L.units : (long long)L.p.max_chunks * L.p.N * L.p.Hkv * L.p.nsub;
     if (units <= 0) return KVC_OK;
-    if (units > (long long)INT_MAX - kWavesPerBlock) return set_error(KVC_ERR_ARG, "decode grid too large");
-    const dim3 grid((unsigned)((units + kWavesPerBlock - 1) / kWavesPerBlock));
+    if (units > (long long)INT_MAX) return set_error(KVC_ERR_ARG, "decode grid too large");
+    const dim3 grid((unsigned)units);
     int rc;
     switch (L.D) {
         case 32:  rc = launch_split_g<T, 32>(L, grid, st); break;
@@ -429,14 +624,14 @@ int launch_typed(const DecodeLaunch& L, hipStream_t st) {
     }
     if (rc != KVC_OK) return rc;
     rc = hip_check(hipGetLastError(), "decode split launch");
-    if (rc != KVC_OK || !L.need_merge || L.p.counters != nullptr) return rc;
-    const long long waves = (long long)L.p.N * L.p.Hq;
-    const dim3 mgrid((unsigned)((waves + kWavesPerBlock - 1) / kWavesPerBlock));
+    if (rc != KVC_OK || !L.need_merge || L.p.merge_mode != kMergeKernel) return rc;
+    const dim3 mgrid((unsigned)((long long)L.p.N * L.p.Hq));
+    const dim3 mblock(kMergeThreads);
     switch (L.D) {
-        case 32:  hipLaunchKernelGGL((merge_kernel<T, 32>), mgrid, dim3(kThreads), 0, st, L.p); break;
-        case 64:  hipLaunchKernelGGL((merge_kernel<T, 64>), mgrid, dim3(kThreads), 0, st, L.p); break;
-        case 128: hipLaunchKernelGGL((merge_kernel<T, 128>), mgrid, dim3(kThreads), 0, st, L.p); break;
-        case 256: hipLaunchKernelGGL((merge_kernel<T, 256>), mgrid, dim3(kThreads), 0, st, L.p); break;
+        case 32:  hipLaunchKernelGGL((merge_kernel<T, 32>), mgrid, mblock, 0, st, L.p); break;
+        case 64:  hipLaunchKernelGGL((merge_kernel<T, 64>), mgrid, mblock, 0, st, L.p); break;
+        case 128: hipLaunchKernelGGL((merge_kernel<T, 128>), mgrid, mblock, 0, st, L.p); break;
+        case 256: hipLaunchKernelGGL((merge_kernel<T, 256>), mgrid, mblock, 0, st, L.p); break;
     }
     return hip_check(hipGetLastError(), "decode merge launch");
 }

@@ -15,7 +15,7 @@ int hip_check(hipError_t e, const char* what);
 
 // ---------------------------------------------------------------------------
 // Decode launch description (host side).  One "unit" = (sequence s, KV head hk,
-// query-head subgroup sub, chunk c); each unit is one wave64.
+// query-head subgroup sub, chunk c); each unit is one workgroup of `wpb` waves.
 // ---------------------------------------------------------------------------
 enum DecodeMode { kContiguous = 0, kPagedUniform = 1, kPagedPerLane = 2 };
 
@@ -39,8 +39,22 @@ struct DecodeParams {
     int num_splits;           // >0: chunk = ceil(L / num_splits) per sequence
     int max_chunks;           // chunks per sequence covered by the grid
     int fixed_len;            // length used when cur_len == nullptr
+    int cap;                  // lengths are clamped to cap (the caller's stated maximum)
+    int lpb_shift;            // kPagedUniform: log2(wave-loads per block)
     float scale_log2;         // softmax scale * log2(e)
     unsigned epoch;           // per-call tag of the arrival counters
+    int merge_mode;           // MergeMode
+    int last_chunk_first;     // 1: dispatch the highest chunk index first
+    const int* work;          // planned units (8 ints each, see kvc_decode_plan), or nullptr
+    int table_len;            // planned: ints in table_all (bounds every block-id read)
+};
+
+// How the chunk partials of a split sequence are combined.
+enum MergeMode {
+    kMergeKernel = 0,   // separate merge kernel after the split kernel
+    kMergeFence = 1,    // last-arriving chunk merges; agent-scope release/acquire fences
+    kMergeAtomic = 2    // last-arriving chunk merges; partials written and read with
+                        // coherent (agent-scope atomic) accesses, ordered by a wave-local wait
 };
 
 struct DecodeLaunch {
@@ -49,6 +63,9 @@ struct DecodeLaunch {
     int D;
     int G;       // query heads per unit
     int mode;    // DecodeMode
+    int wpb;     // waves per workgroup (4 or 8); one workgroup per unit
+    int batch;   // wave-loads per double-buffered batch (2, 4 or 8; used for G <= 2)
+    int units;   // planned launches: number of work-list units (the grid); else 0
     bool need_merge;
 };
 
@@ -57,9 +74,13 @@ int launch_decode(const DecodeLaunch& L, hipStream_t stream);
 
 // Tuning knobs (kvc_set_tuning).
 struct Tuning {
-    int fused_merge = 1;        // last-arriving chunk merges (single kernel) instead of a merge kernel
-    int target_units = 4096;    // automatic split: waves to aim for
-    int min_chunk_bytes = 32768;// automatic split: least K+V bytes per wave
+    int fused_merge = -1;       // MergeMode, or -1: automatic (kMergeAtomic when a sequence
+                                // has at most 8 chunks, else kMergeKernel)
+    int target_units = 2048;    // automatic split: workgroups to aim for
+    int min_chunk_bytes = 32768;// automatic split: least K+V bytes per workgroup
+    int waves_per_block = 0;    // 0: automatic (8 for small grids, else 4)
+    int batch = 4;              // wave-loads per batch for <= 2 query heads per wave
+    int last_chunk_first = 1;   // dispatch order of chunks
 };
 Tuning& tuning();
 

@@ -17,6 +17,7 @@ __all__ = [
     "launch_append", "launch_decode", "launch_paged", "launch_batched_decode", "launch_batched_paged",
     "launch_batched_paged_flash", "launch_flash_decode", "qk_write_kv", "qk_batched_write_kv",
     "qk_batched_paged_decode_attn", "write_kv_slots", "decode_workspace_size", "decode_auto_split",
+    "decode_plan", "planned_workspace_size", "launch_batched_paged_planned",
     "flash_decode_workspace_size", "KVC_F16", "KVC_F32",
 ]
 
@@ -94,6 +95,37 @@ def qk_batched_paged_decode_attn(q, out, k_pool, v_pool, table_all, tab_off, cur
     check(lib().kvc_batched_paged_decode_split(_p(q), _p(k_pool), _p(v_pool), _p(table_all), _p(tab_off),
                                                _p(cur_len), _p(out), N, Hq, Hkv, D, BLOCK, cap, scale, dtype, split,
                                                ws, wsb, stream))
+
+
+def decode_plan(lens, Hq, Hkv, D, BLOCK, *, tab_off=None, dtype=KVC_F16, target_tokens=0):
+    """Host-side plan of a batched paged decode (kvc_decode_plan): returns
+    (work [units, 8] int32, n_units, n_records)."""
+    import ctypes as C
+
+    import numpy as np
+    lens = np.ascontiguousarray(np.asarray(lens, dtype=np.int32))
+    toff = None if tab_off is None else np.ascontiguousarray(np.asarray(tab_off, dtype=np.int32))
+    tp = None if toff is None else toff.ctypes.data
+    nu, nr = C.c_int(0), C.c_int(0)
+    L = lib()
+    check(L.kvc_decode_plan(lens.ctypes.data, tp, len(lens), Hq, Hkv, D, BLOCK, dtype, target_tokens, None, 0,
+                            C.byref(nu), C.byref(nr)))
+    work = np.zeros((max(nu.value, 1), 8), dtype=np.int32)
+    check(L.kvc_decode_plan(lens.ctypes.data, tp, len(lens), Hq, Hkv, D, BLOCK, dtype, target_tokens,
+                            work.ctypes.data, nu.value, C.byref(nu), C.byref(nr)))
+    return work[: nu.value], nu.value, nr.value
+
+
+def planned_workspace_size(Hq, Hkv, D, n_records) -> int:
+    return int(lib().kvc_decode_planned_workspace_size(Hq, Hkv, D, n_records))
+
+
+def launch_batched_paged_planned(q, k_pool, v_pool, table_all, table_len, out, N, Hq, Hkv, D, BLOCK, scale,
+                                 work_dev, n_units, n_records, *, dtype=KVC_F16, workspace=None, stream=None):
+    ws, wsb = _ws(workspace)
+    check(lib().kvc_batched_paged_decode_planned(_p(q), _p(k_pool), _p(v_pool), _p(table_all), int(table_len),
+                                                 _p(out), N, Hq, Hkv, D, BLOCK, scale, dtype, _p(work_dev), n_units,
+                                                 n_records, ws, wsb, stream))
 
 
 def write_kv_slots(k, v, k_pool, v_pool, slot_map, rows, Hkv, D, BLOCK, *, dtype=KVC_F16, stream=None):

@@ -38,7 +38,7 @@ def paged_layout(K, V, lens, block, perm=None):
     total = int(sum(nb))
     tab_off = np.concatenate([[0], np.cumsum(nb)]).astype(np.int32)
     table = np.arange(total, dtype=np.int32) if perm is None else np.asarray(perm, np.int32)[:total]
-    NB = max(total, 1)
+    NB = max(total, int(table.max()) + 1 if total else 1)  # a permutation may point past `total`
     kp = np.zeros((NB, Hkv, block, D), K.dtype)
     vp = np.zeros_like(kp)
     for s in range(N):

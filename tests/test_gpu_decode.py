@@ -126,21 +126,24 @@ def test_c2_ragged_batch(orc, lengths):
     assert err <= 2e-3, err
 
 
-def test_fused_and_separate_merge_agree(orc):
-    say("fused vs separate merge")
+def test_merge_modes_agree(orc):
+    say("merge modes 0/1/2")
     lens = np.array([1, 300, 2000, 777, 16, 5000], np.int32)
     N, Hq, Hkv, D, B = len(lens), 8, 2, 64, 16
     S = int(lens.max())
     q, K, V = normal((N, Hq, D), 30, np.float16), normal((N, Hkv, S, D), 31, np.float16), normal((N, Hkv, S, D), 32, np.float16)
     L = lib()
-    a = run_batched(q, K, V, lens, Hkv, B, KVC_F16, split=256)
-    check(L.kvc_set_tuning(b"fused_merge", 0))
+    outs = {}
     try:
-        b = run_batched(q, K, V, lens, Hkv, B, KVC_F16, split=256)
+        for mode in (0, 1, 2):   # merge kernel, fused behind fences, fused with coherent partials
+            check(L.kvc_set_tuning(b"fused_merge", mode))
+            outs[mode] = [run_batched(q, K, V, lens, Hkv, B, KVC_F16, split=sp) for sp in (256, 1024)]
     finally:
-        check(L.kvc_set_tuning(b"fused_merge", 1))
-    np.testing.assert_array_equal(a, b)
-    assert np.abs(a - oracle_out(orc, q, K, V, lens)).max() <= 2e-3
+        check(L.kvc_set_tuning(b"fused_merge", -1))
+    for mode in (1, 2):
+        for a, b in zip(outs[0], outs[mode]):
+            np.testing.assert_array_equal(a, b)
+    assert np.abs(outs[0][0] - oracle_out(orc, q, K, V, lens)).max() <= 2e-3
 
 
 # ---- GQA, split sizes, block sizes, head dims ----------------------------------------
@@ -247,3 +250,62 @@ def test_c3_long_context_split_k(orc):
     assert np.abs(split - ref).max() <= 2e-3
     assert np.abs(unsplit - ref).max() <= 2e-3
     assert np.abs(split - unsplit).max() <= 2e-3
+
+
+# ---- planned path (host-known lengths; the serving scheduler's path) ----------------
+def run_planned(q, K, V, lens, Hkv, block, dtype, perm=None, target=0, workspace=None):
+    N, Hq, D = q.shape
+    kp, vp, table, tab_off = paged_layout(K, V, lens, block, perm)
+    work, nu, nr = ops.decode_plan(lens, Hq, Hkv, D, block, tab_off=tab_off, dtype=dtype, target_tokens=target)
+    out = DeviceBuffer(q.nbytes)
+    ops.launch_batched_paged_planned(dev(q), dev(kp), dev(vp), dev(table), len(table), out, N, Hq, Hkv, D, block,
+                                     float(1.0 / np.sqrt(D)), dev(work), nu, nr, dtype=dtype, workspace=workspace)
+    return host(out, q.dtype, q.shape).astype(np.float64)
+
+
+@pytest.mark.parametrize("lengths", ["reference", "loguniform"])
+def test_planned_c2_ragged(orc, lengths):
+    lens = W.ref_lengths() if lengths == "reference" else W.loguniform_lengths(128, 16, 2048, 7)
+    say(f"planned c2 lengths={lengths}")
+    N, H, D, B = 128, 8, 64, 16
+    S = int(lens.max())
+    q, K, V = normal((N, H, D), 120, np.float16), normal((N, H, S, D), 121, np.float16), normal((N, H, S, D), 122, np.float16)
+    nb = sum((int(x) + B - 1) // B for x in lens)
+    got = run_planned(q, K, V, lens, H, B, KVC_F16, perm=np.random.default_rng(5).permutation(nb))
+    assert np.abs(got - oracle_out(orc, q, K, V, lens)).max() <= 2e-3
+
+
+@pytest.mark.parametrize("dtype", [KVC_F32, KVC_F16])
+@pytest.mark.parametrize("target", [0, 64, 256, 4096])
+def test_planned_gqa_targets(orc, dtype, target):
+    say(f"planned gqa target={target} dtype={dtype}")
+    lens = np.array([0, 1, 15, 16, 17, 100, 1000, 3000, 2048], np.int32)
+    N, Hq, Hkv, D, B = len(lens), 14, 2, 64, 16
+    nt = as_np(dtype)
+    S = int(lens.max())
+    q, K, V = normal((N, Hq, D), 130, nt), normal((N, Hkv, S, D), 131, nt), normal((N, Hkv, S, D), 132, nt)
+    ws = DeviceBuffer(1 << 22)
+    ws.upload(np.random.default_rng(4).integers(0, 256, 1 << 22, dtype=np.uint8))  # never cleared
+    got = run_planned(q, K, V, lens, Hkv, B, dtype, perm=np.random.default_rng(3).permutation(500), target=target,
+                      workspace=ws)
+    assert np.all(got[0] == 0)
+    assert np.abs(got - oracle_out(orc, q, K, V, lens)).max() <= tol(dtype)
+
+
+@pytest.mark.parametrize("D", [32, 128])
+def test_planned_small_blocks_and_head_dims(orc, D):
+    say(f"planned block 4 D={D}")
+    lens = np.array([5, 8, 13, 700], np.int32)
+    q, K, V = normal((4, 8, D), 140, np.float16), normal((4, 4, 700, D), 141, np.float16), normal((4, 4, 700, D), 142, np.float16)
+    got = run_planned(q, K, V, lens, 4, 4, KVC_F16, perm=np.random.default_rng(6).permutation(300), target=128)
+    assert np.abs(got - oracle_out(orc, q, K, V, lens)).max() <= 2e-3
+
+
+def test_planned_c3_long_context(orc):
+    lens = np.array([8192, 16384, 32768, 32768], np.int32)
+    say("planned c3")
+    N, Hq, Hkv, D, B = 4, 14, 2, 64, 16
+    q = normal((N, Hq, D), 150, np.float16)
+    K, V = normal((N, Hkv, 32768, D), 151, np.float16), normal((N, Hkv, 32768, D), 152, np.float16)
+    got = run_planned(q, K, V, lens, Hkv, B, KVC_F16, target=512)
+    assert np.abs(got - oracle_out(orc, q, K, V, lens)).max() <= 2e-3

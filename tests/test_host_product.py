@@ -174,3 +174,50 @@ def test_gqa_layers_config_is_accepted_host_only(dtype):
     p, g, a = W.ref_trace(nreq=64)
     st = run_continuous(p, g, a, eng)
     assert st.tokens == g.sum()
+
+
+# ---- decode planner (host logic of the planned path) ---------------------------------
+@pytest.mark.parametrize("case", ["ref", "loguniform", "uniform", "tiny", "gqa", "small_block"])
+def test_decode_plan_covers_every_token_once(case):
+    from kvcache_amd import ops
+    Hq, Hkv, D, B = 8, 8, 64, 16
+    if case == "ref":
+        lens = W.ref_lengths()
+    elif case == "loguniform":
+        lens = W.loguniform_lengths(128, 16, 2048, 7)
+    elif case == "uniform":
+        lens = np.full(64, 650, np.int32)
+    elif case == "tiny":
+        lens = np.array([0, 1, 2, 15, 16, 17], np.int32)
+    elif case == "gqa":
+        lens, Hq, Hkv = np.array([8192, 16384, 32768, 32768], np.int32), 14, 2
+    else:
+        lens, B = np.array([5, 8, 13, 3000], np.int32), 4
+    work, nu, nr = ops.decode_plan(lens, Hq, Hkv, D, B)
+    assert nu == len(work) > 0
+    sizes = work[:, 3] - work[:, 2]
+    assert np.all(np.diff(sizes) <= 0), "units are sorted longest first"
+    nsub = Hq // Hkv // (7 if Hq // Hkv == 7 else Hq // Hkv)
+    hks = Hkv * nsub
+    cover = {}
+    groups = {}
+    tab_off = np.concatenate([[0], np.cumsum([(int(x) + B - 1) // B for x in lens])])
+    for s, hc, j0, j1, nc, rec, ctr, tab in work.tolist():
+        h, c = hc & 0xFFFF, hc >> 16
+        assert 0 <= s < len(lens) and 0 <= h < hks and 0 <= j0 <= j1 <= lens[s] and 0 <= c < nc
+        assert tab == tab_off[s] + j0 // B
+        cover.setdefault((s, h), []).append((j0, j1, c, nc))
+        if nc > 1:
+            assert j0 % B == 0 and rec >= 0 and ctr >= 0
+            assert groups.setdefault((s, h), (rec, ctr, nc)) == (rec, ctr, nc)
+        else:
+            assert rec == -1 and ctr == -1
+    for s in range(len(lens)):
+        for h in range(hks):
+            parts = sorted(cover[(s, h)])
+            assert [c for _, _, c, _ in sorted(parts, key=lambda x: x[2])] == list(range(parts[0][3]))
+            assert parts[0][0] == 0 and parts[-1][1] == lens[s]
+            assert all(a[1] == b[0] for a, b in zip(parts, parts[1:])), "chunks tile [0, L) exactly"
+    recs = sorted(v[0] + k for v in groups.values() for k in range(v[2]))
+    assert recs == list(range(nr)), "record ids are dense and disjoint"
+    assert sorted(v[1] for v in groups.values()) == list(range(len(groups)))
