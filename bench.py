@@ -35,6 +35,22 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 METRIC = "paged decode KV GB/s (% of HBM peak) @N=128 ragged; continuous tokens/s"
+# Measured HBM traffic of the headline kernel: a rocprofv3 --pmc summary (FETCH_SIZE and
+# WRITE_SIZE per dispatch, scaled by the same counters read for a plain copy of known size).
+TRAFFIC_SUMMARY = ROOT / "profiles" / "split_kernel_planned_c2_traffic.txt"
+
+
+def measured_traffic():
+    """(bytes per launch, kernel symbol) from the committed --pmc summary, or (None, None)."""
+    try:
+        text = TRAFFIC_SUMMARY.read_text()
+    except OSError:
+        return None, None
+    vals = dict(line.split(":", 1) for line in text.splitlines() if ":" in line and not line.startswith(" "))
+    try:
+        return int(vals["traffic_bytes_per_launch"].split()[0]), vals.get("kernel", "").strip()
+    except (KeyError, ValueError):
+        return None, None
 
 
 def log(msg: str) -> None:
@@ -294,12 +310,15 @@ def main() -> int:
     ap.add_argument("--plan-sweep", type=str, default="", help="comma list of planned targets to time")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="only run 10 device-to-device copies of MIB MiB (HBM counter calibration) and exit")
+    ap.add_argument("--warm", action="store_true",
+                    help="also time the planned path on one pool copy (Infinity-Cache resident)")
     ap.add_argument("--fused", type=int, default=-1,
                     help="merge mode: -1 automatic, 0 merge kernel, 1 fused with fences, 2 fused coherent")
     a = ap.parse_args()
     if a.gpus != 1:
-        print(f"bench.py: this build targets one GPU; --gpus {a.gpus} is not supported (collectives and sharding "
-              "are out of scope -- see DESIGN.md for how the path would shard)", file=sys.stderr)
+        print(f"bench.py: this build runs on one GPU; --gpus {a.gpus} is not supported (the path shards by "
+              "sequence with no exchange, so a single GPU's share at its real shape is what is measured)",
+              file=sys.stderr)
         return 2
 
     from kvcache_amd import ops
@@ -360,11 +379,16 @@ def main() -> int:
         print(json.dumps({"metric": METRIC, "error": f"planned parity failure: max abs err {err_planned}"}))
         return 1
     ms_per_step = t_launch
+    traffic, sym = measured_traffic()
+    traffic_src = (f"rocprofv3 --pmc FETCH_SIZE x2.0 + WRITE_SIZE x1.0 per dispatch of {sym} "
+                   f"({TRAFFIC_SUMMARY.relative_to(ROOT)})") if traffic else None
     achieved = total / (t_launch * 1e-3) / 1e9
     log(f"C2 cold, planned path ({n_units} units): {t_launch * 1e3:.2f} us/launch, {achieved:.1f} GB/s")
-    t_warm, _, _, _ = time_planned(W, lens, Hq, Hkv, D, B, a.steps, a.warmup, target=a.plan_target, rotate=1)
-    warm = total / (t_warm * 1e-3) / 1e9
-    log(f"C2 warm (one pool, Infinity-Cache resident): {t_warm * 1e3:.2f} us, {warm:.1f} GB/s")
+    warm = None
+    if a.warm:
+        t_warm, _, _, _ = time_planned(W, lens, Hq, Hkv, D, B, a.steps, a.warmup, target=a.plan_target, rotate=1)
+        warm = round(total / (t_warm * 1e-3) / 1e9, 1)
+        log(f"C2 warm (one pool, Infinity-Cache resident): {t_warm * 1e3:.2f} us, {warm} GB/s")
 
     extras = {}
     if not a.no_extras:
@@ -382,7 +406,7 @@ def main() -> int:
 
     cpu = None
     if not a.no_cpu_baseline:
-        cpu = cpu_baseline(host_data, W, lens, Hkv, B, D, a.cpu_seconds, kv)
+        cpu = cpu_baseline(host_data, W, lens, Hkv, B, D, a.cpu_seconds, total)
         log(f"CPU baseline: {cpu}")
 
     line = {
@@ -396,11 +420,13 @@ def main() -> int:
         "device_lengths_path": {"split_tokens": split, "us_per_step": round(t_raw * 1e3, 3), "GBps": round(raw, 1)},
         "pct_hbm_peak": round(100 * achieved / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "split_kernel<_Float16,64,1,kPagedUniform,4,4> (planned paged decode, fused LSE merge)",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_source": traffic_src,
+                     "kernel": "split_kernel<_Float16, D=64, G=1, kPlannedUniform, ...> (planned paged decode, "
+                               "fused LSE merge)",
                      "algorithmic_bytes_per_launch": total, "kv_bytes_per_launch": kv,
                      "mean_launch_us": round(t_launch * 1e3, 3)},
-        "warm_GBps": round(warm, 1),
+        "warm_GBps": warm,
         "parity_max_abs_err": err,
         "cpu_baseline": cpu,
         "extras": extras,

@@ -40,6 +40,7 @@ struct EngineConfig {
     double c0 = 0, c1 = 0, c2 = 0;
     bool device = true;
     int split_tokens = 0;
+    int decode_path = KVC_DECODE_PLANNED;
     uint64_t seed = 0x6b76636163686531ull;
 };
 
@@ -84,6 +85,7 @@ inline RunnerOptions runner_options(const EngineConfig& c) {
     o.c0 = c.c0; o.c1 = c.c1; o.c2 = c.c2;
     o.device = c.device;
     o.split_tokens = c.split_tokens;
+    o.decode_path = c.decode_path;
     o.seed = c.seed;
     return o;
 }

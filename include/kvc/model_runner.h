@@ -16,7 +16,11 @@
 //   * every packed step is folded into an FNV-1a digest so the schedule can be
 //     compared bit for bit with an independent restatement;
 //   * the clock is either measured (events around the step's kernels, as the
-//     reference) or a deterministic cost model c0 + c1*N + c2*sum(len).
+//     reference) or a deterministic cost model c0 + c1*N + c2*sum(len);
+//   * decode is host-planned by default: the lengths are known here, so the step
+//     cuts every sequence into near-equal chunks (kvc_decode_plan), appends the
+//     work list to the same upload and launches the planned kernel, which needs
+//     no per-sequence device lookups and balances ragged batches.
 // Query/key/value inputs are synthetic N(0,1) buffers filled once on the device.
 #pragma once
 #include <algorithm>
@@ -36,7 +40,9 @@ struct RunnerOptions {
     int clock_mode = 0;      // 0 measured, 1 virtual
     double c0 = 0, c1 = 0, c2 = 0;
     bool device = true;
-    int split_tokens = 0;    // 0: automatic
+    int split_tokens = 0;    // device-lengths path: 0 automatic
+    int decode_path = KVC_DECODE_PLANNED;  // or KVC_DECODE_DEVICE_LENGTHS
+    int plan_target = 0;     // planned path: tokens per unit (0 automatic)
     uint64_t seed = 0x6b76636163686531ull;
 };
 
@@ -58,7 +64,8 @@ struct ModelRunner {
     void* ws = nullptr;
     size_t ws_bytes = 0;
 
-    std::vector<int> h_tab, h_off, h_len, h_wpos, h_slot;
+    size_t meta_cap = 0;     // ints in d_meta and in each pinned ring buffer
+    std::vector<int> h_tab, h_off, h_len, h_wpos, h_slot, h_work;
     uint64_t digest = 1469598103934665603ull;
     long long last_sum_len = 0;
     int last_cap = 0;
@@ -84,11 +91,9 @@ struct ModelRunner {
         kvc::check(kvc_malloc(&dk, nkv * es), "ModelRunner k");
         kvc::check(kvc_malloc(&dv, nkv * es), "ModelRunner v");
         kvc::check(kvc_malloc(&dout, (size_t)max_batch * n_heads * head_dim * es), "ModelRunner out");
-        kvc::check(kvc_malloc((void**)&d_meta, meta_ints() * sizeof(int)), "ModelRunner meta");
-        for (int i = 0; i < kRing; ++i) {
-            kvc::check(kvc_host_alloc((void**)&h_meta[i], meta_ints() * sizeof(int)), "ModelRunner pinned meta");
-            kvc::check(kvc_event_create(&h_ev[i]), "ModelRunner event");
-        }
+        for (int i = 0; i < kRing; ++i) kvc::check(kvc_event_create(&h_ev[i]), "ModelRunner event");
+        // metadata plus a work list of ~4 units per (sequence, KV head); grown on demand
+        ensure_meta(meta_ints() + (size_t)8 * 4 * max_batch * n_kv_heads * (n_heads / n_kv_heads));
         kvc::check(kvc_event_create(&ev0), "ModelRunner event");
         kvc::check(kvc_event_create(&ev1), "ModelRunner event");
         kvc::check(kvc_fill_normal(dq, nq, opt.dtype, opt.seed, 1.0f, stream), "ModelRunner fill q");
@@ -107,6 +112,34 @@ struct ModelRunner {
     ModelRunner& operator=(const ModelRunner&) = delete;
 
     size_t meta_ints() const { return 1 + (size_t)(max_batch + 1) + 3 * (size_t)max_batch + max_pool_blocks; }
+    // (Re)allocates d_meta and the pinned ring for at least `ints` ints.
+    void ensure_meta(size_t ints) {
+        if (ints <= meta_cap) return;
+        const size_t cap = std::max(ints, meta_cap * 2);
+        if (stream) kvc::check(kvc_stream_synchronize(stream), "meta growth");
+        kvc_free(d_meta);
+        d_meta = nullptr;
+        for (int i = 0; i < kRing; ++i) {
+            kvc_host_free(h_meta[i]);
+            h_meta[i] = nullptr;
+            h_ev_used[i] = false;
+        }
+        meta_cap = 0;
+        kvc::check(kvc_malloc((void**)&d_meta, cap * sizeof(int)), "ModelRunner meta");
+        for (int i = 0; i < kRing; ++i)
+            kvc::check(kvc_host_alloc((void**)&h_meta[i], cap * sizeof(int)), "ModelRunner pinned meta");
+        meta_cap = cap;
+    }
+    void ensure_workspace(size_t need) {
+        if (need <= ws_bytes) return;
+        kvc::check(kvc_stream_synchronize(stream), "workspace growth");
+        kvc_free(ws);
+        ws = nullptr;
+        ws_bytes = 0;
+        const size_t sz = std::max(need * 2, (size_t)1 << 20);
+        kvc::check(kvc_malloc(&ws, sz), "decode workspace");
+        ws_bytes = sz;
+    }
     void reset_digest() { digest = 1469598103934665603ull; }
     void fold(int32_t x) {
         const uint32_t u = (uint32_t)x;
@@ -153,7 +186,22 @@ struct ModelRunner {
         if (!opt.device) return virt;
         if (!kvm.has_device()) throw kvc::Error(KVC_ERR_STATE, "decode_step: KV manager has no device pools");
 
-        // pack: [N | off N+1 | len N | wpos N | slot N | tab T]
+        const int T = (int)h_tab.size();
+        const bool planned = opt.decode_path == KVC_DECODE_PLANNED && T > 0;
+        int n_units = 0, n_records = 0;
+        if (planned) {
+            kvc::check(kvc_decode_plan(h_len.data(), h_off.data(), n, n_heads, n_kv_heads, head_dim, block_size,
+                                       opt.dtype, opt.plan_target, nullptr, 0, &n_units, &n_records),
+                       "decode plan");
+            h_work.resize((size_t)n_units * 8);
+            kvc::check(kvc_decode_plan(h_len.data(), h_off.data(), n, n_heads, n_kv_heads, head_dim, block_size,
+                                       opt.dtype, opt.plan_target, h_work.data(), n_units, &n_units, &n_records),
+                       "decode plan");
+        } else {
+            h_work.clear();
+        }
+        // pack: [N | off N+1 | len N | wpos N | slot N | tab T | work 8*units]
+        ensure_meta(1 + (size_t)(n + 1) + 3 * (size_t)n + T + h_work.size());
         if (h_ev_used[ring]) kvc::check(kvc_event_synchronize(h_ev[ring]), "meta ring wait");
         int* h = h_meta[ring];
         size_t o = 0;
@@ -166,6 +214,7 @@ struct ModelRunner {
         }
         o += 2 * (size_t)n;
         std::memcpy(h + o, h_tab.data(), h_tab.size() * sizeof(int)); o += h_tab.size();
+        std::memcpy(h + o, h_work.data(), h_work.size() * sizeof(int)); o += h_work.size();
         kvc::check(kvc_step_upload(d_meta, h, o * sizeof(int), stream), "step upload");
         kvc::check(kvc_event_record(h_ev[ring], stream), "meta ring record");
         h_ev_used[ring] = true;
@@ -174,28 +223,29 @@ struct ModelRunner {
         const int* d_len = d_off + n + 1;
         const int* d_slot = d_len + 2 * n;
         const int* d_tab = d_len + 3 * n;
+        const int* d_work = d_tab + T;
 
-        const size_t need = kvc_decode_workspace_size(n, n_heads, n_kv_heads, head_dim, block_size, cap,
-                                                      opt.split_tokens, opt.dtype);
-        if (need > ws_bytes) {
-            kvc::check(kvc_stream_synchronize(stream), "workspace growth");
-            kvc_free(ws);
-            ws = nullptr;
-            ws_bytes = 0;
-            const size_t sz = std::max(need * 2, (size_t)1 << 20);
-            kvc::check(kvc_malloc(&ws, sz), "decode workspace");
-            ws_bytes = sz;
-        }
+        ensure_workspace(planned ? kvc_decode_planned_workspace_size(n_heads, n_kv_heads, head_dim, n_records)
+                                 : kvc_decode_workspace_size(n, n_heads, n_kv_heads, head_dim, block_size, cap,
+                                                             opt.split_tokens, opt.dtype));
         kvc::check(kvc_event_record(ev0, stream), "event");
         for (int l = 0; l < opt.n_layers; ++l) {
             if (opt.kv_write)
                 kvc::check(kvc_write_kv_slots(k_layer(l), v_layer(l), kvm.k_layer(l), kvm.v_layer(l), d_slot, n,
                                               n_kv_heads, head_dim, block_size, opt.dtype, stream),
                            "write_kv");
-            kvc::check(kvc_batched_paged_decode_split(q_layer(l), kvm.k_layer(l), kvm.v_layer(l), d_tab, d_off, d_len,
-                                                      dout, n, n_heads, n_kv_heads, head_dim, block_size, cap, scale,
-                                                      opt.dtype, opt.split_tokens, ws, ws_bytes, stream),
-                       "paged decode");
+            if (planned)
+                kvc::check(kvc_batched_paged_decode_planned(q_layer(l), kvm.k_layer(l), kvm.v_layer(l), d_tab, T, dout,
+                                                            n, n_heads, n_kv_heads, head_dim, block_size, scale,
+                                                            opt.dtype, d_work, n_units, n_records, ws, ws_bytes,
+                                                            stream),
+                           "planned paged decode");
+            else
+                kvc::check(kvc_batched_paged_decode_split(q_layer(l), kvm.k_layer(l), kvm.v_layer(l), d_tab, d_off,
+                                                          d_len, dout, n, n_heads, n_kv_heads, head_dim, block_size,
+                                                          cap, scale, opt.dtype, opt.split_tokens, ws, ws_bytes,
+                                                          stream),
+                           "paged decode");
         }
         kvc::check(kvc_event_record(ev1, stream), "event");
         if (opt.clock_mode != 0) return virt;

@@ -42,6 +42,9 @@ enum kvc_status {
     KVC_ERR_STATE = 6        /* call not valid in the object's current state */
 };
 enum kvc_dtype { KVC_F32 = 0, KVC_F16 = 1 };
+/* How an engine step launches decode: host-planned work list (kvc_decode_plan +
+ * kvc_batched_paged_decode_planned) or device lengths (kvc_batched_paged_decode_split). */
+enum kvc_decode_path { KVC_DECODE_PLANNED = 0, KVC_DECODE_DEVICE_LENGTHS = 1 };
 
 /* ---- library ---------------------------------------------------------- */
 int         kvc_version(void);                 /* 100*major + minor */
@@ -223,7 +226,8 @@ typedef struct kvc_engine_config {
                           1: virtual clock, step cost = c0 + c1*N + c2*sum(len) us */
     double virt_c0, virt_c1, virt_c2;
     int device;        /* 1: own device pools and launch kernels; 0: scheduling only (no GPU) */
-    int split_tokens;  /* decode split size; 0 = automatic */
+    int split_tokens;  /* device-lengths decode: split size; 0 = automatic */
+    int decode_path;   /* KVC_DECODE_PLANNED (0, default) or KVC_DECODE_DEVICE_LENGTHS */
     uint64_t seed;     /* seed of the synthetic q/k/v fill */
 } kvc_engine_config;
 

@@ -20,6 +20,8 @@ KVC_ERR_WORKSPACE = 5
 KVC_ERR_STATE = 6
 KVC_F32 = 0
 KVC_F16 = 1
+KVC_DECODE_PLANNED = 0
+KVC_DECODE_DEVICE_LENGTHS = 1
 
 vp = C.c_void_p
 i32 = C.c_int
@@ -41,7 +43,7 @@ class EngineConfigC(C.Structure):
         ("n_heads", i32), ("n_kv_heads", i32), ("head_dim", i32), ("block_size", i32),
         ("num_blocks", i32), ("max_batch", i32), ("n_layers", i32), ("dtype", i32),
         ("kv_write", i32), ("clock_mode", i32), ("virt_c0", f64), ("virt_c1", f64),
-        ("virt_c2", f64), ("device", i32), ("split_tokens", i32), ("seed", u64),
+        ("virt_c2", f64), ("device", i32), ("split_tokens", i32), ("decode_path", i32), ("seed", u64),
     ]
 
 

@@ -623,7 +623,7 @@ int kvc_batched_paged_decode_planned(const void* q, const void* k_pool, const vo
         p.epoch = next_epoch();
         p.merge_mode = tuning().fused_merge == kMergeFence ? kMergeFence : kMergeAtomic;  // planned: always fused
         // the grid is the unit list; chunk_range is not used on this path
-        L.dtype = dtype; L.D = D; L.G = ps.G; L.mode = ps.uniform ? kPagedUniform : kPagedPerLane;
+        L.dtype = dtype; L.D = D; L.G = ps.G; L.mode = ps.uniform ? kPlannedUniform : kPlannedPerLane;
         L.wpb = tuning().waves_per_block ? tuning().waves_per_block : ps.wpb;
         L.batch = tuning().batch;
         L.need_merge = false;

@@ -1,641 +1,23 @@
-// decode.hip -- gfx950 decode attention: split phase + log-sum-exp merge.
-//
-// One wave64 processes one unit = (sequence s, KV head hk, query-head subgroup,
-// token chunk [j0, j1)).  Inside a unit the 64 lanes are laid out as
-// TPW token slots x LPT lanes per token: every lane owns 16 contiguous bytes of a
-// K/V row (8 fp16 or 4 fp32 elements), so one wave-wide 16-byte load reads
-// TPW = 64/LPT whole rows.  For D = 64 fp16 that is 8 tokens x 128 B = 1 KiB per
-// load instruction, fully coalesced.
-//
-//   QK^T  : each lane dots its 16-byte slice against q (v_dot2_f32_f16 for fp16,
-//           fp32 FMAs for fp32), then an LPT-lane butterfly made of DPP adds
-//           (quad_perm, row_half_mirror, row_mirror) finishes the dot product.
-//   softmax: every token slot keeps its own fp32 online (max, sum, acc) state in
-//           log2 units (exp2 via v_exp_f32); the slots are merged once at the end
-//           of the unit, so no per-token barrier or cross-slot exchange exists.
-//   GQA   : all G query heads of a KV group are processed by the same wave from
-//           the same K/V registers -- each KV byte is read from HBM once.
-//   paged : the unit's block-table slice is loaded once into one VGPR (one entry
-//           per lane) and each 16-token block's physical id is taken with
-//           v_readlane into an SGPR, so K/V addresses are scalar base + constant
-//           lane offset (mode kPagedUniform).  kPagedPerLane handles blocks that
-//           are smaller than one wave-load (per-lane table lookup).
-//
-// A unit that covers its whole sequence writes the normalised output directly;
-// otherwise it writes (acc[D], m, l) partials and merge_kernel combines them:
-//   M = max_c m_c,  out = sum_c 2^(m_c-M) acc_c / sum_c 2^(m_c-M) l_c
-// (the flash-decode merge of reference flash_decode.cu:82-101, in log2 units).
-// Contiguous and paged layouts share every arithmetic instruction, so paged and
-// contiguous results are bit-identical on the same logical data.
+// decode.hip -- decode launch dispatch over element type and head_dim.  The
+// kernels live in decode_kernels.hpp; each (type, head_dim) pair is compiled in
+// its own translation unit (decode_<type>_d<D>.hip) so the instantiations build
+// in parallel.
 #include "internal.hpp"
 #include "kvc_abi.h"
 
-#include <cfloat>
-#include <climits>
-
 namespace kvc {
+
 namespace {
-
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-
-constexpr int kWave = 64;
-
-template <int CTRL>
-__device__ __forceinline__ float dpp(float x) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, true));
-}
-__device__ __forceinline__ float shfl_xor(float x, int mask) {
-    const int lane = __lane_id();
-    return __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, __float_as_int(x)));
-}
-
-// Sum over each aligned group of LPT consecutive lanes, result in every lane.
-// quad_perm[1,0,3,2] / [2,3,0,1] give the 4-lane sum; row_half_mirror (lane i
-// reads 7-i) then adds the other quad of the 8-lane half row, row_mirror (lane i
-// reads 15-i) the other half of the 16-lane row.
-template <int LPT>
-__device__ __forceinline__ float group_sum(float x) {
-    if constexpr (LPT >= 2) x += dpp<0xB1>(x);
-    if constexpr (LPT >= 4) x += dpp<0x4E>(x);
-    if constexpr (LPT >= 8) x += dpp<0x141>(x);
-    if constexpr (LPT >= 16) x += dpp<0x140>(x);
-    if constexpr (LPT >= 32) x += shfl_xor(x, 16);
-    if constexpr (LPT >= 64) x += shfl_xor(x, 32);
-    return x;
-}
-
-__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
-template <typename T> struct Traits;
-template <> struct Traits<float> {
-    static constexpr int EPL = 4;
-    static __device__ __forceinline__ float dot(u32x4 a, u32x4 b) {
-        const f32x4 x = __builtin_bit_cast(f32x4, a), y = __builtin_bit_cast(f32x4, b);
-        float s = x[0] * y[0];
-        s = __builtin_fmaf(x[1], y[1], s);
-        s = __builtin_fmaf(x[2], y[2], s);
-        s = __builtin_fmaf(x[3], y[3], s);
-        return s;
-    }
-    static __device__ __forceinline__ void to_float(u32x4 a, float* f) {
-        const f32x4 x = __builtin_bit_cast(f32x4, a);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) f[e] = x[e];
-    }
-    static __device__ __forceinline__ u32x4 from_float(const float* f) {
-        f32x4 x;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) x[e] = f[e];
-        return __builtin_bit_cast(u32x4, x);
-    }
-};
-template <> struct Traits<_Float16> {
-    static constexpr int EPL = 8;
-    static __device__ __forceinline__ float dot(u32x4 a, u32x4 b) {
-        const f16x8 x = __builtin_bit_cast(f16x8, a), y = __builtin_bit_cast(f16x8, b);
-        float s = __builtin_amdgcn_fdot2(__builtin_shufflevector(x, x, 0, 1), __builtin_shufflevector(y, y, 0, 1), 0.0f, false);
-        s = __builtin_amdgcn_fdot2(__builtin_shufflevector(x, x, 2, 3), __builtin_shufflevector(y, y, 2, 3), s, false);
-        s = __builtin_amdgcn_fdot2(__builtin_shufflevector(x, x, 4, 5), __builtin_shufflevector(y, y, 4, 5), s, false);
-        s = __builtin_amdgcn_fdot2(__builtin_shufflevector(x, x, 6, 7), __builtin_shufflevector(y, y, 6, 7), s, false);
-        return s;
-    }
-    static __device__ __forceinline__ void to_float(u32x4 a, float* f) {
-        const f16x8 x = __builtin_bit_cast(f16x8, a);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) f[e] = (float)x[e];
-    }
-    static __device__ __forceinline__ u32x4 from_float(const float* f) {
-        f16x8 x;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = (_Float16)f[e];
-        return __builtin_bit_cast(u32x4, x);
-    }
-};
-
-__device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
-
-// Length and chunk range of unit chunk c of sequence s.  Returns false when the
-// unit has no chunk (beyond the sequence's chunk count).
-__device__ __forceinline__ bool chunk_range(const DecodeParams& p, int s, int c, int& nc, int& j0, int& j1) {
-    int L = p.cur_len ? p.cur_len[s] : p.fixed_len;
-    L = min(max(L, 0), p.cap);  // a length above the stated cap never reads past the caches
-    if (p.num_splits > 0) {
-        nc = p.num_splits;
-        const int ch = (L + nc - 1) / nc;
-        j0 = min(c * ch, L);
-        j1 = min(j0 + ch, L);
-        return c < nc;
-    }
-    const int ch = p.chunk_tokens;
-    L = min(L, ch * p.max_chunks);  // lengths beyond cap stay inside grid and workspace
-    nc = max(1, (L + ch - 1) / ch);
-    j0 = c * ch;
-    j1 = min(j0 + ch, L);
-    return c < nc;
-}
-
-// Log-sum-exp merge of the nc chunk partials of one query head: chunk c's
-// record is rec0 + c*cstride (acc at record*D, (m, l) at record*2):
-//   M = max_c m_c,  out = sum_c 2^(m_c-M) acc_c / sum_c 2^(m_c-M) l_c.
-// One wave; lane d owns output dims d, d+64, ...  COHERENT reads the partials
-// with agent-scope atomic loads (partials written by other XCDs bypass stale
-// L2 lines); otherwise plain loads after an acquire fence.
-template <typename T, int D, bool COHERENT>
-__device__ __forceinline__ void merge_head(const DecodeParams& p, size_t rec0, size_t cstride, int nc, T* ob,
-                                           int lane) {
-    constexpr int DPL = (D + kWave - 1) / kWave;
-    auto ld = [](const float* a) {
-        if constexpr (COHERENT) return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        else return *a;
-    };
-    float M = -FLT_MAX;
-    for (int c = 0; c < nc; ++c) M = fmaxf(M, ld(p.part_ml + (rec0 + (size_t)c * cstride) * 2));
-    float l = 0.f, acc[DPL];
-#pragma unroll
-    for (int j = 0; j < DPL; ++j) acc[j] = 0.f;
-    for (int c = 0; c < nc; ++c) {
-        const size_t rec = rec0 + (size_t)c * cstride;
-        const float w = fast_exp2(ld(p.part_ml + rec * 2) - M);
-        l = __builtin_fmaf(w, ld(p.part_ml + rec * 2 + 1), l);
-#pragma unroll
-        for (int j = 0; j < DPL; ++j) {
-            const int d = lane + j * kWave;
-            if (d < D) acc[j] = __builtin_fmaf(w, ld(p.part_acc + rec * D + d), acc[j]);
-        }
-    }
-    const float inv = l > 0.f ? 1.0f / l : 0.f;
-#pragma unroll
-    for (int j = 0; j < DPL; ++j) {
-        const int d = lane + j * kWave;
-        if (d < D) ob[d] = (T)(acc[j] * inv);
-    }
-}
-
-// Arrival count of a (sequence, KV head, head subgroup) before this unit, in a
-// 64-bit counter tagged with the call's epoch in the high word: a counter from
-// another call (or never initialised) counts as zero, and the last arriver
-// resets it to zero, so neither fresh nor replayed workspaces need clearing.
-__device__ __forceinline__ unsigned arrive(unsigned long long* ctr, unsigned epoch) {
-    unsigned long long old = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    for (;;) {
-        const unsigned base = (unsigned)(old >> 32) == epoch ? (unsigned)old : 0u;
-        const unsigned long long next = ((unsigned long long)epoch << 32) | (unsigned long long)(base + 1u);
-        if (__hip_atomic_compare_exchange_strong(ctr, &old, next, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT))
-            return base;
-    }
-}
-
-// K/V registers of U wave-loads: the double-buffered unit of the inner loop.
-template <int U>
-struct Batch {
-    u32x4 k[U], v[U];
-    int k0;  // this wave's index of the batch's first wave-load
-};
-
-// Buffer descriptor over `bytes` bytes at `base` (raw, unswizzled, 32-bit data
-// format).  Loads whose offset is >= bytes return 0 and touch no memory.
-constexpr int kBufferWord3 = 0x00020000;
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base, int bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, kBufferWord3);
-}
-__device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, int voffset) {
-    return __builtin_amdgcn_raw_buffer_load_b128(r, voffset, 0, 0);
-}
-
-// Largest chunk, in blocks, the per-lane paged path stages in LDS.
-constexpr int kMaxChunkBlocks = 4096;
-
-// One workgroup of WPB waves per unit (sequence s, KV head hk, head subgroup,
-// chunk c).  The chunk's wave-loads (TPW tokens each) are dealt round-robin to
-// the waves; every wave keeps two batches of U wave-loads in flight (ping-pong)
-// and its own online-softmax state per token slot.  Loads carry no control flow:
-// contiguous and uniform-paged tiles are read with buffer loads whose descriptor
-// covers exactly the tile's valid rows (rows past the chunk read as 0 and cost
-// no memory traffic), so the compiler can count outstanding loads exactly and
-// the next batch streams while the current one is consumed.  At the end the
-// token slots are merged with lane shuffles, the waves through LDS, and wave 0
-// writes either the normalised output (single-chunk sequence) or the chunk
-// partial, optionally followed by the fused cross-chunk merge.
-template <typename T, int D, int G, int MODE, int WPB, int U>
-__global__ __launch_bounds__(WPB * kWave) void split_kernel(DecodeParams p) {
-    using Tr = Traits<T>;
-    constexpr int EPL = Tr::EPL;
-    constexpr int LPT = D / EPL;      // lanes per K/V row
-    constexpr int TPW = kWave / LPT;  // rows (tokens) per wave-wide load
-    constexpr int ROW = D * (int)sizeof(T);  // bytes per K/V row
-    static_assert(LPT >= 1 && LPT <= kWave && D % EPL == 0, "unsupported head_dim");
-    __shared__ float s_acc[WPB][G][D];
-    __shared__ float s_m[WPB][G], s_l[WPB][G];
-    __shared__ int s_tab[MODE == kPagedPerLane ? kMaxChunkBlocks : 1];
-
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wave = uniform(threadIdx.x >> 6);
-    const int tslot = lane / LPT;
-    const int dl = lane % LPT;
-
-    int s, hk, sub, c, nc, j0, j1;
-    size_t rec0, cstride, ctr_idx;  // partial record of (this chunk, head 0); stride between chunks; counter
-    int tab_start = 0;  // planned: index into table_all of the chunk's first block
-    if (p.work != nullptr) {
-        // planned unit {s, hks | c << 16, j0, j1, nc, record group, counter, table start}
-        const int* w = p.work + (size_t)blockIdx.x * 8;
-        s = w[0];
-        const int hks = w[1] & 0xFFFF;
-        c = w[1] >> 16;
-        hk = hks / p.nsub;
-        sub = hks % p.nsub;
-        j0 = max(w[2], 0);
-        j1 = max(w[3], j0);
-        nc = max(w[4], 1);
-        rec0 = (size_t)(w[5] > 0 ? w[5] : 0) * G + (size_t)c * G;
-        cstride = G;
-        ctr_idx = w[6] > 0 ? w[6] : 0;
-        tab_start = w[7];
-    } else {
-        int unit = blockIdx.x;
-        sub = unit % p.nsub;  unit /= p.nsub;
-        hk = unit % p.Hkv;    unit /= p.Hkv;
-        s = unit % p.N;
-        // chunk index is the slowest-varying; with last_chunk_first the later chunks
-        // (which only long sequences have, and which are full-size) dispatch first
-        c = p.last_chunk_first ? p.max_chunks - 1 - unit / p.N : unit / p.N;
-        if (c >= p.max_chunks) return;
-        if (!chunk_range(p, s, c, nc, j0, j1)) return;
-        rec0 = ((size_t)s * p.max_chunks + c) * p.Hq + hk * p.group + sub * G;
-        cstride = p.Hq;
-        ctr_idx = ((size_t)s * p.Hkv + hk) * p.nsub + sub;
-    }
-    const int hq0 = hk * p.group + sub * G;
-    const int nwl = (j1 - j0 + TPW - 1) / TPW;                          // wave-loads in the chunk
-    const int kmax = wave < nwl ? (nwl - wave + WPB - 1) / WPB : 0;     // this wave's share
-
-    u32x4 qv[G];
-    {
-        const T* qb = static_cast<const T*>(p.q) + ((size_t)s * p.Hq + hq0) * D + dl * EPL;
-#pragma unroll
-        for (int g = 0; g < G; ++g) qv[g] = *reinterpret_cast<const u32x4*>(qb + (size_t)g * D);
-    }
-    float m[G], l[G], acc[G][EPL];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        m[g] = -FLT_MAX;
-        l[g] = 0.f;
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) acc[g][e] = 0.f;
-    }
-
-    const char* kb = static_cast<const char*>(p.k);
-    const char* vb = static_cast<const char*>(p.v);
-    size_t cbase = 0;         // contiguous: byte offset of (s, hk, token 0)
-    int tbl = 0;              // uniform paged: block ids of the chunk, one per lane
-    const int b0 = j0 / p.block;
-    if constexpr (MODE == kContiguous) {
-        cbase = ((size_t)s * p.seq_stride + (size_t)hk * p.head_stride) * sizeof(T);
-    } else {
-        // blocks the chunk touches (0 for an empty chunk); the planner keeps this
-        // within kMaxChunkBlocks, the min() only guards the LDS staging
-        const int nblk = min(j1 > j0 ? (j1 - 1) / p.block - b0 + 1 : 0, kMaxChunkBlocks);
-        // The block ids are read through a descriptor: on the planned path the
-        // descriptor spans table_all (table_len ints), so any plan reads inside it;
-        // otherwise it spans this chunk's nblk entries.
-        const int first = p.work ? tab_start : (p.tab_off ? p.tab_off[s] : 0) + b0;
-        const __amdgpu_buffer_rsrc_t trs =
-            p.work ? tile_rsrc(p.table_all, p.table_len * 4) : tile_rsrc(p.table_all + first, nblk * 4);
-        const int tb = p.work ? first * 4 : 0;  // byte offset of the chunk's first entry
-        if constexpr (MODE == kPagedUniform) {
-            // unconditional: lanes past the chunk's blocks read a neighbour's id or 0 and
-            // are never selected by the readlane below
-            tbl = (int)__builtin_amdgcn_raw_buffer_load_b32(trs, tb + lane * 4, 0, 0);
-        } else {
-            for (int b = threadIdx.x; b < nblk; b += WPB * kWave)
-                s_tab[b] = (int)__builtin_amdgcn_raw_buffer_load_b32(trs, tb + b * 4, 0, 0);
-            __syncthreads();
-        }
-    }
-
-    auto issue = [&](int k0, Batch<U>& b) {
-        b.k0 = k0;
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int i = wave + WPB * (k0 + u);   // wave-load index within the chunk
-            const int t0 = j0 + i * TPW;
-            if constexpr (MODE == kPagedPerLane) {
-                int tt = t0 + tslot;
-                const bool ok = tt < j1;
-                tt = ok ? tt : j0;                     // a valid row; the value is discarded below
-                const int bb = tt / p.block;
-                const int phys = s_tab[bb - b0];
-                const size_t off = ((size_t)(phys * p.Hkv + hk) * p.block + (tt - bb * p.block)) * ROW + dl * 16;
-                const u32x4 kk = *reinterpret_cast<const u32x4*>(kb + off);
-                const u32x4 vv = *reinterpret_cast<const u32x4*>(vb + off);
-                b.k[u] = kk;
-                b.v[u] = ok ? vv : u32x4{0, 0, 0, 0};
-            } else {
-                // valid rows of this wave-load (kept scalar: the descriptor must live in SGPRs)
-                const int rows = uniform(min(max(j1 - t0, 0), TPW));
-                size_t tile;
-                if constexpr (MODE == kContiguous) {
-                    tile = cbase + (size_t)max(t0, 0) * ROW;
-                } else {
-                    const int rel = i >> p.lpb_shift;           // block of the chunk
-                    const int phys = __builtin_amdgcn_readlane(tbl, min(rel, kWave - 1));
-                    const int in = (i & ((1 << p.lpb_shift) - 1)) * TPW;
-                    tile = ((size_t)(phys * p.Hkv + hk) * p.block + in) * ROW;
-                }
-                b.k[u] = buffer_load16(tile_rsrc(kb + tile, rows * ROW), lane * 16);
-                b.v[u] = buffer_load16(tile_rsrc(vb + tile, rows * ROW), lane * 16);
-            }
-        }
-    };
-
-    auto consume = [&](const Batch<U>& b) {
-        bool valid[U];
-        float vf[U][EPL];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            valid[u] = j0 + (wave + WPB * (b.k0 + u)) * TPW + tslot < j1;
-            Tr::to_float(b.v[u], vf[u]);
-        }
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            float sc[U];
-            float mx = m[g];
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                sc[u] = group_sum<LPT>(Tr::dot(qv[g], b.k[u])) * p.scale_log2;
-                mx = valid[u] ? fmaxf(mx, sc[u]) : mx;
-            }
-            const float corr = fast_exp2(m[g] - mx);
-            float pu[U], ps = 0.f;
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                pu[u] = valid[u] ? fast_exp2(sc[u] - mx) : 0.f;
-                ps += pu[u];
-            }
-            l[g] = __builtin_fmaf(l[g], corr, ps);
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) {
-                float a = acc[g][e] * corr;
-#pragma unroll
-                for (int u = 0; u < U; ++u) a = __builtin_fmaf(pu[u], vf[u][e], a);
-                acc[g][e] = a;
-            }
-            m[g] = mx;
-        }
-    };
-
-    if (kmax > 0) {
-        Batch<U> A, B;
-        issue(0, A);
-        for (int k = 0;; k += 2 * U) {
-            issue(k + U, B);          // past the end it reads nothing (zero-size tiles)
-            consume(A);
-            if (k + U >= kmax) break;
-            issue(k + 2 * U, A);
-            consume(B);
-            if (k + 2 * U >= kmax) break;
-        }
-    }
-
-    // Merge the TPW token slots of the wave (lanes that differ in bits >= log2(LPT)).
-#pragma unroll
-    for (int msk = LPT; msk < kWave; msk <<= 1) {
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const float mo = shfl_xor(m[g], msk), lo = shfl_xor(l[g], msk);
-            const float mx = fmaxf(m[g], mo);
-            const float ws = fast_exp2(m[g] - mx), wo = fast_exp2(mo - mx);
-            l[g] = l[g] * ws + lo * wo;
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) acc[g][e] = acc[g][e] * ws + shfl_xor(acc[g][e], msk) * wo;
-            m[g] = mx;
-        }
-    }
-    if (tslot == 0) {
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) s_acc[wave][g][dl * EPL + e] = acc[g][e];
-    }
-    if (lane == 0) {
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            s_m[wave][g] = m[g];
-            s_l[wave][g] = l[g];
-        }
-    }
-    __syncthreads();
-    if (wave != 0) return;
-
-    // Wave 0 merges the WPB wave partials: lane handles (g, d) = divmod(idx, D).
-    T* ob = static_cast<T*>(p.out) + ((size_t)s * p.Hq + hq0) * D;
-    for (int idx = lane; idx < G * D; idx += kWave) {
-        const int g = idx / D, d = idx % D;
-        float M = -FLT_MAX;
-#pragma unroll
-        for (int w = 0; w < WPB; ++w) M = fmaxf(M, s_m[w][g]);
-        float lt = 0.f, at = 0.f;
-#pragma unroll
-        for (int w = 0; w < WPB; ++w) {
-            const float wt = fast_exp2(s_m[w][g] - M);
-            lt = __builtin_fmaf(wt, s_l[w][g], lt);
-            at = __builtin_fmaf(wt, s_acc[w][g][d], at);
-        }
-        if (nc == 1) {
-            ob[(size_t)g * D + d] = (T)(lt > 0.f ? at * (1.0f / lt) : 0.f);
-        } else if (p.merge_mode == kMergeAtomic) {
-            __hip_atomic_store(p.part_acc + (rec0 + g) * D + d, at, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (d == 0) {
-                __hip_atomic_store(p.part_ml + (rec0 + g) * 2, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(p.part_ml + (rec0 + g) * 2 + 1, lt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-        } else {
-            p.part_acc[(rec0 + g) * D + d] = at;
-            if (d == 0) {
-                p.part_ml[(rec0 + g) * 2] = M;
-                p.part_ml[(rec0 + g) * 2 + 1] = lt;
-            }
-        }
-    }
-    if (nc == 1 || p.merge_mode == kMergeKernel) return;  // single chunk, or a merge kernel follows
-    // Fused merge: publish the partials, count arrivals; the last chunk merges.
-    if (p.merge_mode == kMergeAtomic) {
-        // the partial stores were coherent; wait until this wave's stores completed
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        __builtin_amdgcn_s_waitcnt(0);
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    } else {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    }
-    unsigned long long* ctr = p.counters + ctr_idx;
-    unsigned before = 0;
-    if (lane == 0) before = arrive(ctr, p.epoch);
-    before = (unsigned)uniform((int)before);
-    if (before != (unsigned)(nc - 1)) return;
-    const size_t first = rec0 - (size_t)c * cstride;  // record of chunk 0, head 0
-    if (p.merge_mode == kMergeAtomic) {
-        for (int g = 0; g < G; ++g) merge_head<T, D, true>(p, first + g, cstride, nc, ob + (size_t)g * D, lane);
-    } else {
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-        for (int g = 0; g < G; ++g) merge_head<T, D, false>(p, first + g, cstride, nc, ob + (size_t)g * D, lane);
-    }
-    if (lane == 0) __hip_atomic_store(ctr, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Standalone log-sum-exp merge: one 512-thread workgroup per (sequence, query
-// head).  All chunk maxima are loaded at once and reduced; then MG = 512/D chunk
-// groups x D dims accumulate 2^(m_c-M) * (acc_c, l_c) with independent loads
-// (unrolled), and the groups are summed through LDS.  Sequences with a single
-// chunk were finished by the split kernel and exit at once.
-constexpr int kMergeThreads = 512;
-
-template <typename T, int D>
-__global__ __launch_bounds__(kMergeThreads) void merge_kernel(DecodeParams p) {
-    constexpr int MG = kMergeThreads / D;  // chunk groups
-    __shared__ float s_red[kMergeThreads / kWave];
-    __shared__ float s_acc[MG][D];
-    __shared__ float s_l[MG];
-    const int t = threadIdx.x;
-    const int lane = t & (kWave - 1), wave = t >> 6;
-    const int s = blockIdx.x / p.Hq, hq = blockIdx.x % p.Hq;
-    int nc, j0, j1;
-    chunk_range(p, s, 0, nc, j0, j1);
-    if (nc <= 1) return;
-    const size_t rec0 = (size_t)s * p.max_chunks * p.Hq + hq;
-    const size_t cstride = (size_t)p.Hq;  // records between consecutive chunks
-
-    float mx = -FLT_MAX;
-    for (int c = t; c < nc; c += kMergeThreads) mx = fmaxf(mx, p.part_ml[(rec0 + c * cstride) * 2]);
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, shfl_xor(mx, o));
-    if (lane == 0) s_red[wave] = mx;
-    __syncthreads();
-    float M = s_red[0];
-#pragma unroll
-    for (int w = 1; w < kMergeThreads / kWave; ++w) M = fmaxf(M, s_red[w]);
-
-    const int cg = t / D, d = t % D;
-    float at = 0.f, lt = 0.f;
-    int c = cg;
-    for (; c + 3 * MG < nc; c += 4 * MG) {
-        float w4[4], a4[4], l4[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const size_t rec = rec0 + (size_t)(c + u * MG) * cstride;
-            w4[u] = p.part_ml[rec * 2];
-            l4[u] = p.part_ml[rec * 2 + 1];
-            a4[u] = p.part_acc[rec * D + d];
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const float w = fast_exp2(w4[u] - M);
-            lt = __builtin_fmaf(w, l4[u], lt);
-            at = __builtin_fmaf(w, a4[u], at);
-        }
-    }
-    for (; c < nc; c += MG) {
-        const size_t rec = rec0 + (size_t)c * cstride;
-        const float w = fast_exp2(p.part_ml[rec * 2] - M);
-        lt = __builtin_fmaf(w, p.part_ml[rec * 2 + 1], lt);
-        at = __builtin_fmaf(w, p.part_acc[rec * D + d], at);
-    }
-    s_acc[cg][d] = at;
-    if (d == 0) s_l[cg] = lt;
-    __syncthreads();
-    if (t < D) {
-        float a = 0.f, l = 0.f;
-#pragma unroll
-        for (int g = 0; g < MG; ++g) {
-            a += s_acc[g][t];
-            l += s_l[g];
-        }
-        static_cast<T*>(p.out)[((size_t)s * p.Hq + hq) * D + t] = (T)(l > 0.f ? a * (1.0f / l) : 0.f);
-    }
-}
-
-template <typename T, int D, int G, int WPB, int U>
-int launch_split_mode(const DecodeLaunch& L, dim3 grid, hipStream_t st) {
-    const dim3 block(WPB * kWave);
-    switch (L.mode) {
-        case kContiguous:   hipLaunchKernelGGL((split_kernel<T, D, G, kContiguous, WPB, U>), grid, block, 0, st, L.p); break;
-        case kPagedUniform: hipLaunchKernelGGL((split_kernel<T, D, G, kPagedUniform, WPB, U>), grid, block, 0, st, L.p); break;
-        case kPagedPerLane: hipLaunchKernelGGL((split_kernel<T, D, G, kPagedPerLane, WPB, U>), grid, block, 0, st, L.p); break;
-        default: return set_error(KVC_ERR_ARG, "unknown decode mode");
-    }
-    return KVC_OK;
-}
-
-// Wave-loads per double-buffered batch: 4 for one or two query heads per wave
-// (2 and 8 selectable for D 64/128), 2 for larger head groups (register budget).
-template <typename T, int D, int G, int WPB>
-int launch_split_u(const DecodeLaunch& L, dim3 grid, hipStream_t st) {
-    if constexpr (G <= 2) {
-        if constexpr (D == 64 || D == 128) {
-            if (L.batch == 2) return launch_split_mode<T, D, G, WPB, 2>(L, grid, st);
-            if (L.batch == 8) return launch_split_mode<T, D, G, WPB, 8>(L, grid, st);
-        }
-        return launch_split_mode<T, D, G, WPB, 4>(L, grid, st);
-    } else {
-        return launch_split_mode<T, D, G, WPB, 2>(L, grid, st);
-    }
-}
-
-template <typename T, int D, int G>
-int launch_split_wpb(const DecodeLaunch& L, dim3 grid, hipStream_t st) {
-    if (L.wpb == 8) return launch_split_u<T, D, G, 8>(L, grid, st);
-    if (L.wpb == 4) return launch_split_u<T, D, G, 4>(L, grid, st);
-    return set_error(KVC_ERR_ARG, "waves per block must be 4 or 8");
-}
-
-template <typename T, int D>
-int launch_split_g(const DecodeLaunch& L, dim3 grid, hipStream_t st) {
-    if constexpr (D == 64 || D == 128) {
-        switch (L.G) {
-            case 1: return launch_split_wpb<T, D, 1>(L, grid, st);
-            case 2: return launch_split_wpb<T, D, 2>(L, grid, st);
-            case 4: return launch_split_wpb<T, D, 4>(L, grid, st);
-            case 7: return launch_split_wpb<T, D, 7>(L, grid, st);
-            case 8: return launch_split_wpb<T, D, 8>(L, grid, st);
-            default: break;
-        }
-    } else {
-        if (L.G == 1) return launch_split_wpb<T, D, 1>(L, grid, st);
-    }
-    return set_error(KVC_ERR_UNSUPPORTED, "query heads per unit not instantiated");
-}
-
 template <typename T>
 int launch_typed(const DecodeLaunch& L, hipStream_t st) {
-    const long long units = L.p.work ? (long long)L.units : (long long)L.p.max_chunks * L.p.N * L.p.Hkv * L.p.nsub;
-    if (units <= 0) return KVC_OK;
-    if (units > (long long)INT_MAX) return set_error(KVC_ERR_ARG, "decode grid too large");
-    const dim3 grid((unsigned)units);
-    int rc;
     switch (L.D) {
-        case 32:  rc = launch_split_g<T, 32>(L, grid, st); break;
-        case 64:  rc = launch_split_g<T, 64>(L, grid, st); break;
-        case 128: rc = launch_split_g<T, 128>(L, grid, st); break;
-        case 256: rc = launch_split_g<T, 256>(L, grid, st); break;
+        case 32:  return launch_decode_d<T, 32>(L, st);
+        case 64:  return launch_decode_d<T, 64>(L, st);
+        case 128: return launch_decode_d<T, 128>(L, st);
+        case 256: return launch_decode_d<T, 256>(L, st);
         default: return set_error(KVC_ERR_UNSUPPORTED, "head_dim must be 32, 64, 128 or 256");
     }
-    if (rc != KVC_OK) return rc;
-    rc = hip_check(hipGetLastError(), "decode split launch");
-    if (rc != KVC_OK || !L.need_merge || L.p.merge_mode != kMergeKernel) return rc;
-    const dim3 mgrid((unsigned)((long long)L.p.N * L.p.Hq));
-    const dim3 mblock(kMergeThreads);
-    switch (L.D) {
-        case 32:  hipLaunchKernelGGL((merge_kernel<T, 32>), mgrid, mblock, 0, st, L.p); break;
-        case 64:  hipLaunchKernelGGL((merge_kernel<T, 64>), mgrid, mblock, 0, st, L.p); break;
-        case 128: hipLaunchKernelGGL((merge_kernel<T, 128>), mgrid, mblock, 0, st, L.p); break;
-        case 256: hipLaunchKernelGGL((merge_kernel<T, 256>), mgrid, mblock, 0, st, L.p); break;
-    }
-    return hip_check(hipGetLastError(), "decode merge launch");
 }
-
 }  // namespace
 
 int launch_decode(const DecodeLaunch& L, hipStream_t stream) {

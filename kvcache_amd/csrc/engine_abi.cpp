@@ -91,6 +91,9 @@ int kvc_engine_create(const kvc_engine_config* c, kvc_engine** out) {
         ec.c2 = c->virt_c2;
         ec.device = c->device != 0;
         ec.split_tokens = c->split_tokens;
+        if (c->decode_path != KVC_DECODE_PLANNED && c->decode_path != KVC_DECODE_DEVICE_LENGTHS)
+            return kvc::set_error(KVC_ERR_ARG, "decode_path must be KVC_DECODE_PLANNED or KVC_DECODE_DEVICE_LENGTHS");
+        ec.decode_path = c->decode_path;
         if (c->seed) ec.seed = c->seed;
         if (c->max_batch <= 0) return kvc::set_error(KVC_ERR_ARG, "max_batch must be > 0");
         *out = new kvc_engine(ec);

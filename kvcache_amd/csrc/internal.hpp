@@ -17,7 +17,9 @@ int hip_check(hipError_t e, const char* what);
 // Decode launch description (host side).  One "unit" = (sequence s, KV head hk,
 // query-head subgroup sub, chunk c); each unit is one workgroup of `wpb` waves.
 // ---------------------------------------------------------------------------
-enum DecodeMode { kContiguous = 0, kPagedUniform = 1, kPagedPerLane = 2 };
+// kPlanned*: the grid is a host-built work list (kvc_decode_plan) instead of a
+// (chunk, sequence, head) decomposition; otherwise as kPaged*.
+enum DecodeMode { kContiguous = 0, kPagedUniform = 1, kPagedPerLane = 2, kPlannedUniform = 3, kPlannedPerLane = 4 };
 
 struct DecodeParams {
     const void* q;
@@ -71,6 +73,10 @@ struct DecodeLaunch {
 
 // Launches the split kernel and, when needed and not fused, the merge kernel.
 int launch_decode(const DecodeLaunch& L, hipStream_t stream);
+// The same for one element type and head_dim; each (T, D) pair is instantiated
+// in its own translation unit (decode_<type>_d<D>.hip).
+template <typename T, int D>
+int launch_decode_d(const DecodeLaunch& L, hipStream_t stream);
 
 // Tuning knobs (kvc_set_tuning).
 struct Tuning {

@@ -73,13 +73,14 @@ class EngineConfig:
     virt_c2: float = 0.0
     device: bool = True
     split_tokens: int = 0
+    decode_path: int = 0         # 0 host-planned decode, 1 device-lengths path with split_tokens
     seed: int = 0
 
     def to_c(self) -> EngineConfigC:
         return EngineConfigC(self.n_heads, self.n_kv_heads, self.head_dim, self.block_size, self.num_blocks,
                              self.max_batch, self.n_layers, self.dtype, int(self.kv_write), self.clock_mode,
                              self.virt_c0, self.virt_c1, self.virt_c2, int(self.device), self.split_tokens,
-                             self.seed)
+                             self.decode_path, self.seed)
 
 
 @dataclass

@@ -1,0 +1,73 @@
+// test_runner_paths.cpp -- ModelRunner::decode_step on its two decode paths.
+//
+// The host-planned path (work list appended to the step's one upload) and the
+// device-lengths path (kvc_batched_paged_decode_split) must give the same
+// attention output on the same pools, tables and inputs: within 2e-3 (fp16 K/V,
+// fp32 accumulation; the two paths cut sequences into different chunks).  Both
+// kernels are checked against the CPU restatement elsewhere; this program checks
+// the runner's packing (offsets of tables and work list in the upload, the
+// workspace sizing, growth of the metadata buffers) on a ragged GQA batch with
+// sequences long enough to be split, over two layers with K/V writes.
+#include <cmath>
+#include <cstdio>
+#include <vector>
+
+#include "kvc/model_runner.h"
+
+static std::vector<_Float16> fetch(const ModelRunner& r, int n) {
+    std::vector<_Float16> h((size_t)n * r.n_heads * r.head_dim);
+    kvc::check(kvc_memcpy_d2h(h.data(), r.dout, h.size() * sizeof(_Float16), r.stream), "d2h");
+    kvc::check(kvc_stream_synchronize(r.stream), "sync");
+    return h;
+}
+
+int main() {
+    const int Hq = 14, Hkv = 2, D = 64, B = 16, NB = 4096, L = 2, maxB = 32;
+    KVCacheManager kvm(NB, B, Hkv, D, KVC_F16, L);
+    for (int l = 0; l < L; ++l) {
+        kvc::check(kvc_fill_normal(kvm.k_layer(l), kvm.pool_elems(), KVC_F16, 11 + l, 1.0f, nullptr), "fill k");
+        kvc::check(kvc_fill_normal(kvm.v_layer(l), kvm.pool_elems(), KVC_F16, 23 + l, 1.0f, nullptr), "fill v");
+    }
+    kvc::check(kvc_device_synchronize(), "sync");
+
+    // ragged lengths 1 .. ~6000 tokens (several sequences need more than one chunk)
+    std::vector<Sequence> seqs(maxB);
+    std::vector<Sequence*> batch;
+    unsigned x = 12345;
+    for (int i = 0; i < maxB; ++i) {
+        x = x * 1103515245u + 12345u;
+        const double r = ((x >> 9) & 0x7FFFFF) / 8388608.0;
+        seqs[i].id = i;
+        seqs[i].prompt_len = seqs[i].cur_len = 1 + (int)(5999 * r * r * r);
+        if (!kvm.allocate_prompt(seqs[i])) { std::printf("pool too small\n"); return 2; }
+        batch.push_back(&seqs[i]);
+    }
+    std::vector<int> wpos(maxB);
+    for (int i = 0; i < maxB; ++i) wpos[i] = seqs[i].cur_len - 1;  // rewrite each sequence's last row
+
+    int worst = 0;
+    for (int kv_write = 0; kv_write <= 1; ++kv_write) {
+        for (int n : {maxB, 5}) {
+            RunnerOptions po;
+            po.n_kv_heads = Hkv; po.n_layers = L; po.dtype = KVC_F16; po.kv_write = kv_write;
+            RunnerOptions so = po;
+            so.decode_path = KVC_DECODE_DEVICE_LENGTHS;
+            ModelRunner planned(Hq, D, B, maxB, NB, po), split(Hq, D, B, maxB, NB, so);
+            std::vector<Sequence*> b(batch.begin(), batch.begin() + n);
+            planned.decode_step(b, kvm, kv_write ? wpos.data() : nullptr);
+            split.decode_step(b, kvm, kv_write ? wpos.data() : nullptr);
+            const auto a = fetch(planned, n), c = fetch(split, n);
+            double err = 0;
+            bool finite = true;
+            for (size_t i = 0; i < a.size(); ++i) {
+                finite = finite && std::isfinite((double)a[i]);
+                err = std::fmax(err, std::fabs((double)a[i] - (double)c[i]));
+            }
+            std::printf("kv_write=%d N=%d: max |planned - device-lengths| = %.3e (digests %s)\n", kv_write, n, err,
+                        planned.digest == split.digest ? "equal" : "DIFFER");
+            if (!(err <= 2e-3) || !finite || planned.digest != split.digest) worst = 1;
+        }
+    }
+    std::printf(worst ? "=== RUNNER PATHS MISMATCH ===\n" : "=== RUNNER PATHS OK ===\n");
+    return worst;
+}

@@ -39,3 +39,8 @@ def test_demo_engine_device():
 @pytest.mark.gpu
 def test_paged_flash_device():
     assert run("test_paged_flash").returncode == 0
+
+
+@pytest.mark.gpu
+def test_runner_planned_and_device_length_paths_agree():
+    assert run("test_runner_paths").returncode == 0
