@@ -140,7 +140,7 @@ def time_planned(W, lens, Hq, Hkv, D, B, steps, warmup, target=0, rotate=None):
     work, nu, nr = ops.decode_plan(lens, Hq, Hkv, D, B, tab_off=W["tab_off_host"], dtype=KVC_F16,
                                    target_tokens=target)
     wdev = DeviceBuffer.from_numpy(work)
-    ws = DeviceBuffer(max(ops.planned_workspace_size(Hq, Hkv, D, nr), 256))
+    ws = DeviceBuffer(max(ops.planned_workspace_size(Hq, Hkv, D, nr, BLOCK=B, dtype=KVC_F16), 256))
     pools = W["pools"] if rotate is None else W["pools"][:rotate]
     N = len(lens)
 
@@ -227,16 +227,24 @@ def cpu_baseline(host_data, W, lens, Hkv, B, D, budget_s, kv_bytes):
             "host_cpus": os.cpu_count()}
 
 
-def bench_c3(steps, warmup):
-    """Config 3: Hq 14 / Hkv 2, D 64, lengths {8192,16384,32768,32768}, 512-token splits."""
+def bench_c3(steps, warmup, plan_sweep=()):
+    """Config 3: Hq 14 / Hkv 2, D 64, lengths {8192,16384,32768,32768}: 512-token splits on the
+    device-lengths path (the configuration as stated) and the planned path (host-chosen chunks)."""
     lens = np.array([8192, 16384, 32768, 32768], np.int32)
     Hq, Hkv, D, B = 14, 2, 64, 16
     W = build_c2(lens, Hq, Hkv, D, B, rotate=8, seed=3)   # 8 x 46 MB rotate past the Infinity Cache
     t, _ = time_decode(W, lens, Hq, Hkv, D, B, 512, steps, warmup)
     kv, total = alg_bytes(lens, Hq, Hkv, D, B)
-    return {"workload": "C3 long-context split-K 14q/2kv D64 ctx {8k,16k,32k,32k} fp16 split 512",
-            "us_per_step": round(t * 1e3, 2), "GBps": round(total / (t * 1e-3) / 1e9, 1),
-            "frac_hbm_peak": round(total / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "kv_bytes": kv}
+    res = {"workload": "C3 long-context split-K 14q/2kv D64 ctx {8k,16k,32k,32k} fp16 split 512",
+           "us_per_step": round(t * 1e3, 2), "GBps": round(total / (t * 1e-3) / 1e9, 1),
+           "frac_hbm_peak": round(total / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "kv_bytes": kv}
+    for tgt in plan_sweep:
+        tp, nu, nr, _ = time_planned(W, lens, Hq, Hkv, D, B, 30, 5, target=tgt)
+        log(f"C3 sweep planned target={tgt}: {tp * 1e3:.2f} us ({nu} units, {nr} records)")
+    tp, nu, _, _ = time_planned(W, lens, Hq, Hkv, D, B, steps, warmup)
+    res["planned"] = {"us_per_step": round(tp * 1e3, 2), "GBps": round(total / (tp * 1e-3) / 1e9, 1),
+                      "frac_hbm_peak": round(total / (tp * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "units": nu}
+    return res
 
 
 def bench_c4():
@@ -310,8 +318,12 @@ def main() -> int:
     ap.add_argument("--plan-sweep", type=str, default="", help="comma list of planned targets to time")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="only run 10 device-to-device copies of MIB MiB (HBM counter calibration) and exit")
+    ap.add_argument("--only", choices=["c3", "c4"], default=None,
+                    help="run only config 3 or config 4 and print its result (profiling)")
     ap.add_argument("--warm", action="store_true",
                     help="also time the planned path on one pool copy (Infinity-Cache resident)")
+    ap.add_argument("--tune", action="append", default=[], metavar="KEY=VALUE",
+                    help="set a library tuning knob (kvc_set_tuning), e.g. wg_per_cu=4")
     ap.add_argument("--fused", type=int, default=-1,
                     help="merge mode: -1 automatic, 0 merge kernel, 1 fused with fences, 2 fused coherent")
     a = ap.parse_args()
@@ -331,8 +343,16 @@ def main() -> int:
     set_tuning("waves_per_block", a.wpb)
     set_tuning("fused_merge", a.fused)
     set_tuning("batch", a.batch)
+    for kv in a.tune:
+        key, val = kv.split("=", 1)
+        set_tuning(key, int(val))
     if a.copy_calib:
         return copy_calibration(a.copy_calib)
+    sweep_targets = [int(x) for x in a.plan_sweep.split(",") if x]
+    if a.only:
+        res = bench_c3(a.steps, a.warmup, sweep_targets) if a.only == "c3" else bench_c4()
+        print(json.dumps(res), flush=True)
+        return 0
     if a.lengths == "reference":
         lens = Wl.ref_lengths()
     elif a.lengths == "loguniform":

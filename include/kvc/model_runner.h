@@ -225,7 +225,8 @@ struct ModelRunner {
         const int* d_tab = d_len + 3 * n;
         const int* d_work = d_tab + T;
 
-        ensure_workspace(planned ? kvc_decode_planned_workspace_size(n_heads, n_kv_heads, head_dim, n_records)
+        ensure_workspace(planned ? kvc_decode_planned_workspace_size(n_heads, n_kv_heads, head_dim, block_size,
+                                                                   opt.dtype, n_records)
                                  : kvc_decode_workspace_size(n, n_heads, n_kv_heads, head_dim, block_size, cap,
                                                              opt.split_tokens, opt.dtype));
         kvc::check(kvc_event_record(ev0, stream), "event");

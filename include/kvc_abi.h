@@ -59,7 +59,11 @@ int         kvc_device_count(int* count);
  * "min_chunk_bytes" (automatic split: least K+V bytes per workgroup),
  * "waves_per_block" (0 automatic, 4 or 8 waves cooperating on one chunk),
  * "batch" (2, 4 or 8 wave-loads per double-buffered batch when a wave serves at
- * most two query heads), "last_chunk_first" (1: dispatch later chunks first). */
+ * most two query heads), "last_chunk_first" (1: dispatch later chunks first),
+ * "mfma" (grouped-query heads on the matrix cores: -1 automatic, 0 off, 1 on),
+ * "wg_per_cu" (cap on decode workgroups per CU through reserved LDS: -1
+ * automatic, 0 none, n), "split_first" (planner: chunks of split sequences
+ * before whole sequences). */
 int         kvc_set_tuning(const char* key, int value);
 int         kvc_get_tuning(const char* key, int* value);
 
@@ -176,10 +180,13 @@ int kvc_decode_auto_split(int N, int Hq, int Hkv, int D, int BLOCK, int cap, int
  * caller copies the work list to the device (e.g. inside its per-step upload) and
  * runs kvc_batched_paged_decode_planned with the same shape and tables; every
  * block-id read is bounded by table_len (ints in table_all).  Partials of split
- * sequences are merged by the last chunk to finish, inside the same kernel. */
+ * sequences are merged by the last chunk to finish, inside the same kernel.
+ * A plan depends on the tuning knobs ("mfma", "waves_per_block"): plan and launch
+ * under the same settings.  Units naming a sequence or KV head outside N / Hkv
+ * are skipped. */
 int kvc_decode_plan(const int* host_lens, const int* host_tab_off, int N, int Hq, int Hkv, int D, int BLOCK,
                     int dtype, int target_tokens, int* work, int capacity, int* n_units, int* n_records);
-size_t kvc_decode_planned_workspace_size(int Hq, int Hkv, int D, int n_records);
+size_t kvc_decode_planned_workspace_size(int Hq, int Hkv, int D, int BLOCK, int dtype, int n_records);
 int kvc_batched_paged_decode_planned(const void* q, const void* k_pool, const void* v_pool,
                                      const int* table_all, int table_len, void* out,
                                      int N, int Hq, int Hkv, int D, int BLOCK, float scale,

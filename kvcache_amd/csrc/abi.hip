@@ -32,6 +32,13 @@ Tuning& tuning() {
     return t;
 }
 
+size_t occupancy_lds(size_t static_lds, int n) {
+    constexpr size_t kLdsPerCu = 160 * 1024;
+    if (n <= 0) return 0;
+    const size_t per = kLdsPerCu / (size_t)n;
+    return per > static_lds + 256 ? per - static_lds - 256 : 0;
+}
+
 int hip_check(hipError_t e, const char* what) {
     if (e == hipSuccess) return KVC_OK;
     return set_error(KVC_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
@@ -57,6 +64,17 @@ int choose_g(int group, int D) {
         if (group % c == 0 && g_instantiated(D, c)) return c;
     return 1;
 }
+// Grouped-query decode on the matrix cores (gqa_mfma.hpp): fp16 K/V, head_dim 64
+// or 128, groups of 3..16 query heads per KV head (automatic: 4..16), blocks that
+// hold whole 16-token subtiles.
+constexpr int kMfmaMaxChunkBlocksHost = 1024;
+constexpr int kMfmaMaxFusedChunks = 64;
+inline bool mfma_path(int group, int D, int dtype, int BLOCK, bool paged) {
+    const int t = tuning().mfma;
+    if (t == 0 || dtype != KVC_F16 || (D != 64 && D != 128) || group > 16 || group < (t == 1 ? 3 : 4)) return false;
+    return !paged || BLOCK % 16 == 0;
+}
+
 // Tokens covered by one wave-wide 16-byte load.
 inline int tokens_per_wave_load(int D, int dtype) { return 64 / (D * esize(dtype) / 16); }
 
@@ -80,6 +98,7 @@ int auto_split(int N, int Hq, int Hkv, int D, int BLOCK, int cap, int dtype) {
 
 struct Plan {
     int G = 1, nsub = 1, mode = kContiguous, chunk = 1, max_chunks = 1, wpb = 4, lpb_shift = 0;
+    bool mfma = false;
     bool chunk_blocks_ok = true;  // the per-lane path stages at most 4096 block ids per chunk
     size_t acc_bytes = 0, ml_bytes = 0, ws_bytes = 0;
 };
@@ -108,9 +127,40 @@ void size_workspace(Plan& pl, int N, int Hq, int Hkv, int D) {
     pl.ws_bytes = pl.acc_bytes + pl.ml_bytes + align_up((size_t)N * Hkv * pl.nsub * sizeof(uint64_t), kAlign);
 }
 
-Plan plan_batched(int N, int Hq, int Hkv, int D, int BLOCK, int cap, int dtype, int split, bool paged) {
+// Matrix-core path: all heads of the group per unit, 8 waves per unit, chunks of
+// at least two 32-token tiles per wave, about 512 units over the longest length.
+Plan plan_batched_mfma(int N, int Hq, int Hkv, int D, int BLOCK, int cap, int split, bool paged) {
     Plan pl;
+    pl.mfma = true;
+    pl.G = Hq / Hkv;
+    pl.nsub = 1;
+    const int t = tuning().waves_per_block;
+    pl.wpb = (t == 4 || t == 8) ? t : 8;
+    long long ch = split;
+    if (ch <= 0) {
+        const long long units = (long long)N * Hkv;
+        ch = std::max<long long>((long long)pl.wpb * 64, ((long long)std::max(cap, 1) * units + 511) / 512);
+        long long p2 = 1;
+        while (p2 < ch) p2 <<= 1;
+        ch = p2;
+        if (paged) ch = std::min<long long>(ch, (long long)kMfmaMaxChunkBlocksHost * BLOCK);
+    }
+    if (paged && ch % BLOCK) ch = (ch + BLOCK - 1) / BLOCK * BLOCK;
+    pl.chunk = (int)std::min<long long>(ch, 1 << 24);
+    pl.max_chunks = std::max(1, (std::max(cap, 0) + pl.chunk - 1) / pl.chunk);
+    pl.mode = paged ? kPagedUniform : kContiguous;
+    pl.chunk_blocks_ok = !paged || pl.chunk / BLOCK <= kMfmaMaxChunkBlocksHost;
+    size_workspace(pl, N, Hq, Hkv, D);
+    return pl;
+}
+
+Plan plan_batched(int N, int Hq, int Hkv, int D, int BLOCK, int cap, int dtype, int split, bool paged) {
     const int group = Hq / Hkv;
+    if (mfma_path(group, D, dtype, BLOCK, paged)) {
+        Plan pm = plan_batched_mfma(N, Hq, Hkv, D, BLOCK, cap, split, paged);
+        if (pm.chunk_blocks_ok) return pm;  // else the chunk is too long for the staged table
+    }
+    Plan pl;
     pl.G = choose_g(group, D);
     pl.nsub = group / pl.G;
     pl.chunk = split > 0 ? split : auto_split(N, Hq, Hkv, D, paged ? BLOCK : 0, cap, dtype);
@@ -184,6 +234,8 @@ int resolve_workspace(const Plan& pl, void* ws, size_t ws_bytes, DecodeParams& p
     p.epoch = next_epoch();
     const int t = tuning().fused_merge;
     p.merge_mode = t >= 0 ? t : (pl.max_chunks <= 8 ? kMergeAtomic : kMergeKernel);
+    // the matrix-core kernel's fused merge holds one chunk per lane
+    if (pl.mfma && pl.max_chunks > kMfmaMaxFusedChunks) p.merge_mode = kMergeKernel;
     return KVC_OK;
 }
 
@@ -229,6 +281,8 @@ int run_batched(const void* q, const void* k, const void* v, const int* table_al
     p.last_chunk_first = tuning().last_chunk_first;
     L.dtype = dtype; L.D = D; L.G = pl.G; L.mode = pl.mode; L.wpb = pl.wpb; L.batch = tuning().batch;
     L.need_merge = pl.max_chunks > 1;
+    L.mfma = pl.mfma;
+    L.wg_per_cu = std::max(tuning().wg_per_cu, 0);
     return launch_decode(L, st);
 }
 
@@ -241,13 +295,29 @@ int run_batched(const void* q, const void* k, const void* v, const int* table_al
 constexpr int kPlanInts = 8;
 
 struct PlanShape {
-    int G, nsub, hks, tpw, wpb, min_chunk, max_chunk;
-    bool uniform;
+    int G, nsub, hks, tpw, wpb, min_chunk, max_chunk, slots;
+    bool uniform, mfma;
 };
 
 PlanShape plan_shape(int Hq, int Hkv, int D, int BLOCK, int dtype) {
     PlanShape ps{};
     const int group = Hq / Hkv;
+    if (mfma_path(group, D, dtype, BLOCK, true)) {
+        // all heads of the group per unit; 8 waves; at least two 32-token tiles per
+        // wave; about two units resident per CU
+        ps.mfma = true;
+        ps.uniform = true;
+        ps.G = group;
+        ps.nsub = 1;
+        ps.hks = Hkv;
+        ps.tpw = 32;
+        const int t = tuning().waves_per_block;
+        ps.wpb = (t == 4 || t == 8) ? t : 8;
+        ps.min_chunk = ((ps.wpb * 64 + BLOCK - 1) / BLOCK) * BLOCK;
+        ps.max_chunk = kMfmaMaxChunkBlocksHost * BLOCK;
+        ps.slots = 256 * 2;
+        return ps;
+    }
     ps.G = choose_g(group, D);
     ps.nsub = group / ps.G;
     ps.hks = Hkv * ps.nsub;
@@ -258,6 +328,9 @@ PlanShape plan_shape(int Hq, int Hkv, int D, int BLOCK, int dtype) {
     // each wave should stream at least two batches of 4 wave-loads
     ps.min_chunk = ((ps.wpb * ps.tpw * 8 + BLOCK - 1) / BLOCK) * BLOCK;
     ps.max_chunk = ps.uniform ? 64 * BLOCK : std::max(BLOCK, 4095 * BLOCK);
+    // units to aim for per CU: ~3.5 for one or two heads per wave (about 1.3 rounds
+    // of the 4 units a CU runs at once), ~3 for larger groups
+    ps.slots = ps.G <= 2 ? 256 * 7 / 2 : 256 * 3;
     return ps;
 }
 
@@ -268,11 +341,7 @@ int make_plan(const int* lens, const int* tab_off, int N, int Hq, int Hkv, int D
     long long total = 0;
     for (int i = 0; i < N; ++i) total += std::max(lens[i], 1);
     total *= ps.hks;
-    if (target <= 0) {
-        // resident workgroups: ~7 per CU for one or two heads per wave, ~3 for larger groups
-        const long long slots = 256LL * (ps.G <= 2 ? 7 : 3);
-        target = (int)std::min<long long>((total + slots - 1) / slots, INT_MAX / 2);
-    }
+    if (target <= 0) target = (int)std::min<long long>((total + ps.slots - 1) / ps.slots, INT_MAX / 2);
     int T = std::max(target, ps.min_chunk);
     T = (T + BLOCK - 1) / BLOCK * BLOCK;
     T = std::min(T, ps.max_chunk);
@@ -289,11 +358,14 @@ int make_plan(const int* lens, const int* tab_off, int N, int Hq, int Hkv, int D
         if (L > ps.max_chunk || L > T + T / 2) {
             nc = std::max(2, (L + T / 2) / T);                      // nearest whole number of chunks
             nc = std::max(nc, (L + ps.max_chunk - 1) / ps.max_chunk);
+            if (ps.mfma) nc = std::min(nc, kMfmaMaxFusedChunks);  // the fused merge holds 64 chunks
             chunk = (L + nc - 1) / nc;
             chunk = (chunk + BLOCK - 1) / BLOCK * BLOCK;            // block-aligned chunk starts
             nc = (L + chunk - 1) / chunk;
         }
         if (nc > 0x7FFF) return set_error(KVC_ERR_UNSUPPORTED, "too many chunks per sequence for the plan encoding");
+        if (ps.mfma && (nc > kMfmaMaxFusedChunks || (chunk + BLOCK - 1) / BLOCK + 1 > kMfmaMaxChunkBlocksHost))
+            return set_error(KVC_ERR_UNSUPPORTED, "sequence too long for the grouped-query planned path");
         for (int h = 0; h < ps.hks; ++h) {
             const int r = nc > 1 ? rec : -1, k = nc > 1 ? ctr : -1;
             for (int c = 0; c < nc; ++c) {
@@ -303,7 +375,13 @@ int make_plan(const int* lens, const int* tab_off, int N, int Hq, int Hkv, int D
             if (nc > 1) { rec += nc; ++ctr; }
         }
     }
-    std::stable_sort(units.begin(), units.end(), [](const U& a, const U& b) { return a.len > b.len; });
+    // longest first; with split_first the chunks of split sequences go before every
+    // whole sequence, so their cross-chunk merges overlap later units' streaming
+    const bool split_first = tuning().split_first != 0;
+    std::stable_sort(units.begin(), units.end(), [&](const U& a, const U& b) {
+        if (split_first && (a.nc > 1) != (b.nc > 1)) return a.nc > 1;
+        return a.len > b.len;
+    });
     *n_units = (int)units.size();
     *n_records = rec;
     if (!work) return KVC_OK;  // size query
@@ -318,11 +396,10 @@ int make_plan(const int* lens, const int* tab_off, int N, int Hq, int Hkv, int D
     return KVC_OK;
 }
 
-size_t planned_workspace(int Hq, int Hkv, int D, int n_records) {
+size_t planned_workspace(int Hq, int Hkv, int D, int BLOCK, int dtype, int n_records) {
     if (n_records <= 0) return 0;
     Plan pl;
-    const int group = Hq / Hkv;
-    pl.G = choose_g(group, D);
+    pl.G = plan_shape(Hq, Hkv, D, BLOCK, dtype).G;
     const size_t recs = (size_t)n_records * pl.G;
     pl.acc_bytes = align_up(recs * D * sizeof(float), kAlign);
     pl.ml_bytes = align_up(recs * 2 * sizeof(float), kAlign);
@@ -577,9 +654,9 @@ int kvc_decode_plan(const int* host_lens, const int* host_tab_off, int N, int Hq
     });
 }
 
-size_t kvc_decode_planned_workspace_size(int Hq, int Hkv, int D, int n_records) {
+size_t kvc_decode_planned_workspace_size(int Hq, int Hkv, int D, int BLOCK, int dtype, int n_records) {
     if (Hq <= 0 || Hkv <= 0 || Hq % Hkv || !d_ok(D) || n_records < 0) return 0;
-    return planned_workspace(Hq, Hkv, D, n_records);
+    return planned_workspace(Hq, Hkv, D, BLOCK, dtype, n_records);
 }
 
 int kvc_batched_paged_decode_planned(const void* q, const void* k_pool, const void* v_pool, const int* table_all,
@@ -602,9 +679,10 @@ int kvc_batched_paged_decode_planned(const void* q, const void* k_pool, const vo
         p.chunk_tokens = 1; p.max_chunks = 1; p.cap = INT_MAX;
         p.scale_log2 = scale * 1.4426950408889634f;
         p.work = work;
+        p.n_records = n_records;
         p.lpb_shift = ps.uniform ? ilog2_exact(BLOCK / ps.tpw) : 0;
         if (n_records > 0) {
-            const size_t need = planned_workspace(Hq, Hkv, D, n_records);
+            const size_t need = planned_workspace(Hq, Hkv, D, BLOCK, dtype, n_records);
             if (!ws) {
                 rc = default_workspace(need, &ws);
                 if (rc) return rc;
@@ -624,6 +702,9 @@ int kvc_batched_paged_decode_planned(const void* q, const void* k_pool, const vo
         p.merge_mode = tuning().fused_merge == kMergeFence ? kMergeFence : kMergeAtomic;  // planned: always fused
         // the grid is the unit list; chunk_range is not used on this path
         L.dtype = dtype; L.D = D; L.G = ps.G; L.mode = ps.uniform ? kPlannedUniform : kPlannedPerLane;
+        L.mfma = ps.mfma;
+        // a cap on co-resident units lets the longest-first order work as a queue
+        L.wg_per_cu = tuning().wg_per_cu >= 0 ? tuning().wg_per_cu : (!ps.mfma && ps.G <= 2 ? 4 : 0);
         L.wpb = tuning().waves_per_block ? tuning().waves_per_block : ps.wpb;
         L.batch = tuning().batch;
         L.need_merge = false;
@@ -659,6 +740,9 @@ int kvc_set_tuning(const char* key, int value) {
     else if (k == "waves_per_block" && (value == 0 || value == 4 || value == 8)) tuning().waves_per_block = value;
     else if (k == "batch" && (value == 2 || value == 4 || value == 8)) tuning().batch = value;
     else if (k == "last_chunk_first" && (value == 0 || value == 1)) tuning().last_chunk_first = value;
+    else if (k == "mfma" && value >= -1 && value <= 1) tuning().mfma = value;
+    else if (k == "wg_per_cu" && value >= -1 && value <= 32) tuning().wg_per_cu = value;
+    else if (k == "split_first" && (value == 0 || value == 1)) tuning().split_first = value;
     else return set_error(KVC_ERR_ARG, "unknown tuning key or bad value: " + k);
     return KVC_OK;
 }
@@ -672,6 +756,9 @@ int kvc_get_tuning(const char* key, int* value) {
     else if (k == "waves_per_block") *value = tuning().waves_per_block;
     else if (k == "batch") *value = tuning().batch;
     else if (k == "last_chunk_first") *value = tuning().last_chunk_first;
+    else if (k == "mfma") *value = tuning().mfma;
+    else if (k == "wg_per_cu") *value = tuning().wg_per_cu;
+    else if (k == "split_first") *value = tuning().split_first;
     else return set_error(KVC_ERR_ARG, "unknown tuning key: " + k);
     return KVC_OK;
 }

@@ -34,6 +34,9 @@
 #include "kvc_abi.h"
 
 #include <cfloat>
+#include <mutex>
+#include <type_traits>
+#include <unordered_map>
 #include <climits>
 
 namespace kvc {
@@ -143,32 +146,90 @@ __device__ __forceinline__ bool chunk_range(const DecodeParams& p, int s, int c,
 // Log-sum-exp merge of the nc chunk partials of one query head: chunk c's
 // record is rec0 + c*cstride (acc at record*D, (m, l) at record*2):
 //   M = max_c m_c,  out = sum_c 2^(m_c-M) acc_c / sum_c 2^(m_c-M) l_c.
-// One wave; lane d owns output dims d, d+64, ...  COHERENT reads the partials
-// with agent-scope atomic loads (partials written by other XCDs bypass stale
-// L2 lines); otherwise plain loads after an acquire fence.
+// One wave.  The chunk statistics (one chunk per lane) and the accumulators of
+// the first eight chunks are read in one round of independent loads; the
+// statistics are reduced across the wave, and lane d accumulates output dims d,
+// d+64, ... with each chunk's weight taken from the lane that holds it (further
+// chunks eight at a time).  COHERENT reads the
+// partials with agent-scope atomic loads (partials written by other XCDs bypass
+// stale L2 lines); otherwise plain loads after an acquire fence.
 template <typename T, int D, bool COHERENT>
 __device__ __forceinline__ void merge_head(const DecodeParams& p, size_t rec0, size_t cstride, int nc, T* ob,
                                            int lane) {
     constexpr int DPL = (D + kWave - 1) / kWave;
+    constexpr int E = 8;  // chunk partials in flight per lane
     auto ld = [](const float* a) {
         if constexpr (COHERENT) return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         else return *a;
     };
-    float M = -FLT_MAX;
-    for (int c = 0; c < nc; ++c) M = fmaxf(M, ld(p.part_ml + (rec0 + (size_t)c * cstride) * 2));
+    auto rec_of = [&](int c) { return rec0 + (size_t)c * cstride; };
+    // statistics of up to 64 chunks and the accumulators of the first E chunks in
+    // one round of independent loads
+    const bool in0 = lane < nc;
+    const size_t r0 = rec_of(in0 ? lane : 0);
+    const float m0 = in0 ? ld(p.part_ml + r0 * 2) : -FLT_MAX;
+    const float l0 = in0 ? ld(p.part_ml + r0 * 2 + 1) : 0.f;
+    float a0[E][DPL];
+#pragma unroll
+    for (int u = 0; u < E; ++u)
+#pragma unroll
+        for (int j = 0; j < DPL; ++j)
+            a0[u][j] = u < nc ? ld(p.part_acc + rec_of(u) * D + min(lane + j * kWave, D - 1)) : 0.f;
+    float M = m0;
+    for (int c0 = kWave; c0 < nc; c0 += kWave) {
+        const int c = c0 + lane;
+        M = fmaxf(M, c < nc ? ld(p.part_ml + rec_of(c) * 2) : -FLT_MAX);
+    }
+#pragma unroll
+    for (int o = kWave / 2; o >= 1; o >>= 1) M = fmaxf(M, shfl_xor(M, o));
     float l = 0.f, acc[DPL];
 #pragma unroll
     for (int j = 0; j < DPL; ++j) acc[j] = 0.f;
-    for (int c = 0; c < nc; ++c) {
-        const size_t rec = rec0 + (size_t)c * cstride;
-        const float w = fast_exp2(ld(p.part_ml + rec * 2) - M);
-        l = __builtin_fmaf(w, ld(p.part_ml + rec * 2 + 1), l);
+    for (int c0 = 0; c0 < nc; c0 += kWave) {
+        const int c = c0 + lane;
+        const bool in = c < nc;
+        float w;
+        if (c0 == 0) {
+            w = in ? fast_exp2(m0 - M) : 0.f;
+            l += in ? w * l0 : 0.f;
+        } else {
+            const size_t rc = rec_of(in ? c : c0);
+            w = in ? fast_exp2(ld(p.part_ml + rc * 2) - M) : 0.f;
+            l += in ? w * ld(p.part_ml + rc * 2 + 1) : 0.f;
+        }
+        const int cn = min(kWave, nc - c0);
+        int e = 0;
+        if (c0 == 0) {
 #pragma unroll
-        for (int j = 0; j < DPL; ++j) {
-            const int d = lane + j * kWave;
-            if (d < D) acc[j] = __builtin_fmaf(w, ld(p.part_acc + rec * D + d), acc[j]);
+            for (int u = 0; u < E; ++u) {
+                const float we = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), u));
+#pragma unroll
+                for (int j = 0; j < DPL; ++j) acc[j] = __builtin_fmaf(we, a0[u][j], acc[j]);  // 0 past nc
+            }
+            e = E;
+        }
+        for (; e + E <= cn; e += E) {
+            float a[E][DPL], we[E];
+#pragma unroll
+            for (int u = 0; u < E; ++u) {
+                we[u] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), e + u));
+#pragma unroll
+                for (int j = 0; j < DPL; ++j) a[u][j] = ld(p.part_acc + rec_of(c0 + e + u) * D + min(lane + j * kWave, D - 1));
+            }
+#pragma unroll
+            for (int u = 0; u < E; ++u)
+#pragma unroll
+                for (int j = 0; j < DPL; ++j) acc[j] = __builtin_fmaf(we[u], a[u][j], acc[j]);
+        }
+        for (; e < cn; ++e) {
+            const float we = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), e));
+#pragma unroll
+            for (int j = 0; j < DPL; ++j)
+                acc[j] = __builtin_fmaf(we, ld(p.part_acc + rec_of(c0 + e) * D + min(lane + j * kWave, D - 1)), acc[j]);
         }
     }
+#pragma unroll
+    for (int o = kWave / 2; o >= 1; o >>= 1) l += shfl_xor(l, o);
     const float inv = l > 0.f ? 1.0f / l : 0.f;
 #pragma unroll
     for (int j = 0; j < DPL; ++j) {
@@ -181,14 +242,18 @@ __device__ __forceinline__ void merge_head(const DecodeParams& p, size_t rec0, s
 // 64-bit counter tagged with the call's epoch in the high word: a counter from
 // another call (or never initialised) counts as zero, and the last arriver
 // resets it to zero, so neither fresh nor replayed workspaces need clearing.
+// Only the first arrivals of a call see a stale tag and swap in (epoch, 1) with a
+// compare-and-swap; once the tag is current every arrival is one fetch-and-add,
+// so many chunks finishing together do not retry against each other.
 __device__ __forceinline__ unsigned arrive(unsigned long long* ctr, unsigned epoch) {
+    const unsigned long long tag = (unsigned long long)epoch << 32;
     unsigned long long old = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     for (;;) {
-        const unsigned base = (unsigned)(old >> 32) == epoch ? (unsigned)old : 0u;
-        const unsigned long long next = ((unsigned long long)epoch << 32) | (unsigned long long)(base + 1u);
-        if (__hip_atomic_compare_exchange_strong(ctr, &old, next, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+        if ((old >> 32) == epoch)
+            return (unsigned)__hip_atomic_fetch_add(ctr, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (__hip_atomic_compare_exchange_strong(ctr, &old, tag | 1ull, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_AGENT))
-            return base;
+            return 0u;
     }
 }
 
@@ -207,6 +272,48 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base, in
 }
 __device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, int voffset) {
     return __builtin_amdgcn_raw_buffer_load_b128(r, voffset, 0, 0);
+}
+
+// The unit of a workgroup: from the planned work list or from the
+// (chunk, sequence, KV head, subgroup) decomposition of the grid.
+struct Unit {
+    int s, hk, sub, c, nc, j0, j1, tab_start;
+    size_t rec0, cstride, ctr_idx;
+};
+
+template <bool PLANNED>
+__device__ __forceinline__ bool load_unit(const DecodeParams& p, int heads, Unit& u) {
+    if constexpr (PLANNED) {
+        const int* w = p.work + (size_t)blockIdx.x * 8;
+        u.s = w[0];
+        const int hks = w[1] & 0xFFFF;
+        u.c = w[1] >> 16;
+        u.hk = hks / p.nsub;
+        u.sub = hks % p.nsub;
+        u.j0 = max(w[2], 0);
+        u.j1 = max(w[3], u.j0);
+        u.nc = max(w[4], 1);
+        u.rec0 = ((size_t)(w[5] > 0 ? w[5] : 0) + (size_t)u.c) * heads;
+        u.cstride = heads;
+        u.ctr_idx = w[6] > 0 ? w[6] : 0;
+        u.tab_start = w[7];
+        // a unit outside the launch's shape (a stale or foreign plan) is skipped
+        if (u.s < 0 || u.s >= p.N || u.hk < 0 || u.hk >= p.Hkv || u.c < 0 || u.c >= u.nc) return false;
+        return u.nc == 1 || (w[5] >= 0 && (long long)w[5] + u.nc <= p.n_records && w[6] >= 0 && w[6] < p.n_records);
+    } else {
+        int unit = blockIdx.x;
+        u.sub = unit % p.nsub;  unit /= p.nsub;
+        u.hk = unit % p.Hkv;    unit /= p.Hkv;
+        u.s = unit % p.N;
+        u.c = p.last_chunk_first ? p.max_chunks - 1 - unit / p.N : unit / p.N;
+        u.tab_start = 0;
+        if (u.c >= p.max_chunks) return false;
+        if (!chunk_range(p, u.s, u.c, u.nc, u.j0, u.j1)) return false;
+        u.rec0 = ((size_t)u.s * p.max_chunks + u.c) * p.Hq + u.hk * p.group + u.sub * heads;
+        u.cstride = p.Hq;
+        u.ctr_idx = ((size_t)u.s * p.Hkv + u.hk) * p.nsub + u.sub;
+        return true;
+    }
 }
 
 // Largest chunk, in blocks, the per-lane paged path stages in LDS.
@@ -243,38 +350,11 @@ __global__ __launch_bounds__(WPB * kWave) void split_kernel(DecodeParams p) {
     const int tslot = lane / LPT;
     const int dl = lane % LPT;
 
-    int s, hk, sub, c, nc, j0, j1;
-    size_t rec0, cstride, ctr_idx;  // partial record of (this chunk, head 0); stride between chunks; counter
-    int tab_start = 0;  // planned: index into table_all of the chunk's first block
-    if constexpr (PLANNED) {
-        // planned unit {s, hks | c << 16, j0, j1, nc, record group, counter, table start}
-        const int* w = p.work + (size_t)blockIdx.x * 8;
-        s = w[0];
-        const int hks = w[1] & 0xFFFF;
-        c = w[1] >> 16;
-        hk = hks / p.nsub;
-        sub = hks % p.nsub;
-        j0 = max(w[2], 0);
-        j1 = max(w[3], j0);
-        nc = max(w[4], 1);
-        rec0 = (size_t)(w[5] > 0 ? w[5] : 0) * G + (size_t)c * G;
-        cstride = G;
-        ctr_idx = w[6] > 0 ? w[6] : 0;
-        tab_start = w[7];
-    } else {
-        int unit = blockIdx.x;
-        sub = unit % p.nsub;  unit /= p.nsub;
-        hk = unit % p.Hkv;    unit /= p.Hkv;
-        s = unit % p.N;
-        // chunk index is the slowest-varying; with last_chunk_first the later chunks
-        // (which only long sequences have, and which are full-size) dispatch first
-        c = p.last_chunk_first ? p.max_chunks - 1 - unit / p.N : unit / p.N;
-        if (c >= p.max_chunks) return;
-        if (!chunk_range(p, s, c, nc, j0, j1)) return;
-        rec0 = ((size_t)s * p.max_chunks + c) * p.Hq + hk * p.group + sub * G;
-        cstride = p.Hq;
-        ctr_idx = ((size_t)s * p.Hkv + hk) * p.nsub + sub;
-    }
+    Unit u;
+    if (!load_unit<PLANNED>(p, G, u)) return;
+    const int s = u.s, hk = u.hk, sub = u.sub, c = u.c, nc = u.nc, j0 = u.j0, j1 = u.j1;
+    const int tab_start = u.tab_start;
+    const size_t rec0 = u.rec0, cstride = u.cstride, ctr_idx = u.ctr_idx;
     const int hq0 = hk * p.group + sub * G;
     const int nwl = (j1 - j0 + TPW - 1) / TPW;                          // wave-loads in the chunk
     const int kmax = wave < nwl ? (nwl - wave + WPB - 1) / WPB : 0;     // this wave's share
@@ -563,15 +643,42 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(DecodeParams p) {
     }
 }
 
+#include "gqa_mfma.hpp"
+
+// Dynamic LDS that caps workgroups per CU (tuning "wg_per_cu"), from the
+// kernel's static LDS (queried once per kernel).
+inline unsigned lds_pad_for(const void* kernel, int wg_per_cu) {
+    static std::mutex mu;
+    static std::unordered_map<const void*, size_t> static_lds;
+    size_t st = 0;
+    {
+        std::lock_guard<std::mutex> lk(mu);
+        auto it = static_lds.find(kernel);
+        if (it == static_lds.end()) {
+            hipFuncAttributes a{};
+            st = hipFuncGetAttributes(&a, kernel) == hipSuccess ? a.sharedSizeBytes : 0;
+            static_lds.emplace(kernel, st);
+        } else {
+            st = it->second;
+        }
+    }
+    return (unsigned)occupancy_lds(st, wg_per_cu);
+}
+
+template <typename K>
+unsigned lds_pad(K kernel, int wg_per_cu) {
+    return wg_per_cu > 0 ? lds_pad_for(reinterpret_cast<const void*>(kernel), wg_per_cu) : 0u;
+}
+
 template <typename T, int D, int G, int WPB, int U>
-int launch_split_mode(const DecodeLaunch& L, dim3 grid, hipStream_t st) {
+int launch_split_mode(DecodeLaunch L, dim3 grid, hipStream_t st) {
     const dim3 block(WPB * kWave);
     switch (L.mode) {
-        case kContiguous:   hipLaunchKernelGGL((split_kernel<T, D, G, kContiguous, WPB, U>), grid, block, 0, st, L.p); break;
-        case kPagedUniform: hipLaunchKernelGGL((split_kernel<T, D, G, kPagedUniform, WPB, U>), grid, block, 0, st, L.p); break;
-        case kPagedPerLane: hipLaunchKernelGGL((split_kernel<T, D, G, kPagedPerLane, WPB, U>), grid, block, 0, st, L.p); break;
-        case kPlannedUniform: hipLaunchKernelGGL((split_kernel<T, D, G, kPlannedUniform, WPB, U>), grid, block, 0, st, L.p); break;
-        case kPlannedPerLane: hipLaunchKernelGGL((split_kernel<T, D, G, kPlannedPerLane, WPB, U>), grid, block, 0, st, L.p); break;
+        case kContiguous:   L.lds_pad = lds_pad(split_kernel<T, D, G, kContiguous, WPB, U>, L.wg_per_cu); hipLaunchKernelGGL((split_kernel<T, D, G, kContiguous, WPB, U>), grid, block, L.lds_pad, st, L.p); break;
+        case kPagedUniform: L.lds_pad = lds_pad(split_kernel<T, D, G, kPagedUniform, WPB, U>, L.wg_per_cu); hipLaunchKernelGGL((split_kernel<T, D, G, kPagedUniform, WPB, U>), grid, block, L.lds_pad, st, L.p); break;
+        case kPagedPerLane: L.lds_pad = lds_pad(split_kernel<T, D, G, kPagedPerLane, WPB, U>, L.wg_per_cu); hipLaunchKernelGGL((split_kernel<T, D, G, kPagedPerLane, WPB, U>), grid, block, L.lds_pad, st, L.p); break;
+        case kPlannedUniform: L.lds_pad = lds_pad(split_kernel<T, D, G, kPlannedUniform, WPB, U>, L.wg_per_cu); hipLaunchKernelGGL((split_kernel<T, D, G, kPlannedUniform, WPB, U>), grid, block, L.lds_pad, st, L.p); break;
+        case kPlannedPerLane: L.lds_pad = lds_pad(split_kernel<T, D, G, kPlannedPerLane, WPB, U>, L.wg_per_cu); hipLaunchKernelGGL((split_kernel<T, D, G, kPlannedPerLane, WPB, U>), grid, block, L.lds_pad, st, L.p); break;
         default: return set_error(KVC_ERR_ARG, "unknown decode mode");
     }
     return KVC_OK;
@@ -616,6 +723,30 @@ int launch_split_g(const DecodeLaunch& L, dim3 grid, hipStream_t st) {
     return set_error(KVC_ERR_UNSUPPORTED, "query heads per unit not instantiated");
 }
 
+template <int D, int WPB>
+int launch_gqa_mode(DecodeLaunch L, dim3 grid, hipStream_t st) {
+    const dim3 block(WPB * kWave);
+    switch (L.mode) {
+        case kContiguous:     L.lds_pad = lds_pad(gqa_mfma_kernel<D, kContiguous, WPB>, L.wg_per_cu); hipLaunchKernelGGL((gqa_mfma_kernel<D, kContiguous, WPB>), grid, block, L.lds_pad, st, L.p); break;
+        case kPagedUniform:   L.lds_pad = lds_pad(gqa_mfma_kernel<D, kPagedUniform, WPB>, L.wg_per_cu); hipLaunchKernelGGL((gqa_mfma_kernel<D, kPagedUniform, WPB>), grid, block, L.lds_pad, st, L.p); break;
+        case kPlannedUniform: L.lds_pad = lds_pad(gqa_mfma_kernel<D, kPlannedUniform, WPB>, L.wg_per_cu); hipLaunchKernelGGL((gqa_mfma_kernel<D, kPlannedUniform, WPB>), grid, block, L.lds_pad, st, L.p); break;
+        default: return set_error(KVC_ERR_ARG, "matrix-core decode: unsupported addressing mode");
+    }
+    return KVC_OK;
+}
+
+template <typename T, int D>
+int launch_gqa(const DecodeLaunch& L, dim3 grid, hipStream_t st) {
+    if constexpr (std::is_same<T, _Float16>::value && (D == 64 || D == 128)) {
+        if (L.p.group > kMfmaMaxHeads || L.p.nsub != 1) return set_error(KVC_ERR_ARG, "matrix-core decode: bad group");
+        if (L.wpb == 8) return launch_gqa_mode<D, 8>(L, grid, st);
+        if (L.wpb == 4) return launch_gqa_mode<D, 4>(L, grid, st);
+        return set_error(KVC_ERR_ARG, "waves per block must be 4 or 8");
+    } else {
+        return set_error(KVC_ERR_UNSUPPORTED, "matrix-core decode needs fp16 and head_dim 64 or 128");
+    }
+}
+
 }  // namespace
 
 template <typename T, int D>
@@ -624,7 +755,7 @@ int launch_decode_d(const DecodeLaunch& L, hipStream_t st) {
     const long long units = planned ? (long long)L.units : (long long)L.p.max_chunks * L.p.N * L.p.Hkv * L.p.nsub;
     if (units <= 0) return KVC_OK;
     if (units > (long long)INT_MAX) return set_error(KVC_ERR_ARG, "decode grid too large");
-    int rc = launch_split_g<T, D>(L, dim3((unsigned)units), st);
+    int rc = L.mfma ? launch_gqa<T, D>(L, dim3((unsigned)units), st) : launch_split_g<T, D>(L, dim3((unsigned)units), st);
     if (rc != KVC_OK) return rc;
     rc = hip_check(hipGetLastError(), "decode split launch");
     if (rc != KVC_OK || !L.need_merge || L.p.merge_mode != kMergeKernel) return rc;

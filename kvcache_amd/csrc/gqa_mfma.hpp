@@ -1,0 +1,332 @@
+// gqa_mfma.hpp -- grouped-query decode on the matrix cores (fp16 K/V, head_dim 64/128).
+//
+// Included by decode_kernels.hpp inside namespace kvc::{anonymous}; uses its helpers.
+//
+// When one KV head serves a group of g > 2 query heads, the per-head VALU dot
+// products of split_kernel cost ~g times more instructions per K/V byte and the
+// kernel stops being bandwidth-bound.  Here one wave computes all heads of the
+// group at once with v_mfma_f32_16x16x32_f16 (heads padded to 16):
+//
+//   QK^T : S[16 tok][16 heads] = K[16 tok][32 dims] x Q^T[32 dims][16 heads],
+//          D/32 MFMAs per 16-token subtile.  The A operand is the K rows exactly as
+//          loaded (lane l: row l%16, 16 contiguous bytes at dim 8*(l/16) + 32j);
+//          the B operand is q in the same lane layout (loaded once per unit).
+//   softmax: the result layout gives lane l the scores of head l%16 for tokens
+//          4*(l/16)+r (r = 0..3) of each subtile, i.e. 8 scores per lane for a
+//          32-token tile; the tile max per head needs two lane exchanges (xor 16,
+//          xor 32); online (max, sum) per head in log2 units.
+//   PV   : O[16 heads][16 dims] += P[16 heads][32 tok] x V[32 tok][16 dims] per
+//          16-dim column tile.  The A operand is the lane's own 8 probabilities
+//          (token order tau(g, i) = 4g+i for i < 4, 16+4g+i-4 otherwise); the B
+//          operand needs V transposed (8 tokens of one dim per lane), so each
+//          wave stages its 32-token V tile in LDS, row-major with the dword column
+//          XOR-swizzled by ((row >> 2) & 3) << 3, and reads it back with 16-bit
+//          loads: the four lane groups then hit disjoint banks.
+//
+// Unit decomposition, partial records, arrival counters and merge modes are those
+// of split_kernel (one unit = sequence x KV head x chunk, all query heads of the
+// group).  The chunk's block ids are staged in LDS, so chunks may span up to
+// kMfmaMaxChunkBlocks blocks; BLOCK must be a multiple of 16 (each 16-token
+// subtile lies inside one block and is read through one buffer descriptor whose
+// size admits only the valid rows).  The fused cross-chunk merge runs on every
+// thread of the last-arriving workgroup (weights per chunk in LDS, then each
+// thread accumulates one (head, dim) over the chunks with independent loads).
+
+constexpr int kMfmaTile = 32;             // tokens per wave tile (two 16-row subtiles)
+constexpr int kMfmaMaxChunkBlocks = 1024; // block ids staged per unit
+constexpr int kMfmaMaxHeads = 16;         // query heads per KV head on this path
+constexpr int kMaxFusedChunks = 64;       // chunks the fused merge combines (one per lane)
+
+typedef _Float16 f16x8v __attribute__((ext_vector_type(8)));
+
+template <int D, int MODE, int WPB>
+__global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(DecodeParams p) {
+    static_assert(D == 64 || D == 128, "MFMA decode is built for head_dim 64 and 128");
+    constexpr int ROW = D * 2;                 // bytes per fp16 K/V row
+    constexpr int KJ = D / 32;                 // MFMA k-steps over the head dimension
+    constexpr int NT = D / 16;                 // 16-dim output column tiles
+    constexpr int VL = 16 * ROW / 1024;        // 1 KiB wave loads per 16-row V subtile
+    constexpr bool PLANNED = MODE == kPlannedUniform;
+    constexpr bool PAGED = MODE != kContiguous;
+    constexpr int kTileBytes = kMfmaTile * ROW;
+    constexpr int kMainBytes = WPB * kTileBytes;
+    constexpr int kEpiBytes = WPB * kMfmaMaxHeads * (D + 2) * 4;
+    __shared__ __attribute__((aligned(16))) char s_buf[kMainBytes > kEpiBytes ? kMainBytes : kEpiBytes];
+    __shared__ int s_tab[PAGED ? kMfmaMaxChunkBlocks : 1];
+    __shared__ float s_w[kMfmaMaxHeads][kMaxFusedChunks];
+    __shared__ float s_L[kMfmaMaxHeads];
+    __shared__ int s_last;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = uniform(tid >> 6);
+    const int n16 = lane & 15;   // head (S layout) / output column within a tile
+    const int g4 = lane >> 4;    // lane group
+    const int heads = p.group;   // query heads of the KV group, <= 16 (host-checked)
+
+    Unit u;
+    if (!load_unit<PLANNED>(p, heads, u)) return;
+    const int s = u.s, hk = u.hk, j0 = u.j0, j1 = u.j1, nc = u.nc;
+    const int hq0 = hk * p.group;
+    const int ntiles = (j1 - j0 + kMfmaTile - 1) / kMfmaTile;
+    const int kmax = wave < ntiles ? (ntiles - wave + WPB - 1) / WPB : 0;
+
+    // q as the B operand of QK^T: lane l holds head l%16, dims 8*(l/16) + 32j .. +7;
+    // heads past the group read as zero through the descriptor bound.
+    f16x8v qb[KJ];
+    {
+        const char* qbase = static_cast<const char*>(p.q) + ((size_t)s * p.Hq + hq0) * ROW;
+        const __amdgpu_buffer_rsrc_t qr = tile_rsrc(qbase, heads * ROW);
+#pragma unroll
+        for (int j = 0; j < KJ; ++j)
+            qb[j] = __builtin_bit_cast(f16x8v, buffer_load16(qr, n16 * ROW + g4 * 16 + j * 64));
+    }
+
+    const char* kb = static_cast<const char*>(p.k);
+    const char* vb = static_cast<const char*>(p.v);
+    size_t cbase = 0;
+    const int b0 = PAGED ? j0 / p.block : 0;
+    int nblk = 0;
+    if constexpr (MODE == kContiguous) {
+        cbase = ((size_t)s * p.seq_stride + (size_t)hk * p.head_stride) * 2;
+    } else {
+        nblk = min(j1 > j0 ? (j1 - 1) / p.block - b0 + 1 : 0, kMfmaMaxChunkBlocks);
+        const int first = PLANNED ? u.tab_start : (p.tab_off ? p.tab_off[s] : 0) + b0;
+        const __amdgpu_buffer_rsrc_t trs =
+            PLANNED ? tile_rsrc(p.table_all, p.table_len * 4) : tile_rsrc(p.table_all + first, nblk * 4);
+        const int tb = PLANNED ? first * 4 : 0;
+        for (int b = tid; b < nblk; b += WPB * kWave)
+            s_tab[b] = (int)__builtin_amdgcn_raw_buffer_load_b32(trs, tb + b * 4, 0, 0);
+        __syncthreads();
+    }
+
+    struct Tile {
+        u32x4 k[2][KJ];
+        u32x4 v[2][VL];
+    };
+    // Byte offset of the 16-row subtile starting at token t (inside one block).
+    auto subtile = [&](int t) -> size_t {
+        if constexpr (MODE == kContiguous) {
+            return cbase + (size_t)t * ROW;
+        } else {
+            const int rel = min(max(t / p.block - b0, 0), max(nblk - 1, 0));
+            const int phys = uniform(s_tab[rel]);
+            return ((size_t)(phys * p.Hkv + hk) * p.block + (t % p.block)) * ROW;
+        }
+    };
+    auto issue = [&](int k, Tile& T) {
+        const int t0 = j0 + (wave + WPB * k) * kMfmaTile;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int t = t0 + 16 * h;
+            // valid rows, never past the end of the block holding the subtile
+            int rows = min(max(j1 - t, 0), 16);
+            if constexpr (PAGED) rows = min(rows, p.block - t % p.block);
+            rows = uniform(rows);
+            const size_t off = rows > 0 ? subtile(t) : 0;
+            const __amdgpu_buffer_rsrc_t kr = tile_rsrc(kb + off, rows * ROW);
+            const __amdgpu_buffer_rsrc_t vr = tile_rsrc(vb + off, rows * ROW);
+#pragma unroll
+            for (int j = 0; j < KJ; ++j) T.k[h][j] = buffer_load16(kr, n16 * ROW + g4 * 16 + j * 64);
+#pragma unroll
+            for (int q = 0; q < VL; ++q) T.v[h][q] = buffer_load16(vr, q * 1024 + lane * 16);
+        }
+    };
+
+    char* vt = s_buf + wave * kTileBytes;   // this wave's V tile
+    float m = -FLT_MAX, l = 0.f;            // per head n16 (identical in the four lane groups)
+    f32x4 O[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) O[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    auto consume = [&](int k, const Tile& T) {
+        const int t0 = j0 + (wave + WPB * k) * kMfmaTile;
+        // V rows -> LDS, dword column swizzled by ((row >> 2) & 3) << 3
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int q = 0; q < VL; ++q) {
+                const int off = q * 1024 + lane * 16;
+                const int r = 16 * h + off / ROW;
+                const int dw = ((off % ROW) >> 2) ^ (((r >> 2) & 3) << 3);
+                *reinterpret_cast<u32x4*>(vt + r * ROW + dw * 4) = T.v[h][q];
+            }
+        // scores of the 32 tokens for all heads
+        f32x4 S[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < KJ; ++j)
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8v, T.k[h][j]), qb[j], acc, 0, 0, 0);
+            S[h] = acc;
+        }
+        float sc[8];
+        bool ok[8];
+        float mx = -FLT_MAX;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int h = i >> 2, r = i & 3;
+            ok[i] = t0 + 16 * h + 4 * g4 + r < j1;
+            sc[i] = S[h][r] * p.scale_log2;
+            mx = ok[i] ? fmaxf(mx, sc[i]) : mx;
+        }
+        mx = fmaxf(mx, shfl_xor(mx, 16));
+        mx = fmaxf(mx, shfl_xor(mx, 32));
+        const float mn = fmaxf(m, mx);
+        const float corr = fast_exp2(m - mn);
+        float ps = 0.f;
+        f16x8v pa;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float pi = ok[i] ? fast_exp2(sc[i] - mn) : 0.f;
+            ps += pi;
+            pa[i] = (_Float16)pi;
+        }
+        l = __builtin_fmaf(l, corr, ps);
+        m = mn;
+        // rescale O: row 4*g4 + r of the output tile belongs to head 4*g4 + r,
+        // whose factor is held by lane 4*g4 + r
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float cr = __int_as_float(__builtin_amdgcn_ds_bpermute((4 * g4 + r) << 2, __float_as_int(corr)));
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) O[nt][r] *= cr;
+        }
+        __builtin_amdgcn_wave_barrier();
+        asm volatile("" ::: "memory");
+        // V^T operand: 8 tokens tau(g4, i) of dim n16 + 16 nt
+        const _Float16* vh = reinterpret_cast<const _Float16*>(vt);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            f16x8v vbv;
+            const int dw = ((n16 + 16 * nt) >> 1) ^ (g4 << 3);
+            const int col = dw * 2 + (n16 & 1);   // in halfs
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int r = (i < 4) ? 4 * g4 + i : 16 + 4 * g4 + (i - 4);
+                vbv[i] = vh[r * D + col];
+            }
+            O[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vbv, O[nt], 0, 0, 0);
+        }
+        __builtin_amdgcn_wave_barrier();
+        asm volatile("" ::: "memory");
+    };
+
+    if (kmax > 0) {
+        Tile A, B;
+        issue(0, A);
+        for (int k = 0;; k += 2) {
+            issue(k + 1, B);
+            consume(k, A);
+            if (k + 1 >= kmax) break;
+            issue(k + 2, A);
+            consume(k + 1, B);
+            if (k + 2 >= kmax) break;
+        }
+    }
+    l += shfl_xor(l, 16);
+    l += shfl_xor(l, 32);
+
+    // Combine the waves: per-wave (m, l) per head and O through LDS.
+    __syncthreads();  // every wave is done with its V tile
+    float* e_acc = reinterpret_cast<float*>(s_buf);                    // [WPB][16][D]
+    float* e_ml = e_acc + WPB * kMfmaMaxHeads * D;                      // [WPB][16][2]
+    if (lane < 16) {
+        e_ml[(wave * kMfmaMaxHeads + lane) * 2] = m;
+        e_ml[(wave * kMfmaMaxHeads + lane) * 2 + 1] = l;
+    }
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) e_acc[(wave * kMfmaMaxHeads + 4 * g4 + r) * D + n16 + 16 * nt] = O[nt][r];
+    __syncthreads();
+
+    _Float16* ob = static_cast<_Float16*>(p.out) + ((size_t)s * p.Hq + hq0) * D;
+    const bool atomic_parts = p.merge_mode == kMergeAtomic;
+    for (int idx = tid; idx < heads * D; idx += WPB * kWave) {
+        const int g = idx / D, d = idx % D;
+        float M = -FLT_MAX;
+#pragma unroll
+        for (int w = 0; w < WPB; ++w) M = fmaxf(M, e_ml[(w * kMfmaMaxHeads + g) * 2]);
+        float lt = 0.f, at = 0.f;
+#pragma unroll
+        for (int w = 0; w < WPB; ++w) {
+            const float wt = fast_exp2(e_ml[(w * kMfmaMaxHeads + g) * 2] - M);
+            lt = __builtin_fmaf(wt, e_ml[(w * kMfmaMaxHeads + g) * 2 + 1], lt);
+            at = __builtin_fmaf(wt, e_acc[(w * kMfmaMaxHeads + g) * D + d], at);
+        }
+        if (nc == 1) {
+            ob[(size_t)g * D + d] = (_Float16)(lt > 0.f ? at * (1.0f / lt) : 0.f);
+        } else {
+            const size_t rec = u.rec0 + g;
+            if (atomic_parts) {
+                __hip_atomic_store(p.part_acc + rec * D + d, at, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (d == 0) {
+                    __hip_atomic_store(p.part_ml + rec * 2, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(p.part_ml + rec * 2 + 1, lt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            } else {
+                p.part_acc[rec * D + d] = at;
+                if (d == 0) {
+                    p.part_ml[rec * 2] = M;
+                    p.part_ml[rec * 2 + 1] = lt;
+                }
+            }
+        }
+    }
+    if (nc == 1 || p.merge_mode == kMergeKernel) return;
+
+    // Fused merge: every thread's partial stores complete, then one arrival per unit.
+    if (atomic_parts) {
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_waitcnt(0);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    } else {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    }
+    __syncthreads();
+    unsigned long long* ctr = p.counters + u.ctr_idx;
+    if (tid == 0) s_last = arrive(ctr, p.epoch) == (unsigned)(nc - 1);
+    __syncthreads();
+    if (!s_last) return;
+    if (!atomic_parts) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    auto ld = [&](const float* a) {
+        return atomic_parts ? __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : *a;
+    };
+    const size_t first = u.rec0 - (size_t)u.c * u.cstride;  // record of chunk 0, head 0
+    const int ncm = min(nc, kMaxFusedChunks);                // the host keeps nc within this
+    // per head: chunk weights 2^(m_c - M) (one chunk per lane) and the total sum
+    for (int g = wave; g < heads; g += WPB) {
+        const bool in = lane < ncm;
+        const size_t rec = first + (size_t)(in ? lane : 0) * u.cstride + g;
+        const float mc = in ? ld(p.part_ml + rec * 2) : -FLT_MAX;
+        float M = mc;
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, shfl_xor(M, o));
+        const float w = in ? fast_exp2(mc - M) : 0.f;
+        float lw = in ? w * ld(p.part_ml + rec * 2 + 1) : 0.f;
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) lw += shfl_xor(lw, o);
+        s_w[g][lane] = w;
+        if (lane == 0) s_L[g] = lw;
+    }
+    __syncthreads();
+    for (int idx = tid; idx < heads * D; idx += WPB * kWave) {
+        const int g = idx / D, d = idx % D;
+        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        int c = 0;
+        for (; c + 8 <= ncm; c += 8) {
+            float a[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) a[e] = ld(p.part_acc + (first + (size_t)(c + e) * u.cstride + g) * D + d);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[e] = __builtin_fmaf(s_w[g][c + e], a[e], acc[e]);
+        }
+        for (; c < ncm; ++c) acc[0] = __builtin_fmaf(s_w[g][c], ld(p.part_acc + (first + (size_t)c * u.cstride + g) * D + d), acc[0]);
+        const float a = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+        const float L = s_L[g];
+        ob[(size_t)g * D + d] = (_Float16)(L > 0.f ? a * (1.0f / L) : 0.f);
+    }
+    if (tid == 0) __hip_atomic_store(ctr, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}

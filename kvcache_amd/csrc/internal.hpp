@@ -49,6 +49,7 @@ struct DecodeParams {
     int last_chunk_first;     // 1: dispatch the highest chunk index first
     const int* work;          // planned units (8 ints each, see kvc_decode_plan), or nullptr
     int table_len;            // planned: ints in table_all (bounds every block-id read)
+    int n_records;            // planned: record groups of the plan (bounds partials and counters)
 };
 
 // How the chunk partials of a split sequence are combined.
@@ -69,6 +70,9 @@ struct DecodeLaunch {
     int batch;   // wave-loads per double-buffered batch (2, 4 or 8; used for G <= 2)
     int units;   // planned launches: number of work-list units (the grid); else 0
     bool need_merge;
+    bool mfma;   // grouped-query matrix-core kernel (fp16, head_dim 64/128, G = group <= 16)
+    unsigned lds_pad;  // dynamic LDS bytes reserved per workgroup (occupancy cap)
+    int wg_per_cu;     // >0: at most this many workgroups per CU (through lds_pad)
 };
 
 // Launches the split kernel and, when needed and not fused, the merge kernel.
@@ -87,7 +91,13 @@ struct Tuning {
     int waves_per_block = 0;    // 0: automatic (8 for small grids, else 4)
     int batch = 4;              // wave-loads per batch for <= 2 query heads per wave
     int last_chunk_first = 1;   // dispatch order of chunks
+    int mfma = -1;              // grouped-query heads on the matrix cores: -1 automatic, 0 off, 1 on
+    int wg_per_cu = -1;         // >0: reserve LDS so at most this many decode workgroups share a CU;
+                                // 0: no cap; -1: automatic (4 on the planned one/two-head path)
+    int split_first = 1;        // planner: chunks of split sequences before whole sequences
 };
+// Dynamic LDS that caps decode workgroups per CU at wg_per_cu (0: none).
+size_t occupancy_lds(size_t static_lds, int wg_per_cu);
 Tuning& tuning();
 
 // ---------------------------------------------------------------------------

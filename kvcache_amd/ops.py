@@ -116,8 +116,8 @@ def decode_plan(lens, Hq, Hkv, D, BLOCK, *, tab_off=None, dtype=KVC_F16, target_
     return work[: nu.value], nu.value, nr.value
 
 
-def planned_workspace_size(Hq, Hkv, D, n_records) -> int:
-    return int(lib().kvc_decode_planned_workspace_size(Hq, Hkv, D, n_records))
+def planned_workspace_size(Hq, Hkv, D, n_records, *, BLOCK=16, dtype=KVC_F16) -> int:
+    return int(lib().kvc_decode_planned_workspace_size(Hq, Hkv, D, BLOCK, dtype, n_records))
 
 
 def launch_batched_paged_planned(q, k_pool, v_pool, table_all, table_len, out, N, Hq, Hkv, D, BLOCK, scale,

@@ -61,3 +61,25 @@ def as_np(dtype: int):
 
 
 __all__ = ["say", "normal", "dev", "host", "paged_layout", "tol", "as_np", "KVC_F16", "KVC_F32"]
+
+
+class tuning:
+    """Sets a library tuning knob for the duration of a with-block."""
+
+    def __init__(self, key: str, value: int):
+        self.key, self.value = key.encode(), value
+
+    def __enter__(self):
+        import ctypes as C
+
+        from kvcache_amd._native import check, lib
+        old = C.c_int(0)
+        check(lib().kvc_get_tuning(self.key, C.byref(old)))
+        self.old = old.value
+        check(lib().kvc_set_tuning(self.key, self.value))
+        return self
+
+    def __exit__(self, *exc):
+        from kvcache_amd._native import check, lib
+        check(lib().kvc_set_tuning(self.key, self.old))
+        return False

@@ -196,7 +196,10 @@ def test_decode_plan_covers_every_token_once(case):
     work, nu, nr = ops.decode_plan(lens, Hq, Hkv, D, B)
     assert nu == len(work) > 0
     sizes = work[:, 3] - work[:, 2]
-    assert np.all(np.diff(sizes) <= 0), "units are sorted longest first"
+    split = work[:, 4] > 1
+    # chunks of split sequences first (their merges overlap later units), each group longest first
+    assert not np.any(np.diff(split.astype(int)) > 0), "split chunks precede whole sequences"
+    assert np.all(np.diff(sizes[split]) <= 0) and np.all(np.diff(sizes[~split]) <= 0), "longest first"
     nsub = Hq // Hkv // (7 if Hq // Hkv == 7 else Hq // Hkv)
     hks = Hkv * nsub
     cover = {}
