@@ -43,6 +43,7 @@ struct RunnerOptions {
     int split_tokens = 0;    // device-lengths path: 0 automatic
     int decode_path = KVC_DECODE_PLANNED;  // or KVC_DECODE_DEVICE_LENGTHS
     int plan_target = 0;     // planned path: tokens per unit (0 automatic)
+    bool fuse_append = true; // planned path with kv_write: write the new rows inside the decode launch
     uint64_t seed = 0x6b76636163686531ull;
 };
 
@@ -230,7 +231,17 @@ struct ModelRunner {
                                  : kvc_decode_workspace_size(n, n_heads, n_kv_heads, head_dim, block_size, cap,
                                                              opt.split_tokens, opt.dtype));
         kvc::check(kvc_event_record(ev0, stream), "event");
+        const bool fused = planned && opt.kv_write && opt.fuse_append;
+        const int* d_wpos = d_len + n;
         for (int l = 0; l < opt.n_layers; ++l) {
+            if (fused) {
+                kvc::check(kvc_batched_paged_append_decode_planned(
+                               q_layer(l), k_layer(l), v_layer(l), d_wpos, kvm.k_layer(l), kvm.v_layer(l), d_tab, T,
+                               dout, n, n_heads, n_kv_heads, head_dim, block_size, scale, opt.dtype, d_work, n_units,
+                               n_records, ws, ws_bytes, stream),
+                           "planned append + decode");
+                continue;
+            }
             if (opt.kv_write)
                 kvc::check(kvc_write_kv_slots(k_layer(l), v_layer(l), kvm.k_layer(l), kvm.v_layer(l), d_slot, n,
                                               n_kv_heads, head_dim, block_size, opt.dtype, stream),

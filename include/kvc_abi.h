@@ -192,6 +192,19 @@ int kvc_batched_paged_decode_planned(const void* q, const void* k_pool, const vo
                                      int N, int Hq, int Hkv, int D, int BLOCK, float scale,
                                      int dtype, const int* work, int n_units, int n_records,
                                      void* workspace, size_t workspace_bytes, kvc_stream_t stream);
+/* The model step's per-layer pair qk_batched_write_kv + qk_batched_paged_decode_attn
+ * (qwen_kernels.h:15-16,30-37; qwen_serve.cu:130-160) in one planned launch: row
+ * s of k_new / v_new ([N][Hkv][D]) belongs at position wpos[s] of sequence s, a
+ * position inside its attended length (the step's new token, wpos = len - 1).
+ * The unit whose chunk holds it attends over the new row taken from k_new/v_new
+ * and stores the row into the pools, so the result and the pools afterwards
+ * equal those of the write followed by the decode.  wpos[s] outside [0, len) is
+ * not written. */
+int kvc_batched_paged_append_decode_planned(const void* q, const void* k_new, const void* v_new, const int* wpos,
+                                            void* k_pool, void* v_pool, const int* table_all, int table_len,
+                                            void* out, int N, int Hq, int Hkv, int D, int BLOCK, float scale,
+                                            int dtype, const int* work, int n_units, int n_records,
+                                            void* workspace, size_t workspace_bytes, kvc_stream_t stream);
 
 /* launch_flash_decode (kv_cache.h:32-34, flash_decode.cu:103-126): one sequence,
  * contiguous [H,S,D], num_splits clamped to [1, cur_len]; split j covers

@@ -419,6 +419,61 @@ int guarded(F&& f) {
 
 inline hipStream_t S(kvc_stream_t s) { return static_cast<hipStream_t>(s); }
 
+int run_planned(const void* q, const void* k_new, const void* v_new, const int* wpos, const void* k_pool,
+                const void* v_pool, const int* table_all, int table_len, void* out, int N, int Hq, int Hkv, int D,
+                int BLOCK, float scale, int dtype, const int* work, int n_units, int n_records, void* ws,
+                size_t ws_bytes, hipStream_t st) {
+    {
+        int rc = check_common(N, Hq, Hkv, D, dtype, q, k_pool, v_pool, out);
+        if (rc || N == 0 || n_units == 0) return rc;
+        if (BLOCK <= 0 || !table_all || table_len <= 0 || !work || n_units < 0 || n_records < 0)
+            return set_error(KVC_ERR_ARG, "planned decode needs BLOCK > 0, a block table and a work list");
+        if (!std::isfinite(scale)) return set_error(KVC_ERR_ARG, "scale must be finite");
+        const PlanShape ps = plan_shape(Hq, Hkv, D, BLOCK, dtype);
+        DecodeLaunch L{};
+        DecodeParams& p = L.p;
+        p.q = q; p.k = k_pool; p.v = v_pool; p.out = out;
+        p.table_all = table_all; p.table_len = table_len;
+        p.N = N; p.Hq = Hq; p.Hkv = Hkv; p.block = BLOCK;
+        p.group = Hq / Hkv; p.nsub = ps.nsub;
+        p.chunk_tokens = 1; p.max_chunks = 1; p.cap = INT_MAX;
+        p.scale_log2 = scale * 1.4426950408889634f;
+        p.work = work;
+        p.n_records = n_records;
+        p.lpb_shift = ps.uniform ? ilog2_exact(BLOCK / ps.tpw) : 0;
+        if (n_records > 0) {
+            const size_t need = planned_workspace(Hq, Hkv, D, BLOCK, dtype, n_records);
+            if (!ws) {
+                rc = default_workspace(need, &ws);
+                if (rc) return rc;
+            } else if (ws_bytes < need) {
+                return set_error(KVC_ERR_WORKSPACE, "workspace too small: need " + std::to_string(need) +
+                                                        " bytes, got " + std::to_string(ws_bytes));
+            } else if (((uintptr_t)ws & 15u) != 0) {
+                return set_error(KVC_ERR_ARG, "workspace must be 16-byte aligned");
+            }
+            const size_t recs = (size_t)n_records * ps.G;
+            const size_t acc = align_up(recs * D * sizeof(float), kAlign), ml = align_up(recs * 2 * sizeof(float), kAlign);
+            p.part_acc = static_cast<float*>(ws);
+            p.part_ml = reinterpret_cast<float*>(static_cast<char*>(ws) + acc);
+            p.counters = reinterpret_cast<unsigned long long*>(static_cast<char*>(ws) + acc + ml);
+        }
+        p.epoch = next_epoch();
+        p.merge_mode = tuning().fused_merge == kMergeFence ? kMergeFence : kMergeAtomic;  // planned: always fused
+        // the grid is the unit list; chunk_range is not used on this path
+        L.dtype = dtype; L.D = D; L.G = ps.G; L.mode = ps.uniform ? kPlannedUniform : kPlannedPerLane;
+        L.mfma = ps.mfma;
+        // a cap on co-resident units lets the longest-first order work as a queue
+        L.wg_per_cu = tuning().wg_per_cu >= 0 ? tuning().wg_per_cu : (!ps.mfma && ps.G <= 2 ? 4 : 0);
+        L.wpb = tuning().waves_per_block ? tuning().waves_per_block : ps.wpb;
+        L.batch = tuning().batch;
+        L.need_merge = false;
+        L.units = n_units;
+        p.k_new = k_new; p.v_new = v_new; p.wpos = wpos;
+        return launch_decode(L, st);
+    }
+}
+
 }  // namespace
 }  // namespace kvc
 
@@ -659,57 +714,28 @@ size_t kvc_decode_planned_workspace_size(int Hq, int Hkv, int D, int BLOCK, int 
     return planned_workspace(Hq, Hkv, D, BLOCK, dtype, n_records);
 }
 
+
 int kvc_batched_paged_decode_planned(const void* q, const void* k_pool, const void* v_pool, const int* table_all,
                                      int table_len, void* out, int N, int Hq, int Hkv, int D, int BLOCK,
                                      float scale, int dtype, const int* work, int n_units, int n_records, void* ws,
                                      size_t ws_bytes, kvc_stream_t st) {
     return guarded([&]() -> int {
-        int rc = check_common(N, Hq, Hkv, D, dtype, q, k_pool, v_pool, out);
-        if (rc || N == 0 || n_units == 0) return rc;
-        if (BLOCK <= 0 || !table_all || table_len <= 0 || !work || n_units < 0 || n_records < 0)
-            return set_error(KVC_ERR_ARG, "planned decode needs BLOCK > 0, a block table and a work list");
-        if (!std::isfinite(scale)) return set_error(KVC_ERR_ARG, "scale must be finite");
-        const PlanShape ps = plan_shape(Hq, Hkv, D, BLOCK, dtype);
-        DecodeLaunch L{};
-        DecodeParams& p = L.p;
-        p.q = q; p.k = k_pool; p.v = v_pool; p.out = out;
-        p.table_all = table_all; p.table_len = table_len;
-        p.N = N; p.Hq = Hq; p.Hkv = Hkv; p.block = BLOCK;
-        p.group = Hq / Hkv; p.nsub = ps.nsub;
-        p.chunk_tokens = 1; p.max_chunks = 1; p.cap = INT_MAX;
-        p.scale_log2 = scale * 1.4426950408889634f;
-        p.work = work;
-        p.n_records = n_records;
-        p.lpb_shift = ps.uniform ? ilog2_exact(BLOCK / ps.tpw) : 0;
-        if (n_records > 0) {
-            const size_t need = planned_workspace(Hq, Hkv, D, BLOCK, dtype, n_records);
-            if (!ws) {
-                rc = default_workspace(need, &ws);
-                if (rc) return rc;
-            } else if (ws_bytes < need) {
-                return set_error(KVC_ERR_WORKSPACE, "workspace too small: need " + std::to_string(need) +
-                                                        " bytes, got " + std::to_string(ws_bytes));
-            } else if (((uintptr_t)ws & 15u) != 0) {
-                return set_error(KVC_ERR_ARG, "workspace must be 16-byte aligned");
-            }
-            const size_t recs = (size_t)n_records * ps.G;
-            const size_t acc = align_up(recs * D * sizeof(float), kAlign), ml = align_up(recs * 2 * sizeof(float), kAlign);
-            p.part_acc = static_cast<float*>(ws);
-            p.part_ml = reinterpret_cast<float*>(static_cast<char*>(ws) + acc);
-            p.counters = reinterpret_cast<unsigned long long*>(static_cast<char*>(ws) + acc + ml);
-        }
-        p.epoch = next_epoch();
-        p.merge_mode = tuning().fused_merge == kMergeFence ? kMergeFence : kMergeAtomic;  // planned: always fused
-        // the grid is the unit list; chunk_range is not used on this path
-        L.dtype = dtype; L.D = D; L.G = ps.G; L.mode = ps.uniform ? kPlannedUniform : kPlannedPerLane;
-        L.mfma = ps.mfma;
-        // a cap on co-resident units lets the longest-first order work as a queue
-        L.wg_per_cu = tuning().wg_per_cu >= 0 ? tuning().wg_per_cu : (!ps.mfma && ps.G <= 2 ? 4 : 0);
-        L.wpb = tuning().waves_per_block ? tuning().waves_per_block : ps.wpb;
-        L.batch = tuning().batch;
-        L.need_merge = false;
-        L.units = n_units;
-        return launch_decode(L, S(st));
+        return kvc::run_planned(q, nullptr, nullptr, nullptr, k_pool, v_pool, table_all, table_len, out, N, Hq, Hkv,
+                                D, BLOCK, scale, dtype, work, n_units, n_records, ws, ws_bytes, S(st));
+    });
+}
+
+int kvc_batched_paged_append_decode_planned(const void* q, const void* k_new, const void* v_new, const int* wpos,
+                                            void* k_pool, void* v_pool, const int* table_all, int table_len,
+                                            void* out, int N, int Hq, int Hkv, int D, int BLOCK, float scale,
+                                            int dtype, const int* work, int n_units, int n_records, void* ws,
+                                            size_t ws_bytes, kvc_stream_t st) {
+    return guarded([&]() -> int {
+        if (N > 0 && (!k_new || !v_new || !wpos)) return set_error(KVC_ERR_ARG, "null k_new / v_new / wpos");
+        if (N > 0 && (!aligned16(k_new) || !aligned16(v_new)))
+            return set_error(KVC_ERR_ARG, "k_new and v_new must be 16-byte aligned");
+        return kvc::run_planned(q, k_new, v_new, wpos, k_pool, v_pool, table_all, table_len, out, N, Hq, Hkv, D,
+                                BLOCK, scale, dtype, work, n_units, n_records, ws, ws_bytes, S(st));
     });
 }
 

@@ -379,6 +379,20 @@ __global__ __launch_bounds__(WPB * kWave) void split_kernel(DecodeParams p) {
     size_t cbase = 0;         // contiguous: byte offset of (s, hk, token 0)
     int tbl = 0;              // uniform paged: block ids of the chunk, one per lane
     const int b0 = j0 / p.block;
+    // fused append: the new row's slice of this lane, used in place of the pool's
+    int wp = -1;
+    u32x4 knew = {0, 0, 0, 0}, vnew = {0, 0, 0, 0};
+    if constexpr (PLANNED) {
+        if (p.wpos != nullptr) {
+            const int w = p.wpos[s];
+            if (w >= j0 && w < j1) {
+                wp = w;
+                const size_t row = ((size_t)s * p.Hkv + hk) * ROW + dl * 16;
+                knew = *reinterpret_cast<const u32x4*>(static_cast<const char*>(p.k_new) + row);
+                vnew = *reinterpret_cast<const u32x4*>(static_cast<const char*>(p.v_new) + row);
+            }
+        }
+    }
     if constexpr (MODE == kContiguous) {
         cbase = ((size_t)s * p.seq_stride + (size_t)hk * p.head_stride) * sizeof(T);
     } else {
@@ -400,6 +414,16 @@ __global__ __launch_bounds__(WPB * kWave) void split_kernel(DecodeParams p) {
             for (int b = threadIdx.x; b < nblk; b += WPB * kWave)
                 s_tab[b] = (int)__builtin_amdgcn_raw_buffer_load_b32(trs, tb + b * 4, 0, 0);
             __syncthreads();
+        }
+        // fused append: one unit per (sequence, KV head) stores the new row in the pool
+        if (PLANNED && wp >= 0 && sub == 0 && wave == 0 && lane < LPT) {
+            const int rel = wp / p.block - b0;
+            int phys;
+            if constexpr (UNIFORM) phys = __builtin_amdgcn_readlane(tbl, min(rel, kWave - 1));
+            else phys = s_tab[min(rel, kMaxChunkBlocks - 1)];
+            const size_t off = ((size_t)(phys * p.Hkv + hk) * p.block + wp % p.block) * ROW + lane * 16;
+            *reinterpret_cast<u32x4*>(const_cast<char*>(kb) + off) = knew;
+            *reinterpret_cast<u32x4*>(const_cast<char*>(vb) + off) = vnew;
         }
     }
 
@@ -441,10 +465,13 @@ __global__ __launch_bounds__(WPB * kWave) void split_kernel(DecodeParams p) {
     auto consume = [&](const Batch<U>& b) {
         bool valid[U];
         float vf[U][EPL];
+        u32x4 kq[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            valid[u] = j0 + (wave + WPB * (b.k0 + u)) * TPW + tslot < j1;
-            Tr::to_float(b.v[u], vf[u]);
+            const int tok = j0 + (wave + WPB * (b.k0 + u)) * TPW + tslot;
+            valid[u] = tok < j1;
+            kq[u] = tok == wp ? knew : b.k[u];
+            Tr::to_float(tok == wp ? vnew : b.v[u], vf[u]);
         }
 #pragma unroll
         for (int g = 0; g < G; ++g) {
@@ -452,7 +479,7 @@ __global__ __launch_bounds__(WPB * kWave) void split_kernel(DecodeParams p) {
             float mx = m[g];
 #pragma unroll
             for (int u = 0; u < U; ++u) {
-                sc[u] = group_sum<LPT>(Tr::dot(qv[g], b.k[u])) * p.scale_log2;
+                sc[u] = group_sum<LPT>(Tr::dot(qv[g], kq[u])) * p.scale_log2;
                 mx = valid[u] ? fmaxf(mx, sc[u]) : mx;
             }
             const float corr = fast_exp2(m[g] - mx);

@@ -100,6 +100,33 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(DecodeParams p) {
         __syncthreads();
     }
 
+    // Fused append (planned launches): the chunk holding the step's new row uses
+    // the new K/V in place of the pool's (this lane's slices of it below), and the
+    // unit of the first head subgroup stores the row in the pool.
+    int wp = -1;
+    u32x4 knew[KJ], vnew = {0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < KJ; ++j) knew[j] = u32x4{0, 0, 0, 0};
+    if constexpr (PLANNED) {
+        if (p.wpos != nullptr) {
+            const int w = p.wpos[s];
+            if (w >= j0 && w < j1) {
+                wp = w;
+                const char* kn = static_cast<const char*>(p.k_new) + ((size_t)s * p.Hkv + hk) * ROW;
+                const char* vn = static_cast<const char*>(p.v_new) + ((size_t)s * p.Hkv + hk) * ROW;
+#pragma unroll
+                for (int j = 0; j < KJ; ++j) knew[j] = *reinterpret_cast<const u32x4*>(kn + g4 * 16 + j * 64);
+                vnew = *reinterpret_cast<const u32x4*>(vn + (lane * 16) % ROW);
+                if (u.sub == 0 && wave == 0 && lane < ROW / 16) {
+                    const int phys = s_tab[min(max(w / p.block - b0, 0), kMfmaMaxChunkBlocks - 1)];
+                    const size_t off = ((size_t)(phys * p.Hkv + hk) * p.block + w % p.block) * ROW + lane * 16;
+                    *reinterpret_cast<u32x4*>(const_cast<char*>(kb) + off) = *reinterpret_cast<const u32x4*>(kn + lane * 16);
+                    *reinterpret_cast<u32x4*>(const_cast<char*>(vb) + off) = *reinterpret_cast<const u32x4*>(vn + lane * 16);
+                }
+            }
+        }
+    }
+
     struct Tile {
         u32x4 k[2][KJ];
         u32x4 v[2][VL];
@@ -149,16 +176,18 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(DecodeParams p) {
                 const int off = q * 1024 + lane * 16;
                 const int r = 16 * h + off / ROW;
                 const int dw = ((off % ROW) >> 2) ^ (((r >> 2) & 3) << 3);
-                *reinterpret_cast<u32x4*>(vt + r * ROW + dw * 4) = T.v[h][q];
+                *reinterpret_cast<u32x4*>(vt + r * ROW + dw * 4) = t0 + r == wp ? vnew : T.v[h][q];
             }
         // scores of the 32 tokens for all heads
         f32x4 S[2];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            const bool nr = t0 + 16 * h + n16 == wp;   // this lane's K row is the new one
 #pragma unroll
             for (int j = 0; j < KJ; ++j)
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8v, T.k[h][j]), qb[j], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8v, nr ? knew[j] : T.k[h][j]), qb[j],
+                                                             acc, 0, 0, 0);
             S[h] = acc;
         }
         float sc[8];

@@ -50,6 +50,12 @@ struct DecodeParams {
     const int* work;          // planned units (8 ints each, see kvc_decode_plan), or nullptr
     int table_len;            // planned: ints in table_all (bounds every block-id read)
     int n_records;            // planned: record groups of the plan (bounds partials and counters)
+    // planned launches with a fused append: the step's new K/V rows [N][Hkv][D] and
+    // their positions wpos[N]; the unit whose chunk holds wpos[s] uses the new row in
+    // place of the pool's and (first head subgroup) writes it to the pool
+    const void* k_new;
+    const void* v_new;
+    const int* wpos;
 };
 
 // How the chunk partials of a split sequence are combined.

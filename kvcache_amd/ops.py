@@ -17,7 +17,7 @@ __all__ = [
     "launch_append", "launch_decode", "launch_paged", "launch_batched_decode", "launch_batched_paged",
     "launch_batched_paged_flash", "launch_flash_decode", "qk_write_kv", "qk_batched_write_kv",
     "qk_batched_paged_decode_attn", "write_kv_slots", "decode_workspace_size", "decode_auto_split",
-    "decode_plan", "planned_workspace_size", "launch_batched_paged_planned",
+    "decode_plan", "planned_workspace_size", "launch_batched_paged_planned", "launch_batched_paged_append_planned",
     "flash_decode_workspace_size", "KVC_F16", "KVC_F32",
 ]
 
@@ -126,6 +126,17 @@ def launch_batched_paged_planned(q, k_pool, v_pool, table_all, table_len, out, N
     check(lib().kvc_batched_paged_decode_planned(_p(q), _p(k_pool), _p(v_pool), _p(table_all), int(table_len),
                                                  _p(out), N, Hq, Hkv, D, BLOCK, scale, dtype, _p(work_dev), n_units,
                                                  n_records, ws, wsb, stream))
+
+
+def launch_batched_paged_append_planned(q, k_new, v_new, wpos, k_pool, v_pool, table_all, table_len, out, N, Hq,
+                                        Hkv, D, BLOCK, scale, work_dev, n_units, n_records, *, dtype=KVC_F16,
+                                        workspace=None, stream=None):
+    """qk_batched_write_kv followed by qk_batched_paged_decode_attn as one planned launch."""
+    ws, wsb = _ws(workspace)
+    check(lib().kvc_batched_paged_append_decode_planned(_p(q), _p(k_new), _p(v_new), _p(wpos), _p(k_pool), _p(v_pool),
+                                                        _p(table_all), int(table_len), _p(out), N, Hq, Hkv, D, BLOCK,
+                                                        scale, dtype, _p(work_dev), n_units, n_records, ws, wsb,
+                                                        stream))
 
 
 def write_kv_slots(k, v, k_pool, v_pool, slot_map, rows, Hkv, D, BLOCK, *, dtype=KVC_F16, stream=None):

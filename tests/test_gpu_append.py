@@ -85,3 +85,47 @@ def test_fill_normal_is_deterministic_and_normal():
     x = host(a, np.float16, (n,)).astype(np.float64)
     np.testing.assert_array_equal(x, host(b, np.float16, (n,)).astype(np.float64))
     assert abs(x.mean()) < 0.01 and abs(x.std() - 1) < 0.01 and np.all(np.isfinite(x))
+
+
+# ---- fused append + decode (planned launch) ------------------------------------------
+@pytest.mark.parametrize("dtype,Hq,Hkv,block", [(KVC_F16, 14, 2, 16), (KVC_F16, 8, 8, 16), (KVC_F32, 14, 2, 16),
+                                                (KVC_F16, 8, 4, 4), (KVC_F16, 16, 2, 32)])
+def test_fused_append_decode_equals_write_then_decode(orc, dtype, Hq, Hkv, block):
+    """The step's write (qk_batched_write_kv) followed by the decode equals the fused
+    launch bit for bit: the same outputs and the same pools afterwards; rows with
+    wpos = -1 or outside the attended length are not written."""
+    say(f"fused append+decode dtype={dtype} Hq={Hq} Hkv={Hkv} block={block}")
+    D = 64
+    nt = as_np(dtype)
+    lens = np.array([1, 17, 300, 1200, 33, 0, 640, 2000], np.int32)
+    wpos = lens - 1
+    wpos[4] = -1                      # an idle slot: nothing written
+    N = len(lens)
+    nb = [(int(L) + block - 1) // block for L in lens]
+    tab_off = np.concatenate([[0], np.cumsum(nb)]).astype(np.int32)
+    table = np.random.default_rng(21).permutation(int(tab_off[-1]) + 7)[: tab_off[-1]].astype(np.int32)
+    NB = int(table.max()) + 1
+    kp0, vp0 = normal((NB, Hkv, block, D), 22, nt), normal((NB, Hkv, block, D), 23, nt)
+    q, kn, vn = normal((N, Hq, D), 24, nt), normal((N, Hkv, D), 25, nt), normal((N, Hkv, D), 26, nt)
+    work, nu, nr = ops.decode_plan(lens, Hq, Hkv, D, block, tab_off=tab_off, dtype=dtype)
+    scale = float(1.0 / np.sqrt(D))
+    dq, dkn, dvn, dtab, dwp, dw = dev(q), dev(kn), dev(vn), dev(table), dev(wpos), dev(work)
+
+    # reference order: write the rows, then the planned decode
+    kr, vr, outr = dev(kp0), dev(vp0), DeviceBuffer(q.nbytes)
+    ops.qk_batched_write_kv(dkn, dvn, kr, vr, dtab, dev(tab_off), dwp, N, Hkv, D, block, dtype=dtype)
+    ops.launch_batched_paged_planned(dq, kr, vr, dtab, len(table), outr, N, Hq, Hkv, D, block, scale, dw, nu, nr,
+                                     dtype=dtype)
+    # fused
+    kf, vf, outf = dev(kp0), dev(vp0), DeviceBuffer(q.nbytes)
+    ops.launch_batched_paged_append_planned(dq, dkn, dvn, dwp, kf, vf, dtab, len(table), outf, N, Hq, Hkv, D, block,
+                                            scale, dw, nu, nr, dtype=dtype)
+    got, ref = host(outf, nt, q.shape), host(outr, nt, q.shape)
+    np.testing.assert_array_equal(got, ref)
+    np.testing.assert_array_equal(host(kf, nt, kp0.shape), host(kr, nt, kp0.shape))
+    np.testing.assert_array_equal(host(vf, nt, kp0.shape), host(vr, nt, kp0.shape))
+    # and against the CPU restatement on the written pools
+    kw, vw = host(kr, nt, kp0.shape), host(vr, nt, kp0.shape)
+    want = orc.batched_paged(q, kw, vw, table, tab_off, lens, Hkv, block, scale)
+    bar = 2e-3 if dtype == KVC_F16 else 1e-5
+    assert np.abs(got.astype(np.float64) - want).max() <= bar
