@@ -134,12 +134,10 @@ Plan plan_batched_mfma(int N, int Hq, int Hkv, int D, int BLOCK, int cap, int sp
     pl.mfma = true;
     pl.G = Hq / Hkv;
     pl.nsub = 1;
-    const int t = tuning().waves_per_block;
-    pl.wpb = (t == 4 || t == 8) ? t : 8;
     long long ch = split;
     if (ch <= 0) {
         const long long units = (long long)N * Hkv;
-        ch = std::max<long long>((long long)pl.wpb * 64, ((long long)std::max(cap, 1) * units + 511) / 512);
+        ch = std::max<long long>(512, ((long long)std::max(cap, 1) * units + 511) / 512);
         long long p2 = 1;
         while (p2 < ch) p2 <<= 1;
         ch = p2;
@@ -148,6 +146,9 @@ Plan plan_batched_mfma(int N, int Hq, int Hkv, int D, int BLOCK, int cap, int sp
     if (paged && ch % BLOCK) ch = (ch + BLOCK - 1) / BLOCK * BLOCK;
     pl.chunk = (int)std::min<long long>(ch, 1 << 24);
     pl.max_chunks = std::max(1, (std::max(cap, 0) + pl.chunk - 1) / pl.chunk);
+    // 4 waves per unit once there are enough units to fill the CUs, else 8
+    const int t = tuning().waves_per_block;
+    pl.wpb = (t == 4 || t == 8) ? t : ((long long)pl.max_chunks * N * Hkv >= 256 ? 4 : 8);
     pl.mode = paged ? kPagedUniform : kContiguous;
     pl.chunk_blocks_ok = !paged || pl.chunk / BLOCK <= kMfmaMaxChunkBlocksHost;
     size_workspace(pl, N, Hq, Hkv, D);
@@ -304,7 +305,8 @@ PlanShape plan_shape(int Hq, int Hkv, int D, int BLOCK, int dtype) {
     const int group = Hq / Hkv;
     if (mfma_path(group, D, dtype, BLOCK, true)) {
         // all heads of the group per unit; 8 waves; at least two 32-token tiles per
-        // wave; about two units resident per CU
+        // wave; about 0.7 units per CU: each unit streams ~1000 tokens, which keeps
+        // the chunks of long sequences few (their fused merge is the tail)
         ps.mfma = true;
         ps.uniform = true;
         ps.G = group;
@@ -315,7 +317,7 @@ PlanShape plan_shape(int Hq, int Hkv, int D, int BLOCK, int dtype) {
         ps.wpb = (t == 4 || t == 8) ? t : 8;
         ps.min_chunk = ((ps.wpb * 64 + BLOCK - 1) / BLOCK) * BLOCK;
         ps.max_chunk = kMfmaMaxChunkBlocksHost * BLOCK;
-        ps.slots = 256 * 2;
+        ps.slots = 176;
         return ps;
     }
     ps.G = choose_g(group, D);

@@ -341,19 +341,20 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(DecodeParams p) {
         if (lane == 0) s_L[g] = lw;
     }
     __syncthreads();
+    // each thread owns one (head, dim) and keeps 16 chunk partials in flight
+    constexpr int E = 16;
     for (int idx = tid; idx < heads * D; idx += WPB * kWave) {
         const int g = idx / D, d = idx % D;
-        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        int c = 0;
-        for (; c + 8 <= ncm; c += 8) {
-            float a[8];
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int c = 0; c < ncm; c += E) {
+            float a[E];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) a[e] = ld(p.part_acc + (first + (size_t)(c + e) * u.cstride + g) * D + d);
+            for (int e = 0; e < E; ++e)
+                a[e] = c + e < ncm ? ld(p.part_acc + (first + (size_t)(c + e) * u.cstride + g) * D + d) : 0.f;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) acc[e] = __builtin_fmaf(s_w[g][c + e], a[e], acc[e]);
+            for (int e = 0; e < E; ++e) acc[e & 3] = __builtin_fmaf(c + e < ncm ? s_w[g][c + e] : 0.f, a[e], acc[e & 3]);
         }
-        for (; c < ncm; ++c) acc[0] = __builtin_fmaf(s_w[g][c], ld(p.part_acc + (first + (size_t)c * u.cstride + g) * D + d), acc[0]);
-        const float a = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+        const float a = (acc[0] + acc[1]) + (acc[2] + acc[3]);
         const float L = s_L[g];
         ob[(size_t)g * D + d] = (_Float16)(L > 0.f ? a * (1.0f / L) : 0.f);
     }
