@@ -137,8 +137,8 @@ def time_planned(W, lens, Hq, Hkv, D, B, steps, warmup, target=0, rotate=None):
     from kvcache_amd import KVC_F16, ops
     from kvcache_amd.device import DeviceBuffer, Event, synchronize
 
-    work, nu, nr = ops.decode_plan(lens, Hq, Hkv, D, B, tab_off=W["tab_off_host"], dtype=KVC_F16,
-                                   target_tokens=target)
+    work, nu, nr = ops.decode_plan(lens, Hq, Hkv, D, B, tab_off=W["tab_off_host"], table=W["table_host"],
+                                   dtype=KVC_F16, target_tokens=target)
     wdev = DeviceBuffer.from_numpy(work)
     ws = DeviceBuffer(max(ops.planned_workspace_size(Hq, Hkv, D, nr, BLOCK=B, dtype=KVC_F16), 256))
     pools = W["pools"] if rotate is None else W["pools"][:rotate]

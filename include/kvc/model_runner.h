@@ -191,17 +191,19 @@ struct ModelRunner {
         const bool planned = opt.decode_path == KVC_DECODE_PLANNED && T > 0;
         int n_units = 0, n_records = 0;
         if (planned) {
-            kvc::check(kvc_decode_plan(h_len.data(), h_off.data(), n, n_heads, n_kv_heads, head_dim, block_size,
-                                       opt.dtype, opt.plan_target, nullptr, 0, &n_units, &n_records),
+            kvc::check(kvc_decode_plan(h_len.data(), h_off.data(), h_tab.data(), T, n, n_heads, n_kv_heads, head_dim,
+                                       block_size, opt.dtype, opt.plan_target, nullptr, 0, &n_units, &n_records),
                        "decode plan");
-            h_work.resize((size_t)n_units * 8);
-            kvc::check(kvc_decode_plan(h_len.data(), h_off.data(), n, n_heads, n_kv_heads, head_dim, block_size,
-                                       opt.dtype, opt.plan_target, h_work.data(), n_units, &n_units, &n_records),
+            const int ipu = kvc_decode_plan_entry_ints(n_heads, n_kv_heads, head_dim, block_size, opt.dtype);
+            h_work.resize((size_t)n_units * ipu);
+            kvc::check(kvc_decode_plan(h_len.data(), h_off.data(), h_tab.data(), T, n, n_heads, n_kv_heads, head_dim,
+                                       block_size, opt.dtype, opt.plan_target, h_work.data(), n_units, &n_units,
+                                       &n_records),
                        "decode plan");
         } else {
             h_work.clear();
         }
-        // pack: [N | off N+1 | len N | wpos N | slot N | tab T | work 8*units]
+        // pack: [N | off N+1 | len N | wpos N | slot N | tab T | work units*entry_ints]
         ensure_meta(1 + (size_t)(n + 1) + 3 * (size_t)n + T + h_work.size());
         if (h_ev_used[ring]) kvc::check(kvc_event_synchronize(h_ev[ring]), "meta ring wait");
         int* h = h_meta[ring];

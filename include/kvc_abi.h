@@ -171,12 +171,15 @@ int kvc_decode_auto_split(int N, int Hq, int Hkv, int D, int BLOCK, int cap, int
 
 /* Planned decode for host-known lengths (the serving path: the scheduler knows
  * every length when it builds the step).  kvc_decode_plan cuts each sequence into
- * near-equal block-aligned chunks sized so the batch fills the GPU about once and
- * writes the units, longest first, as 8 ints each {s, kv_head_slot | chunk << 16,
- * j0, j1, chunks, record group, counter, table index of the chunk's first block}
- * into `work` (host memory; work == NULL only reports *n_units / *n_records).
- * host_tab_off (N+1, may be NULL: tables packed in sequence order) locates each
- * sequence's table in table_all.  target_tokens = 0 picks the chunk size.  The
+ * near-equal block-aligned chunks and writes the units (chunks of split sequences
+ * first, each group longest first) into `work` (host memory; work == NULL only
+ * reports *n_units / *n_records), kvc_decode_plan_entry_ints() ints per unit:
+ * {s, kv_head_slot | chunk << 16, j0, j1, chunks | inline_ids << 16, record group,
+ * counter, table index of the chunk's first block}, followed on the grouped-query
+ * matrix-core path (64-int entries) by up to 56 of the chunk's block ids copied
+ * from host_table_all (may be NULL: then none are inlined).  host_tab_off (N+1,
+ * may be NULL: tables packed in sequence order) locates each sequence's table in
+ * table_all.  target_tokens = 0 picks the chunk size.  capacity is in units.  The
  * caller copies the work list to the device (e.g. inside its per-step upload) and
  * runs kvc_batched_paged_decode_planned with the same shape and tables; every
  * block-id read is bounded by table_len (ints in table_all).  Partials of split
@@ -184,8 +187,10 @@ int kvc_decode_auto_split(int N, int Hq, int Hkv, int D, int BLOCK, int cap, int
  * A plan depends on the tuning knobs ("mfma", "waves_per_block"): plan and launch
  * under the same settings.  Units naming a sequence or KV head outside N / Hkv
  * are skipped. */
-int kvc_decode_plan(const int* host_lens, const int* host_tab_off, int N, int Hq, int Hkv, int D, int BLOCK,
-                    int dtype, int target_tokens, int* work, int capacity, int* n_units, int* n_records);
+int kvc_decode_plan_entry_ints(int Hq, int Hkv, int D, int BLOCK, int dtype);
+int kvc_decode_plan(const int* host_lens, const int* host_tab_off, const int* host_table_all, int host_table_len,
+                    int N, int Hq, int Hkv, int D, int BLOCK, int dtype, int target_tokens, int* work, int capacity,
+                    int* n_units, int* n_records);
 size_t kvc_decode_planned_workspace_size(int Hq, int Hkv, int D, int BLOCK, int dtype, int n_records);
 int kvc_batched_paged_decode_planned(const void* q, const void* k_pool, const void* v_pool,
                                      const int* table_all, int table_len, void* out,

@@ -100,7 +100,8 @@ _SIGS = {
         i32, [vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, f32, i32, i32, vp, sz, vp]),
     "kvc_decode_workspace_size": (sz, [i32, i32, i32, i32, i32, i32, i32, i32]),
     "kvc_decode_auto_split": (i32, [i32, i32, i32, i32, i32, i32, i32]),
-    "kvc_decode_plan": (i32, [vp, vp, i32, i32, i32, i32, i32, i32, i32, vp, i32, ip, ip]),
+    "kvc_decode_plan_entry_ints": (i32, [i32, i32, i32, i32, i32]),
+    "kvc_decode_plan": (i32, [vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, i32, vp, i32, ip, ip]),
     "kvc_decode_planned_workspace_size": (sz, [i32, i32, i32, i32, i32, i32]),
     "kvc_batched_paged_decode_planned": (
         i32, [vp, vp, vp, vp, i32, vp, i32, i32, i32, i32, i32, f32, i32, vp, i32, i32, vp, sz, vp]),

@@ -293,10 +293,11 @@ int run_batched(const void* q, const void* k, const void* v, const int* table_al
 // blocks so the uniform paged path applies) sized so the whole batch fills the
 // resident workgroup slots about once; units are sorted longest first so the
 // hardware dispatcher fills the machine greedily (longest-processing-time order).
-constexpr int kPlanInts = 8;
+constexpr int kPlanInts = 8;          // header ints of a unit
+constexpr int kPlanIntsInline = 64;   // grouped-query units: header + up to 56 block ids
 
 struct PlanShape {
-    int G, nsub, hks, tpw, wpb, min_chunk, max_chunk, slots;
+    int G, nsub, hks, tpw, wpb, min_chunk, max_chunk, slots, entry_ints;
     bool uniform, mfma;
 };
 
@@ -315,9 +316,14 @@ PlanShape plan_shape(int Hq, int Hkv, int D, int BLOCK, int dtype) {
         ps.tpw = 32;
         const int t = tuning().waves_per_block;
         ps.wpb = (t == 4 || t == 8) ? t : 8;
-        ps.min_chunk = ((ps.wpb * 64 + BLOCK - 1) / BLOCK) * BLOCK;
+        // a split costs the chunk tail a store, an arrival and a merge: below ~1024
+        // tokens a sequence stays in one unit
+        ps.min_chunk = ((1024 + BLOCK - 1) / BLOCK) * BLOCK;
         ps.max_chunk = kMfmaMaxChunkBlocksHost * BLOCK;
         ps.slots = 176;
+        // the unit's first block ids travel in its entry: the kernel reads entry and
+        // ids in one round instead of entry, then table
+        ps.entry_ints = kPlanIntsInline;
         return ps;
     }
     ps.G = choose_g(group, D);
@@ -333,11 +339,12 @@ PlanShape plan_shape(int Hq, int Hkv, int D, int BLOCK, int dtype) {
     // units to aim for per CU: ~3.5 for one or two heads per wave (about 1.3 rounds
     // of the 4 units a CU runs at once), ~3 for larger groups
     ps.slots = ps.G <= 2 ? 256 * 7 / 2 : 256 * 3;
+    ps.entry_ints = kPlanInts;
     return ps;
 }
 
-int make_plan(const int* lens, const int* tab_off, int N, int Hq, int Hkv, int D, int BLOCK, int dtype, int target,
-              int* work, int capacity, int* n_units, int* n_records) {
+int make_plan(const int* lens, const int* tab_off, const int* table, int table_len, int N, int Hq, int Hkv, int D,
+              int BLOCK, int dtype, int target, int* work, int capacity, int* n_units, int* n_records) {
     const PlanShape ps = plan_shape(Hq, Hkv, D, BLOCK, dtype);
     if (ps.hks > 0xFFFF) return set_error(KVC_ERR_UNSUPPORTED, "too many KV heads for the plan encoding");
     long long total = 0;
@@ -390,10 +397,19 @@ int make_plan(const int* lens, const int* tab_off, int N, int Hq, int Hkv, int D
     if (capacity < (int)units.size())
         return set_error(KVC_ERR_WORKSPACE, "plan capacity " + std::to_string(capacity) + " < " +
                                                 std::to_string(units.size()) + " units");
+    const int inline_max = ps.entry_ints - kPlanInts;
     for (size_t u = 0; u < units.size(); ++u) {
-        int* w = work + u * kPlanInts;
-        w[0] = units[u].s; w[1] = units[u].hks | (units[u].c << 16); w[2] = units[u].j0; w[3] = units[u].j1;
-        w[4] = units[u].nc; w[5] = units[u].rec; w[6] = units[u].ctr; w[7] = units[u].tab;
+        int* w = work + u * (size_t)ps.entry_ints;
+        const U& x = units[u];
+        int n_inl = 0;
+        if (inline_max > 0) {
+            const int nblk = x.j1 > x.j0 ? (x.j1 - 1) / BLOCK - x.j0 / BLOCK + 1 : 0;
+            if (table && x.tab >= 0 && (long long)x.tab + std::min(nblk, inline_max) <= table_len)
+                n_inl = std::min(nblk, inline_max);
+            for (int b = 0; b < inline_max; ++b) w[kPlanInts + b] = b < n_inl ? table[x.tab + b] : 0;
+        }
+        w[0] = x.s; w[1] = x.hks | (x.c << 16); w[2] = x.j0; w[3] = x.j1;
+        w[4] = x.nc | (n_inl << 16); w[5] = x.rec; w[6] = x.ctr; w[7] = x.tab;
     }
     return KVC_OK;
 }
@@ -441,6 +457,7 @@ int run_planned(const void* q, const void* k_new, const void* v_new, const int* 
         p.chunk_tokens = 1; p.max_chunks = 1; p.cap = INT_MAX;
         p.scale_log2 = scale * 1.4426950408889634f;
         p.work = work;
+        p.work_ints = ps.entry_ints;
         p.n_records = n_records;
         p.lpb_shift = ps.uniform ? ilog2_exact(BLOCK / ps.tpw) : 0;
         if (n_records > 0) {
@@ -698,16 +715,23 @@ int kvc_batched_paged_decode_split(const void* q, const void* k_pool, const void
     });
 }
 
-int kvc_decode_plan(const int* host_lens, const int* host_tab_off, int N, int Hq, int Hkv, int D, int BLOCK,
-                    int dtype, int target_tokens, int* work, int capacity, int* n_units, int* n_records) {
+int kvc_decode_plan_entry_ints(int Hq, int Hkv, int D, int BLOCK, int dtype) {
+    if (Hq <= 0 || Hkv <= 0 || Hq % Hkv || BLOCK <= 0 || !d_ok(D) || !dtype_ok(dtype)) return 0;
+    return plan_shape(Hq, Hkv, D, BLOCK, dtype).entry_ints;
+}
+
+int kvc_decode_plan(const int* host_lens, const int* host_tab_off, const int* host_table_all, int host_table_len,
+                    int N, int Hq, int Hkv, int D, int BLOCK, int dtype, int target_tokens, int* work, int capacity,
+                    int* n_units, int* n_records) {
     return guarded([&]() -> int {
         if (!n_units || !n_records) return set_error(KVC_ERR_ARG, "null output pointer");
         if (N < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || BLOCK <= 0) return set_error(KVC_ERR_ARG, "bad shape");
         if (!d_ok(D)) return set_error(KVC_ERR_UNSUPPORTED, "head_dim must be 32, 64, 128 or 256");
         if (!dtype_ok(dtype)) return set_error(KVC_ERR_ARG, "bad dtype");
         if (N > 0 && !host_lens) return set_error(KVC_ERR_ARG, "null lengths");
-        return make_plan(host_lens, host_tab_off, N, Hq, Hkv, D, BLOCK, dtype, target_tokens, work, capacity, n_units,
-                         n_records);
+        if (host_table_all && host_table_len < 0) return set_error(KVC_ERR_ARG, "negative table length");
+        return make_plan(host_lens, host_tab_off, host_table_all, host_table_all ? host_table_len : 0, N, Hq, Hkv, D,
+                         BLOCK, dtype, target_tokens, work, capacity, n_units, n_records);
     });
 }
 

@@ -278,13 +278,14 @@ __device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, int vof
 // (chunk, sequence, KV head, subgroup) decomposition of the grid.
 struct Unit {
     int s, hk, sub, c, nc, j0, j1, tab_start;
+    int n_inline = 0;  // planned grouped-query units: block ids carried in the entry
     size_t rec0, cstride, ctr_idx;
 };
 
 template <bool PLANNED>
 __device__ __forceinline__ bool load_unit(const DecodeParams& p, int heads, Unit& u) {
     if constexpr (PLANNED) {
-        const int* w = p.work + (size_t)blockIdx.x * 8;
+        const int* w = p.work + (size_t)blockIdx.x * p.work_ints;
         u.s = w[0];
         const int hks = w[1] & 0xFFFF;
         u.c = w[1] >> 16;
@@ -292,7 +293,8 @@ __device__ __forceinline__ bool load_unit(const DecodeParams& p, int heads, Unit
         u.sub = hks % p.nsub;
         u.j0 = max(w[2], 0);
         u.j1 = max(w[3], u.j0);
-        u.nc = max(w[4], 1);
+        u.nc = max(w[4] & 0xFFFF, 1);
+        u.n_inline = (unsigned)w[4] >> 16;
         u.rec0 = ((size_t)(w[5] > 0 ? w[5] : 0) + (size_t)u.c) * heads;
         u.cstride = heads;
         u.ctr_idx = w[6] > 0 ? w[6] : 0;
@@ -380,17 +382,16 @@ __global__ __launch_bounds__(WPB * kWave) void split_kernel(DecodeParams p) {
     int tbl = 0;              // uniform paged: block ids of the chunk, one per lane
     const int b0 = j0 / p.block;
     // fused append: the new row's slice of this lane, used in place of the pool's
+    // when the chunk holds its position (loads issued without waiting for wpos)
     int wp = -1;
     u32x4 knew = {0, 0, 0, 0}, vnew = {0, 0, 0, 0};
     if constexpr (PLANNED) {
         if (p.wpos != nullptr) {
+            const size_t row = ((size_t)s * p.Hkv + hk) * ROW + dl * 16;
+            knew = *reinterpret_cast<const u32x4*>(static_cast<const char*>(p.k_new) + row);
+            vnew = *reinterpret_cast<const u32x4*>(static_cast<const char*>(p.v_new) + row);
             const int w = p.wpos[s];
-            if (w >= j0 && w < j1) {
-                wp = w;
-                const size_t row = ((size_t)s * p.Hkv + hk) * ROW + dl * 16;
-                knew = *reinterpret_cast<const u32x4*>(static_cast<const char*>(p.k_new) + row);
-                vnew = *reinterpret_cast<const u32x4*>(static_cast<const char*>(p.v_new) + row);
-            }
+            wp = (w >= j0 && w < j1) ? w : -1;
         }
     }
     if constexpr (MODE == kContiguous) {

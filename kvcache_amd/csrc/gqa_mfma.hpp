@@ -64,12 +64,39 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(DecodeParams p) {
     const int g4 = lane >> 4;    // lane group
     const int heads = p.group;   // query heads of the KV group, <= 16 (host-checked)
 
+    // planned entries may carry the unit's block ids after the 8-int header: one
+    // int per lane, read together with the header
+    int ev = 0;
+    if constexpr (PLANNED) {
+        if (p.work_ints == kWave) ev = p.work[(size_t)blockIdx.x * kWave + lane];
+    }
     Unit u;
     if (!load_unit<PLANNED>(p, heads, u)) return;
     const int s = u.s, hk = u.hk, j0 = u.j0, j1 = u.j1, nc = u.nc;
     const int hq0 = hk * p.group;
     const int ntiles = (j1 - j0 + kMfmaTile - 1) / kMfmaTile;
     const int kmax = wave < ntiles ? (ntiles - wave + WPB - 1) / WPB : 0;
+
+    // Fused append (planned launches): the chunk holding the step's new row uses
+    // the new K/V in place of the pool's (this lane's slices of it, loaded here,
+    // ahead of the table), and the unit of the first head subgroup stores the row
+    // in the pool once the block ids are staged.
+    int wp = -1;
+    u32x4 knew[KJ], vnew = {0, 0, 0, 0}, kst = {0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < KJ; ++j) knew[j] = u32x4{0, 0, 0, 0};
+    if constexpr (PLANNED) {
+        if (p.wpos != nullptr) {
+            const char* kn = static_cast<const char*>(p.k_new) + ((size_t)s * p.Hkv + hk) * ROW;
+            const char* vn = static_cast<const char*>(p.v_new) + ((size_t)s * p.Hkv + hk) * ROW;
+#pragma unroll
+            for (int j = 0; j < KJ; ++j) knew[j] = *reinterpret_cast<const u32x4*>(kn + g4 * 16 + j * 64);
+            vnew = *reinterpret_cast<const u32x4*>(vn + (lane * 16) % ROW);  // = bytes lane*16 for lane < ROW/16
+            kst = *reinterpret_cast<const u32x4*>(kn + (lane * 16) % ROW);
+            const int w = p.wpos[s];
+            wp = (w >= j0 && w < j1) ? w : -1;
+        }
+    }
 
     // q as the B operand of QK^T: lane l holds head l%16, dims 8*(l/16) + 32j .. +7;
     // heads past the group read as zero through the descriptor bound.
@@ -87,44 +114,32 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(DecodeParams p) {
     size_t cbase = 0;
     const int b0 = PAGED ? j0 / p.block : 0;
     int nblk = 0;
+    bool inl = false;  // block ids from the entry (no table read, no LDS staging)
     if constexpr (MODE == kContiguous) {
         cbase = ((size_t)s * p.seq_stride + (size_t)hk * p.head_stride) * 2;
     } else {
         nblk = min(j1 > j0 ? (j1 - 1) / p.block - b0 + 1 : 0, kMfmaMaxChunkBlocks);
-        const int first = PLANNED ? u.tab_start : (p.tab_off ? p.tab_off[s] : 0) + b0;
-        const __amdgpu_buffer_rsrc_t trs =
-            PLANNED ? tile_rsrc(p.table_all, p.table_len * 4) : tile_rsrc(p.table_all + first, nblk * 4);
-        const int tb = PLANNED ? first * 4 : 0;
-        for (int b = tid; b < nblk; b += WPB * kWave)
-            s_tab[b] = (int)__builtin_amdgcn_raw_buffer_load_b32(trs, tb + b * 4, 0, 0);
-        __syncthreads();
-    }
-
-    // Fused append (planned launches): the chunk holding the step's new row uses
-    // the new K/V in place of the pool's (this lane's slices of it below), and the
-    // unit of the first head subgroup stores the row in the pool.
-    int wp = -1;
-    u32x4 knew[KJ], vnew = {0, 0, 0, 0};
-#pragma unroll
-    for (int j = 0; j < KJ; ++j) knew[j] = u32x4{0, 0, 0, 0};
-    if constexpr (PLANNED) {
-        if (p.wpos != nullptr) {
-            const int w = p.wpos[s];
-            if (w >= j0 && w < j1) {
-                wp = w;
-                const char* kn = static_cast<const char*>(p.k_new) + ((size_t)s * p.Hkv + hk) * ROW;
-                const char* vn = static_cast<const char*>(p.v_new) + ((size_t)s * p.Hkv + hk) * ROW;
-#pragma unroll
-                for (int j = 0; j < KJ; ++j) knew[j] = *reinterpret_cast<const u32x4*>(kn + g4 * 16 + j * 64);
-                vnew = *reinterpret_cast<const u32x4*>(vn + (lane * 16) % ROW);
-                if (u.sub == 0 && wave == 0 && lane < ROW / 16) {
-                    const int phys = s_tab[min(max(w / p.block - b0, 0), kMfmaMaxChunkBlocks - 1)];
-                    const size_t off = ((size_t)(phys * p.Hkv + hk) * p.block + w % p.block) * ROW + lane * 16;
-                    *reinterpret_cast<u32x4*>(const_cast<char*>(kb) + off) = *reinterpret_cast<const u32x4*>(kn + lane * 16);
-                    *reinterpret_cast<u32x4*>(const_cast<char*>(vb) + off) = *reinterpret_cast<const u32x4*>(vn + lane * 16);
-                }
-            }
+        inl = PLANNED && p.work_ints == kWave && u.n_inline >= nblk;
+        if (!inl) {
+            const int first = PLANNED ? u.tab_start : (p.tab_off ? p.tab_off[s] : 0) + b0;
+            const __amdgpu_buffer_rsrc_t trs =
+                PLANNED ? tile_rsrc(p.table_all, p.table_len * 4) : tile_rsrc(p.table_all + first, nblk * 4);
+            const int tb = PLANNED ? first * 4 : 0;
+            for (int b = tid; b < nblk; b += WPB * kWave)
+                s_tab[b] = (int)__builtin_amdgcn_raw_buffer_load_b32(trs, tb + b * 4, 0, 0);
+            __syncthreads();
         }
+    }
+    // physical block of the chunk's rel-th block (rel uniform, < nblk)
+    auto block_id = [&](int rel) -> int {
+        if (inl) return __builtin_amdgcn_readlane(ev, 8 + min(rel, kWave - 9));
+        return s_tab[min(rel, kMfmaMaxChunkBlocks - 1)];
+    };
+    if (PLANNED && wp >= 0 && u.sub == 0 && wave == 0 && lane < ROW / 16) {
+        const int phys = block_id(max(wp / p.block - b0, 0));
+        const size_t off = ((size_t)(phys * p.Hkv + hk) * p.block + wp % p.block) * ROW + lane * 16;
+        *reinterpret_cast<u32x4*>(const_cast<char*>(kb) + off) = kst;
+        *reinterpret_cast<u32x4*>(const_cast<char*>(vb) + off) = vnew;
     }
 
     struct Tile {
@@ -137,7 +152,7 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(DecodeParams p) {
             return cbase + (size_t)t * ROW;
         } else {
             const int rel = min(max(t / p.block - b0, 0), max(nblk - 1, 0));
-            const int phys = uniform(s_tab[rel]);
+            const int phys = uniform(block_id(rel));
             return ((size_t)(phys * p.Hkv + hk) * p.block + (t % p.block)) * ROW;
         }
     };

@@ -47,7 +47,8 @@ struct DecodeParams {
     unsigned epoch;           // per-call tag of the arrival counters
     int merge_mode;           // MergeMode
     int last_chunk_first;     // 1: dispatch the highest chunk index first
-    const int* work;          // planned units (8 ints each, see kvc_decode_plan), or nullptr
+    const int* work;          // planned units (work_ints ints each, see kvc_decode_plan), or nullptr
+    int work_ints;            // planned: ints per unit (8, or 64 with inline block ids)
     int table_len;            // planned: ints in table_all (bounds every block-id read)
     int n_records;            // planned: record groups of the plan (bounds partials and counters)
     // planned launches with a fused append: the step's new K/V rows [N][Hkv][D] and

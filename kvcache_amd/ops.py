@@ -97,21 +97,27 @@ def qk_batched_paged_decode_attn(q, out, k_pool, v_pool, table_all, tab_off, cur
                                                ws, wsb, stream))
 
 
-def decode_plan(lens, Hq, Hkv, D, BLOCK, *, tab_off=None, dtype=KVC_F16, target_tokens=0):
+def decode_plan(lens, Hq, Hkv, D, BLOCK, *, tab_off=None, table=None, dtype=KVC_F16, target_tokens=0):
     """Host-side plan of a batched paged decode (kvc_decode_plan): returns
-    (work [units, 8] int32, n_units, n_records)."""
+    (work [units, entry_ints] int32, n_units, n_records).  `table` (the host copy of
+    table_all) lets grouped-query plans carry each unit's block ids."""
     import ctypes as C
 
     import numpy as np
     lens = np.ascontiguousarray(np.asarray(lens, dtype=np.int32))
     toff = None if tab_off is None else np.ascontiguousarray(np.asarray(tab_off, dtype=np.int32))
+    tab = None if table is None else np.ascontiguousarray(np.asarray(table, dtype=np.int32))
     tp = None if toff is None else toff.ctypes.data
+    tbp, tbl = (None, 0) if tab is None else (tab.ctypes.data, len(tab))
     nu, nr = C.c_int(0), C.c_int(0)
     L = lib()
-    check(L.kvc_decode_plan(lens.ctypes.data, tp, len(lens), Hq, Hkv, D, BLOCK, dtype, target_tokens, None, 0,
-                            C.byref(nu), C.byref(nr)))
-    work = np.zeros((max(nu.value, 1), 8), dtype=np.int32)
-    check(L.kvc_decode_plan(lens.ctypes.data, tp, len(lens), Hq, Hkv, D, BLOCK, dtype, target_tokens,
+    ipu = int(L.kvc_decode_plan_entry_ints(Hq, Hkv, D, BLOCK, dtype))
+    if ipu <= 0:
+        raise ValueError("bad plan shape")
+    check(L.kvc_decode_plan(lens.ctypes.data, tp, tbp, tbl, len(lens), Hq, Hkv, D, BLOCK, dtype, target_tokens, None,
+                            0, C.byref(nu), C.byref(nr)))
+    work = np.zeros((max(nu.value, 1), ipu), dtype=np.int32)
+    check(L.kvc_decode_plan(lens.ctypes.data, tp, tbp, tbl, len(lens), Hq, Hkv, D, BLOCK, dtype, target_tokens,
                             work.ctypes.data, nu.value, C.byref(nu), C.byref(nr)))
     return work[: nu.value], nu.value, nr.value
 

@@ -107,7 +107,7 @@ def test_fused_append_decode_equals_write_then_decode(orc, dtype, Hq, Hkv, block
     NB = int(table.max()) + 1
     kp0, vp0 = normal((NB, Hkv, block, D), 22, nt), normal((NB, Hkv, block, D), 23, nt)
     q, kn, vn = normal((N, Hq, D), 24, nt), normal((N, Hkv, D), 25, nt), normal((N, Hkv, D), 26, nt)
-    work, nu, nr = ops.decode_plan(lens, Hq, Hkv, D, block, tab_off=tab_off, dtype=dtype)
+    work, nu, nr = ops.decode_plan(lens, Hq, Hkv, D, block, tab_off=tab_off, table=table, dtype=dtype)
     scale = float(1.0 / np.sqrt(D))
     dq, dkn, dvn, dtab, dwp, dw = dev(q), dev(kn), dev(vn), dev(table), dev(wpos), dev(work)
 

@@ -255,10 +255,11 @@ def test_c3_long_context_split_k(orc):
 
 
 # ---- planned path (host-known lengths; the serving scheduler's path) ----------------
-def run_planned(q, K, V, lens, Hkv, block, dtype, perm=None, target=0, workspace=None):
+def run_planned(q, K, V, lens, Hkv, block, dtype, perm=None, target=0, workspace=None, inline=True):
     N, Hq, D = q.shape
     kp, vp, table, tab_off = paged_layout(K, V, lens, block, perm)
-    work, nu, nr = ops.decode_plan(lens, Hq, Hkv, D, block, tab_off=tab_off, dtype=dtype, target_tokens=target)
+    work, nu, nr = ops.decode_plan(lens, Hq, Hkv, D, block, tab_off=tab_off, table=table if inline else None,
+                                   dtype=dtype, target_tokens=target)
     out = DeviceBuffer(q.nbytes)
     ops.launch_batched_paged_planned(dev(q), dev(kp), dev(vp), dev(table), len(table), out, N, Hq, Hkv, D, block,
                                      float(1.0 / np.sqrt(D)), dev(work), nu, nr, dtype=dtype, workspace=workspace)
@@ -339,7 +340,9 @@ def test_mfma_gqa_matches_valu_and_oracle(orc, Hq, Hkv, D):
         assert np.abs(mf - va).max() <= 2e-3, split
     with tuning("mfma", 1):
         pl = run_planned(q, K, V, lens, Hkv, B, KVC_F16, perm=perm)
+        pn = run_planned(q, K, V, lens, Hkv, B, KVC_F16, perm=perm, inline=False)  # block ids from the table only
     assert np.abs(pl - ref).max() <= 2e-3
+    np.testing.assert_array_equal(pl, pn)
 
 
 @pytest.mark.parametrize("block", [8, 32, 64])

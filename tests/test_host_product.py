@@ -193,8 +193,21 @@ def test_decode_plan_covers_every_token_once(case):
         lens, Hq, Hkv = np.array([8192, 16384, 32768, 32768], np.int32), 14, 2
     else:
         lens, B = np.array([5, 8, 13, 3000], np.int32), 4
-    work, nu, nr = ops.decode_plan(lens, Hq, Hkv, D, B)
+    tab_off = np.concatenate([[0], np.cumsum([(int(x) + B - 1) // B for x in lens])]).astype(np.int32)
+    table = np.random.default_rng(3).permutation(int(tab_off[-1]) + 5)[: tab_off[-1]].astype(np.int32)
+    work, nu, nr = ops.decode_plan(lens, Hq, Hkv, D, B, tab_off=tab_off, table=table)
     assert nu == len(work) > 0
+    # grouped-query fp16 units carry their first block ids after the 8-int header
+    n_inl = work[:, 4] >> 16
+    if work.shape[1] > 8:
+        for row, k in zip(work, n_inl):
+            nblk = (row[3] - 1) // B - row[2] // B + 1 if row[3] > row[2] else 0
+            assert k == min(nblk, work.shape[1] - 8)
+            np.testing.assert_array_equal(row[8: 8 + k], table[row[7]: row[7] + k])
+    else:
+        assert np.all(n_inl == 0)
+    work = work[:, :8].copy()
+    work[:, 4] &= 0xFFFF
     sizes = work[:, 3] - work[:, 2]
     split = work[:, 4] > 1
     # chunks of split sequences first (their merges overlap later units), each group longest first
@@ -204,7 +217,6 @@ def test_decode_plan_covers_every_token_once(case):
     hks = Hkv * nsub
     cover = {}
     groups = {}
-    tab_off = np.concatenate([[0], np.cumsum([(int(x) + B - 1) // B for x in lens])])
     for s, hc, j0, j1, nc, rec, ctr, tab in work.tolist():
         h, c = hc & 0xFFFF, hc >> 16
         assert 0 <= s < len(lens) and 0 <= h < hks and 0 <= j0 <= j1 <= lens[s] and 0 <= c < nc
