@@ -247,6 +247,47 @@ def bench_c3(steps, warmup, plan_sweep=()):
     return res
 
 
+def bench_prefill(steps, warmup):
+    """Prompt attention (qk_paged_causal_attn) of one sequence, Qwen attention shape
+    (14q/2kv, D 64, fp16, BLOCK 16), prompts of 256 and 2048 tokens at position 0."""
+    from kvcache_amd import KVC_F16, ops
+    from kvcache_amd.device import DeviceBuffer, Event, fill_normal, synchronize
+    Hq, Hkv, D, B = 14, 2, 64, 16
+    res = {"workload": "prefill attention, one sequence, 14q/2kv D64 fp16 BLOCK 16, causal from position 0"}
+    for P in (256, 2048):
+        nb = (P + B - 1) // B
+        table = np.random.default_rng(P).permutation(nb).astype(np.int32)
+        kp, vp = DeviceBuffer(nb * Hkv * B * D * 2), DeviceBuffer(nb * Hkv * B * D * 2)
+        q, out = DeviceBuffer(P * Hq * D * 2), DeviceBuffer(P * Hq * D * 2)
+        for i, buf in enumerate((kp, vp, q)):
+            fill_normal(buf, buf.nbytes // 2, KVC_F16, seed=70 + i)
+        dt = DeviceBuffer.from_numpy(table)
+        ws = DeviceBuffer(max(int(lib_call("kvc_paged_causal_attn_workspace_size", 0, P, Hq, Hkv, D, B, KVC_F16)), 256))
+
+        def launch():
+            ops.qk_paged_causal_attn(q, out, kp, vp, dt, 0, P, Hq, Hkv, D, B, 1.0 / np.sqrt(D), workspace=ws)
+        for _ in range(warmup):
+            launch()
+        synchronize()
+        e0, e1 = Event(), Event()
+        e0.record()
+        for _ in range(steps):
+            launch()
+        e1.record()
+        synchronize()
+        us = e0.elapsed_ms(e1) / steps * 1e3
+        kv_once = P * Hkv * D * 2 * 2
+        kv_per_query = (P * (P + 1) // 2) * Hkv * D * 2 * 2
+        res[f"P{P}"] = {"us": round(us, 2), "kv_bytes_once": kv_once, "kv_bytes_read": kv_per_query,
+                        "GBps_read": round(kv_per_query / (us * 1e-6) / 1e9, 1)}
+    return res
+
+
+def lib_call(name, *args):
+    from kvcache_amd._native import lib
+    return getattr(lib(), name)(*args)
+
+
 def bench_c4():
     """Config 4: 256 requests, width 32, 2048 MB pool, 24 layers of write + GQA decode
     per step (14q/2kv, D 64, fp16); continuous vs static, offline and Poisson 400/s."""
@@ -318,7 +359,7 @@ def main() -> int:
     ap.add_argument("--plan-sweep", type=str, default="", help="comma list of planned targets to time")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="only run 10 device-to-device copies of MIB MiB (HBM counter calibration) and exit")
-    ap.add_argument("--only", choices=["c3", "c4"], default=None,
+    ap.add_argument("--only", choices=["c3", "c4", "prefill"], default=None,
                     help="run only config 3 or config 4 and print its result (profiling)")
     ap.add_argument("--warm", action="store_true",
                     help="also time the planned path on one pool copy (Infinity-Cache resident)")
@@ -350,7 +391,8 @@ def main() -> int:
         return copy_calibration(a.copy_calib)
     sweep_targets = [int(x) for x in a.plan_sweep.split(",") if x]
     if a.only:
-        res = bench_c3(a.steps, a.warmup, sweep_targets) if a.only == "c3" else bench_c4()
+        res = (bench_c3(a.steps, a.warmup, sweep_targets) if a.only == "c3" else
+               bench_prefill(a.steps, a.warmup) if a.only == "prefill" else bench_c4())
         print(json.dumps(res), flush=True)
         return 0
     if a.lengths == "reference":
@@ -418,6 +460,11 @@ def main() -> int:
             log(f"C3: {extras['c3']}")
         except Exception as e:  # noqa: BLE001 -- extras never hide the headline
             extras["c3"] = {"error": repr(e)}
+        try:
+            extras["prefill"] = bench_prefill(a.steps, a.warmup)
+            log(f"prefill: {extras['prefill']}")
+        except Exception as e:  # noqa: BLE001
+            extras["prefill"] = {"error": repr(e)}
         try:
             extras["c4"] = bench_c4()
             log(f"C4: {json.dumps(extras['c4'])}")

@@ -70,6 +70,13 @@ inline int qk_batched_write_kv(const half* k, const half* v, half* k_pool, half*
     return kvc_batched_write_kv(k, v, k_pool, v_pool, table_all, tab_off, wpos, N, Hkv, D, BLOCK, KVC_F16, stream);
 }
 
+inline int qk_paged_causal_attn(const half* q, half* out, const half* k_pool, const half* v_pool,
+                                const int* block_table_dev, int q_pos_base, int Nq, int Hq, int Hkv, int D, int BLOCK,
+                                float scale, kvc_stream_t stream = nullptr) {
+    return kvc_paged_causal_attn(q, out, k_pool, v_pool, block_table_dev, q_pos_base, Nq, Hq, Hkv, D, BLOCK, scale,
+                                 KVC_F16, nullptr, 0, stream);
+}
+
 // The reference sizes nothing by the longest sequence here; the split-K plan
 // needs an upper bound, so `cap` (max cur_len) is an extra trailing argument
 // with a generous default.

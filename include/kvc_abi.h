@@ -211,6 +211,18 @@ int kvc_batched_paged_append_decode_planned(const void* q, const void* k_new, co
                                             int dtype, const int* work, int n_units, int n_records,
                                             void* workspace, size_t workspace_bytes, kvc_stream_t stream);
 
+/* qk_paged_causal_attn (qwen_kernels.h:19-21, qwen_kernels.cu:146-181): the prompt
+ * (prefill) attention of one sequence.  Query i of q [Nq, Hq, D] sits at position
+ * q_pos_base + i and attends causally to positions 0 .. q_pos_base + i of the
+ * paged pools through block_table; out is [Nq, Hq, D].  Runs the batched decode
+ * kernels with query i as a sequence of length q_pos_base + i + 1 sharing the one
+ * table (grouped-query heads on the matrix cores, long prefixes split and merged).
+ * workspace as for the batched decode (NULL: library-owned). */
+int kvc_paged_causal_attn(const void* q, void* out, const void* k_pool, const void* v_pool, const int* block_table,
+                          int q_pos_base, int Nq, int Hq, int Hkv, int D, int BLOCK, float scale, int dtype,
+                          void* workspace, size_t workspace_bytes, kvc_stream_t stream);
+size_t kvc_paged_causal_attn_workspace_size(int q_pos_base, int Nq, int Hq, int Hkv, int D, int BLOCK, int dtype);
+
 /* launch_flash_decode (kv_cache.h:32-34, flash_decode.cu:103-126): one sequence,
  * contiguous [H,S,D], num_splits clamped to [1, cur_len]; split j covers
  * [j*ceil(L/ns), ...) and the partials are merged by log-sum-exp.  Unlike the

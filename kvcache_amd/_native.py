@@ -107,6 +107,8 @@ _SIGS = {
         i32, [vp, vp, vp, vp, i32, vp, i32, i32, i32, i32, i32, f32, i32, vp, i32, i32, vp, sz, vp]),
     "kvc_batched_paged_append_decode_planned": (
         i32, [vp, vp, vp, vp, vp, vp, vp, i32, vp, i32, i32, i32, i32, i32, f32, i32, vp, i32, i32, vp, sz, vp]),
+    "kvc_paged_causal_attn": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, f32, i32, vp, sz, vp]),
+    "kvc_paged_causal_attn_workspace_size": (sz, [i32, i32, i32, i32, i32, i32, i32]),
     "kvc_flash_decode": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, f32, i32, i32, vp, sz, vp]),
     "kvc_flash_decode_workspace_size": (sz, [i32, i32, i32]),
     "kvc_block_allocator_create": (i32, [i32, C.POINTER(vp)]),

@@ -256,7 +256,7 @@ int check_common(int N, int Hq, int Hkv, int D, int dtype, const void* q, const 
 int run_batched(const void* q, const void* k, const void* v, const int* table_all, const int* tab_off,
                 const int* cur_len, int fixed_len, void* out, int N, int Hq, int Hkv, int D, int BLOCK,
                 long long seq_stride, long long head_stride, int cap, float scale, int dtype, int split,
-                bool paged, void* ws, size_t ws_bytes, hipStream_t st) {
+                bool paged, void* ws, size_t ws_bytes, hipStream_t st, int causal = 0) {
     int rc = check_common(N, Hq, Hkv, D, dtype, q, k, v, out);
     if (rc || N == 0) return rc;
     if (paged && (BLOCK <= 0 || !table_all)) return set_error(KVC_ERR_ARG, "paged decode needs BLOCK > 0 and a block table");
@@ -271,6 +271,7 @@ int run_batched(const void* q, const void* k, const void* v, const int* table_al
     DecodeParams& p = L.p;
     p.q = q; p.k = k; p.v = v; p.out = out;
     p.table_all = table_all; p.tab_off = tab_off; p.cur_len = cur_len; p.fixed_len = fixed_len; p.cap = cap;
+    p.causal = causal;
     p.seq_stride = seq_stride; p.head_stride = head_stride;
     p.N = N; p.Hq = Hq; p.Hkv = Hkv; p.block = paged ? BLOCK : 1;
     p.group = Hq / Hkv; p.nsub = pl.nsub;
@@ -713,6 +714,23 @@ int kvc_batched_paged_decode_split(const void* q, const void* k_pool, const void
         return run_batched(q, k_pool, v_pool, table_all, tab_off, cur_len, 0, out, N, Hq, Hkv, D, BLOCK, 0, 0, cap,
                            scale, dtype, split, true, ws, ws_bytes, S(st));
     });
+}
+
+int kvc_paged_causal_attn(const void* q, void* out, const void* k_pool, const void* v_pool, const int* block_table,
+                          int q_pos_base, int Nq, int Hq, int Hkv, int D, int BLOCK, float scale, int dtype, void* ws,
+                          size_t ws_bytes, kvc_stream_t st) {
+    return guarded([&]() -> int {
+        if (q_pos_base < 0 || Nq < 0) return set_error(KVC_ERR_ARG, "q_pos_base and Nq must be >= 0");
+        if ((long long)q_pos_base + Nq > INT_MAX) return set_error(KVC_ERR_ARG, "q_pos_base + Nq overflows");
+        // query i is a sequence of length q_pos_base + i + 1 over the one block table
+        return run_batched(q, k_pool, v_pool, block_table, nullptr, nullptr, q_pos_base, out, Nq, Hq, Hkv, D, BLOCK,
+                           0, 0, q_pos_base + Nq, scale, dtype, 0, true, ws, ws_bytes, S(st), 1);
+    });
+}
+
+size_t kvc_paged_causal_attn_workspace_size(int q_pos_base, int Nq, int Hq, int Hkv, int D, int BLOCK, int dtype) {
+    if (q_pos_base < 0 || Nq < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || !d_ok(D) || BLOCK <= 0) return 0;
+    return plan_batched(Nq, Hq, Hkv, D, BLOCK, q_pos_base + Nq, dtype, 0, true).ws_bytes;
 }
 
 int kvc_decode_plan_entry_ints(int Hq, int Hkv, int D, int BLOCK, int dtype) {

@@ -126,7 +126,7 @@ __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirs
 // Length and chunk range of unit chunk c of sequence s.  Returns false when the
 // unit has no chunk (beyond the sequence's chunk count).
 __device__ __forceinline__ bool chunk_range(const DecodeParams& p, int s, int c, int& nc, int& j0, int& j1) {
-    int L = p.cur_len ? p.cur_len[s] : p.fixed_len;
+    int L = p.cur_len ? p.cur_len[s] : (p.causal ? p.fixed_len + s + 1 : p.fixed_len);
     L = min(max(L, 0), p.cap);  // a length above the stated cap never reads past the caches
     if (p.num_splits > 0) {
         nc = p.num_splits;

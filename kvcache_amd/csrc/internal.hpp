@@ -41,6 +41,7 @@ struct DecodeParams {
     int num_splits;           // >0: chunk = ceil(L / num_splits) per sequence
     int max_chunks;           // chunks per sequence covered by the grid
     int fixed_len;            // length used when cur_len == nullptr
+    int causal;               // 1: sequence s has length fixed_len + s + 1 (prompt queries, causal mask)
     int cap;                  // lengths are clamped to cap (the caller's stated maximum)
     int lpb_shift;            // kPagedUniform: log2(wave-loads per block)
     float scale_log2;         // softmax scale * log2(e)

@@ -18,7 +18,7 @@ __all__ = [
     "launch_batched_paged_flash", "launch_flash_decode", "qk_write_kv", "qk_batched_write_kv",
     "qk_batched_paged_decode_attn", "write_kv_slots", "decode_workspace_size", "decode_auto_split",
     "decode_plan", "planned_workspace_size", "launch_batched_paged_planned", "launch_batched_paged_append_planned",
-    "flash_decode_workspace_size", "KVC_F16", "KVC_F32",
+    "flash_decode_workspace_size", "qk_paged_causal_attn", "KVC_F16", "KVC_F32",
 ]
 
 
@@ -143,6 +143,15 @@ def launch_batched_paged_append_planned(q, k_new, v_new, wpos, k_pool, v_pool, t
                                                         _p(table_all), int(table_len), _p(out), N, Hq, Hkv, D, BLOCK,
                                                         scale, dtype, _p(work_dev), n_units, n_records, ws, wsb,
                                                         stream))
+
+
+def qk_paged_causal_attn(q, out, k_pool, v_pool, block_table, q_pos_base, Nq, Hq, Hkv, D, BLOCK, scale, *,
+                         dtype=KVC_F16, workspace=None, stream=None):
+    """Prompt attention of one sequence (qwen_kernels.h:19-21): query i at position
+    q_pos_base + i attends causally over the paged pools through block_table."""
+    ws, wsb = _ws(workspace)
+    check(lib().kvc_paged_causal_attn(_p(q), _p(out), _p(k_pool), _p(v_pool), _p(block_table), q_pos_base, Nq, Hq,
+                                      Hkv, D, BLOCK, scale, dtype, ws, wsb, stream))
 
 
 def write_kv_slots(k, v, k_pool, v_pool, slot_map, rows, Hkv, D, BLOCK, *, dtype=KVC_F16, stream=None):

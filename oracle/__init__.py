@@ -236,3 +236,16 @@ def run_ref_alloc_driver(script: str) -> list[int]:
     """Runs the reference's own BlockAllocator/Sequence (oracle/_ref) over a script."""
     r = subprocess.run([str(REF_DRIVER)], input=script, capture_output=True, text=True, check=True)
     return [int(x) for x in r.stdout.split()]
+
+
+def paged_causal(q, k_pool, v_pool, block_table, q_pos_base, Hkv, BLOCK, scale, nthreads=1):
+    """Prompt attention of one sequence (qwen_kernels.cu:146-181): query i at position
+    q_pos_base + i over positions 0..q_pos_base + i.  Each query is the batched paged
+    decode of a sequence of that length over the same table (batched.cu:91-130 with
+    the causal length of qwen_kernels.cu:151)."""
+    import numpy as np
+    n = q.shape[0]
+    lens = np.arange(q_pos_base + 1, q_pos_base + n + 1, dtype=np.int32)
+    tab_off = np.zeros(n + 1, dtype=np.int32)
+    return batched_paged(q, k_pool, v_pool, np.asarray(block_table, np.int32), tab_off, lens, Hkv, BLOCK, scale,
+                         nthreads=nthreads)

@@ -372,3 +372,45 @@ def test_mfma_merge_modes(orc, mode):
         for split in (512, 1024):  # 8 and 4 chunks of the longest sequence
             got = run_batched(q, K, V, lens, Hkv, B, KVC_F16, split=split)
             assert np.abs(got - ref).max() <= 2e-3
+
+
+# ---- prompt (prefill) attention: qk_paged_causal_attn (qwen_kernels.h:19-21) ---------
+@pytest.mark.parametrize("dtype,Hq,Hkv", [(KVC_F16, 14, 2), (KVC_F16, 8, 8), (KVC_F32, 8, 2)])
+@pytest.mark.parametrize("base,n", [(0, 1), (0, 37), (100, 64), (0, 600)])
+def test_paged_causal_attn(orc, dtype, Hq, Hkv, base, n):
+    say(f"causal prefill dtype={dtype} Hq={Hq} Hkv={Hkv} base={base} n={n}")
+    D, B = 64, 16
+    nt = as_np(dtype)
+    S = base + n
+    nb = (S + B - 1) // B
+    table = np.random.default_rng(base + n).permutation(nb + 9)[:nb].astype(np.int32)
+    NB = int(table.max()) + 1
+    kp, vp = normal((NB, Hkv, B, D), 190, nt), normal((NB, Hkv, B, D), 191, nt)
+    q = normal((n, Hq, D), 192, nt)
+    scale = float(1.0 / np.sqrt(D))
+    out = DeviceBuffer(q.nbytes)
+    ops.qk_paged_causal_attn(dev(q), out, dev(kp), dev(vp), dev(table), base, n, Hq, Hkv, D, B, scale, dtype=dtype)
+    got = host(out, nt, q.shape).astype(np.float64)
+    want = orc.paged_causal(q, kp, vp, table, base, Hkv, B, scale)
+    assert np.abs(got - want).max() <= tol(dtype)
+
+
+def test_prefill_flow_write_then_causal_attn(orc):
+    """The model path's prefill (qwen_serve.cu:106-108): write the P prompt rows of
+    K/V through the sequence's table, then causal attention over them."""
+    say("prefill flow")
+    P, Hq, Hkv, D, B = 200, 14, 2, 64, 16
+    nb = (P + B - 1) // B
+    table = np.random.default_rng(11).permutation(40)[:nb].astype(np.int32)
+    kp0 = np.zeros((40, Hkv, B, D), np.float16)
+    K, V, q = normal((P, Hkv, D), 193, np.float16), normal((P, Hkv, D), 194, np.float16), normal((P, Hq, D), 195, np.float16)
+    dk, dv, dt = dev(kp0), dev(kp0), dev(table)
+    ops.qk_write_kv(dev(K), dev(V), dk, dv, dt, 0, P, Hkv, D, B)
+    out = DeviceBuffer(q.nbytes)
+    scale = float(1.0 / np.sqrt(D))
+    ops.qk_paged_causal_attn(dev(q), out, dk, dv, dt, 0, P, Hq, Hkv, D, B, scale)
+    got = host(out, np.float16, q.shape).astype(np.float64)
+    # expected: causal attention over the contiguous rows
+    Kc, Vc = K.transpose(1, 0, 2)[None], V.transpose(1, 0, 2)[None]          # [1, Hkv, P, D]
+    want = np.stack([orc.batched_contig(q[i:i + 1], Kc, Vc, np.array([i + 1], np.int32), scale)[0] for i in range(P)])
+    assert np.abs(got - want).max() <= 2e-3

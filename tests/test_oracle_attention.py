@@ -189,3 +189,44 @@ def test_fp16_inputs_decoded_exactly(orc):
     a = orc.batched_contig(q, K, V, lens, 0.125)
     b = orc.batched_contig(q.astype(np.float32), K.astype(np.float32), V.astype(np.float32), lens, 0.125)
     np.testing.assert_array_equal(a, b)
+
+
+# ---- prompt (prefill) attention: qwen_kernels.cu:146-181 ------------------------------
+def _scatter(K, V, block, perm):
+    """K/V [Hkv, S, D] of one sequence into a pool through table perm."""
+    Hkv, S, D = K.shape
+    nb = (S + block - 1) // block
+    NB = int(perm[:nb].max()) + 1
+    kp = np.zeros((NB, Hkv, block, D))
+    vp = np.zeros_like(kp)
+    for b in range(nb):
+        t0, t1 = b * block, min(S, (b + 1) * block)
+        kp[perm[b], :, : t1 - t0] = K[:, t0:t1]
+        vp[perm[b], :, : t1 - t0] = V[:, t0:t1]
+    return kp, vp, perm[:nb].astype(np.int32)
+
+
+@pytest.mark.parametrize("base,n", [(0, 1), (0, 23), (40, 9)])
+def test_paged_causal_against_masked_softmax(orc, base, n):
+    """The causal restatement against a masked score matrix (-inf above the
+    diagonal, row softmax): a different formulation of the same attention."""
+    rng = np.random.default_rng(base + n)
+    Hq, Hkv, D, B = 6, 2, 16, 4
+    S = base + n
+    # fp32 inputs (the restatement's storage type), compared in double
+    q = rng.standard_normal((n, Hq, D)).astype(np.float32)
+    K, V = rng.standard_normal((Hkv, S, D)).astype(np.float32), rng.standard_normal((Hkv, S, D)).astype(np.float32)
+    kp, vp, table = _scatter(K, V, B, rng.permutation(64))
+    kp, vp = kp.astype(np.float32), vp.astype(np.float32)
+    q64, K, V = q.astype(np.float64), K.astype(np.float64), V.astype(np.float64)
+    scale = 1 / np.sqrt(D)
+    got = orc.paged_causal(q, kp, vp, table, base, Hkv, B, scale)
+    g = Hq // Hkv
+    for h in range(Hq):
+        sc = q64[:, h] @ K[h // g].T * scale                     # [n, S]
+        mask = np.arange(S)[None, :] > (base + np.arange(n))[:, None]
+        sc[mask] = -np.inf
+        want = softmax(sc, axis=1) @ V[h // g]
+        np.testing.assert_allclose(got[:, h], want, rtol=1e-12, atol=1e-12)
+    if base == 0:
+        np.testing.assert_allclose(got[0], np.repeat(V[:, 0], g, axis=0), rtol=0, atol=0)  # first query sees only key 0
