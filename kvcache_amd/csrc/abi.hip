@@ -340,7 +340,9 @@ PlanShape plan_shape(int Hq, int Hkv, int D, int BLOCK, int dtype) {
     // units to aim for per CU: ~3.5 for one or two heads per wave (about 1.3 rounds
     // of the 4 units a CU runs at once), ~3 for larger groups
     ps.slots = ps.G <= 2 ? 256 * 7 / 2 : 256 * 3;
-    ps.entry_ints = kPlanInts;
+    // uniform paging: the first 8 block ids ride in the entry (the first batch of
+    // every wave of a 4-wave unit touches at most 8 blocks for 16-token blocks)
+    ps.entry_ints = ps.uniform ? kPlanInts + 8 : kPlanInts;
     return ps;
 }
 

@@ -352,10 +352,18 @@ __global__ __launch_bounds__(WPB * kWave) void split_kernel(DecodeParams p) {
     const int tslot = lane / LPT;
     const int dl = lane % LPT;
 
+    // planned entries may carry the chunk's first block ids after the 8-int header
+    // (one int per lane, read together with the header), so the first batch of
+    // loads does not wait for the table
+    int ev = 0;
+    if constexpr (PLANNED && UNIFORM) {
+        if (p.work_ints > 8 && lane < p.work_ints) ev = p.work[(size_t)blockIdx.x * p.work_ints + lane];
+    }
     Unit u;
     if (!load_unit<PLANNED>(p, G, u)) return;
     const int s = u.s, hk = u.hk, sub = u.sub, c = u.c, nc = u.nc, j0 = u.j0, j1 = u.j1;
     const int tab_start = u.tab_start;
+    const int n_inl = u.n_inline;  // block ids carried by the planned entry
     const size_t rec0 = u.rec0, cstride = u.cstride, ctr_idx = u.ctr_idx;
     const int hq0 = hk * p.group + sub * G;
     const int nwl = (j1 - j0 + TPW - 1) / TPW;                          // wave-loads in the chunk
@@ -453,7 +461,9 @@ __global__ __launch_bounds__(WPB * kWave) void split_kernel(DecodeParams p) {
                     tile = cbase + (size_t)max(t0, 0) * ROW;
                 } else {
                     const int rel = i >> p.lpb_shift;           // block of the chunk
-                    const int phys = __builtin_amdgcn_readlane(tbl, min(rel, kWave - 1));
+                    int phys;
+                    if (PLANNED && rel < n_inl) phys = __builtin_amdgcn_readlane(ev, 8 + min(rel, kWave - 9));
+                    else phys = __builtin_amdgcn_readlane(tbl, min(rel, kWave - 1));
                     const int in = (i & ((1 << p.lpb_shift) - 1)) * TPW;
                     tile = ((size_t)(phys * p.Hkv + hk) * p.block + in) * ROW;
                 }
