@@ -440,6 +440,62 @@ int guarded(F&& f) {
 
 inline hipStream_t S(kvc_stream_t s) { return static_cast<hipStream_t>(s); }
 
+// ---- prompt attention on the matrix cores: 16 queries of one head per unit ----
+bool causal_tile_path(int Nq, int Hq, int Hkv, int D, int BLOCK, int dtype) {
+    if (tuning().mfma == 0 || dtype != KVC_F16 || (D != 64 && D != 128) || BLOCK <= 0 || BLOCK % 16) return false;
+    if (Hq <= 0 || Hkv <= 0 || Hq % Hkv) return false;
+    return (long long)Nq * Hq * D * 2 < (1LL << 31);  // the q descriptor spans all queries
+}
+
+// Key chunks: enough units (query tiles x heads x chunks) to fill the CUs about
+// twice, chunks of at least 512 tokens and at most 1024 blocks.
+Plan plan_causal_tile(int base, int Nq, int Hq, int Hkv, int D, int BLOCK) {
+    Plan pl;
+    pl.mfma = true;
+    pl.G = Hq / Hkv;
+    pl.nsub = 1;
+    pl.mode = kCausalTile;
+    const long long lmax = std::max(1LL, (long long)base + Nq);
+    const long long tiles = (long long)((Nq + 15) / 16) * Hq;
+    const long long want = std::max(1LL, (512 + tiles - 1) / std::max(tiles, 1LL));
+    long long ch = std::max<long long>(512, (lmax + want - 1) / want);
+    long long p2 = 1;
+    while (p2 < ch) p2 <<= 1;
+    ch = std::min<long long>(p2, (long long)kMfmaMaxChunkBlocksHost * BLOCK);
+    ch = (ch + BLOCK - 1) / BLOCK * BLOCK;
+    pl.chunk = (int)ch;
+    pl.max_chunks = (int)((lmax + ch - 1) / ch);
+    const int t = tuning().waves_per_block;
+    pl.wpb = (t == 4 || t == 8) ? t : (tiles * pl.max_chunks >= 512 ? 4 : 8);
+    size_workspace(pl, Nq, Hq, Hkv, D);
+    return pl;
+}
+
+int run_causal_tile(const void* q, void* out, const void* k, const void* v, const int* table, int base, int Nq, int Hq,
+                    int Hkv, int D, int BLOCK, float scale, void* ws, size_t ws_bytes, hipStream_t st) {
+    int rc = check_common(Nq, Hq, Hkv, D, KVC_F16, q, k, v, out);
+    if (rc || Nq == 0) return rc;
+    if (!table) return set_error(KVC_ERR_ARG, "null block table");
+    if (!std::isfinite(scale)) return set_error(KVC_ERR_ARG, "scale must be finite");
+    const Plan pl = plan_causal_tile(base, Nq, Hq, Hkv, D, BLOCK);
+    DecodeLaunch L{};
+    DecodeParams& p = L.p;
+    p.q = q; p.k = k; p.v = v; p.out = out;
+    p.table_all = table;
+    p.N = Nq; p.Hq = Hq; p.Hkv = Hkv; p.block = BLOCK;
+    p.group = Hq / Hkv; p.nsub = 1;
+    p.chunk_tokens = pl.chunk; p.max_chunks = pl.max_chunks;
+    p.fixed_len = base; p.cap = base + Nq; p.causal = 1;
+    p.scale_log2 = scale * 1.4426950408889634f;
+    rc = resolve_workspace(pl, ws, ws_bytes, p);
+    if (rc) return rc;
+    p.merge_mode = kMergeKernel;
+    L.dtype = KVC_F16; L.D = D; L.G = pl.G; L.mode = kCausalTile; L.wpb = pl.wpb; L.batch = tuning().batch;
+    L.need_merge = pl.max_chunks > 1;
+    L.mfma = true;
+    return launch_decode(L, st);
+}
+
 int run_planned(const void* q, const void* k_new, const void* v_new, const int* wpos, const void* k_pool,
                 const void* v_pool, const int* table_all, int table_len, void* out, int N, int Hq, int Hkv, int D,
                 int BLOCK, float scale, int dtype, const int* work, int n_units, int n_records, void* ws,
@@ -724,6 +780,9 @@ int kvc_paged_causal_attn(const void* q, void* out, const void* k_pool, const vo
     return guarded([&]() -> int {
         if (q_pos_base < 0 || Nq < 0) return set_error(KVC_ERR_ARG, "q_pos_base and Nq must be >= 0");
         if ((long long)q_pos_base + Nq > INT_MAX) return set_error(KVC_ERR_ARG, "q_pos_base + Nq overflows");
+        if (causal_tile_path(Nq, Hq, Hkv, D, BLOCK, dtype))
+            return run_causal_tile(q, out, k_pool, v_pool, block_table, q_pos_base, Nq, Hq, Hkv, D, BLOCK, scale, ws,
+                                   ws_bytes, S(st));
         // query i is a sequence of length q_pos_base + i + 1 over the one block table
         return run_batched(q, k_pool, v_pool, block_table, nullptr, nullptr, q_pos_base, out, Nq, Hq, Hkv, D, BLOCK,
                            0, 0, q_pos_base + Nq, scale, dtype, 0, true, ws, ws_bytes, S(st), 1);
@@ -732,6 +791,7 @@ int kvc_paged_causal_attn(const void* q, void* out, const void* k_pool, const vo
 
 size_t kvc_paged_causal_attn_workspace_size(int q_pos_base, int Nq, int Hq, int Hkv, int D, int BLOCK, int dtype) {
     if (q_pos_base < 0 || Nq < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || !d_ok(D) || BLOCK <= 0) return 0;
+    if (causal_tile_path(Nq, Hq, Hkv, D, BLOCK, dtype)) return plan_causal_tile(q_pos_base, Nq, Hq, Hkv, D, BLOCK).ws_bytes;
     return plan_batched(Nq, Hq, Hkv, D, BLOCK, q_pos_base + Nq, dtype, 0, true).ws_bytes;
 }
 

@@ -768,6 +768,7 @@ int launch_gqa_mode(DecodeLaunch L, dim3 grid, hipStream_t st) {
         case kContiguous:     L.lds_pad = lds_pad(gqa_mfma_kernel<D, kContiguous, WPB>, L.wg_per_cu); hipLaunchKernelGGL((gqa_mfma_kernel<D, kContiguous, WPB>), grid, block, L.lds_pad, st, L.p); break;
         case kPagedUniform:   L.lds_pad = lds_pad(gqa_mfma_kernel<D, kPagedUniform, WPB>, L.wg_per_cu); hipLaunchKernelGGL((gqa_mfma_kernel<D, kPagedUniform, WPB>), grid, block, L.lds_pad, st, L.p); break;
         case kPlannedUniform: L.lds_pad = lds_pad(gqa_mfma_kernel<D, kPlannedUniform, WPB>, L.wg_per_cu); hipLaunchKernelGGL((gqa_mfma_kernel<D, kPlannedUniform, WPB>), grid, block, L.lds_pad, st, L.p); break;
+        case kCausalTile:     hipLaunchKernelGGL((gqa_mfma_kernel<D, kCausalTile, WPB>), grid, block, 0, st, L.p); break;
         default: return set_error(KVC_ERR_ARG, "matrix-core decode: unsupported addressing mode");
     }
     return KVC_OK;
@@ -776,7 +777,8 @@ int launch_gqa_mode(DecodeLaunch L, dim3 grid, hipStream_t st) {
 template <typename T, int D>
 int launch_gqa(const DecodeLaunch& L, dim3 grid, hipStream_t st) {
     if constexpr (std::is_same<T, _Float16>::value && (D == 64 || D == 128)) {
-        if (L.p.group > kMfmaMaxHeads || L.p.nsub != 1) return set_error(KVC_ERR_ARG, "matrix-core decode: bad group");
+        if (L.mode != kCausalTile && (L.p.group > kMfmaMaxHeads || L.p.nsub != 1))
+            return set_error(KVC_ERR_ARG, "matrix-core decode: bad group");
         if (L.wpb == 8) return launch_gqa_mode<D, 8>(L, grid, st);
         if (L.wpb == 4) return launch_gqa_mode<D, 4>(L, grid, st);
         return set_error(KVC_ERR_ARG, "waves per block must be 4 or 8");
@@ -790,7 +792,9 @@ int launch_gqa(const DecodeLaunch& L, dim3 grid, hipStream_t st) {
 template <typename T, int D>
 int launch_decode_d(const DecodeLaunch& L, hipStream_t st) {
     const bool planned = L.mode == kPlannedUniform || L.mode == kPlannedPerLane;
-    const long long units = planned ? (long long)L.units : (long long)L.p.max_chunks * L.p.N * L.p.Hkv * L.p.nsub;
+    const long long units = planned ? (long long)L.units
+                          : L.mode == kCausalTile ? (long long)L.p.max_chunks * ((L.p.N + 15) / 16) * L.p.Hq
+                                                  : (long long)L.p.max_chunks * L.p.N * L.p.Hkv * L.p.nsub;
     if (units <= 0) return KVC_OK;
     if (units > (long long)INT_MAX) return set_error(KVC_ERR_ARG, "decode grid too large");
     int rc = L.mfma ? launch_gqa<T, D>(L, dim3((unsigned)units), st) : launch_split_g<T, D>(L, dim3((unsigned)units), st);

@@ -48,6 +48,9 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(DecodeParams p) {
     constexpr int VL = 16 * ROW / 1024;        // 1 KiB wave loads per 16-row V subtile
     constexpr bool PLANNED = MODE == kPlannedUniform;
     constexpr bool PAGED = MODE != kContiguous;
+    // prompt attention: the 16 columns are 16 consecutive queries of one head (not
+    // the heads of one query); query q attends to positions 0 .. fixed_len + q
+    constexpr bool CAUSAL = MODE == kCausalTile;
     constexpr int kTileBytes = kMfmaTile * ROW;
     constexpr int kMainBytes = WPB * kTileBytes;
     constexpr int kEpiBytes = WPB * kMfmaMaxHeads * (D + 2) * 4;
@@ -71,9 +74,29 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(DecodeParams p) {
         if (p.work_ints == kWave) ev = p.work[(size_t)blockIdx.x * kWave + lane];
     }
     Unit u;
-    if (!load_unit<PLANNED>(p, heads, u)) return;
+    int qh = 0, q0 = 0;  // causal: query head and first query of the tile
+    if constexpr (CAUSAL) {
+        int unit = blockIdx.x;
+        const int ntq = (p.N + 15) / 16;
+        qh = unit % p.Hq;  unit /= p.Hq;
+        q0 = (unit % ntq) * 16;  unit /= ntq;
+        u.c = unit;
+        u.s = 0;
+        u.sub = 0;
+        u.hk = qh / p.group;
+        u.tab_start = 0;
+        const int lmax = min(p.fixed_len + min(q0 + 16, p.N), p.cap);  // keys of the tile's last query
+        u.j0 = u.c * p.chunk_tokens;
+        u.j1 = min(u.j0 + p.chunk_tokens, lmax);
+        if (u.c >= p.max_chunks || u.j0 >= lmax) return;
+        u.nc = (lmax + p.chunk_tokens - 1) / p.chunk_tokens;  // chunks of the tile's last query
+        u.rec0 = 0; u.cstride = 0; u.ctr_idx = 0;
+    } else {
+        if (!load_unit<PLANNED>(p, heads, u)) return;
+    }
     const int s = u.s, hk = u.hk, j0 = u.j0, j1 = u.j1, nc = u.nc;
     const int hq0 = hk * p.group;
+    const int rows = CAUSAL ? 16 : heads;  // output rows of the unit's 16-column block
     const int ntiles = (j1 - j0 + kMfmaTile - 1) / kMfmaTile;
     const int kmax = wave < ntiles ? (ntiles - wave + WPB - 1) / WPB : 0;
 
@@ -101,13 +124,20 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(DecodeParams p) {
     // q as the B operand of QK^T: lane l holds head l%16, dims 8*(l/16) + 32j .. +7;
     // heads past the group read as zero through the descriptor bound.
     f16x8v qb[KJ];
-    {
+    if constexpr (CAUSAL) {
+        // lane l holds query q0 + l%16 of head qh; queries past N read as zero
+        const __amdgpu_buffer_rsrc_t qr = tile_rsrc(p.q, p.N * p.Hq * ROW);
+        const int qoff = ((q0 + n16) * p.Hq + qh) * ROW + g4 * 16;
+#pragma unroll
+        for (int j = 0; j < KJ; ++j) qb[j] = __builtin_bit_cast(f16x8v, buffer_load16(qr, qoff + j * 64));
+    } else {
         const char* qbase = static_cast<const char*>(p.q) + ((size_t)s * p.Hq + hq0) * ROW;
         const __amdgpu_buffer_rsrc_t qr = tile_rsrc(qbase, heads * ROW);
 #pragma unroll
         for (int j = 0; j < KJ; ++j)
             qb[j] = __builtin_bit_cast(f16x8v, buffer_load16(qr, n16 * ROW + g4 * 16 + j * 64));
     }
+    const int qlast = CAUSAL ? p.fixed_len + q0 + n16 : INT_MAX;  // last key this column may see
 
     const char* kb = static_cast<const char*>(p.k);
     const char* vb = static_cast<const char*>(p.v);
@@ -211,7 +241,7 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(DecodeParams p) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int h = i >> 2, r = i & 3;
-            ok[i] = t0 + 16 * h + 4 * g4 + r < j1;
+            ok[i] = t0 + 16 * h + 4 * g4 + r < j1 && t0 + 16 * h + 4 * g4 + r <= qlast;
             sc[i] = S[h][r] * p.scale_log2;
             mx = ok[i] ? fmaxf(mx, sc[i]) : mx;
         }
@@ -288,7 +318,39 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(DecodeParams p) {
 
     _Float16* ob = static_cast<_Float16*>(p.out) + ((size_t)s * p.Hq + hq0) * D;
     const bool atomic_parts = p.merge_mode == kMergeAtomic;
-    for (int idx = tid; idx < heads * D; idx += WPB * kWave) {
+    if constexpr (CAUSAL) {
+        // row g is query q0 + g: written directly when its keys fit one chunk, else as
+        // chunk record ((q * max_chunks + c) * Hq + qh) for the merge kernel
+        for (int idx = tid; idx < 16 * D; idx += WPB * kWave) {
+            const int g = idx / D, d = idx % D, q = q0 + g;
+            if (q >= p.N) continue;
+            const int ncq = (min(p.fixed_len + q + 1, p.cap) + p.chunk_tokens - 1) / p.chunk_tokens;
+            if (u.c >= ncq) continue;  // this chunk lies past the query's keys
+            float M = -FLT_MAX;
+#pragma unroll
+            for (int w = 0; w < WPB; ++w) M = fmaxf(M, e_ml[(w * kMfmaMaxHeads + g) * 2]);
+            float lt = 0.f, at = 0.f;
+#pragma unroll
+            for (int w = 0; w < WPB; ++w) {
+                const float wt = fast_exp2(e_ml[(w * kMfmaMaxHeads + g) * 2] - M);
+                lt = __builtin_fmaf(wt, e_ml[(w * kMfmaMaxHeads + g) * 2 + 1], lt);
+                at = __builtin_fmaf(wt, e_acc[(w * kMfmaMaxHeads + g) * D + d], at);
+            }
+            if (ncq == 1) {
+                static_cast<_Float16*>(p.out)[((size_t)q * p.Hq + qh) * D + d] =
+                    (_Float16)(lt > 0.f ? at * (1.0f / lt) : 0.f);
+            } else {
+                const size_t rec = ((size_t)q * p.max_chunks + u.c) * p.Hq + qh;
+                p.part_acc[rec * D + d] = at;
+                if (d == 0) {
+                    p.part_ml[rec * 2] = M;
+                    p.part_ml[rec * 2 + 1] = lt;
+                }
+            }
+        }
+        return;  // split queries are merged by merge_kernel
+    }
+    for (int idx = tid; idx < rows * D; idx += WPB * kWave) {
         const int g = idx / D, d = idx % D;
         float M = -FLT_MAX;
 #pragma unroll

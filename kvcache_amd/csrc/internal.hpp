@@ -19,7 +19,10 @@ int hip_check(hipError_t e, const char* what);
 // ---------------------------------------------------------------------------
 // kPlanned*: the grid is a host-built work list (kvc_decode_plan) instead of a
 // (chunk, sequence, head) decomposition; otherwise as kPaged*.
-enum DecodeMode { kContiguous = 0, kPagedUniform = 1, kPagedPerLane = 2, kPlannedUniform = 3, kPlannedPerLane = 4 };
+// kCausalTile (matrix-core kernel only): prompt attention, a unit is 16 consecutive
+// queries of one query head over one chunk of keys of the shared block table.
+enum DecodeMode { kContiguous = 0, kPagedUniform = 1, kPagedPerLane = 2, kPlannedUniform = 3, kPlannedPerLane = 4,
+                  kCausalTile = 5 };
 
 struct DecodeParams {
     const void* q;

@@ -376,7 +376,7 @@ def test_mfma_merge_modes(orc, mode):
 
 # ---- prompt (prefill) attention: qk_paged_causal_attn (qwen_kernels.h:19-21) ---------
 @pytest.mark.parametrize("dtype,Hq,Hkv", [(KVC_F16, 14, 2), (KVC_F16, 8, 8), (KVC_F32, 8, 2)])
-@pytest.mark.parametrize("base,n", [(0, 1), (0, 37), (100, 64), (0, 600)])
+@pytest.mark.parametrize("base,n", [(0, 1), (0, 37), (100, 64), (0, 600), (5000, 3)])
 def test_paged_causal_attn(orc, dtype, Hq, Hkv, base, n):
     say(f"causal prefill dtype={dtype} Hq={Hq} Hkv={Hkv} base={base} n={n}")
     D, B = 64, 16
@@ -393,6 +393,11 @@ def test_paged_causal_attn(orc, dtype, Hq, Hkv, base, n):
     got = host(out, nt, q.shape).astype(np.float64)
     want = orc.paged_causal(q, kp, vp, table, base, Hkv, B, scale)
     assert np.abs(got - want).max() <= tol(dtype)
+    if dtype == KVC_F16:  # the query-tiled matrix-core path against the per-query decode path
+        with tuning("mfma", 0):
+            alt = DeviceBuffer(q.nbytes)
+            ops.qk_paged_causal_attn(dev(q), alt, dev(kp), dev(vp), dev(table), base, n, Hq, Hkv, D, B, scale)
+        assert np.abs(got - host(alt, nt, q.shape).astype(np.float64)).max() <= 2e-3
 
 
 def test_prefill_flow_write_then_causal_attn(orc):
