@@ -316,6 +316,21 @@ def bench_c4():
                         "p99_ms": round(st.p99_latency_us / 1e3, 3), "avg_ms": round(st.avg_latency_us / 1e3, 3),
                         "gpu_ms": round(st.gpu_us / 1e3, 2), "makespan_ms": round(st.wall_us / 1e3, 2)}
         out[name] = res
+    # the same offline trace with each admitted prompt processed (K/V writes + causal
+    # attention for all 24 layers) on the measured clock
+    eng_pf = Engine(EngineConfig(n_heads=14, n_kv_heads=2, head_dim=64, block_size=16, num_blocks=num_blocks,
+                                 max_batch=32, n_layers=24, dtype=KVC_F16, kv_write=True, clock_mode=0, prefill=True))
+    p, g, a = Wl.baseline_trace(256, 0.0, 11)
+    res = {}
+    for pol, fn in (("continuous", lambda: run_continuous(p, g, a, eng_pf)),
+                    ("static", lambda: run_static(p, g, a, eng_pf, 32))):
+        st = fn()
+        res[pol] = {"iters": st.iters, "tokens": st.tokens,
+                    "tokens_per_s": round(st.tokens / (st.wall_us * 1e-6), 1) if st.wall_us else 0.0,
+                    "prefill_ms": round(st.prefill_us / 1e3, 2), "gpu_ms": round(st.gpu_us / 1e3, 2),
+                    "slot_util": round(st.slot_util, 4), "p50_ms": round(st.p50_latency_us / 1e3, 3),
+                    "p99_ms": round(st.p99_latency_us / 1e3, 3)}
+    out["offline_with_prefill"] = res
     return out
 
 

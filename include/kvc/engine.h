@@ -41,6 +41,7 @@ struct EngineConfig {
     bool device = true;
     int split_tokens = 0;
     int decode_path = KVC_DECODE_PLANNED;
+    bool prefill = false;     // admitted prompts run K/V writes + causal attention (measured clock)
     uint64_t seed = 0x6b76636163686531ull;
 };
 
@@ -59,6 +60,7 @@ struct EngineStats {
     double p50_latency_us = 0;
     uint64_t step_digest = 0;
     double host_wall_us = 0;
+    double prefill_us = 0;    // GPU time of prompt processing (included in gpu_us and the clock)
 };
 
 // avg / p50 / p99 (nearest rank: sorted[min(floor(q*n), n-1)], engine.h:48-54).
@@ -86,6 +88,7 @@ inline RunnerOptions runner_options(const EngineConfig& c) {
     o.device = c.device;
     o.split_tokens = c.split_tokens;
     o.decode_path = c.decode_path;
+    o.prefill = c.prefill;
     o.seed = c.seed;
     return o;
 }
@@ -159,6 +162,12 @@ struct Engine {
             s->status = SeqStatus::Running;
             running.push_back(s);
             waiting.pop_front();
+            if (cfg.prefill) {  // the prompt is processed on admission
+                const double pu = runner.prefill(*s, kvm);
+                stats.prefill_us += pu;
+                stats.gpu_us += pu;
+                clock += pu;
+            }
         }
         if (running.empty()) {  // 3) idle or done
             if (waiting.empty()) return false;

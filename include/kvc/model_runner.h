@@ -44,6 +44,7 @@ struct RunnerOptions {
     int decode_path = KVC_DECODE_PLANNED;  // or KVC_DECODE_DEVICE_LENGTHS
     int plan_target = 0;     // planned path: tokens per unit (0 automatic)
     bool fuse_append = true; // planned path with kv_write: write the new rows inside the decode launch
+    bool prefill = false;    // run each admitted prompt's K/V writes + causal attention (prefill)
     uint64_t seed = 0x6b76636163686531ull;
 };
 
@@ -67,6 +68,13 @@ struct ModelRunner {
 
     size_t meta_cap = 0;     // ints in d_meta and in each pinned ring buffer
     std::vector<int> h_tab, h_off, h_len, h_wpos, h_slot, h_work;
+    // prefill: synthetic prompt q/k/v and output for up to pf_cap tokens, the prompt's table
+    void *pq = nullptr, *pk = nullptr, *pv = nullptr, *pout = nullptr;
+    int* d_ptab = nullptr;
+    int* h_ptab = nullptr;
+    void* h_ptab_ev = nullptr;
+    int pf_cap = 0, ptab_cap = 0;
+    double last_prefill_us = 0;
     uint64_t digest = 1469598103934665603ull;
     long long last_sum_len = 0;
     int last_cap = 0;
@@ -105,6 +113,8 @@ struct ModelRunner {
     ~ModelRunner() {
         if (stream) kvc_stream_synchronize(stream);
         kvc_free(dq); kvc_free(dk); kvc_free(dv); kvc_free(dout); kvc_free(d_meta); kvc_free(ws);
+        kvc_free(pq); kvc_free(pk); kvc_free(pv); kvc_free(pout); kvc_free(d_ptab); kvc_host_free(h_ptab);
+        kvc_event_destroy(h_ptab_ev);
         for (int i = 0; i < kRing; ++i) { kvc_host_free(h_meta[i]); kvc_event_destroy(h_ev[i]); }
         kvc_event_destroy(ev0); kvc_event_destroy(ev1);
         kvc_stream_destroy(stream);
@@ -266,6 +276,67 @@ struct ModelRunner {
         float ms = 0.f;
         kvc::check(kvc_event_elapsed_ms(&ms, ev0, ev1), "event elapsed");
         return (double)ms * 1e3;
+    }
+
+    // Prompt processing of one admitted sequence, the attention part of the model
+    // path's prefill (qwen_serve.cu:90-124): per layer, write the prompt's K/V rows
+    // through its table (qk_write_kv) and run the causal prompt attention
+    // (qk_paged_causal_attn).  Inputs are synthetic.  Returns the GPU time (us)
+    // on the measured clock, 0 on the virtual clock.
+    double prefill(const Sequence& s, KVCacheManager& kvm) {
+        last_prefill_us = 0;
+        if (!opt.device || !opt.prefill || s.prompt_len <= 0) return 0.0;
+        if (!kvm.has_device()) throw kvc::Error(KVC_ERR_STATE, "prefill: KV manager has no device pools");
+        const int P = s.prompt_len;
+        const int nb = (int)s.block_table.size();
+        const size_t es = kvc::dtype_size(opt.dtype);
+        if (P > pf_cap) {
+            kvc::check(kvc_stream_synchronize(stream), "prefill growth");
+            kvc_free(pq); kvc_free(pk); kvc_free(pv); kvc_free(pout);
+            pq = pk = pv = pout = nullptr;
+            pf_cap = 0;
+            const int cap = std::max(P, 256);
+            kvc::check(kvc_malloc(&pq, (size_t)cap * n_heads * head_dim * es), "prefill q");
+            kvc::check(kvc_malloc(&pout, (size_t)cap * n_heads * head_dim * es), "prefill out");
+            kvc::check(kvc_malloc(&pk, (size_t)cap * n_kv_heads * head_dim * es), "prefill k");
+            kvc::check(kvc_malloc(&pv, (size_t)cap * n_kv_heads * head_dim * es), "prefill v");
+            kvc::check(kvc_fill_normal(pq, (size_t)cap * n_heads * head_dim, opt.dtype, opt.seed + 3, 1.0f, stream), "fill");
+            kvc::check(kvc_fill_normal(pk, (size_t)cap * n_kv_heads * head_dim, opt.dtype, opt.seed + 4, 1.0f, stream), "fill");
+            kvc::check(kvc_fill_normal(pv, (size_t)cap * n_kv_heads * head_dim, opt.dtype, opt.seed + 5, 1.0f, stream), "fill");
+            pf_cap = cap;
+        }
+        if (nb > ptab_cap) {
+            kvc::check(kvc_stream_synchronize(stream), "prefill table growth");
+            kvc_free(d_ptab); kvc_host_free(h_ptab);
+            d_ptab = nullptr; h_ptab = nullptr;
+            const int cap = std::max(nb, 64);
+            kvc::check(kvc_malloc((void**)&d_ptab, cap * sizeof(int)), "prefill table");
+            kvc::check(kvc_host_alloc((void**)&h_ptab, cap * sizeof(int)), "prefill pinned table");
+            if (!h_ptab_ev) kvc::check(kvc_event_create(&h_ptab_ev), "prefill event");
+            ptab_cap = cap;
+        } else {
+            kvc::check(kvc_event_synchronize(h_ptab_ev), "prefill table wait");  // previous upload done
+        }
+        std::memcpy(h_ptab, s.block_table.data(), nb * sizeof(int));
+        kvc::check(kvc_step_upload(d_ptab, h_ptab, nb * sizeof(int), stream), "prefill table upload");
+        kvc::check(kvc_event_record(h_ptab_ev, stream), "prefill event");
+        ensure_workspace(kvc_paged_causal_attn_workspace_size(0, P, n_heads, n_kv_heads, head_dim, block_size,
+                                                              opt.dtype));
+        kvc::check(kvc_event_record(ev0, stream), "event");
+        for (int l = 0; l < opt.n_layers; ++l) {
+            kvc::check(kvc_write_kv(pk, pv, kvm.k_layer(l), kvm.v_layer(l), d_ptab, 0, P, n_kv_heads, head_dim,
+                                    block_size, opt.dtype, stream),
+                       "prefill write_kv");
+            kvc::check(kvc_paged_causal_attn(pq, pout, kvm.k_layer(l), kvm.v_layer(l), d_ptab, 0, P, n_heads,
+                                             n_kv_heads, head_dim, block_size, scale, opt.dtype, ws, ws_bytes, stream),
+                       "prefill attention");
+        }
+        kvc::check(kvc_event_record(ev1, stream), "event");
+        if (opt.clock_mode != 0) return 0.0;
+        float ms = 0.f;
+        kvc::check(kvc_event_elapsed_ms(&ms, ev0, ev1), "event elapsed");
+        last_prefill_us = (double)ms * 1e3;
+        return last_prefill_us;
     }
 
     void synchronize() {

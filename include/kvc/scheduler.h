@@ -54,6 +54,12 @@ inline EngineStats run_static(std::vector<Request> reqs, KVCacheManager& kvm, Mo
             if (reserved + fp > kvm.num_blocks) break;
             kvm.allocate_prompt(seqs[idx]);
             reserved += fp;
+            if (runner.opt.prefill) {  // the prompt is processed on admission
+                const double pu = runner.prefill(seqs[idx], kvm);
+                R.prefill_us += pu;
+                R.gpu_us += pu;
+                clock += pu;
+            }
             group.push_back(&seqs[idx]);
             ++idx;
         }

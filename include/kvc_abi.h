@@ -265,6 +265,8 @@ typedef struct kvc_engine_config {
     int device;        /* 1: own device pools and launch kernels; 0: scheduling only (no GPU) */
     int split_tokens;  /* device-lengths decode: split size; 0 = automatic */
     int decode_path;   /* KVC_DECODE_PLANNED (0, default) or KVC_DECODE_DEVICE_LENGTHS */
+    int prefill;       /* 1: admitted prompts run qk_write_kv + qk_paged_causal_attn per layer; the
+                          GPU time advances the measured clock (the virtual clock ignores it) */
     uint64_t seed;     /* seed of the synthetic q/k/v fill */
 } kvc_engine_config;
 
@@ -282,6 +284,7 @@ typedef struct kvc_engine_stats {     /* EngineStats (engine.h:33-45) + p50 + di
     double p99_latency_us;
     uint64_t step_digest;   /* FNV-1a 64 over every step's packed metadata */
     double host_wall_us;    /* real elapsed time of the whole run on the host clock */
+    double prefill_us;      /* GPU time of prompt processing (part of gpu_us) */
 } kvc_engine_stats;
 
 typedef struct kvc_request { int id; double arrival_us; int prompt_len; int gen_len; } kvc_request;

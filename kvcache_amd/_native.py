@@ -43,7 +43,7 @@ class EngineConfigC(C.Structure):
         ("n_heads", i32), ("n_kv_heads", i32), ("head_dim", i32), ("block_size", i32),
         ("num_blocks", i32), ("max_batch", i32), ("n_layers", i32), ("dtype", i32),
         ("kv_write", i32), ("clock_mode", i32), ("virt_c0", f64), ("virt_c1", f64),
-        ("virt_c2", f64), ("device", i32), ("split_tokens", i32), ("decode_path", i32), ("seed", u64),
+        ("virt_c2", f64), ("device", i32), ("split_tokens", i32), ("decode_path", i32), ("prefill", i32), ("seed", u64),
     ]
 
 
@@ -52,7 +52,7 @@ class EngineStatsC(C.Structure):
         ("iters", i32), ("tokens", C.c_longlong), ("gpu_us", f64), ("wall_us", f64),
         ("slot_steps", C.c_longlong), ("useful_steps", C.c_longlong), ("peak_blocks", i32),
         ("finished", i32), ("avg_latency_us", f64), ("p50_latency_us", f64),
-        ("p99_latency_us", f64), ("step_digest", u64), ("host_wall_us", f64),
+        ("p99_latency_us", f64), ("step_digest", u64), ("host_wall_us", f64), ("prefill_us", f64),
     ]
 
 

@@ -47,6 +47,7 @@ void to_c(const EngineStats& s, kvc_engine_stats* o) {
     o->p99_latency_us = s.p99_latency_us;
     o->step_digest = s.step_digest;
     o->host_wall_us = s.host_wall_us;
+    o->prefill_us = s.prefill_us;
 }
 }  // namespace
 
@@ -94,6 +95,7 @@ int kvc_engine_create(const kvc_engine_config* c, kvc_engine** out) {
         if (c->decode_path != KVC_DECODE_PLANNED && c->decode_path != KVC_DECODE_DEVICE_LENGTHS)
             return kvc::set_error(KVC_ERR_ARG, "decode_path must be KVC_DECODE_PLANNED or KVC_DECODE_DEVICE_LENGTHS");
         ec.decode_path = c->decode_path;
+        ec.prefill = c->prefill != 0;
         if (c->seed) ec.seed = c->seed;
         if (c->max_batch <= 0) return kvc::set_error(KVC_ERR_ARG, "max_batch must be > 0");
         *out = new kvc_engine(ec);

@@ -74,13 +74,14 @@ class EngineConfig:
     device: bool = True
     split_tokens: int = 0
     decode_path: int = 0         # 0 host-planned decode, 1 device-lengths path with split_tokens
+    prefill: bool = False        # admitted prompts run K/V writes + causal attention (measured clock)
     seed: int = 0
 
     def to_c(self) -> EngineConfigC:
         return EngineConfigC(self.n_heads, self.n_kv_heads, self.head_dim, self.block_size, self.num_blocks,
                              self.max_batch, self.n_layers, self.dtype, int(self.kv_write), self.clock_mode,
                              self.virt_c0, self.virt_c1, self.virt_c2, int(self.device), self.split_tokens,
-                             self.decode_path, self.seed)
+                             self.decode_path, int(self.prefill), self.seed)
 
 
 @dataclass
@@ -99,13 +100,14 @@ class EngineStats:
     p99_latency_us: float = 0.0
     step_digest: int = 0
     host_wall_us: float = 0.0
+    prefill_us: float = 0.0
     extra: dict = field(default_factory=dict)
 
     @classmethod
     def from_c(cls, name: str, s: EngineStatsC) -> "EngineStats":
         return cls(name, s.iters, s.tokens, s.gpu_us, s.wall_us, s.slot_steps, s.useful_steps, s.peak_blocks,
                    s.finished, s.avg_latency_us, s.p50_latency_us, s.p99_latency_us, s.step_digest,
-                   s.host_wall_us)
+                   s.host_wall_us, s.prefill_us)
 
     @property
     def slot_util(self) -> float:

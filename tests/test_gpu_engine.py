@@ -59,3 +59,23 @@ def test_measured_clock_invariants(orc):
     assert st.gpu_us > 0 and st.wall_us == pytest.approx(st.gpu_us)
     ss = run_static(p, g, np.zeros(256), eng, 32)
     assert ss.tokens == g.sum() and ss.finished == 256 and ss.iters >= st.iters
+
+
+def test_prefill_on_admission(orc):
+    """Admitted prompts run qk_write_kv + qk_paged_causal_attn per layer.  On the
+    virtual clock the schedule is unchanged (the oracle's digest); on the measured
+    clock the prefill time is part of the GPU time and of the latencies."""
+    say("engine prefill on admission")
+    p, g, a = W.baseline_trace(48, 0.0, 11)
+    num_blocks = (2048 * 1024 * 1024) // (24 * 2 * 16 * 64 * 2 * 2)
+    base = dict(n_heads=14, n_kv_heads=2, head_dim=64, block_size=16, num_blocks=num_blocks, max_batch=32,
+                n_layers=24, dtype=KVC_F16, kv_write=True, prefill=True)
+    eng = Engine(EngineConfig(**base, clock_mode=1, virt_c0=COST[0], virt_c1=COST[1], virt_c2=COST[2]))
+    rc, ref = orc.sim_engine(p, g, a, 16, num_blocks, 32, True, COST)
+    _same(run_continuous(p, g, a, eng), ref)
+    meas = Engine(EngineConfig(**base))
+    st = run_continuous(p, g, a, meas)
+    assert st.tokens == g.sum() and st.finished == len(p)
+    assert st.prefill_us > 0 and st.gpu_us > st.prefill_us and st.wall_us == pytest.approx(st.gpu_us)
+    ss = run_static(p, g, a, meas, 32)
+    assert ss.tokens == g.sum() and ss.prefill_us > 0
