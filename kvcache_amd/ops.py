@@ -10,7 +10,7 @@ drivers call the CUDA launchers.
 """
 from __future__ import annotations
 
-from ._native import KVC_F16, KVC_F32, check, lib
+from ._native import KVC_ERR_ARG, KVC_F16, KVC_F32, KvcError, check, lib
 from .device import DeviceBuffer
 
 __all__ = [
@@ -113,7 +113,7 @@ def decode_plan(lens, Hq, Hkv, D, BLOCK, *, tab_off=None, table=None, dtype=KVC_
     L = lib()
     ipu = int(L.kvc_decode_plan_entry_ints(Hq, Hkv, D, BLOCK, dtype))
     if ipu <= 0:
-        raise ValueError("bad plan shape")
+        raise KvcError(KVC_ERR_ARG, f"no plan for Hq={Hq} Hkv={Hkv} D={D} BLOCK={BLOCK} dtype={dtype}")
     check(L.kvc_decode_plan(lens.ctypes.data, tp, tbp, tbl, len(lens), Hq, Hkv, D, BLOCK, dtype, target_tokens, None,
                             0, C.byref(nu), C.byref(nr)))
     work = np.zeros((max(nu.value, 1), ipu), dtype=np.int32)

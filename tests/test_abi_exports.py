@@ -88,3 +88,60 @@ def test_workspace_size_and_auto_split():
     assert ops.decode_workspace_size(4, 8, 8, 64, 16, 100, 128) == 0  # single chunk: no partials
     assert ops.flash_decode_workspace_size(8, 64, 1) == 0
     assert ops.flash_decode_workspace_size(8, 64, 7) >= 8 * 7 * 66 * 4
+
+
+# ---- planned / prefill entry points: validation before any HIP call -------------------
+def test_plan_entry_sizes():
+    L = N.lib()
+    assert L.kvc_decode_plan_entry_ints(8, 8, 64, 16, N.KVC_F16) == 16    # VALU, uniform paging: 8 inline ids
+    assert L.kvc_decode_plan_entry_ints(14, 2, 64, 16, N.KVC_F16) == 64   # matrix cores: up to 56 inline ids
+    assert L.kvc_decode_plan_entry_ints(8, 8, 64, 4, N.KVC_F16) == 8      # per-lane paging: header only
+    assert L.kvc_decode_plan_entry_ints(8, 3, 64, 16, N.KVC_F16) == 0     # bad shape
+
+
+def test_plan_argument_errors():
+    import numpy as np
+    L = N.lib()
+    lens = np.array([5, 100], np.int32)
+    nu, nr = C.c_int(0), C.c_int(0)
+    assert L.kvc_decode_plan(lens.ctypes.data, None, None, 0, 2, 8, 8, 64, 16, N.KVC_F16, 0, None, 0, None,
+                             C.byref(nr)) == N.KVC_ERR_ARG
+    assert L.kvc_decode_plan(lens.ctypes.data, None, None, 0, 2, 8, 3, 64, 16, N.KVC_F16, 0, None, 0, C.byref(nu),
+                             C.byref(nr)) == N.KVC_ERR_ARG
+    assert L.kvc_decode_plan(lens.ctypes.data, None, None, -1, 2, 8, 8, 64, 16, N.KVC_F16, 0, None, 0,
+                             C.byref(nu), C.byref(nr)) == N.KVC_OK          # no table: length ignored
+    tab = np.zeros(4, np.int32)
+    assert L.kvc_decode_plan(lens.ctypes.data, None, tab.ctypes.data, -1, 2, 8, 8, 64, 16, N.KVC_F16, 0, None, 0,
+                             C.byref(nu), C.byref(nr)) == N.KVC_ERR_ARG
+    assert nu.value > 0
+    work = np.zeros((1, 16), np.int32)
+    assert L.kvc_decode_plan(lens.ctypes.data, None, None, 0, 2, 8, 8, 64, 16, N.KVC_F16, 0, work.ctypes.data,
+                             0, C.byref(nu), C.byref(nr)) == N.KVC_ERR_WORKSPACE
+    with pytest.raises(N.KvcError):
+        ops.decode_plan(lens, 8, 3, 64, 16)
+
+
+def test_planned_and_prefill_argument_errors():
+    L = N.lib()
+    fake = C.c_void_p(16)  # never dereferenced: validation fails first
+    assert L.kvc_batched_paged_append_decode_planned(fake, None, None, None, fake, fake, fake, 4, fake, 2, 8, 8, 64,
+                                                     16, 0.125, N.KVC_F16, fake, 2, 0, None, 0,
+                                                     None) == N.KVC_ERR_ARG
+    assert L.kvc_batched_paged_decode_planned(fake, fake, fake, None, 0, fake, 2, 8, 8, 64, 16, 0.125, N.KVC_F16,
+                                              None, 2, 0, None, 0, None) == N.KVC_ERR_ARG
+    assert L.kvc_paged_causal_attn(fake, fake, fake, fake, fake, -1, 4, 8, 8, 64, 16, 0.125, N.KVC_F16, None, 0,
+                                   None) == N.KVC_ERR_ARG
+    assert L.kvc_paged_causal_attn(fake, fake, fake, fake, fake, 0, 0, 8, 8, 64, 16, 0.125, N.KVC_F16, None, 0,
+                                   None) == N.KVC_OK                        # empty prompt: nothing to do
+    assert L.kvc_paged_causal_attn_workspace_size(0, 4, 8, 3, 64, 16, N.KVC_F16) == 0
+
+
+def test_tuning_round_trip_and_rejects():
+    L = N.lib()
+    v = C.c_int(0)
+    for key in (b"mfma", b"wg_per_cu", b"split_first", b"fused_merge", b"waves_per_block"):
+        assert L.kvc_get_tuning(key, C.byref(v)) == N.KVC_OK
+        old = v.value
+        assert L.kvc_set_tuning(key, old) == N.KVC_OK
+    assert L.kvc_set_tuning(b"mfma", 7) == N.KVC_ERR_ARG
+    assert L.kvc_set_tuning(b"no_such_knob", 1) == N.KVC_ERR_ARG
