@@ -223,6 +223,26 @@ int kvc_paged_causal_attn(const void* q, void* out, const void* k_pool, const vo
                           void* workspace, size_t workspace_bytes, kvc_stream_t stream);
 size_t kvc_paged_causal_attn_workspace_size(int q_pos_base, int Nq, int Hq, int Hkv, int D, int BLOCK, int dtype);
 
+/* ---- decoder-step operations around the attention path (a Qwen2-shaped layer) ----
+ * fp16 activations and weights, fp32 arithmetic; row widths multiples of 8.
+ * qk_embed_gather (qwen_kernels.h:7): out[L,H] = embed[ids[r]] (ids outside [0,V) give zeros).
+ * qk_rmsnorm (:8): out = in * rsqrt(mean(in^2) + eps) * w per row of H.
+ * qk_add_bias (:9): x[L,N] += bias[N].   qk_add_residual (:10): x[n] += y[n].
+ * qk_silu_mul (:12): out = silu(gate) * up.
+ * qk_rope / qk_rope_pos (:11,24): x [L, n_heads, D], rotate-half rotary embedding at
+ *   position pos[r] (pos != NULL) or pos_base + r, frequencies theta^(-2t/D).
+ * qk_argmax (:22): out[r] = first index of the maximum of fp32 logits[r, 0..V).
+ * kvc_linear: the linear layers (cuBLAS in the reference, rocBLAS here):
+ *   y[M,N] = x[M,K] w[N,K]^T, fp16 inputs, fp32 accumulation, y fp16 or fp32. */
+int kvc_embed_gather(void* out, const void* embed, const int* ids, int L, int H, int V, kvc_stream_t stream);
+int kvc_rmsnorm(void* out, const void* in, const void* w, int L, int H, float eps, kvc_stream_t stream);
+int kvc_add_bias(void* x, const void* bias, int L, int N, kvc_stream_t stream);
+int kvc_add_residual(void* x, const void* y, size_t n, kvc_stream_t stream);
+int kvc_silu_mul(void* out, const void* gate, const void* up, size_t n, kvc_stream_t stream);
+int kvc_rope(void* x, const int* pos, int pos_base, int L, int n_heads, int D, float theta, kvc_stream_t stream);
+int kvc_argmax(const float* logits, int L, int V, int* out, kvc_stream_t stream);
+int kvc_linear(void* y, const void* x, const void* w, int M, int N, int K, int out_dtype, kvc_stream_t stream);
+
 /* launch_flash_decode (kv_cache.h:32-34, flash_decode.cu:103-126): one sequence,
  * contiguous [H,S,D], num_splits clamped to [1, cur_len]; split j covers
  * [j*ceil(L/ns), ...) and the partials are merged by log-sum-exp.  Unlike the

@@ -109,6 +109,14 @@ _SIGS = {
         i32, [vp, vp, vp, vp, vp, vp, vp, i32, vp, i32, i32, i32, i32, i32, f32, i32, vp, i32, i32, vp, sz, vp]),
     "kvc_paged_causal_attn": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, f32, i32, vp, sz, vp]),
     "kvc_paged_causal_attn_workspace_size": (sz, [i32, i32, i32, i32, i32, i32, i32]),
+    "kvc_embed_gather": (i32, [vp, vp, vp, i32, i32, i32, vp]),
+    "kvc_rmsnorm": (i32, [vp, vp, vp, i32, i32, f32, vp]),
+    "kvc_add_bias": (i32, [vp, vp, i32, i32, vp]),
+    "kvc_add_residual": (i32, [vp, vp, sz, vp]),
+    "kvc_silu_mul": (i32, [vp, vp, vp, sz, vp]),
+    "kvc_rope": (i32, [vp, vp, i32, i32, i32, i32, f32, vp]),
+    "kvc_argmax": (i32, [vp, i32, i32, vp, vp]),
+    "kvc_linear": (i32, [vp, vp, vp, i32, i32, i32, i32, vp]),
     "kvc_flash_decode": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, f32, i32, i32, vp, sz, vp]),
     "kvc_flash_decode_workspace_size": (sz, [i32, i32, i32]),
     "kvc_block_allocator_create": (i32, [i32, C.POINTER(vp)]),

@@ -57,7 +57,7 @@ def build_library(jobs: int | None = None) -> Path:
         objs = list(ex.map(_compile, srcs))
     tmp = LIB.with_suffix(".so.tmp")
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs),
-          "-Wl,-rpath,/opt/rocm/lib"])
+          "-L/opt/rocm/lib", "-lrocblas", "-Wl,-rpath,/opt/rocm/lib"])
     os.replace(tmp, LIB)
     return LIB
 

@@ -154,6 +154,44 @@ def qk_paged_causal_attn(q, out, k_pool, v_pool, block_table, q_pos_base, Nq, Hq
                                       Hkv, D, BLOCK, scale, dtype, ws, wsb, stream))
 
 
+# ---- decoder-step operations (qwen_kernels.h:7-13,22-24) -----------------------------
+def qk_embed_gather(out, embed, ids, L, H, V, *, stream=None):
+    check(lib().kvc_embed_gather(_p(out), _p(embed), _p(ids), L, H, V, stream))
+
+
+def qk_rmsnorm(out, x, w, L, H, eps, *, stream=None):
+    check(lib().kvc_rmsnorm(_p(out), _p(x), _p(w), L, H, eps, stream))
+
+
+def qk_add_bias(x, bias, L, N, *, stream=None):
+    check(lib().kvc_add_bias(_p(x), _p(bias), L, N, stream))
+
+
+def qk_add_residual(x, y, n, *, stream=None):
+    check(lib().kvc_add_residual(_p(x), _p(y), n, stream))
+
+
+def qk_silu_mul(out, gate, up, n, *, stream=None):
+    check(lib().kvc_silu_mul(_p(out), _p(gate), _p(up), n, stream))
+
+
+def qk_rope(x, L, n_heads, D, pos_base, theta, *, stream=None):
+    check(lib().kvc_rope(_p(x), None, pos_base, L, n_heads, D, theta, stream))
+
+
+def qk_rope_pos(x, n_rows, n_heads, D, pos, theta, *, stream=None):
+    check(lib().kvc_rope(_p(x), _p(pos), 0, n_rows, n_heads, D, theta, stream))
+
+
+def qk_argmax(logits, L, V, out, *, stream=None):
+    check(lib().kvc_argmax(_p(logits), L, V, _p(out), stream))
+
+
+def linear(y, x, w, M, N, K, *, out_dtype=KVC_F16, stream=None):
+    """y[M,N] = x[M,K] w[N,K]^T (fp16 inputs, fp32 accumulation)."""
+    check(lib().kvc_linear(_p(y), _p(x), _p(w), M, N, K, out_dtype, stream))
+
+
 def write_kv_slots(k, v, k_pool, v_pool, slot_map, rows, Hkv, D, BLOCK, *, dtype=KVC_F16, stream=None):
     check(lib().kvc_write_kv_slots(_p(k), _p(v), _p(k_pool), _p(v_pool), _p(slot_map), rows, Hkv, D, BLOCK, dtype,
                                    stream))
