@@ -283,6 +283,30 @@ def bench_prefill(steps, warmup):
     return res
 
 
+def bench_c5(n_req=64, gen=64, seed=5):
+    """Config 5: the Qwen2-shaped decoder (24 layers, hidden 896, 14q/2kv, D 64, SwiGLU 4864, vocab 151936,
+    random N(0, 0.02) fp16 weights) serving n_req requests greedily with continuous batching at batch 32;
+    prompts of 16..256 random tokens, gen tokens each.  Throughput on the host clock around the whole run
+    (each step ends with the sampled tokens on the host, as serving needs them)."""
+    from kvcache_amd.model import QwenConfig, QwenModel
+    rng = np.random.default_rng(seed)
+    cfg = QwenConfig(max_batch=32, max_rows=256, seed=seed)
+    m = QwenModel(cfg)
+    try:
+        prompts = [rng.integers(0, cfg.vocab, int(n)) for n in rng.integers(16, 257, n_req)]
+        m.serve(prompts[:4], [4] * 4)  # warm-up (library loading, GEMM kernel selection)
+        out, st = m.serve(prompts, [gen] * n_req)
+    finally:
+        m.close()
+    return {"workload": f"C5 Qwen2-shaped decoder, {n_req} requests, prompts 16-256 tokens, {gen} generated each, "
+                        "greedy, continuous batching width 32, random fp16 weights",
+            "tokens": st["tokens"], "prompt_tokens": st["prompt_tokens"], "steps": st["steps"],
+            "tokens_per_s": round(st["tokens"] / (st["wall_us"] * 1e-6), 1),
+            "wall_ms": round(st["wall_us"] / 1e3, 2), "prefill_ms": round(st["prefill_us"] / 1e3, 2),
+            "decode_ms": round(st["decode_us"] / 1e3, 2),
+            "ms_per_decode_step": round(st["decode_us"] / 1e3 / max(st["steps"], 1), 3)}
+
+
 def lib_call(name, *args):
     from kvcache_amd._native import lib
     return getattr(lib(), name)(*args)
@@ -374,7 +398,7 @@ def main() -> int:
     ap.add_argument("--plan-sweep", type=str, default="", help="comma list of planned targets to time")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="only run 10 device-to-device copies of MIB MiB (HBM counter calibration) and exit")
-    ap.add_argument("--only", choices=["c3", "c4", "prefill"], default=None,
+    ap.add_argument("--only", choices=["c3", "c4", "c5", "prefill"], default=None,
                     help="run only config 3 or config 4 and print its result (profiling)")
     ap.add_argument("--warm", action="store_true",
                     help="also time the planned path on one pool copy (Infinity-Cache resident)")
@@ -407,7 +431,8 @@ def main() -> int:
     sweep_targets = [int(x) for x in a.plan_sweep.split(",") if x]
     if a.only:
         res = (bench_c3(a.steps, a.warmup, sweep_targets) if a.only == "c3" else
-               bench_prefill(a.steps, a.warmup) if a.only == "prefill" else bench_c4())
+               bench_prefill(a.steps, a.warmup) if a.only == "prefill" else
+               bench_c5() if a.only == "c5" else bench_c4())
         print(json.dumps(res), flush=True)
         return 0
     if a.lengths == "reference":
@@ -480,6 +505,11 @@ def main() -> int:
             log(f"prefill: {extras['prefill']}")
         except Exception as e:  # noqa: BLE001
             extras["prefill"] = {"error": repr(e)}
+        try:
+            extras["c5"] = bench_c5()
+            log(f"C5: {extras['c5']}")
+        except Exception as e:  # noqa: BLE001
+            extras["c5"] = {"error": repr(e)}
         try:
             extras["c4"] = bench_c4()
             log(f"C4: {json.dumps(extras['c4'])}")

@@ -1,0 +1,332 @@
+// qwen_model.h -- a Qwen2-shaped decoder served with continuous batching over the
+// paged KV cache (the model track of the reference, qwen_serve.cu:60-210), built on
+// the C ABI: embedding, RMSNorm, biased q/k/v projections, rotary embedding, K/V
+// writes into the paged pool, causal prompt attention (prefill) and the planned
+// grouped-query decode with the new token's K/V written in the same launch, output
+// projection, SwiGLU MLP, residuals, final norm, tied lm_head (fp32 logits) and
+// greedy argmax.  Weights are random N(0, init_std) (norm weights 1), generated on
+// the device from a seed; activations fp16, arithmetic fp32.
+//
+// Greedy serving (QwenModel::serve): requests are admitted FIFO up to max_batch
+// running sequences; an admitted request is prefilled (its first token comes from
+// the prompt's last position), then every step decodes one token for every running
+// sequence; a sequence retires after gen_len tokens.
+#pragma once
+#include <chrono>
+#include <cstring>
+#include <deque>
+#include <string>
+#include <vector>
+
+#include "../kvc_abi.h"
+#include "kv_cache_manager.h"
+#include "sequence.h"
+
+struct QwenConfig {
+    int layers = 24, hidden = 896, n_heads = 14, n_kv_heads = 2, head_dim = 64, inter = 4864, vocab = 151936;
+    float eps = 1e-6f, theta = 1e6f, init_std = 0.02f;
+    int block_size = 16, num_blocks = 10922, max_batch = 32, max_rows = 1024;  // max_rows: prompt rows per prefill
+    uint64_t seed = 0x71776e32ull;
+};
+
+struct QwenModel {
+    struct Layer {
+        void *ln1, *wq, *bq, *wk, *bk, *wv, *bv, *wo, *ln2, *wg, *wu, *wd;
+    };
+    QwenConfig c;
+    KVCacheManager kvm;
+    kvc_stream_t stream = nullptr;
+    std::vector<void*> owned;
+    void *embed = nullptr, *normf = nullptr;
+    std::vector<Layer> L;
+    // activations for up to max(max_rows, max_batch) rows
+    void *x = nullptr, *nrm = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *o = nullptr,
+         *gate = nullptr, *up = nullptr;
+    float* logits = nullptr;
+    int* d_meta = nullptr;
+    int* h_meta = nullptr;
+    size_t meta_cap = 0;
+    int* d_tok = nullptr;  // argmax results
+    int* h_tok = nullptr;
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
+    std::vector<int> h_work, h_tab, h_off, h_len;
+
+    explicit QwenModel(const QwenConfig& cfg)
+        : c(cfg), kvm(cfg.num_blocks, cfg.block_size, cfg.n_kv_heads, cfg.head_dim, KVC_F16, cfg.layers) {
+        if (c.hidden % 8 || c.inter % 8 || (c.n_heads * c.head_dim) % 8 || (c.n_kv_heads * c.head_dim) % 8 ||
+            c.n_heads % c.n_kv_heads)
+            throw kvc::Error(KVC_ERR_ARG, "QwenModel: unsupported shape");
+        kvc::check(kvc_stream_create(&stream), "stream");
+        const int H = c.hidden, QD = c.n_heads * c.head_dim, KD = c.n_kv_heads * c.head_dim, I = c.inter;
+        uint64_t s = c.seed;
+        auto param = [&](size_t n, bool ones = false) {
+            void* p = alloc(n * 2);
+            if (ones) fill_ones(p, n);
+            else kvc::check(kvc_fill_normal(p, n, KVC_F16, s++, c.init_std, stream), "init");
+            return p;
+        };
+        embed = param((size_t)c.vocab * H);
+        L.resize(c.layers);
+        for (auto& l : L) {
+            l.ln1 = param(H, true);
+            l.wq = param((size_t)QD * H); l.bq = param(QD);
+            l.wk = param((size_t)KD * H); l.bk = param(KD);
+            l.wv = param((size_t)KD * H); l.bv = param(KD);
+            l.wo = param((size_t)H * QD);
+            l.ln2 = param(H, true);
+            l.wg = param((size_t)I * H); l.wu = param((size_t)I * H); l.wd = param((size_t)H * I);
+        }
+        normf = param(H, true);
+        const size_t R = std::max(c.max_rows, c.max_batch);
+        x = alloc(R * H * 2); nrm = alloc(R * H * 2); o = alloc(R * H * 2);
+        q = alloc(R * QD * 2); att = alloc(R * QD * 2); k = alloc(R * KD * 2); v = alloc(R * KD * 2);
+        gate = alloc(R * I * 2); up = alloc(R * I * 2);
+        logits = static_cast<float*>(alloc((size_t)c.max_batch * c.vocab * 4));
+        d_tok = static_cast<int*>(alloc(c.max_batch * 4));
+        kvc::check(kvc_host_alloc((void**)&h_tok, c.max_batch * 4), "pinned tokens");
+        kvc::check(kvc_stream_synchronize(stream), "init");
+    }
+    ~QwenModel() {
+        if (stream) kvc_stream_synchronize(stream);
+        for (void* p : owned) kvc_free(p);
+        kvc_free(d_meta); kvc_free(ws);
+        kvc_host_free(h_meta); kvc_host_free(h_tok);
+        kvc_stream_destroy(stream);
+    }
+    QwenModel(const QwenModel&) = delete;
+    QwenModel& operator=(const QwenModel&) = delete;
+
+    void* alloc(size_t bytes) {
+        void* p = nullptr;
+        kvc::check(kvc_malloc(&p, (bytes + 255) / 256 * 256), "model allocation");
+        owned.push_back(p);
+        return p;
+    }
+    void fill_ones(void* p, size_t n) {
+        std::vector<uint16_t> h(n, 0x3C00);  // fp16 1.0
+        kvc::check(kvc_memcpy_h2d(p, h.data(), n * 2, stream), "ones");
+        kvc::check(kvc_stream_synchronize(stream), "ones");
+    }
+    void ensure_meta(size_t ints) {
+        if (ints <= meta_cap) return;
+        kvc::check(kvc_stream_synchronize(stream), "meta growth");
+        kvc_free(d_meta); kvc_host_free(h_meta);
+        d_meta = nullptr; h_meta = nullptr;
+        meta_cap = std::max(ints, meta_cap * 2);
+        kvc::check(kvc_malloc((void**)&d_meta, meta_cap * 4), "meta");
+        kvc::check(kvc_host_alloc((void**)&h_meta, meta_cap * 4), "pinned meta");
+    }
+    void ensure_ws(size_t need) {
+        if (need <= ws_bytes) return;
+        kvc::check(kvc_stream_synchronize(stream), "workspace growth");
+        kvc_free(ws);
+        ws = nullptr;
+        ws_bytes = std::max(need, (size_t)1 << 20) * 2;
+        kvc::check(kvc_malloc(&ws, ws_bytes), "workspace");
+    }
+    void* kl(int l) const { return kvm.k_layer(l); }
+    void* vl(int l) const { return kvm.v_layer(l); }
+
+    // Rows [0, M) of x hold the layer input; attention is supplied by `attend(l)`.
+    template <typename Attend>
+    void layers(int M, const int* d_pos, int pos_base, Attend&& attend) {
+        const int H = c.hidden, QD = c.n_heads * c.head_dim, KD = c.n_kv_heads * c.head_dim, I = c.inter;
+        for (int l = 0; l < c.layers; ++l) {
+            const Layer& w = L[l];
+            kvc::check(kvc_rmsnorm(nrm, x, w.ln1, M, H, c.eps, stream), "rmsnorm");
+            kvc::check(kvc_linear(q, nrm, w.wq, M, QD, H, KVC_F16, stream), "q_proj");
+            kvc::check(kvc_add_bias(q, w.bq, M, QD, stream), "q bias");
+            kvc::check(kvc_linear(k, nrm, w.wk, M, KD, H, KVC_F16, stream), "k_proj");
+            kvc::check(kvc_add_bias(k, w.bk, M, KD, stream), "k bias");
+            kvc::check(kvc_linear(v, nrm, w.wv, M, KD, H, KVC_F16, stream), "v_proj");
+            kvc::check(kvc_add_bias(v, w.bv, M, KD, stream), "v bias");
+            kvc::check(kvc_rope(q, d_pos, pos_base, M, c.n_heads, c.head_dim, c.theta, stream), "rope q");
+            kvc::check(kvc_rope(k, d_pos, pos_base, M, c.n_kv_heads, c.head_dim, c.theta, stream), "rope k");
+            attend(l);
+            kvc::check(kvc_linear(o, att, w.wo, M, H, QD, KVC_F16, stream), "o_proj");
+            kvc::check(kvc_add_residual(x, o, (size_t)M * H, stream), "residual");
+            kvc::check(kvc_rmsnorm(nrm, x, w.ln2, M, H, c.eps, stream), "rmsnorm");
+            kvc::check(kvc_linear(gate, nrm, w.wg, M, I, H, KVC_F16, stream), "gate_proj");
+            kvc::check(kvc_linear(up, nrm, w.wu, M, I, H, KVC_F16, stream), "up_proj");
+            kvc::check(kvc_silu_mul(gate, gate, up, (size_t)M * I, stream), "silu");
+            kvc::check(kvc_linear(o, gate, w.wd, M, H, I, KVC_F16, stream), "down_proj");
+            kvc::check(kvc_add_residual(x, o, (size_t)M * H, stream), "residual");
+        }
+    }
+
+    // Final norm of `rows` rows starting at x row `first` (consecutive), fp32 logits, argmax.
+    void head(int first, int rows) {
+        const int H = c.hidden;
+        const void* xr = static_cast<const char*>(x) + (size_t)first * H * 2;
+        kvc::check(kvc_rmsnorm(nrm, xr, normf, rows, H, c.eps, stream), "final norm");
+        kvc::check(kvc_linear(logits, nrm, embed, rows, c.vocab, H, KVC_F32, stream), "lm_head");
+        kvc::check(kvc_argmax(logits, rows, c.vocab, d_tok, stream), "argmax");
+    }
+
+    // Prompt processing of one admitted sequence (kvm.allocate_prompt done): writes the
+    // prompt's K/V for every layer and returns the first generated token.
+    int prefill(const Sequence& s, const int* tokens) {
+        const int P = s.prompt_len;
+        if (P <= 0 || P > c.max_rows) throw kvc::Error(KVC_ERR_ARG, "prefill: prompt length outside [1, max_rows]");
+        const int nb = (int)s.block_table.size();
+        ensure_meta((size_t)P + nb);
+        kvc::check(kvc_stream_synchronize(stream), "meta reuse");
+        std::memcpy(h_meta, tokens, P * 4);
+        std::memcpy(h_meta + P, s.block_table.data(), nb * 4);
+        kvc::check(kvc_step_upload(d_meta, h_meta, ((size_t)P + nb) * 4, stream), "prefill upload");
+        const int* d_ids = d_meta;
+        const int* d_table = d_meta + P;
+        ensure_ws(kvc_paged_causal_attn_workspace_size(0, P, c.n_heads, c.n_kv_heads, c.head_dim, c.block_size,
+                                                       KVC_F16));
+        kvc::check(kvc_embed_gather(x, embed, d_ids, P, c.hidden, c.vocab, stream), "embed");
+        const float scale = 1.0f / __builtin_sqrtf((float)c.head_dim);
+        layers(P, nullptr, 0, [&](int l) {
+            kvc::check(kvc_write_kv(k, v, kl(l), vl(l), d_table, 0, P, c.n_kv_heads, c.head_dim, c.block_size,
+                                    KVC_F16, stream),
+                       "prefill write_kv");
+            kvc::check(kvc_paged_causal_attn(q, att, kl(l), vl(l), d_table, 0, P, c.n_heads, c.n_kv_heads,
+                                             c.head_dim, c.block_size, scale, KVC_F16, ws, ws_bytes, stream),
+                       "prefill attention");
+        });
+        head(P - 1, 1);
+        kvc::check(kvc_memcpy_d2h(h_tok, d_tok, 4, stream), "token");
+        kvc::check(kvc_stream_synchronize(stream), "prefill");
+        return h_tok[0];
+    }
+
+    // One decode step: row r feeds token in[r] of batch[r] at position cur_len (the
+    // manager has already grown the sequence by that token); returns next tokens.
+    void decode(const std::vector<Sequence*>& batch, const int* in, int* out) {
+        const int n = (int)batch.size();
+        if (n == 0) return;
+        if (n > c.max_batch) throw kvc::Error(KVC_ERR_ARG, "decode: batch larger than max_batch");
+        h_tab.clear(); h_off.clear(); h_len.clear();
+        for (const Sequence* s : batch) {
+            h_off.push_back((int)h_tab.size());
+            h_tab.insert(h_tab.end(), s->block_table.begin(), s->block_table.end());
+            h_len.push_back(s->cur_len);
+        }
+        h_off.push_back((int)h_tab.size());
+        const int T = (int)h_tab.size();
+        int nu = 0, nr = 0;
+        kvc::check(kvc_decode_plan(h_len.data(), h_off.data(), h_tab.data(), T, n, c.n_heads, c.n_kv_heads,
+                                   c.head_dim, c.block_size, KVC_F16, 0, nullptr, 0, &nu, &nr),
+                   "plan");
+        const int ipu = kvc_decode_plan_entry_ints(c.n_heads, c.n_kv_heads, c.head_dim, c.block_size, KVC_F16);
+        h_work.resize((size_t)nu * ipu);
+        kvc::check(kvc_decode_plan(h_len.data(), h_off.data(), h_tab.data(), T, n, c.n_heads, c.n_kv_heads,
+                                   c.head_dim, c.block_size, KVC_F16, 0, h_work.data(), nu, &nu, &nr),
+                   "plan");
+        // upload: [ids n | pos n | table T | work]
+        const size_t ints = 2 * (size_t)n + T + h_work.size();
+        ensure_meta(ints);
+        kvc::check(kvc_stream_synchronize(stream), "meta reuse");
+        std::memcpy(h_meta, in, n * 4);
+        for (int r = 0; r < n; ++r) h_meta[n + r] = h_len[r] - 1;  // the new token's position
+        std::memcpy(h_meta + 2 * n, h_tab.data(), (size_t)T * 4);
+        std::memcpy(h_meta + 2 * n + T, h_work.data(), h_work.size() * 4);
+        kvc::check(kvc_step_upload(d_meta, h_meta, ints * 4, stream), "decode upload");
+        const int* d_ids = d_meta;
+        const int* d_pos = d_meta + n;
+        const int* d_table = d_meta + 2 * n;
+        const int* d_work = d_table + T;
+        ensure_ws(kvc_decode_planned_workspace_size(c.n_heads, c.n_kv_heads, c.head_dim, c.block_size, KVC_F16, nr));
+        kvc::check(kvc_embed_gather(x, embed, d_ids, n, c.hidden, c.vocab, stream), "embed");
+        const float scale = 1.0f / __builtin_sqrtf((float)c.head_dim);
+        layers(n, d_pos, 0, [&](int l) {
+            kvc::check(kvc_batched_paged_append_decode_planned(q, k, v, d_pos, kl(l), vl(l), d_table, T, att, n,
+                                                               c.n_heads, c.n_kv_heads, c.head_dim, c.block_size,
+                                                               scale, KVC_F16, d_work, nu, nr, ws, ws_bytes, stream),
+                       "decode attention");
+        });
+        head(0, n);
+        kvc::check(kvc_memcpy_d2h(h_tok, d_tok, n * 4, stream), "tokens");
+        kvc::check(kvc_stream_synchronize(stream), "decode");
+        std::memcpy(out, h_tok, n * 4);
+    }
+
+    struct Request {
+        std::vector<int> prompt;
+        int gen_len = 0;
+    };
+    struct ServeStats {
+        int steps = 0, finished = 0;
+        long long tokens = 0, prompt_tokens = 0;
+        double wall_us = 0, prefill_us = 0, decode_us = 0;
+    };
+
+    // Continuous-batching greedy generation; out[i] receives request i's gen_len tokens.
+    ServeStats serve(const std::vector<Request>& reqs, std::vector<std::vector<int>>& out) {
+        using clk = std::chrono::steady_clock;
+        ServeStats st;
+        kvm.reset();
+        out.assign(reqs.size(), {});
+        std::vector<Sequence> seqs(reqs.size());
+        std::deque<int> waiting;
+        for (size_t i = 0; i < reqs.size(); ++i) {
+            seqs[i].id = (int)i;
+            seqs[i].prompt_len = (int)reqs[i].prompt.size();
+            seqs[i].max_new_tokens = reqs[i].gen_len;
+            waiting.push_back((int)i);
+        }
+        std::vector<int> run, in, nxt;
+        int reserved = 0;  // worst-case blocks of the running sequences (engine.h:118-124)
+        auto worst = [&](int i) { return blocks_needed(seqs[i].prompt_len + reqs[i].gen_len, c.block_size); };
+        const auto t0 = clk::now();
+        while (!waiting.empty() || !run.empty()) {
+            for (size_t r = 0; r < run.size();) {  // retire
+                Sequence& s = seqs[run[r]];
+                if ((int)out[run[r]].size() >= reqs[run[r]].gen_len) {
+                    kvm.free(s);
+                    reserved -= worst(run[r]);
+                    st.finished++;
+                    run[r] = run.back();
+                    run.pop_back();
+                } else {
+                    ++r;
+                }
+            }
+            while ((int)run.size() < c.max_batch && !waiting.empty()) {  // admit + prefill
+                const int i = waiting.front();
+                Sequence& s = seqs[i];
+                if (reqs[i].gen_len < 1 || s.prompt_len < 1) throw kvc::Error(KVC_ERR_ARG, "serve: empty request");
+                if (reserved + worst(i) > c.num_blocks) break;
+                if (!kvm.allocate_prompt(s)) break;
+                reserved += worst(i);
+                waiting.pop_front();
+                const auto p0 = clk::now();
+                const int t = prefill(s, reqs[i].prompt.data());
+                st.prefill_us += std::chrono::duration<double, std::micro>(clk::now() - p0).count();
+                st.prompt_tokens += s.prompt_len;
+                out[i].push_back(t);
+                st.tokens++;
+                run.push_back(i);
+            }
+            std::vector<Sequence*> batch;
+            in.clear();
+            for (int i : run)
+                if ((int)out[i].size() < reqs[i].gen_len) {
+                    if (!kvm.append_token(seqs[i])) throw kvc::Error(KVC_ERR_NOMEM, "serve: pool exhausted");
+                    batch.push_back(&seqs[i]);
+                    in.push_back(out[i].back());
+                }
+            if (batch.empty()) {
+                if (run.empty() && !waiting.empty())
+                    throw kvc::Error(KVC_ERR_STATE, "serve: a request can never be admitted");
+                continue;
+            }
+            nxt.resize(batch.size());
+            const auto d0 = clk::now();
+            decode(batch, in.data(), nxt.data());
+            st.decode_us += std::chrono::duration<double, std::micro>(clk::now() - d0).count();
+            st.steps++;
+            for (size_t r = 0; r < batch.size(); ++r) {
+                out[batch[r]->id].push_back(nxt[r]);
+                st.tokens++;
+            }
+        }
+        st.wall_us = std::chrono::duration<double, std::micro>(clk::now() - t0).count();
+        return st;
+    }
+};

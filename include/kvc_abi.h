@@ -243,6 +243,35 @@ int kvc_rope(void* x, const int* pos, int pos_base, int L, int n_heads, int D, f
 int kvc_argmax(const float* logits, int L, int V, int* out, kvc_stream_t stream);
 int kvc_linear(void* y, const void* x, const void* w, int M, int N, int K, int out_dtype, kvc_stream_t stream);
 
+/* ---- Qwen2-shaped decoder served with continuous batching (include/kvc/qwen_model.h;
+ * the model track of the reference, qwen_serve.cu:60-210) ----
+ * Random N(0, init_std) fp16 weights from `seed` (norm weights 1, lm_head tied to the
+ * embedding); greedy decoding; requests admitted FIFO up to max_batch running. */
+typedef struct kvc_qwen_config {
+    int layers, hidden, n_heads, n_kv_heads, head_dim, inter, vocab;
+    float eps, theta, init_std;
+    int block_size, num_blocks, max_batch, max_rows;  /* max_rows: longest prompt */
+    uint64_t seed;                                      /* 0: default */
+} kvc_qwen_config;
+typedef struct kvc_qwen_stats {
+    int steps, finished;
+    long long tokens, prompt_tokens;
+    double wall_us, prefill_us, decode_us;   /* host clock around the whole run / prefills / decode steps */
+} kvc_qwen_stats;
+typedef struct kvc_qwen kvc_qwen;
+int  kvc_qwen_create(const kvc_qwen_config* cfg, kvc_qwen** out);
+void kvc_qwen_destroy(kvc_qwen* h);
+/* device address and size of a weight: "embed", "norm", or per layer "ln1", "wq", "bq",
+ * "wk", "bk", "wv", "bv", "wo", "ln2", "wg", "wu", "wd" ([out, in] row-major fp16) */
+int  kvc_qwen_tensor(kvc_qwen* h, const char* name, int layer, void** ptr, size_t* bytes);
+/* requests i: prompt tokens [prompt_off[i], prompt_off[i+1]), gen_len[i] >= 1 tokens
+ * generated (the first from the prompt's last position); out_tokens gets them in
+ * request order (sum of gen_len ints). */
+int  kvc_qwen_serve(kvc_qwen* h, int n_req, const int* prompt_off, const int* prompt_tokens, const int* gen_len,
+                    int* out_tokens, kvc_qwen_stats* stats);
+/* one prompt: its first generated token and the fp32 logits of its last position (vocab floats) */
+int  kvc_qwen_prefill_logits(kvc_qwen* h, const int* tokens, int P, float* logits_host, int* token);
+
 /* launch_flash_decode (kv_cache.h:32-34, flash_decode.cu:103-126): one sequence,
  * contiguous [H,S,D], num_splits clamped to [1, cur_len]; split j covers
  * [j*ceil(L/ns), ...) and the partials are merged by log-sum-exp.  Unlike the

@@ -47,6 +47,21 @@ class EngineConfigC(C.Structure):
     ]
 
 
+class QwenConfigC(C.Structure):
+    _fields_ = [
+        ("layers", i32), ("hidden", i32), ("n_heads", i32), ("n_kv_heads", i32), ("head_dim", i32),
+        ("inter", i32), ("vocab", i32), ("eps", C.c_float), ("theta", C.c_float), ("init_std", C.c_float),
+        ("block_size", i32), ("num_blocks", i32), ("max_batch", i32), ("max_rows", i32), ("seed", u64),
+    ]
+
+
+class QwenStatsC(C.Structure):
+    _fields_ = [
+        ("steps", i32), ("finished", i32), ("tokens", C.c_longlong), ("prompt_tokens", C.c_longlong),
+        ("wall_us", f64), ("prefill_us", f64), ("decode_us", f64),
+    ]
+
+
 class EngineStatsC(C.Structure):
     _fields_ = [
         ("iters", i32), ("tokens", C.c_longlong), ("gpu_us", f64), ("wall_us", f64),
@@ -129,6 +144,11 @@ _SIGS = {
     "kvc_block_allocator_shuffle": (None, [vp, u64]),
     "kvc_blocks_needed": (i32, [i32, i32]),
     "kvc_engine_create": (i32, [C.POINTER(EngineConfigC), C.POINTER(vp)]),
+    "kvc_qwen_create": (i32, [C.POINTER(QwenConfigC), C.POINTER(vp)]),
+    "kvc_qwen_destroy": (None, [vp]),
+    "kvc_qwen_tensor": (i32, [vp, C.c_char_p, i32, C.POINTER(vp), C.POINTER(sz)]),
+    "kvc_qwen_serve": (i32, [vp, i32, vp, vp, vp, vp, C.POINTER(QwenStatsC)]),
+    "kvc_qwen_prefill_logits": (i32, [vp, vp, i32, vp, vp]),
     "kvc_engine_destroy": (None, [vp]),
     "kvc_engine_reset": (i32, [vp]),
     "kvc_engine_add_request": (i32, [vp, i32, i32, f64]),

@@ -54,3 +54,64 @@ def argmax(logits):
 def linear(x, w):
     """y = x w^T (the reference's cuBLAS linear layers)."""
     return np.asarray(x, np.float64) @ np.asarray(w, np.float64).T
+
+
+def _r16(a):
+    """Round to fp16 and back: the GPU stores every kernel's output in fp16."""
+    return np.asarray(a, np.float32).astype(np.float16).astype(np.float32)
+
+
+def decoder_logits(W, cfg, tokens):
+    """Teacher-forced forward of one token sequence through the Qwen2-shaped decoder
+    (qwen_serve.cu:97-121 for every position at once: causal attention over the
+    prefix), returning float64 logits [T, vocab].  W maps names to fp16 arrays
+    (kvcache_amd.model.QwenModel.tensor layout: [out, in] row-major); fp16 rounding is
+    applied where the GPU stores a kernel's output, arithmetic is float32 (GEMMs) and
+    float64 (norms, softmax)."""
+    H, Hq, Hkv, D = cfg.hidden, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim
+    I, V = cfg.inter, cfg.vocab
+    tok = np.asarray(tokens)
+    T = len(tok)
+    f32 = lambda a: np.asarray(a, np.float32)
+    embed = W["embed"].reshape(V, H)
+    x = f32(embed[tok])
+    pos = np.arange(T)
+    mask = np.triu(np.ones((T, T), bool), 1)
+    g = Hq // Hkv
+    for l in range(cfg.layers):
+        w = lambda n, shape: f32(W[f"{n}.{l}"].reshape(shape))
+        n = _r16(rmsnorm(x, w("ln1", (H,)), cfg.eps))
+        q = _r16(_r16(n @ w("wq", (Hq * D, H)).T) + w("bq", (Hq * D,)))
+        k = _r16(_r16(n @ w("wk", (Hkv * D, H)).T) + w("bk", (Hkv * D,)))
+        v = _r16(_r16(n @ w("wv", (Hkv * D, H)).T) + w("bv", (Hkv * D,)))
+        q = _r16(rope(q.reshape(T, Hq, D), pos, D, cfg.theta))
+        k = _r16(rope(k.reshape(T, Hkv, D), pos, D, cfg.theta))
+        v = v.reshape(T, Hkv, D).astype(np.float64)
+        att = np.empty((T, Hq, D))
+        for h in range(Hq):
+            s = q[:, h].astype(np.float64) @ k[:, h // g].astype(np.float64).T / np.sqrt(D)
+            s[mask] = -np.inf
+            s = np.exp(s - s.max(axis=1, keepdims=True))
+            att[:, h] = (s / s.sum(axis=1, keepdims=True)) @ v[:, h // g]
+        att = _r16(att.reshape(T, Hq * D))
+        x = _r16(x + _r16(att @ w("wo", (H, Hq * D)).T))
+        n = _r16(rmsnorm(x, w("ln2", (H,)), cfg.eps))
+        a = _r16(silu_mul(_r16(n @ w("wg", (I, H)).T), _r16(n @ w("wu", (I, H)).T)))
+        x = _r16(x + _r16(a @ w("wd", (H, I)).T))
+    n = _r16(rmsnorm(x, f32(W["norm"]), cfg.eps))
+    return (n @ f32(embed).T).astype(np.float64)
+
+
+def teacher_forced_check(logits_cpu, prompt_len, generated, margin):
+    """Generated token i is predicted at position prompt_len - 1 + i.  Returns
+    (exact matches, list of (i, gpu token, cpu top token, cpu logit gap)) for the
+    mismatches whose CPU gap exceeds `margin` (near-ties within it are tolerated)."""
+    exact, bad = 0, []
+    for i, t in enumerate(generated):
+        row = logits_cpu[prompt_len - 1 + i]
+        top = int(np.argmax(row))
+        if top == int(t):
+            exact += 1
+        elif row[top] - row[int(t)] > margin:
+            bad.append((i, int(t), top, float(row[top] - row[int(t)])))
+    return exact, bad
