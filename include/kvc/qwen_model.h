@@ -7,11 +7,19 @@
 // greedy argmax.  Weights are random N(0, init_std) (norm weights 1), generated on
 // the device from a seed; activations fp16, arithmetic fp32.
 //
+// Decode steps of at most 32 rows run five fused kernels per layer (step_path 0):
+// RMSNorm + q/k/v projection + bias + rotary; the planned attention with the new
+// K/V written in the same launch; output projection + residual; RMSNorm + gate/up
+// projection + SwiGLU; down projection + residual; then final norm + lm_head +
+// argmax.  step_path 1 (and larger batches, and prompts) run one kernel per op with
+// rocBLAS linear layers; both round to fp16 at the same points.
+//
 // Greedy serving (QwenModel::serve): requests are admitted FIFO up to max_batch
 // running sequences; an admitted request is prefilled (its first token comes from
 // the prompt's last position), then every step decodes one token for every running
 // sequence; a sequence retires after gen_len tokens.
 #pragma once
+#include <algorithm>
 #include <chrono>
 #include <cstring>
 #include <deque>
@@ -27,12 +35,14 @@ struct QwenConfig {
     float eps = 1e-6f, theta = 1e6f, init_std = 0.02f;
     int block_size = 16, num_blocks = 10922, max_batch = 32, max_rows = 1024;  // max_rows: prompt rows per prefill
     uint64_t seed = 0x71776e32ull;
+    int step_path = 0;  // 0: fused kernels for steps of <= 32 rows; 1: one kernel per op
 };
 
 struct QwenModel {
     struct Layer {
-        void *ln1, *wq, *bq, *wk, *bk, *wv, *bv, *wo, *ln2, *wg, *wu, *wd;
+        void *ln1, *wq, *bq, *wk, *bk, *wv, *bv, *wo, *ln2, *wg, *wu, *wd;  // wq|wk|wv, bq|bk|bv, wg|wu adjacent
     };
+    static constexpr int kRowsMax = 32;  // rows of the fused decode-step kernels
     QwenConfig c;
     KVCacheManager kvm;
     kvc_stream_t stream = nullptr;
@@ -50,6 +60,9 @@ struct QwenModel {
     int* h_tok = nullptr;
     void* ws = nullptr;
     size_t ws_bytes = 0;
+    void* rws = nullptr;  // fused kernels' workspace (zero between calls)
+    size_t rws_bytes = 0;
+    bool rows_ok = false;
     std::vector<int> h_work, h_tab, h_off, h_len;
 
     explicit QwenModel(const QwenConfig& cfg)
@@ -60,22 +73,31 @@ struct QwenModel {
         kvc::check(kvc_stream_create(&stream), "stream");
         const int H = c.hidden, QD = c.n_heads * c.head_dim, KD = c.n_kv_heads * c.head_dim, I = c.inter;
         uint64_t s = c.seed;
+        auto fill = [&](void* p, size_t n) {
+            kvc::check(kvc_fill_normal(p, n, KVC_F16, s++, c.init_std, stream), "init");
+            return p;
+        };
         auto param = [&](size_t n, bool ones = false) {
             void* p = alloc(n * 2);
             if (ones) fill_ones(p, n);
-            else kvc::check(kvc_fill_normal(p, n, KVC_F16, s++, c.init_std, stream), "init");
+            else fill(p, n);
             return p;
         };
+        auto at = [](void* p, size_t elems) { return static_cast<void*>(static_cast<char*>(p) + elems * 2); };
         embed = param((size_t)c.vocab * H);
         L.resize(c.layers);
         for (auto& l : L) {
             l.ln1 = param(H, true);
-            l.wq = param((size_t)QD * H); l.bq = param(QD);
-            l.wk = param((size_t)KD * H); l.bk = param(KD);
-            l.wv = param((size_t)KD * H); l.bv = param(KD);
+            void* wqkv = alloc((size_t)(QD + 2 * KD) * H * 2);
+            void* bqkv = alloc((size_t)(QD + 2 * KD) * 2);
+            l.wq = fill(wqkv, (size_t)QD * H); l.bq = fill(bqkv, QD);
+            l.wk = fill(at(wqkv, (size_t)QD * H), (size_t)KD * H); l.bk = fill(at(bqkv, QD), KD);
+            l.wv = fill(at(wqkv, (size_t)(QD + KD) * H), (size_t)KD * H); l.bv = fill(at(bqkv, QD + KD), KD);
             l.wo = param((size_t)H * QD);
             l.ln2 = param(H, true);
-            l.wg = param((size_t)I * H); l.wu = param((size_t)I * H); l.wd = param((size_t)H * I);
+            void* wgu = alloc((size_t)2 * I * H * 2);
+            l.wg = fill(wgu, (size_t)I * H); l.wu = fill(at(wgu, (size_t)I * H), (size_t)I * H);
+            l.wd = param((size_t)H * I);
         }
         normf = param(H, true);
         const size_t R = std::max(c.max_rows, c.max_batch);
@@ -85,6 +107,14 @@ struct QwenModel {
         logits = static_cast<float*>(alloc((size_t)c.max_batch * c.vocab * 4));
         d_tok = static_cast<int*>(alloc(c.max_batch * 4));
         kvc::check(kvc_host_alloc((void**)&h_tok, c.max_batch * 4), "pinned tokens");
+        rows_ok = c.step_path == 0 && H % 32 == 0 && H <= 1024 && QD % 32 == 0 && I % 32 == 0 &&
+                  c.vocab % 32 == 0 && c.head_dim % 32 == 0;
+        if (rows_ok) {
+            rws_bytes = std::max({kvc_rows_workspace_size(H, QD), kvc_rows_workspace_size(H, I),
+                                  kvc_rows_workspace_size(c.vocab, H)});
+            rws = alloc(rws_bytes);
+            kvc::check(kvc_memset(rws, 0, rws_bytes, stream), "rows workspace");
+        }
         kvc::check(kvc_stream_synchronize(stream), "init");
     }
     ~QwenModel() {
@@ -155,10 +185,38 @@ struct QwenModel {
         }
     }
 
-    // Final norm of `rows` rows starting at x row `first` (consecutive), fp32 logits, argmax.
-    void head(int first, int rows) {
+    // Decode-step layers over M <= 32 rows with the fused kernels.
+    void rows_layers(int M, const int* d_pos, const int* d_table, int T, const int* d_work, int nu, int nr) {
+        const int H = c.hidden, QD = c.n_heads * c.head_dim, I = c.inter;
+        const float scale = 1.0f / __builtin_sqrtf((float)c.head_dim);
+        for (int l = 0; l < c.layers; ++l) {
+            const Layer& w = L[l];
+            kvc::check(kvc_rows_qkv(q, k, v, x, w.ln1, c.eps, w.wq, w.bq, d_pos, M, H, c.n_heads, c.n_kv_heads,
+                                    c.head_dim, c.theta, stream),
+                       "norm + qkv + rope");
+            kvc::check(kvc_batched_paged_append_decode_planned(q, k, v, d_pos, kl(l), vl(l), d_table, T, att, M,
+                                                               c.n_heads, c.n_kv_heads, c.head_dim, c.block_size,
+                                                               scale, KVC_F16, d_work, nu, nr, ws, ws_bytes, stream),
+                       "decode attention");
+            kvc::check(kvc_rows_linear(x, att, w.wo, M, H, QD, nullptr, 0.f, 1, rws, rws_bytes, stream),
+                       "o_proj + residual");
+            kvc::check(kvc_rows_swiglu(gate, x, w.ln2, c.eps, w.wg, M, I, H, stream), "norm + gate/up + swiglu");
+            kvc::check(kvc_rows_linear(x, gate, w.wd, M, H, I, nullptr, 0.f, 1, rws, rws_bytes, stream),
+                       "down_proj + residual");
+        }
+    }
+
+    // Final norm of `rows` rows starting at x row `first` (consecutive), fp32 logits
+    // (optional on the fused path), argmax.
+    void head(int first, int rows, bool want_logits = true) {
         const int H = c.hidden;
         const void* xr = static_cast<const char*>(x) + (size_t)first * H * 2;
+        if (rows_ok && rows <= kRowsMax) {
+            kvc::check(kvc_rows_lm_head(want_logits ? logits : nullptr, d_tok, xr, normf, c.eps, embed, rows, c.vocab,
+                                        H, rws, rws_bytes, stream),
+                       "final norm + lm_head + argmax");
+            return;
+        }
         kvc::check(kvc_rmsnorm(nrm, xr, normf, rows, H, c.eps, stream), "final norm");
         kvc::check(kvc_linear(logits, nrm, embed, rows, c.vocab, H, KVC_F32, stream), "lm_head");
         kvc::check(kvc_argmax(logits, rows, c.vocab, d_tok, stream), "argmax");
@@ -234,13 +292,18 @@ struct QwenModel {
         ensure_ws(kvc_decode_planned_workspace_size(c.n_heads, c.n_kv_heads, c.head_dim, c.block_size, KVC_F16, nr));
         kvc::check(kvc_embed_gather(x, embed, d_ids, n, c.hidden, c.vocab, stream), "embed");
         const float scale = 1.0f / __builtin_sqrtf((float)c.head_dim);
-        layers(n, d_pos, 0, [&](int l) {
-            kvc::check(kvc_batched_paged_append_decode_planned(q, k, v, d_pos, kl(l), vl(l), d_table, T, att, n,
-                                                               c.n_heads, c.n_kv_heads, c.head_dim, c.block_size,
-                                                               scale, KVC_F16, d_work, nu, nr, ws, ws_bytes, stream),
-                       "decode attention");
-        });
-        head(0, n);
+        if (rows_ok && n <= kRowsMax) {
+            rows_layers(n, d_pos, d_table, T, d_work, nu, nr);
+        } else {
+            layers(n, d_pos, 0, [&](int l) {
+                kvc::check(kvc_batched_paged_append_decode_planned(q, k, v, d_pos, kl(l), vl(l), d_table, T, att, n,
+                                                                   c.n_heads, c.n_kv_heads, c.head_dim, c.block_size,
+                                                                   scale, KVC_F16, d_work, nu, nr, ws, ws_bytes,
+                                                                   stream),
+                           "decode attention");
+            });
+        }
+        head(0, n, false);
         kvc::check(kvc_memcpy_d2h(h_tok, d_tok, n * 4, stream), "tokens");
         kvc::check(kvc_stream_synchronize(stream), "decode");
         std::memcpy(out, h_tok, n * 4);

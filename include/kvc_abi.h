@@ -243,6 +243,41 @@ int kvc_rope(void* x, const int* pos, int pos_base, int L, int n_heads, int D, f
 int kvc_argmax(const float* logits, int L, int V, int* out, kvc_stream_t stream);
 int kvc_linear(void* y, const void* x, const void* w, int M, int N, int K, int out_dtype, kvc_stream_t stream);
 
+/* ---- decode-step linear layers over at most 32 rows (one per running sequence) ----
+ * Weight-streaming matrix-core kernels with the surrounding ops fused; each replaces a
+ * cuBLAS GEMM plus the elementwise kernels after it in the reference's decode step
+ * (qwen_serve.cu:127-175).  fp16 rows and weights ([out, in] row-major), fp32
+ * accumulation, results rounded to fp16 where the op-by-op path stores them.
+ * 1 <= M <= 32; K a multiple of 32; norm_w != NULL applies RMSNorm(x) * norm_w
+ * (qk_rmsnorm, qwen_kernels.h:8) to the rows first (K <= 1024 then; kvc_rows_qkv,
+ * kvc_rows_swiglu and kvc_rows_lm_head need K <= 1024 in any case).
+ * Workspace (split-K partials, arrival counters, argmax candidates): 256-byte aligned,
+ * kvc_rows_workspace_size(N, K) bytes, ZERO-FILLED before its first use; every call
+ * leaves its counters zero again, so one workspace serves all calls of a stream.
+ * kvc_rows_linear: y[M,N] = A W^T (fp16), or y += A W^T when residual != 0 (qk_add,
+ *   qwen_kernels.h:10); N a multiple of 32; y must not alias x.
+ * kvc_rows_qkv: q|k|v = A [wq;wk;wv]^T + [bq;bk;bv] (w_qkv [(Hq+2Hkv)D, H]), then the
+ *   rotary embedding of q and k at position pos[r] (qk_rope_pos, qwen_kernels.h:24);
+ *   q [M, Hq*D], k and v [M, Hkv*D]; D a multiple of 32.
+ * kvc_rows_swiglu: act[M,I] = silu(A wg^T) * (A wu^T) (qk_silu_mul, qwen_kernels.h:12),
+ *   w_gate_up = [wg; wu] as [2I, H]; I a multiple of 16.
+ * kvc_rows_lm_head: logits[M,V] = A w^T in fp32 (logits may be NULL) and tokens[r] =
+ *   first index of the row maximum (qk_argmax, qwen_kernels.h:22); V a multiple of 32.
+ * kvc_rows_set_tuning: overrides, -1 = automatic: K splits of layers with K > 1024,
+ *   column groups (32 outputs) per workgroup, kernel shape 0..2 (4 waves x 7 k steps,
+ *   8 waves x 4, 4 waves x 4 with K split).  The workspace size depends on them. */
+size_t kvc_rows_workspace_size(int N, int K);
+int kvc_rows_linear(void* y, const void* x, const void* w, int M, int N, int K, const void* norm_w, float eps,
+                    int residual, void* workspace, size_t workspace_bytes, kvc_stream_t stream);
+int kvc_rows_qkv(void* q, void* k, void* v, const void* x, const void* norm_w, float eps, const void* w_qkv,
+                 const void* b_qkv, const int* pos, int M, int H, int Hq, int Hkv, int D, float theta,
+                 kvc_stream_t stream);
+int kvc_rows_swiglu(void* act, const void* x, const void* norm_w, float eps, const void* w_gate_up, int M, int I,
+                    int H, kvc_stream_t stream);
+int kvc_rows_lm_head(float* logits, int* tokens, const void* x, const void* norm_w, float eps, const void* w, int M,
+                     int V, int H, void* workspace, size_t workspace_bytes, kvc_stream_t stream);
+int kvc_rows_set_tuning(int splits, int groups_per_wg, int shape);
+
 /* ---- Qwen2-shaped decoder served with continuous batching (include/kvc/qwen_model.h;
  * the model track of the reference, qwen_serve.cu:60-210) ----
  * Random N(0, init_std) fp16 weights from `seed` (norm weights 1, lm_head tied to the
@@ -252,6 +287,7 @@ typedef struct kvc_qwen_config {
     float eps, theta, init_std;
     int block_size, num_blocks, max_batch, max_rows;  /* max_rows: longest prompt */
     uint64_t seed;                                      /* 0: default */
+    int step_path;  /* 0: fused decode-step kernels when a step has <= 32 rows; 1: one kernel per op */
 } kvc_qwen_config;
 typedef struct kvc_qwen_stats {
     int steps, finished;

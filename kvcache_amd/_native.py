@@ -52,6 +52,7 @@ class QwenConfigC(C.Structure):
         ("layers", i32), ("hidden", i32), ("n_heads", i32), ("n_kv_heads", i32), ("head_dim", i32),
         ("inter", i32), ("vocab", i32), ("eps", C.c_float), ("theta", C.c_float), ("init_std", C.c_float),
         ("block_size", i32), ("num_blocks", i32), ("max_batch", i32), ("max_rows", i32), ("seed", u64),
+        ("step_path", i32),
     ]
 
 
@@ -132,6 +133,12 @@ _SIGS = {
     "kvc_rope": (i32, [vp, vp, i32, i32, i32, i32, f32, vp]),
     "kvc_argmax": (i32, [vp, i32, i32, vp, vp]),
     "kvc_linear": (i32, [vp, vp, vp, i32, i32, i32, i32, vp]),
+    "kvc_rows_workspace_size": (sz, [i32, i32]),
+    "kvc_rows_linear": (i32, [vp, vp, vp, i32, i32, i32, vp, f32, i32, vp, sz, vp]),
+    "kvc_rows_qkv": (i32, [vp, vp, vp, vp, vp, f32, vp, vp, vp, i32, i32, i32, i32, i32, f32, vp]),
+    "kvc_rows_swiglu": (i32, [vp, vp, vp, f32, vp, i32, i32, i32, vp]),
+    "kvc_rows_lm_head": (i32, [vp, vp, vp, vp, f32, vp, i32, i32, i32, vp, sz, vp]),
+    "kvc_rows_set_tuning": (i32, [i32, i32, i32]),
     "kvc_flash_decode": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, f32, i32, i32, vp, sz, vp]),
     "kvc_flash_decode_workspace_size": (sz, [i32, i32, i32]),
     "kvc_block_allocator_create": (i32, [i32, C.POINTER(vp)]),

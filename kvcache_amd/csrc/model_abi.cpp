@@ -43,6 +43,8 @@ int kvc_qwen_create(const kvc_qwen_config* cfg, kvc_qwen** out) {
         c.block_size = cfg->block_size; c.num_blocks = cfg->num_blocks; c.max_batch = cfg->max_batch;
         c.max_rows = cfg->max_rows;
         if (cfg->seed) c.seed = cfg->seed;
+        if (cfg->step_path != 0 && cfg->step_path != 1) return kvc::set_error(KVC_ERR_ARG, "qwen config: step_path 0 or 1");
+        c.step_path = cfg->step_path;
         if (c.layers <= 0 || c.hidden <= 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 || c.head_dim <= 0 || c.inter <= 0 ||
             c.vocab <= 0 || c.block_size <= 0 || c.num_blocks <= 0 || c.max_batch <= 0 || c.max_rows <= 0)
             return kvc::set_error(KVC_ERR_ARG, "qwen config: sizes must be positive");

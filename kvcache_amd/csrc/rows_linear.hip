@@ -1,0 +1,611 @@
+// rows_linear.hip -- the linear layers of one decode step (at most 32 rows, one per
+// running sequence) as weight-streaming matrix-core kernels, with the operations
+// around each layer fused in: the RMSNorm of the input rows as a prologue, and as
+// epilogues the q/k/v bias plus rotary embedding, the residual add, SwiGLU, and the
+// fp32 logits with per-row argmax candidates.  The reference runs each of these as a
+// cuBLAS GEMM followed by one small kernel per elementwise op (qwen_serve.cu:127-175,
+// qwen_kernels.cu:24-107, qwen_kernels.cu:229-247).
+//
+// y[M, N] = A[M, K] W[N, K]^T with M <= 32.  At so few rows a linear layer is a
+// stream over its weights (N*K*2 bytes, read once from HBM) that all rows share, so
+// the kernel is laid out for that stream:
+//  * a column group = two 16-column tiles of W rows (32 outputs, or one SwiGLU
+//    gate/up tile pair, or one rotary pair of q/k half-heads); one workgroup of
+//    WAVES waves per (column group, K split);
+//  * each wave owns a range of 32-wide k steps and issues every load of its range
+//    at once (two weight tiles + the A rows per step, 16 bytes per lane with
+//    buffer loads whose descriptors bound the weight tile and the M valid rows, so
+//    the tail steps and the rows >= M read as zero with no branches), then runs the
+//    16x16x32 fp16 MFMAs: A lane l = row l%16, B lane l = W row l%16, both with the
+//    8 k values at 8*(l/16) of the step;
+//  * waves are summed through LDS; when K is split across workgroups, each writes
+//    its 32x32 partial and the last to arrive (agent-scope counter, reset by it)
+//    sums the partials in split order -- deterministic -- and runs the epilogue.
+//    Partials are written and read with agent-scope atomic stores and loads, which
+//    go to the memory side past the per-XCD L2s; the writer waits for its stores
+//    to complete before it counts itself in.  (An agent-scope fence instead writes
+//    back / invalidates the whole L2 of the XCD for every workgroup, which costs
+//    microseconds per split.)
+// Every output rounds where the op-by-op path stores fp16 (GEMM result, then the
+// bias/residual/activation), so results equal that path up to fp32 summation order.
+#include "internal.hpp"
+#include "kvc_abi.h"
+
+#include <algorithm>
+#include <cfloat>
+#include <climits>
+#include <cmath>
+
+namespace kvc {
+namespace {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef unsigned u4 __attribute__((ext_vector_type(4)));
+
+constexpr int kRows = 32;      // rows per call (two 16-row MFMA tiles)
+constexpr int kCols = 32;      // outputs per column group (two 16-column tiles)
+constexpr int kOob = 0x7FFFFFF0;  // buffer offset past every descriptor: loads return 0
+
+enum RowsEpi { kEpiStore = 0, kEpiResidual = 1, kEpiQkv = 2, kEpiSwiglu = 3, kEpiLogits = 4 };
+
+struct RowsParams {
+    const _Float16* a;       // [M, K] input rows
+    const _Float16* w;       // weight rows [*, K]
+    const _Float16* norm_w;  // prologue RMSNorm weight [K]
+    float eps;
+    int M, N, K;             // N: outputs per row (kEpiSwiglu: I; W holds 2I rows, gate then up)
+    int splits;              // workgroups per column group along K
+    int gpw;                 // column groups per workgroup (splits == 1)
+    int groups;              // column groups in all
+    float* part;             // [groups * splits][kRows][kCols] split partials
+    unsigned* ctr;           // [groups] arrival counters (zero between calls)
+    _Float16* out;           // store: y; residual: x (+=); swiglu: act; qkv: q
+    const _Float16* bias;    // qkv: [q_cols + 2 kv_cols]
+    _Float16* k_out;
+    _Float16* v_out;
+    const int* pos;          // qkv: rotary position of each row
+    float log2_theta;
+    int q_cols, kv_cols, head_dim;
+    float* logits;           // logits: fp32 [M, N] or nullptr
+    float* best_v;           // logits: [groups][kRows] per-group row maxima
+    int* best_i;
+};
+
+__device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
+
+__device__ __forceinline__ h8 as_h8(u4 v) { return __builtin_bit_cast(h8, v); }
+
+// First W row of tile t (0/1) of column group g; output column = that + lane column.
+template <int EPI>
+__device__ __forceinline__ int tile_row(const RowsParams& p, int g, int t) {
+    if constexpr (EPI == kEpiQkv) {
+        const int gph = p.head_dim / 32;  // column groups per head: (d, d + D/2) rotary pairs
+        return (g / gph) * p.head_dim + 16 * (g % gph) + t * (p.head_dim / 2);
+    } else if constexpr (EPI == kEpiSwiglu) {
+        return t * p.N + 16 * g;
+    } else {
+        return kCols * g + 16 * t;
+    }
+}
+
+__device__ __forceinline__ void better(float& bv, int& bi, float v, int i) {
+    if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
+}
+
+__device__ __forceinline__ _Float16 ld_h(__amdgpu_buffer_rsrc_t r, int byte_ofs) {
+    return __builtin_bit_cast(_Float16, __builtin_amdgcn_raw_buffer_load_b16(r, byte_ofs, 0, 0));
+}
+__device__ __forceinline__ void st_h(__amdgpu_buffer_rsrc_t r, int byte_ofs, _Float16 v) {
+    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, v), r, byte_ofs, 0, 0);
+}
+__device__ __forceinline__ void st_f(__amdgpu_buffer_rsrc_t r, int byte_ofs, float v) {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, byte_ofs, 0, 0);
+}
+
+// Epilogue of one (row m, lane column c) pair: v0 from tile 0, v1 from tile 1.  All
+// memory traffic goes through buffer descriptors bounded by the M valid rows, so
+// rows >= M (and invalid groups, `ok` false) drop their stores without a branch:
+// a branch around a store would make the compiler's load counters inexact and
+// force a full wait on the weight loads in flight.
+template <int EPI>
+__device__ __forceinline__ void epilogue(const RowsParams& p, int g, int m, int c, float v0, float v1, bool ok,
+                                         float& bv, int& bi) {
+    const int c0 = tile_row<EPI>(p, g, 0) + c, c1 = tile_row<EPI>(p, g, 1) + c;
+    const int mm = ok ? m : kRows;  // row index past the descriptors when the group is not valid
+    if constexpr (EPI == kEpiStore) {
+        const auto r = rsrc(p.out, p.M * p.N * 2);
+        st_h(r, (mm * p.N + c0) * 2, (_Float16)v0);
+        st_h(r, (mm * p.N + c1) * 2, (_Float16)v1);
+    } else if constexpr (EPI == kEpiResidual) {
+        const auto r = rsrc(p.out, p.M * p.N * 2);
+        const int o0 = (mm * p.N + c0) * 2, o1 = (mm * p.N + c1) * 2;
+        const float x0 = (float)ld_h(r, o0), x1 = (float)ld_h(r, o1);
+        st_h(r, o0, (_Float16)(x0 + (float)(_Float16)v0));
+        st_h(r, o1, (_Float16)(x1 + (float)(_Float16)v1));
+    } else if constexpr (EPI == kEpiSwiglu) {
+        const float gf = (float)(_Float16)v0, uf = (float)(_Float16)v1;
+        st_h(rsrc(p.out, p.M * p.N * 2), (mm * p.N + 16 * g + c) * 2, (_Float16)(gf / (1.0f + expf(-gf)) * uf));
+    } else if constexpr (EPI == kEpiQkv) {
+        // q/k/v projection + bias (qwen_serve.cu:140-147), rotary on q and k (qwen_kernels.cu:64-79).
+        // The group's columns lie in one head, so its region (q, k or v) is uniform.
+        _Float16 y0 = (_Float16)((float)(_Float16)v0 + (float)p.bias[c0]);
+        _Float16 y1 = (_Float16)((float)(_Float16)v1 + (float)p.bias[c1]);
+        const int t = c0 % p.head_dim;  // < D/2: pair (t, t + D/2)
+        const float inv = exp2f(-p.log2_theta * (2.0f * (float)t / (float)p.head_dim));
+        const int posm = (int)__builtin_amdgcn_raw_buffer_load_b32(rsrc(p.pos, p.M * 4), m * 4, 0, 0);
+        float sn, co;
+        sincosf((float)posm * inv, &sn, &co);
+        const float x1 = (float)y0, x2 = (float)y1;
+        const bool rot = c0 < p.q_cols + p.kv_cols;
+        if (rot) {  // uniform
+            y0 = (_Float16)(x1 * co - x2 * sn);
+            y1 = (_Float16)(x2 * co + x1 * sn);
+        }
+        const bool isq = c0 < p.q_cols;
+        _Float16* base = isq ? p.out : rot ? p.k_out : p.v_out;
+        const int width = isq ? p.q_cols : p.kv_cols;
+        const int col = isq ? c0 : rot ? c0 - p.q_cols : c0 - p.q_cols - p.kv_cols;
+        const auto r = rsrc(base, p.M * width * 2);
+        st_h(r, (mm * width + col) * 2, y0);
+        st_h(r, (mm * width + col + (c1 - c0)) * 2, y1);
+    } else {  // kEpiLogits
+        const auto r = rsrc(p.logits, p.logits ? p.M * p.N * 4 : 0);
+        st_f(r, (mm * p.N + c0) * 4, v0);
+        st_f(r, (mm * p.N + c1) * 4, v1);
+        if (m < p.M) {  // (no memory access inside)
+            better(bv, bi, v0, c0);
+            better(bv, bi, v1, c1);
+        }
+    }
+}
+
+// MT: 16-row tiles of A in use (1 when M <= 16).  S: k steps per wave.  A
+// workgroup runs `gpw` consecutive column groups: the A fragments of each wave's k
+// range stay in registers (normalised once), and the weight loads of the next group
+// are in flight while the current one is reduced across the waves (LDS, double
+// buffered, one barrier per group) and stored.  SPLIT: the K range is split across
+// workgroups (one group per workgroup) and the last to arrive finishes the group.
+template <int EPI, bool NORM, int MT, int WAVES, int S, bool SPLIT>
+__global__ __launch_bounds__(WAVES * 64) void rows_kernel(RowsParams p) {
+    constexpr int kThreads = WAVES * 64;
+    constexpr int kItems = kRows * 16 / kThreads;  // (row, column pair) items per thread
+    __shared__ float s_red[2][WAVES][kRows][kCols + 1];
+    __shared__ float s_ss[WAVES][kRows];
+    __shared__ unsigned s_last;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = uniform(threadIdx.x >> 6);
+    const int unit = uniform(blockIdx.x / p.splits), sp = uniform(blockIdx.x % p.splits);
+    const int g0 = unit * p.gpw;
+    const int ng = min(p.gpw, p.groups - g0);
+    const int ksteps = p.K / 32;
+    const int first = (sp * WAVES + wave) * S;
+    const int nsteps = max(0, min(S, ksteps - first));
+    const int r16 = lane & 15, q4 = lane >> 4;
+    const int kbytes = p.K * 2;
+
+    // A fragments of this wave's k range (rows >= M and steps past K read as zero)
+    const auto ar = rsrc(p.a, p.M * kbytes);
+    u4 af[S][MT];
+    u4 nw[NORM ? S : 1];
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+        const int kofs = (first + i) * 64 + q4 * 16;  // byte offset of the lane's 8 k values
+        const bool in = i < nsteps;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+            af[i][mt] = __builtin_amdgcn_raw_buffer_load_b128(ar, in ? (mt * 16 + r16) * kbytes + kofs : kOob, 0, 0);
+        if constexpr (NORM) nw[i] = __builtin_amdgcn_raw_buffer_load_b128(rsrc(p.norm_w, kbytes), in ? kofs : kOob, 0, 0);
+    }
+    // Weight tiles of group g: two 16-row tiles, S steps each.  Always issued (a
+    // group past the end reads zeros without touching memory), so the instruction
+    // stream has no branches and the compiler's load counters stay exact: the waits
+    // for one group leave the next group's loads in flight.
+    auto load_b = [&](u4 (&b)[S][2], int g, bool valid) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const auto br = rsrc(p.w + (size_t)tile_row<EPI>(p, valid ? g : g0, t) * p.K, 16 * kbytes);
+#pragma unroll
+            for (int i = 0; i < S; ++i)
+                b[i][t] = __builtin_amdgcn_raw_buffer_load_b128(
+                    br, valid && i < nsteps ? r16 * kbytes + (first + i) * 64 + q4 * 16 : kOob, 0, 0);
+        }
+    };
+    u4 b0[S][2], b1[S][2];
+    load_b(b0, g0, true);
+
+    if constexpr (NORM) {
+        // RMSNorm of the rows (qwen_kernels.cu:24-40): sum of squares over this wave's
+        // k range, summed over the waves in LDS, then A = fp16(x * inv_rms * w).
+        float ss[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            ss[mt] = 0.f;
+#pragma unroll
+            for (int i = 0; i < S; ++i) {
+                const h8 x = as_h8(af[i][mt]);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) ss[mt] = __builtin_fmaf((float)x[e], (float)x[e], ss[mt]);
+            }
+            ss[mt] += __shfl_xor(ss[mt], 16);
+            ss[mt] += __shfl_xor(ss[mt], 32);
+            s_ss[wave][mt * 16 + r16] = ss[mt];  // (the four lanes of a row write the same value)
+        }
+        __syncthreads();
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            float tot = 0.f;
+#pragma unroll
+            for (int w = 0; w < WAVES; ++w) tot += s_ss[w][mt * 16 + r16];
+            const float inv = 1.0f / sqrtf(tot / (float)p.K + p.eps);
+#pragma unroll
+            for (int i = 0; i < S; ++i) {
+                const h8 x = as_h8(af[i][mt]), wv = as_h8(nw[i]);
+                h8 y;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) y[e] = (_Float16)((float)x[e] * inv * (float)wv[e]);
+                af[i][mt] = __builtin_bit_cast(u4, y);
+            }
+        }
+    }
+
+    // One column group: MFMAs over this wave's k range, sum over the waves, epilogue.
+    // `ok` false (a group past the end) runs the same code with every store dropped.
+    // Returns false when this workgroup is not the last of a split group (it is done).
+    auto run_group = [&](const u4 (&b)[S][2], int j, bool ok) -> bool {
+        const int g = g0 + j;
+        f4 acc[MT][2];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int t = 0; t < 2; ++t) acc[mt][t] = f4{0.f, 0.f, 0.f, 0.f};
+        // (steps past this wave's range hold zeros: no guard, no branch)
+#pragma unroll
+        for (int i = 0; i < S; ++i)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+                    acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(af[i][mt]), as_h8(b[i][t]), acc[mt][t],
+                                                                        0, 0, 0);
+        // C lane layout: rows 4*(l/16) + r of the 16-row tile, column l%16.
+        float(*red)[kRows][kCols + 1] = s_red[j & 1];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) red[wave][mt * 16 + 4 * q4 + r][t * 16 + r16] = acc[mt][t][r];
+        __syncthreads();
+        float v[kItems][2];
+#pragma unroll
+        for (int it = 0; it < kItems; ++it) {
+            const int item = threadIdx.x + it * kThreads, m = item / 16, c = item % 16;
+            const int mr = m < MT * 16 ? m : 0;  // rows of an unused tile: the sum is never stored
+            v[it][0] = v[it][1] = 0.f;
+#pragma unroll
+            for (int w = 0; w < WAVES; ++w) {
+                v[it][0] += red[w][mr][c];
+                v[it][1] += red[w][mr][c + 16];
+            }
+        }
+        if constexpr (SPLIT) {  // one group per workgroup
+            float* mine = p.part + ((size_t)g * p.splits + sp) * kRows * kCols;
+#pragma unroll
+            for (int it = 0; it < kItems; ++it) {
+                const int item = threadIdx.x + it * kThreads, m = item / 16, c = item % 16;
+                if (m < p.M) {
+                    __hip_atomic_store(mine + m * kCols + c, v[it][0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(mine + m * kCols + c + 16, v[it][1], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+            // every store of this workgroup has completed before the arrival is counted
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            __builtin_amdgcn_s_waitcnt(0);
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            __syncthreads();
+            if (threadIdx.x == 0)
+                s_last = __hip_atomic_fetch_add(p.ctr + g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                         (unsigned)(p.splits - 1);
+            __syncthreads();
+            if (!s_last) return false;
+            const float* all = p.part + (size_t)g * p.splits * kRows * kCols;
+            auto ld = [](const float* a) { return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+#pragma unroll
+            for (int it = 0; it < kItems; ++it) {
+                const int item = threadIdx.x + it * kThreads, m = item / 16, c = item % 16;
+                if (m < p.M) {
+                    float a0 = 0.f, a1 = 0.f;
+                    for (int s2 = 0; s2 < p.splits; ++s2) {
+                        a0 += ld(all + (size_t)s2 * kRows * kCols + m * kCols + c);
+                        a1 += ld(all + (size_t)s2 * kRows * kCols + m * kCols + c + 16);
+                    }
+                    v[it][0] = a0;
+                    v[it][1] = a1;
+                }
+            }
+            if (threadIdx.x == 0) __hip_atomic_store(p.ctr + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+#pragma unroll
+        for (int it = 0; it < kItems; ++it) {
+            const int item = threadIdx.x + it * kThreads, m = item / 16, c = item % 16;
+            float bv = -FLT_MAX;
+            int bi = INT_MAX;
+            epilogue<EPI>(p, ok ? g : g0, m, c, v[it][0], v[it][1], ok, bv, bi);
+            if constexpr (EPI == kEpiLogits) {
+                // the 16 column pairs of row m sit in 16 consecutive lanes
+#pragma unroll
+                for (int o = 1; o < 16; o <<= 1) {
+                    const float ov = __shfl_xor(bv, o);
+                    const int oi = __shfl_xor(bi, o);
+                    better(bv, bi, ov, oi);
+                }
+                // one lane per row stores the group's candidate (rows >= M are never read)
+                const int o = ok && c == 0 ? (g * kRows + m) * 4 : kOob;
+                st_f(rsrc(p.best_v, p.groups * kRows * 4), o, bv);
+                __builtin_amdgcn_raw_buffer_store_b32((unsigned)bi, rsrc(p.best_i, p.groups * kRows * 4), o, 0, 0);
+            }
+        }
+        return true;
+    };
+
+    if constexpr (SPLIT) {
+        run_group(b0, 0, true);
+    } else {
+        // two groups per iteration so the buffers swap roles without register copies
+        for (int j = 0; j < ng; j += 2) {
+            load_b(b1, g0 + j + 1, j + 1 < ng);
+            run_group(b0, j, true);
+            load_b(b0, g0 + j + 2, j + 2 < ng);
+            run_group(b1, j + 1, j + 1 < ng);
+        }
+    }
+}
+
+// tokens[m] = the column of the largest candidate over the groups (first index on ties).
+constexpr int kArgThreads = 256;
+__global__ __launch_bounds__(kArgThreads) void group_argmax_kernel(const float* best_v, const int* best_i, int groups,
+                                                                   int* tokens) {
+    __shared__ float sv[kArgThreads / 64];
+    __shared__ int si[kArgThreads / 64];
+    const int m = blockIdx.x;
+    float bv = -FLT_MAX;
+    int bi = INT_MAX;
+    for (int gi = threadIdx.x; gi < groups; gi += kArgThreads)
+        better(bv, bi, best_v[(size_t)gi * kRows + m], best_i[(size_t)gi * kRows + m]);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float ov = __shfl_xor(bv, o);
+        const int oi = __shfl_xor(bi, o);
+        better(bv, bi, ov, oi);
+    }
+    if ((threadIdx.x & 63) == 0) { sv[threadIdx.x >> 6] = bv; si[threadIdx.x >> 6] = bi; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int k = 1; k < kArgThreads / 64; ++k) better(bv, bi, sv[k], si[k]);
+        tokens[m] = bi == INT_MAX ? 0 : bi;
+    }
+}
+
+// ---- host side ------------------------------------------------------------------
+// Kernel shapes: (waves, k steps per wave) = (4, 7) for K <= 896 with many groups,
+// (8, 4) for K <= 1024 with few groups, (4, 4) with the K range split across
+// workgroups for larger K (no prologue norm then).
+struct Shape {
+    int groups, splits, waves, steps, gpw;
+};
+
+int g_tune_splits = -1, g_tune_gpw = -1, g_tune_shape = -1;  // tuning overrides (-1: automatic)
+
+Shape plan_shape(int groups, int K, bool norm) {
+    const int ks = K / 32;
+    Shape s{groups, 1, 4, 7, 1};
+    int shape = g_tune_shape;
+    if (shape < 0) shape = ks <= 28 && groups >= 128 ? 0 : ks <= 32 ? 1 : 2;
+    if (shape == 0 && ks > 28) shape = 1;
+    if (shape == 1 && ks > 32) shape = 2;
+    if (norm && shape == 2) shape = 1;  // callers reject normalised K above 1024
+    if (shape == 0) { s.waves = 4; s.steps = 7; }
+    else if (shape == 1) { s.waves = 8; s.steps = 4; }
+    else {
+        s.waves = 4; s.steps = 4;
+        const int min_splits = (ks + 15) / 16;
+        s.splits = std::max(min_splits, g_tune_splits > 0 ? std::min(g_tune_splits, ks / 4 > 0 ? ks / 4 : 1) : 0);
+    }
+    if (s.splits == 1) {
+        const int slots = 2 * 256;  // resident workgroups the kernels are sized for
+        s.gpw = g_tune_gpw > 0 ? g_tune_gpw : std::max(1, (groups + slots - 1) / slots);
+    }
+    return s;
+}
+
+size_t part_bytes(const Shape& s) { return s.splits > 1 ? (size_t)s.groups * s.splits * kRows * kCols * 4 : 0; }
+
+template <int EPI, bool NORM>
+int launch_rows(RowsParams p, const Shape& s, hipStream_t st) {
+    p.splits = s.splits;
+    p.gpw = s.gpw;
+    p.groups = s.groups;
+    const dim3 grid((s.groups + s.gpw - 1) / s.gpw * s.splits);
+    const bool two = p.M > 16;
+#define KVC_ROWS_LAUNCH(W, S, SPLIT)                                                                            \
+    do {                                                                                                       \
+        if (two) hipLaunchKernelGGL((rows_kernel<EPI, NORM, 2, W, S, SPLIT>), grid, dim3(W * 64), 0, st, p);   \
+        else hipLaunchKernelGGL((rows_kernel<EPI, NORM, 1, W, S, SPLIT>), grid, dim3(W * 64), 0, st, p);       \
+    } while (0)
+    if (s.waves == 8) KVC_ROWS_LAUNCH(8, 4, false);
+    else if (s.steps == 7) KVC_ROWS_LAUNCH(4, 7, false);
+    else if (s.splits > 1) KVC_ROWS_LAUNCH(4, 4, true);
+    else KVC_ROWS_LAUNCH(4, 4, false);
+#undef KVC_ROWS_LAUNCH
+    return hip_check(hipGetLastError(), "rows linear launch");
+}
+
+// Workspace layout: [counters: 64 KiB][argmax candidates][split partials]
+constexpr size_t kCtrBytes = 64 << 10;
+
+int check_rows(int M, int K, const void* a, const void* w) {
+    if (M < 1 || M > kRows) return set_error(KVC_ERR_ARG, "rows linear: 1 <= M <= 32 rows");
+    if (K <= 0 || K % 32) return set_error(KVC_ERR_ARG, "rows linear: K must be a positive multiple of 32");
+    if ((size_t)K * 2 * kRows > (size_t)INT_MAX) return set_error(KVC_ERR_ARG, "rows linear: K too large");
+    if (!a || !w || ((uintptr_t)a & 15) || ((uintptr_t)w & 15))
+        return set_error(KVC_ERR_ARG, "rows linear: null or misaligned input");
+    return KVC_OK;
+}
+
+int check_norm(const void* norm_w, float eps, int K) {
+    if (!norm_w) return KVC_OK;
+    if (((uintptr_t)norm_w & 15) || !(eps >= 0.f)) return set_error(KVC_ERR_ARG, "rows linear: bad norm weight or eps");
+    if (K > 1024) return set_error(KVC_ERR_UNSUPPORTED, "rows linear: normalised K above 1024");
+    return KVC_OK;
+}
+
+int check_weight_span(size_t rows, int K) {
+    // each 16-row weight tile is addressed with 32-bit offsets
+    if ((size_t)16 * K * 2 > (size_t)INT_MAX || rows == 0) return set_error(KVC_ERR_ARG, "rows linear: bad weight shape");
+    return KVC_OK;
+}
+
+}  // namespace
+}  // namespace kvc
+
+using namespace kvc;
+
+extern "C" {
+
+size_t kvc_rows_workspace_size(int N, int K) {
+    if (N <= 0 || K <= 0 || N % kCols || K % 32) return 0;
+    const Shape s = plan_shape(N / kCols, K, false);
+    const size_t cand = (size_t)(N / kCols) * kRows * 8;
+    return kCtrBytes + (cand + 255) / 256 * 256 + part_bytes(s);
+}
+
+int kvc_rows_linear(void* y, const void* x, const void* w, int M, int N, int K, const void* norm_w, float eps,
+                    int residual, void* ws, size_t ws_bytes, kvc_stream_t st) {
+    try {
+        int rc = check_rows(M, K, x, w);
+        if (!rc) rc = check_norm(norm_w, eps, K);
+        if (!rc) rc = check_weight_span((size_t)N, K);
+        if (rc) return rc;
+        if (N <= 0 || N % kCols || !y || ((uintptr_t)y & 15))
+            return set_error(KVC_ERR_ARG, "rows linear: N must be a positive multiple of 32, y aligned");
+        if (y == x) return set_error(KVC_ERR_ARG, "rows linear: y must not alias x");
+        const int groups = N / kCols;
+        const Shape s = plan_shape(groups, K, norm_w != nullptr);
+        if (s.splits > 1) {
+            if ((size_t)groups * 4 > kCtrBytes) return set_error(KVC_ERR_ARG, "rows linear: N too large to split");
+            if (!ws || ((uintptr_t)ws & 255) || ws_bytes < kCtrBytes + part_bytes(s))
+                return set_error(KVC_ERR_ARG, "rows linear: workspace too small (kvc_rows_workspace_size)");
+        }
+        RowsParams p{};
+        p.a = (const _Float16*)x; p.w = (const _Float16*)w; p.norm_w = (const _Float16*)norm_w; p.eps = eps;
+        p.M = M; p.N = N; p.K = K;
+        p.out = (_Float16*)y;
+        p.ctr = (unsigned*)ws;
+        p.part = ws ? (float*)((char*)ws + kCtrBytes) : nullptr;
+        const hipStream_t hs = (hipStream_t)st;
+        if (norm_w) return residual ? launch_rows<kEpiResidual, true>(p, s, hs) : launch_rows<kEpiStore, true>(p, s, hs);
+        return residual ? launch_rows<kEpiResidual, false>(p, s, hs) : launch_rows<kEpiStore, false>(p, s, hs);
+    } catch (...) {
+        return set_error(KVC_ERR_STATE, "unexpected exception");
+    }
+}
+
+int kvc_rows_qkv(void* q, void* k, void* v, const void* x, const void* norm_w, float eps, const void* w_qkv,
+                 const void* b_qkv, const int* pos, int M, int H, int Hq, int Hkv, int D, float theta,
+                 kvc_stream_t st) {
+    try {
+        int rc = check_rows(M, H, x, w_qkv);
+        if (!rc) rc = check_norm(norm_w, eps, H);
+        if (rc) return rc;
+        if (Hq <= 0 || Hkv <= 0 || D <= 0 || D % 32 || !(theta > 1.f))
+            return set_error(KVC_ERR_ARG, "rows qkv: heads > 0, D a multiple of 32, theta > 1");
+        const int n = (Hq + 2 * Hkv) * D;
+        if ((rc = check_weight_span((size_t)n, H))) return rc;
+        if (!q || !k || !v || !b_qkv || !pos) return set_error(KVC_ERR_ARG, "rows qkv: null pointer");
+        RowsParams p{};
+        p.a = (const _Float16*)x; p.w = (const _Float16*)w_qkv; p.norm_w = (const _Float16*)norm_w; p.eps = eps;
+        p.M = M; p.N = n; p.K = H;
+        p.out = (_Float16*)q; p.k_out = (_Float16*)k; p.v_out = (_Float16*)v;
+        p.bias = (const _Float16*)b_qkv; p.pos = pos; p.log2_theta = log2f(theta);
+        p.q_cols = Hq * D; p.kv_cols = Hkv * D; p.head_dim = D;
+        const Shape s = plan_shape(n / kCols, H, norm_w != nullptr);
+        if (s.splits > 1) return set_error(KVC_ERR_UNSUPPORTED, "rows qkv: K too large for one workgroup");
+        return norm_w ? launch_rows<kEpiQkv, true>(p, s, (hipStream_t)st)
+                      : launch_rows<kEpiQkv, false>(p, s, (hipStream_t)st);
+    } catch (...) {
+        return set_error(KVC_ERR_STATE, "unexpected exception");
+    }
+}
+
+int kvc_rows_swiglu(void* act, const void* x, const void* norm_w, float eps, const void* w_gate_up, int M, int I,
+                    int H, kvc_stream_t st) {
+    try {
+        int rc = check_rows(M, H, x, w_gate_up);
+        if (!rc) rc = check_norm(norm_w, eps, H);
+        if (!rc) rc = check_weight_span((size_t)2 * I, H);
+        if (rc) return rc;
+        if (I <= 0 || I % 16 || !act || ((uintptr_t)act & 15))
+            return set_error(KVC_ERR_ARG, "rows swiglu: I a positive multiple of 16, act aligned");
+        if ((size_t)2 * I * H * 2 > (size_t)UINT32_MAX * 4) return set_error(KVC_ERR_ARG, "rows swiglu: too large");
+        RowsParams p{};
+        p.a = (const _Float16*)x; p.w = (const _Float16*)w_gate_up; p.norm_w = (const _Float16*)norm_w; p.eps = eps;
+        p.M = M; p.N = I; p.K = H;
+        p.out = (_Float16*)act;
+        const Shape s = plan_shape(I / 16, H, norm_w != nullptr);
+        if (s.splits > 1) return set_error(KVC_ERR_UNSUPPORTED, "rows swiglu: K too large for one workgroup");
+        return norm_w ? launch_rows<kEpiSwiglu, true>(p, s, (hipStream_t)st)
+                      : launch_rows<kEpiSwiglu, false>(p, s, (hipStream_t)st);
+    } catch (...) {
+        return set_error(KVC_ERR_STATE, "unexpected exception");
+    }
+}
+
+int kvc_rows_lm_head(float* logits, int* tokens, const void* x, const void* norm_w, float eps, const void* w, int M,
+                     int V, int H, void* ws, size_t ws_bytes, kvc_stream_t st) {
+    try {
+        int rc = check_rows(M, H, x, w);
+        if (!rc) rc = check_norm(norm_w, eps, H);
+        if (!rc) rc = check_weight_span((size_t)V, H);
+        if (rc) return rc;
+        if (V <= 0 || V % kCols) return set_error(KVC_ERR_ARG, "rows lm_head: V must be a positive multiple of 32");
+        if (!tokens) return set_error(KVC_ERR_ARG, "rows lm_head: null tokens");
+        const int groups = V / kCols;
+        const size_t cand = (size_t)groups * kRows * 8;
+        if (!ws || ((uintptr_t)ws & 255) || ws_bytes < kCtrBytes + cand)
+            return set_error(KVC_ERR_ARG, "rows lm_head: workspace too small (kvc_rows_workspace_size)");
+        RowsParams p{};
+        p.a = (const _Float16*)x; p.w = (const _Float16*)w; p.norm_w = (const _Float16*)norm_w; p.eps = eps;
+        p.M = M; p.N = V; p.K = H;
+        p.logits = logits;
+        p.best_v = (float*)((char*)ws + kCtrBytes);
+        p.best_i = (int*)((char*)ws + kCtrBytes + (size_t)groups * kRows * 4);
+        const Shape one = plan_shape(groups, H, true);  // candidates need whole rows: no K split
+        if (one.splits > 1 || H > 1024) return set_error(KVC_ERR_UNSUPPORTED, "rows lm_head: K above 1024");
+        rc = norm_w ? launch_rows<kEpiLogits, true>(p, one, (hipStream_t)st)
+                    : launch_rows<kEpiLogits, false>(p, one, (hipStream_t)st);
+        if (rc) return rc;
+        hipLaunchKernelGGL(group_argmax_kernel, dim3(M), dim3(kArgThreads), 0, (hipStream_t)st, p.best_v, p.best_i,
+                           groups, tokens);
+        return hip_check(hipGetLastError(), "argmax launch");
+    } catch (...) {
+        return set_error(KVC_ERR_STATE, "unexpected exception");
+    }
+}
+
+int kvc_rows_set_tuning(int splits, int groups_per_wg, int shape) {
+    if (splits < -1 || splits == 0 || groups_per_wg < -1 || groups_per_wg == 0 || shape < -1 || shape > 2)
+        return set_error(KVC_ERR_ARG, "rows tuning: splits, groups_per_wg -1 or >= 1; shape -1..2");
+    g_tune_splits = splits;
+    g_tune_gpw = groups_per_wg;
+    g_tune_shape = shape;
+    return KVC_OK;
+}
+
+}  // extern "C"

@@ -28,11 +28,12 @@ class QwenConfig:
     max_batch: int = 32
     max_rows: int = 1024
     seed: int = 0
+    step_path: int = 0  # 0: fused decode-step kernels for steps of <= 32 rows; 1: one kernel per op
 
     def to_c(self) -> QwenConfigC:
         return QwenConfigC(self.layers, self.hidden, self.n_heads, self.n_kv_heads, self.head_dim, self.inter,
                            self.vocab, self.eps, self.theta, self.init_std, self.block_size, self.num_blocks,
-                           self.max_batch, self.max_rows, self.seed)
+                           self.max_batch, self.max_rows, self.seed, self.step_path)
 
 
 class QwenModel:

@@ -24,9 +24,10 @@ def weights(m: QwenModel, cfg: QwenConfig):
     return W
 
 
-@pytest.fixture(scope="module")
-def small():
-    cfg = QwenConfig(layers=2, vocab=4096, num_blocks=512, max_batch=8, max_rows=256, seed=11)
+@pytest.fixture(scope="module", params=[0, 1], ids=["fused", "op-by-op"])
+def small(request):
+    cfg = QwenConfig(layers=2, vocab=4096, num_blocks=512, max_batch=8, max_rows=256, seed=11,
+                     step_path=request.param)
     m = QwenModel(cfg)
     yield cfg, m, weights(m, cfg)
     m.close()
@@ -34,7 +35,7 @@ def small():
 
 def test_small_prefill_logits_and_serving(small):
     cfg, m, W = small
-    say("qwen small: prefill logits")
+    say(f"qwen small: prefill logits, step_path {cfg.step_path}")
     rng = np.random.default_rng(0)
     prompt = rng.integers(0, cfg.vocab, 40)
     tok, lg = m.prefill_logits(prompt)

@@ -1,0 +1,148 @@
+"""Decode-step linear layers over at most 32 rows (fused matrix-core kernels) on the
+GPU, checked against the CPU restatement (oracle/model.py) with the op-by-op
+rounding points (fp16 GEMM result, then bias / residual / activation), and against
+the op-by-op GPU path (rmsnorm + rocBLAS linear + elementwise kernels), which they
+replace in the decode step (qwen_serve.cu:127-175)."""
+import numpy as np
+import pytest
+
+from kvcache_amd import KVC_F16, KVC_F32, ops
+from kvcache_amd.device import DeviceBuffer
+from oracle import model as M
+from oracle.model import _r16
+
+from _helpers import dev, host, normal, say
+
+pytestmark = pytest.mark.gpu
+EPS = 1e-6
+
+
+def close(got, ref, rel=4e-3):
+    got = np.asarray(got, np.float64)
+    err = np.abs(got - ref) - rel * np.maximum(1.0, np.abs(ref))
+    assert np.all(err <= 0), (np.abs(got - ref).max(), np.unravel_index(np.argmax(err), err.shape))
+
+
+def workspace(N, K):
+    ws = DeviceBuffer(max(ops.rows_workspace_size(N, K), 1 << 20))
+    ws.zero()
+    return ws
+
+
+def inputs(M_, K, seed):
+    x = normal((M_, K), seed, np.float16)
+    nw = (1 + 0.1 * normal((K,), seed + 1)).astype(np.float16)
+    return x, nw
+
+
+@pytest.mark.parametrize("M_", [1, 5, 16, 17, 32])
+@pytest.mark.parametrize("norm", [False, True])
+def test_rows_linear_store(M_, norm):
+    say(f"rows linear store M={M_} norm={norm}")
+    N, K = 896, 896
+    x, nw = inputs(M_, K, 300 + M_)
+    w = (0.03 * normal((N, K), 302)).astype(np.float16)
+    y = DeviceBuffer(M_ * N * 2)
+    ops.rows_linear(y, dev(x), dev(w), M_, N, K, norm_w=dev(nw) if norm else None, eps=EPS,
+                    workspace=workspace(N, K))
+    a = _r16(M.rmsnorm(x, nw, EPS)) if norm else x.astype(np.float32)
+    ref = M.linear(a, w)
+    close(host(y, np.float16, (M_, N)), ref)
+
+
+@pytest.mark.parametrize("M_,K,splits", [(32, 896, -1), (7, 896, 1), (32, 4864, -1), (20, 4864, 7), (3, 4864, 40),
+                                         (16, 4864, 5)])
+def test_rows_linear_residual_splits(M_, K, splits):
+    say(f"rows linear residual M={M_} K={K} splits={splits}")
+    N = 896
+    a = normal((M_, K), 310, np.float16)
+    w = (0.03 * normal((N, K), 311)).astype(np.float16)
+    x0 = normal((M_, N), 312, np.float16)
+    ops.rows_set_tuning(splits=splits)  # before sizing: the workspace holds one partial per split
+    try:
+        ws = workspace(N, K)
+        outs = []
+        for _ in range(2):  # deterministic: the split partials are summed in a fixed order
+            x = dev(x0)
+            ops.rows_linear(x, dev(a), dev(w), M_, N, K, residual=True, workspace=ws)
+            outs.append(host(x, np.float16, (M_, N)))
+    finally:
+        ops.rows_set_tuning()
+    np.testing.assert_array_equal(outs[0], outs[1])
+    ref = x0.astype(np.float64) + _r16(M.linear(a, w))
+    close(outs[0], ref)
+    # the op-by-op GPU path: rocBLAS linear, then the residual kernel
+    y = DeviceBuffer(M_ * N * 2)
+    ops.linear(y, dev(a), dev(w), M_, N, K)
+    x = dev(x0)
+    ops.qk_add_residual(x, y, M_ * N)
+    d = np.abs(outs[0].astype(np.float64) - host(x, np.float16, (M_, N)))
+    assert d.max() <= 4e-3 * max(1.0, np.abs(ref).max()), d.max()
+
+
+@pytest.mark.parametrize("M_", [1, 9, 32])
+def test_rows_qkv_rope(M_):
+    say(f"rows qkv M={M_}")
+    H, Hq, Hkv, D, theta = 896, 14, 2, 64, 1e6
+    QD, KD = Hq * D, Hkv * D
+    x, nw = inputs(M_, H, 320)
+    w = (0.03 * normal((QD + 2 * KD, H), 322)).astype(np.float16)
+    b = (0.5 * normal((QD + 2 * KD,), 323)).astype(np.float16)
+    pos = np.random.default_rng(324).integers(0, 40000, M_).astype(np.int32)
+    q, k, v = DeviceBuffer(M_ * QD * 2), DeviceBuffer(M_ * KD * 2), DeviceBuffer(M_ * KD * 2)
+    ops.rows_qkv(q, k, v, dev(x), dev(w), dev(b), dev(pos), M_, H, Hq, Hkv, D, theta, norm_w=dev(nw), eps=EPS)
+    n = _r16(M.rmsnorm(x, nw, EPS))
+    y = _r16(_r16(M.linear(n, w)) + b.astype(np.float32))
+    rq = M.rope(y[:, :QD].reshape(M_, Hq, D), pos, D, theta).reshape(M_, QD)
+    rk = M.rope(y[:, QD:QD + KD].reshape(M_, Hkv, D), pos, D, theta).reshape(M_, KD)
+    close(host(q, np.float16, (M_, QD)), rq)
+    close(host(k, np.float16, (M_, KD)), rk)
+    close(host(v, np.float16, (M_, KD)), y[:, QD + KD:])
+
+
+@pytest.mark.parametrize("M_", [1, 12, 32])
+def test_rows_swiglu(M_):
+    say(f"rows swiglu M={M_}")
+    H, I = 896, 4864
+    x, nw = inputs(M_, H, 330)
+    wgu = (0.03 * normal((2 * I, H), 332)).astype(np.float16)
+    act = DeviceBuffer(M_ * I * 2)
+    ops.rows_swiglu(act, dev(x), dev(wgu), M_, I, H, norm_w=dev(nw), eps=EPS)
+    n = _r16(M.rmsnorm(x, nw, EPS))
+    ref = M.silu_mul(_r16(M.linear(n, wgu[:I])), _r16(M.linear(n, wgu[I:])))
+    close(host(act, np.float16, (M_, I)), ref)
+
+
+@pytest.mark.parametrize("M_,V", [(1, 151936), (32, 151936), (19, 4096)])
+def test_rows_lm_head(M_, V):
+    say(f"rows lm_head M={M_} V={V}")
+    H = 896
+    x, nw = inputs(M_, H, 340)
+    w = (0.03 * normal((V, H), 342)).astype(np.float16)
+    w[V - 1] = w[5]  # identical rows: equal logits, the first index must win
+    ws = workspace(V, H)
+    logits, tok = DeviceBuffer(M_ * V * 4), DeviceBuffer(M_ * 4)
+    ops.rows_lm_head(logits, tok, dev(x), dev(w), M_, V, H, norm_w=dev(nw), eps=EPS, workspace=ws)
+    lg = host(logits, np.float32, (M_, V))
+    ref = M.linear(_r16(M.rmsnorm(x, nw, EPS)), w)
+    close(lg, ref)
+    t = host(tok, np.int32, (M_,))
+    np.testing.assert_array_equal(t, np.argmax(lg, axis=1))
+    # without the logits buffer the tokens are the same
+    tok2 = DeviceBuffer(M_ * 4)
+    ops.rows_lm_head(None, tok2, dev(x), dev(w), M_, V, H, norm_w=dev(nw), eps=EPS, workspace=ws)
+    np.testing.assert_array_equal(host(tok2, np.int32, (M_,)), t)
+
+
+def test_rows_rejects_bad_shapes():
+    say("rows: argument errors")
+    from kvcache_amd import KvcError
+    ws = workspace(896, 896)
+    x, w, y = DeviceBuffer(64 * 896 * 2), DeviceBuffer(896 * 896 * 2), DeviceBuffer(64 * 896 * 2)
+    for M_, N, K in [(0, 896, 896), (33, 896, 896), (4, 900, 896), (4, 896, 900)]:
+        with pytest.raises(KvcError):
+            ops.rows_linear(y, x, w, M_, N, K, workspace=ws)
+    with pytest.raises(KvcError):
+        ops.rows_linear(x, x, w, 4, 896, 896)  # y aliases x
+    with pytest.raises(KvcError):  # split layer without a workspace
+        ops.rows_linear(y, x, DeviceBuffer(896 * 4864 * 2), 4, 896, 4864, residual=True)
