@@ -323,6 +323,8 @@ def bench_c4():
     cfg = EngineConfig(n_heads=14, n_kv_heads=2, head_dim=64, block_size=16, num_blocks=num_blocks, max_batch=32,
                        n_layers=24, dtype=KVC_F16, kv_write=True, clock_mode=0)
     eng = Engine(cfg)
+    import dataclasses
+    eng_g = Engine(dataclasses.replace(cfg, graph=True))  # the 24 launches of a step replayed as one HIP graph
     out = {"workload": "C4 256 requests, width 32, 2048 MB pool, 24 layers write+decode, 14q/2kv D64 fp16",
            "num_blocks": num_blocks}
     for name, trace in (("offline", Wl.baseline_trace(256, 0.0, 11)), ("poisson400", Wl.baseline_trace(256, 400.0, 11)),
@@ -330,6 +332,7 @@ def bench_c4():
         p, g, a = trace
         res = {}
         for pol, fn in (("continuous", lambda: run_continuous(p, g, a, eng)),
+                        ("continuous_graph", lambda: run_continuous(p, g, a, eng_g)),
                         ("static", lambda: run_static(p, g, a, eng, 32))):
             st = fn()
             res[pol] = {"iters": st.iters, "tokens": st.tokens,

@@ -43,6 +43,7 @@ struct EngineConfig {
     int decode_path = KVC_DECODE_PLANNED;
     bool prefill = false;     // admitted prompts run K/V writes + causal attention (measured clock)
     uint64_t seed = 0x6b76636163686531ull;
+    bool graph = false;       // planned decode steps replay one captured HIP graph
 };
 
 struct EngineStats {
@@ -90,6 +91,7 @@ inline RunnerOptions runner_options(const EngineConfig& c) {
     o.decode_path = c.decode_path;
     o.prefill = c.prefill;
     o.seed = c.seed;
+    o.graph = c.graph;
     return o;
 }
 

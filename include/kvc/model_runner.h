@@ -20,7 +20,10 @@
 //   * decode is host-planned by default: the lengths are known here, so the step
 //     cuts every sequence into near-equal chunks (kvc_decode_plan), appends the
 //     work list to the same upload and launches the planned kernel, which needs
-//     no per-sequence device lookups and balances ragged batches.
+//     no per-sequence device lookups and balances ragged batches;
+//   * with `graph` the planned step's n_layers launches are captured once as a HIP
+//     graph of graph-safe launches (counts read from device memory, fixed-capacity
+//     grids) and each step uploads its metadata to fixed places and replays it.
 // Query/key/value inputs are synthetic N(0,1) buffers filled once on the device.
 #pragma once
 #include <algorithm>
@@ -45,6 +48,7 @@ struct RunnerOptions {
     int plan_target = 0;     // planned path: tokens per unit (0 automatic)
     bool fuse_append = true; // planned path with kv_write: write the new rows inside the decode launch
     bool prefill = false;    // run each admitted prompt's K/V writes + causal attention (prefill)
+    bool graph = false;      // planned steps replay one captured HIP graph
     uint64_t seed = 0x6b76636163686531ull;
 };
 
@@ -78,6 +82,16 @@ struct ModelRunner {
     uint64_t digest = 1469598103934665603ull;
     long long last_sum_len = 0;
     int last_cap = 0;
+    // graph replay: metadata at fixed places [N, units, records, 0 | wpos cap_n |
+    // work cap_units*ipu | table cap_tab] in d_g, a pinned ring h_g of the same layout
+    void* gexec = nullptr;
+    const KVCacheManager* g_kvm = nullptr;  // pools the graph was captured with
+    bool graph_failed = false;
+    int* d_g = nullptr;
+    int* h_g[kRing] = {};
+    int g_cap_units = 0, g_ipu = 0;
+    size_t g_off_work = 0, g_off_tab = 0;
+    long long graph_steps = 0;
 
     ModelRunner(int n_heads_, int head_dim_, int block_size_, int max_batch_, int max_pool_blocks_,
                 const RunnerOptions& o = RunnerOptions())
@@ -117,6 +131,9 @@ struct ModelRunner {
         kvc_event_destroy(h_ptab_ev);
         for (int i = 0; i < kRing; ++i) { kvc_host_free(h_meta[i]); kvc_event_destroy(h_ev[i]); }
         kvc_event_destroy(ev0); kvc_event_destroy(ev1);
+        kvc_graph_destroy(gexec);
+        kvc_free(d_g);
+        for (int i = 0; i < kRing; ++i) kvc_host_free(h_g[i]);
         kvc_stream_destroy(stream);
     }
     ModelRunner(const ModelRunner&) = delete;
@@ -144,6 +161,8 @@ struct ModelRunner {
     void ensure_workspace(size_t need) {
         if (need <= ws_bytes) return;
         kvc::check(kvc_stream_synchronize(stream), "workspace growth");
+        kvc_graph_destroy(gexec);  // it holds the old workspace
+        gexec = nullptr;
         kvc_free(ws);
         ws = nullptr;
         ws_bytes = 0;
@@ -238,6 +257,9 @@ struct ModelRunner {
         const int* d_tab = d_len + 3 * n;
         const int* d_work = d_tab + T;
 
+        if (planned && opt.graph && (!opt.kv_write || opt.fuse_append) && ensure_graph(kvm) &&
+            n_units <= g_cap_units && n_records <= g_cap_units)
+            return replay(n, T, n_units, n_records, virt);
         ensure_workspace(planned ? kvc_decode_planned_workspace_size(n_heads, n_kv_heads, head_dim, block_size,
                                                                    opt.dtype, n_records)
                                  : kvc_decode_workspace_size(n, n_heads, n_kv_heads, head_dim, block_size, cap,
@@ -272,6 +294,75 @@ struct ModelRunner {
                            "paged decode");
         }
         kvc::check(kvc_event_record(ev1, stream), "event");
+        if (opt.clock_mode != 0) return virt;
+        float ms = 0.f;
+        kvc::check(kvc_event_elapsed_ms(&ms, ev0, ev1), "event elapsed");
+        return (double)ms * 1e3;
+    }
+
+    // Captures the planned step (n_layers graph-safe launches) for these pools.
+    bool ensure_graph(const KVCacheManager& kvm) {
+        if (gexec && g_kvm == &kvm) return true;
+        if (graph_failed) return false;
+        kvc_graph_destroy(gexec);
+        gexec = nullptr;
+        if (!d_g) {
+            g_ipu = kvc_decode_plan_entry_ints(n_heads, n_kv_heads, head_dim, block_size, opt.dtype);
+            kvc::check(kvc_decode_plan_capacity(max_batch, (long long)max_pool_blocks * block_size, n_heads,
+                                                n_kv_heads, head_dim, block_size, opt.dtype, &g_cap_units),
+                       "plan capacity");
+            g_off_work = 4 + (size_t)max_batch;
+            g_off_tab = g_off_work + (size_t)g_cap_units * g_ipu;
+            const size_t ints = g_off_tab + max_pool_blocks;
+            kvc::check(kvc_malloc((void**)&d_g, ints * sizeof(int)), "graph metadata");
+            for (int i = 0; i < kRing; ++i)
+                kvc::check(kvc_host_alloc((void**)&h_g[i], ints * sizeof(int)), "pinned graph metadata");
+            kvc::check(kvc_memset(d_g, 0, ints * sizeof(int), stream), "graph metadata");
+        }
+        ensure_workspace(kvc_decode_planned_workspace_size(n_heads, n_kv_heads, head_dim, block_size, opt.dtype,
+                                                           g_cap_units));
+        kvc::check(kvc_stream_synchronize(stream), "graph setup");
+        const int* d_counts = d_g;
+        const int* d_wpos = d_g + 4;
+        const int* d_work = d_g + g_off_work;
+        const int* d_tab = d_g + g_off_tab;
+        kvc::check(kvc_graph_begin(stream), "graph capture");
+        int rc = KVC_OK;
+        for (int l = 0; l < opt.n_layers && rc == KVC_OK; ++l)
+            rc = kvc_batched_paged_decode_planned_dev(
+                q_layer(l), opt.kv_write ? k_layer(l) : nullptr, opt.kv_write ? v_layer(l) : nullptr,
+                opt.kv_write ? d_wpos : nullptr, kvm.k_layer(l), kvm.v_layer(l), d_tab, max_pool_blocks, dout,
+                max_batch, n_heads, n_kv_heads, head_dim, block_size, scale, opt.dtype, d_work, g_cap_units,
+                g_cap_units, d_counts, ws, ws_bytes, stream);
+        void* exec = nullptr;
+        const int rc_end = kvc_graph_end(stream, &exec);
+        if (rc != KVC_OK || rc_end != KVC_OK) {
+            kvc_graph_destroy(exec);
+            graph_failed = true;
+            return false;
+        }
+        gexec = exec;
+        g_kvm = &kvm;
+        return true;
+    }
+
+    // One planned step by graph replay (the metadata of h_tab/h_wpos/h_work).
+    double replay(int n, int T, int n_units, int n_records, double virt) {
+        if (h_ev_used[ring]) kvc::check(kvc_event_synchronize(h_ev[ring]), "meta ring wait");
+        int* h = h_g[ring];
+        h[0] = n; h[1] = n_units; h[2] = n_records; h[3] = 0;
+        if (opt.kv_write) std::memcpy(h + 4, h_wpos.data(), n * sizeof(int));
+        std::memcpy(h + g_off_work, h_work.data(), h_work.size() * sizeof(int));
+        std::memcpy(h + g_off_tab, h_tab.data(), (size_t)T * sizeof(int));
+        kvc::check(kvc_step_upload(d_g, h, (g_off_work + h_work.size()) * sizeof(int), stream), "step upload");
+        kvc::check(kvc_step_upload(d_g + g_off_tab, h + g_off_tab, (size_t)T * sizeof(int), stream), "table upload");
+        kvc::check(kvc_event_record(h_ev[ring], stream), "meta ring record");
+        h_ev_used[ring] = true;
+        ring = (ring + 1) % kRing;
+        kvc::check(kvc_event_record(ev0, stream), "event");
+        kvc::check(kvc_graph_launch(gexec, stream), "graph launch");
+        kvc::check(kvc_event_record(ev1, stream), "event");
+        ++graph_steps;
         if (opt.clock_mode != 0) return virt;
         float ms = 0.f;
         kvc::check(kvc_event_elapsed_ms(&ms, ev0, ev1), "event elapsed");

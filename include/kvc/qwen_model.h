@@ -12,7 +12,11 @@
 // K/V written in the same launch; output projection + residual; RMSNorm + gate/up
 // projection + SwiGLU; down projection + residual; then final norm + lm_head +
 // argmax.  step_path 1 (and larger batches, and prompts) run one kernel per op with
-// rocBLAS linear layers; both round to fp16 at the same points.
+// rocBLAS linear layers; both round to fp16 at the same points.  With `graph` the
+// fused step is captured once as a HIP graph whose kernels read the step's counts
+// (rows, attention units, partial records) from device memory; each step then
+// uploads its metadata into fixed places and replays the graph (the reference
+// captures its single-sequence decode step, qwen_infer.cu:135-214).
 //
 // Greedy serving (QwenModel::serve): requests are admitted FIFO up to max_batch
 // running sequences; an admitted request is prefilled (its first token comes from
@@ -36,6 +40,7 @@ struct QwenConfig {
     int block_size = 16, num_blocks = 10922, max_batch = 32, max_rows = 1024;  // max_rows: prompt rows per prefill
     uint64_t seed = 0x71776e32ull;
     int step_path = 0;  // 0: fused kernels for steps of <= 32 rows; 1: one kernel per op
+    int graph = 1;      // fused steps replay one captured HIP graph
 };
 
 struct QwenModel {
@@ -63,6 +68,15 @@ struct QwenModel {
     void* rws = nullptr;  // fused kernels' workspace (zero between calls)
     size_t rws_bytes = 0;
     bool rows_ok = false;
+    // graph-replayed steps: metadata at fixed places,
+    // [n, units, records, 0 | ids B | pos B | work cap_units*ipu | table cap_tab]
+    void* gexec = nullptr;
+    bool graph_failed = false;
+    int* d_g = nullptr;
+    int* h_g = nullptr;
+    int g_cap_units = 0, g_cap_tab = 0, g_ipu = 0;
+    size_t g_off_work = 0, g_off_tab = 0;
+    long long graph_steps = 0;
     std::vector<int> h_work, h_tab, h_off, h_len;
 
     explicit QwenModel(const QwenConfig& cfg)
@@ -119,6 +133,8 @@ struct QwenModel {
     }
     ~QwenModel() {
         if (stream) kvc_stream_synchronize(stream);
+        kvc_graph_destroy(gexec);
+        kvc_free(d_g); kvc_host_free(h_g);
         for (void* p : owned) kvc_free(p);
         kvc_free(d_meta); kvc_free(ws);
         kvc_host_free(h_meta); kvc_host_free(h_tok);
@@ -185,35 +201,49 @@ struct QwenModel {
         }
     }
 
-    // Decode-step layers over M <= 32 rows with the fused kernels.
-    void rows_layers(int M, const int* d_pos, const int* d_table, int T, const int* d_work, int nu, int nr) {
+    // Decode-step layers over M <= 32 rows with the fused kernels.  With d_counts
+    // (graph capture) M, T, nu and nr are capacities and the step's counts are read
+    // from d_counts = {rows, units, records} in device memory.
+    void rows_layers(int M, const int* d_pos, const int* d_table, int T, const int* d_work, int nu, int nr,
+                     const int* d_counts = nullptr) {
+        const int* d_rows = d_counts;
         const int H = c.hidden, QD = c.n_heads * c.head_dim, I = c.inter;
         const float scale = 1.0f / __builtin_sqrtf((float)c.head_dim);
         for (int l = 0; l < c.layers; ++l) {
             const Layer& w = L[l];
             kvc::check(kvc_rows_qkv(q, k, v, x, w.ln1, c.eps, w.wq, w.bq, d_pos, M, H, c.n_heads, c.n_kv_heads,
-                                    c.head_dim, c.theta, stream),
+                                    c.head_dim, c.theta, d_rows, stream),
                        "norm + qkv + rope");
-            kvc::check(kvc_batched_paged_append_decode_planned(q, k, v, d_pos, kl(l), vl(l), d_table, T, att, M,
-                                                               c.n_heads, c.n_kv_heads, c.head_dim, c.block_size,
-                                                               scale, KVC_F16, d_work, nu, nr, ws, ws_bytes, stream),
-                       "decode attention");
-            kvc::check(kvc_rows_linear(x, att, w.wo, M, H, QD, nullptr, 0.f, 1, rws, rws_bytes, stream),
+            if (d_counts)
+                kvc::check(kvc_batched_paged_decode_planned_dev(q, k, v, d_pos, kl(l), vl(l), d_table, T, att, M,
+                                                                c.n_heads, c.n_kv_heads, c.head_dim, c.block_size,
+                                                                scale, KVC_F16, d_work, nu, nr, d_counts, ws,
+                                                                ws_bytes, stream),
+                           "decode attention");
+            else
+                kvc::check(kvc_batched_paged_append_decode_planned(q, k, v, d_pos, kl(l), vl(l), d_table, T, att, M,
+                                                                   c.n_heads, c.n_kv_heads, c.head_dim, c.block_size,
+                                                                   scale, KVC_F16, d_work, nu, nr, ws, ws_bytes,
+                                                                   stream),
+                           "decode attention");
+            kvc::check(kvc_rows_linear(x, att, w.wo, M, H, QD, nullptr, 0.f, 1, d_rows, rws, rws_bytes, stream),
                        "o_proj + residual");
-            kvc::check(kvc_rows_swiglu(gate, x, w.ln2, c.eps, w.wg, M, I, H, stream), "norm + gate/up + swiglu");
-            kvc::check(kvc_rows_linear(x, gate, w.wd, M, H, I, nullptr, 0.f, 1, rws, rws_bytes, stream),
+            kvc::check(kvc_rows_swiglu(gate, x, w.ln2, c.eps, w.wg, M, I, H, d_rows, stream),
+                       "norm + gate/up + swiglu");
+            kvc::check(kvc_rows_linear(x, gate, w.wd, M, H, I, nullptr, 0.f, 1, d_rows, rws, rws_bytes, stream),
                        "down_proj + residual");
         }
     }
 
     // Final norm of `rows` rows starting at x row `first` (consecutive), fp32 logits
-    // (optional on the fused path), argmax.
-    void head(int first, int rows, bool want_logits = true) {
+    // (optional on the fused path), argmax.  d_rows_head: the row count in device
+    // memory (graph capture; `rows` is then the capacity).
+    void head(int first, int rows, bool want_logits = true, const int* d_rows_head = nullptr) {
         const int H = c.hidden;
         const void* xr = static_cast<const char*>(x) + (size_t)first * H * 2;
         if (rows_ok && rows <= kRowsMax) {
             kvc::check(kvc_rows_lm_head(want_logits ? logits : nullptr, d_tok, xr, normf, c.eps, embed, rows, c.vocab,
-                                        H, rws, rws_bytes, stream),
+                                        H, d_rows_head, rws, rws_bytes, stream),
                        "final norm + lm_head + argmax");
             return;
         }
@@ -276,6 +306,11 @@ struct QwenModel {
         kvc::check(kvc_decode_plan(h_len.data(), h_off.data(), h_tab.data(), T, n, c.n_heads, c.n_kv_heads,
                                    c.head_dim, c.block_size, KVC_F16, 0, h_work.data(), nu, &nu, &nr),
                    "plan");
+        if (rows_ok && c.graph && n <= kRowsMax && ensure_graph() && nu <= g_cap_units && nr <= g_cap_units &&
+            T <= g_cap_tab) {
+            decode_graph(n, in, T, nu, nr, ipu, out);
+            return;
+        }
         // upload: [ids n | pos n | table T | work]
         const size_t ints = 2 * (size_t)n + T + h_work.size();
         ensure_meta(ints);
@@ -309,13 +344,72 @@ struct QwenModel {
         std::memcpy(out, h_tok, n * 4);
     }
 
+    // The captured step: capacities fixed here, counts and metadata per step in d_g.
+    bool ensure_graph() {
+        if (gexec) return true;
+        if (graph_failed) return false;
+        const int B = c.max_batch;
+        if (B > kRowsMax) { graph_failed = true; return false; }
+        g_ipu = kvc_decode_plan_entry_ints(c.n_heads, c.n_kv_heads, c.head_dim, c.block_size, KVC_F16);
+        // the planner's bound for B sequences over the whole pool; tables: the whole pool
+        kvc::check(kvc_decode_plan_capacity(B, (long long)c.num_blocks * c.block_size, c.n_heads, c.n_kv_heads,
+                                            c.head_dim, c.block_size, KVC_F16, &g_cap_units),
+                   "plan capacity");
+        g_cap_tab = c.num_blocks;
+        g_off_work = 4 + 2 * (size_t)B;
+        g_off_tab = g_off_work + (size_t)g_cap_units * g_ipu;
+        const size_t ints = g_off_tab + g_cap_tab;
+        kvc::check(kvc_malloc((void**)&d_g, ints * 4), "graph metadata");
+        kvc::check(kvc_host_alloc((void**)&h_g, ints * 4), "pinned graph metadata");
+        kvc::check(kvc_memset(d_g, 0, ints * 4, stream), "graph metadata");  // zero counts: an idle replay
+        ensure_ws(kvc_decode_planned_workspace_size(c.n_heads, c.n_kv_heads, c.head_dim, c.block_size, KVC_F16,
+                                                    g_cap_units));
+        kvc::check(kvc_stream_synchronize(stream), "graph setup");
+        const int* d_counts = d_g;
+        const int* d_ids = d_g + 4;
+        const int* d_pos = d_ids + B;
+        const int* d_work = d_g + g_off_work;
+        const int* d_table = d_g + g_off_tab;
+        kvc::check(kvc_graph_begin(stream), "graph capture");
+        try {
+            kvc::check(kvc_embed_gather_dev(x, embed, d_ids, d_counts, B, c.hidden, c.vocab, stream), "embed");
+            rows_layers(B, d_pos, d_table, g_cap_tab, d_work, g_cap_units, g_cap_units, d_counts);
+            head(0, B, false, d_counts);
+        } catch (...) {
+            void* partial = nullptr;
+            kvc_graph_end(stream, &partial);
+            kvc_graph_destroy(partial);
+            graph_failed = true;
+            throw;
+        }
+        kvc::check(kvc_graph_end(stream, &gexec), "graph instantiate");
+        return true;
+    }
+
+    void decode_graph(int n, const int* in, int T, int nu, int nr, int ipu, int* out) {
+        const int B = c.max_batch;
+        int* h = h_g;
+        h[0] = n; h[1] = nu; h[2] = nr; h[3] = 0;
+        std::memcpy(h + 4, in, n * 4);
+        for (int r = 0; r < n; ++r) h[4 + B + r] = h_len[r] - 1;  // the new token's position
+        std::memcpy(h + g_off_work, h_work.data(), (size_t)nu * ipu * 4);
+        std::memcpy(h + g_off_tab, h_tab.data(), (size_t)T * 4);
+        kvc::check(kvc_step_upload(d_g, h, (g_off_work + (size_t)nu * ipu) * 4, stream), "step upload");
+        kvc::check(kvc_step_upload(d_g + g_off_tab, h + g_off_tab, (size_t)T * 4, stream), "table upload");
+        kvc::check(kvc_graph_launch(gexec, stream), "graph launch");
+        kvc::check(kvc_memcpy_d2h(h_tok, d_tok, n * 4, stream), "tokens");
+        kvc::check(kvc_stream_synchronize(stream), "decode");
+        std::memcpy(out, h_tok, n * 4);
+        ++graph_steps;
+    }
+
     struct Request {
         std::vector<int> prompt;
         int gen_len = 0;
     };
     struct ServeStats {
         int steps = 0, finished = 0;
-        long long tokens = 0, prompt_tokens = 0;
+        long long tokens = 0, prompt_tokens = 0, graph_steps = 0;
         double wall_us = 0, prefill_us = 0, decode_us = 0;
     };
 
@@ -323,6 +417,7 @@ struct QwenModel {
     ServeStats serve(const std::vector<Request>& reqs, std::vector<std::vector<int>>& out) {
         using clk = std::chrono::steady_clock;
         ServeStats st;
+        const long long graph_steps0 = graph_steps;
         kvm.reset();
         out.assign(reqs.size(), {});
         std::vector<Sequence> seqs(reqs.size());
@@ -390,6 +485,7 @@ struct QwenModel {
             }
         }
         st.wall_us = std::chrono::duration<double, std::micro>(clk::now() - t0).count();
+        st.graph_steps = graph_steps - graph_steps0;
         return st;
     }
 };

@@ -85,6 +85,16 @@ int kvc_event_destroy(void* ev);
 int kvc_event_record(void* ev, kvc_stream_t stream);
 int kvc_event_synchronize(void* ev);
 int kvc_event_elapsed_ms(float* ms, void* start, void* stop); /* synchronizes on stop */
+/* HIP graphs (stream capture): the launches made on `stream` between begin and end
+ * are recorded, not run; end instantiates them as one executable graph, launch
+ * replays it on a stream (the reference captures its decode step as a CUDA graph,
+ * qwen_infer.cu:135-214).  Only graph-safe entry points may be captured: those that
+ * allocate nothing and take per-step counts from device memory (the *_dev and
+ * dev_rows forms below). */
+int kvc_graph_begin(kvc_stream_t stream);
+int kvc_graph_end(kvc_stream_t stream, void** graph_exec);
+int kvc_graph_launch(void* graph_exec, kvc_stream_t stream);
+int kvc_graph_destroy(void* graph_exec);
 
 /* One packed per-step upload: copies `bytes` from (preferably pinned) host
  * memory to the device with a single async copy on `stream`.  Replaces the
@@ -211,6 +221,24 @@ int kvc_batched_paged_append_decode_planned(const void* q, const void* k_new, co
                                             int dtype, const int* work, int n_units, int n_records,
                                             void* workspace, size_t workspace_bytes, kvc_stream_t stream);
 
+/* Upper bound on the units (and partial records) of any plan of N sequences holding
+ * at most total_tokens tokens: the capacity a graph-safe launch is sized for. */
+int kvc_decode_plan_capacity(int N, long long total_tokens, int Hq, int Hkv, int D, int BLOCK, int dtype,
+                             int* max_units);
+
+/* Graph-safe form of the two planned launches above (no counterpart in the
+ * reference, whose graph variants read positions through device pointers,
+ * qwen_kernels.cu:83-99,128-143,187-226): the step's {N, n_units, n_records} are
+ * read from dev_counts[0..2] in device memory, so one captured launch serves every
+ * step.  N_cap, units_cap and records_cap are capacities: the grid is units_cap
+ * workgroups (those past the step's n_units exit at once), `work` holds units_cap
+ * entries, the workspace is sized for records_cap.  k_new == NULL: no append. */
+int kvc_batched_paged_decode_planned_dev(const void* q, const void* k_new, const void* v_new, const int* wpos,
+                                        void* k_pool, void* v_pool, const int* table_all, int table_len, void* out,
+                                        int N_cap, int Hq, int Hkv, int D, int BLOCK, float scale, int dtype,
+                                        const int* work, int units_cap, int records_cap, const int* dev_counts,
+                                        void* workspace, size_t workspace_bytes, kvc_stream_t stream);
+
 /* qk_paged_causal_attn (qwen_kernels.h:19-21, qwen_kernels.cu:146-181): the prompt
  * (prefill) attention of one sequence.  Query i of q [Nq, Hq, D] sits at position
  * q_pos_base + i and attends causally to positions 0 .. q_pos_base + i of the
@@ -235,6 +263,9 @@ size_t kvc_paged_causal_attn_workspace_size(int q_pos_base, int Nq, int Hq, int 
  * kvc_linear: the linear layers (cuBLAS in the reference, rocBLAS here):
  *   y[M,N] = x[M,K] w[N,K]^T, fp16 inputs, fp32 accumulation, y fp16 or fp32. */
 int kvc_embed_gather(void* out, const void* embed, const int* ids, int L, int H, int V, kvc_stream_t stream);
+/* graph-safe gather: rows [0, *dev_rows) of at most L_cap (row count in device memory) */
+int kvc_embed_gather_dev(void* out, const void* embed, const int* ids, const int* dev_rows, int L_cap, int H, int V,
+                         kvc_stream_t stream);
 int kvc_rmsnorm(void* out, const void* in, const void* w, int L, int H, float eps, kvc_stream_t stream);
 int kvc_add_bias(void* x, const void* bias, int L, int N, kvc_stream_t stream);
 int kvc_add_residual(void* x, const void* y, size_t n, kvc_stream_t stream);
@@ -263,19 +294,22 @@ int kvc_linear(void* y, const void* x, const void* w, int M, int N, int K, int o
  *   w_gate_up = [wg; wu] as [2I, H]; I a multiple of 16.
  * kvc_rows_lm_head: logits[M,V] = A w^T in fp32 (logits may be NULL) and tokens[r] =
  *   first index of the row maximum (qk_argmax, qwen_kernels.h:22); V a multiple of 32.
+ * dev_rows != NULL (graph-safe launches): the row count is read from device memory and
+ *   M is its capacity (<= 32).
  * kvc_rows_set_tuning: overrides, -1 = automatic: K splits of layers with K > 1024,
  *   column groups (32 outputs) per workgroup, kernel shape 0..2 (4 waves x 7 k steps,
  *   8 waves x 4, 4 waves x 4 with K split).  The workspace size depends on them. */
 size_t kvc_rows_workspace_size(int N, int K);
 int kvc_rows_linear(void* y, const void* x, const void* w, int M, int N, int K, const void* norm_w, float eps,
-                    int residual, void* workspace, size_t workspace_bytes, kvc_stream_t stream);
+                    int residual, const int* dev_rows, void* workspace, size_t workspace_bytes, kvc_stream_t stream);
 int kvc_rows_qkv(void* q, void* k, void* v, const void* x, const void* norm_w, float eps, const void* w_qkv,
                  const void* b_qkv, const int* pos, int M, int H, int Hq, int Hkv, int D, float theta,
-                 kvc_stream_t stream);
+                 const int* dev_rows, kvc_stream_t stream);
 int kvc_rows_swiglu(void* act, const void* x, const void* norm_w, float eps, const void* w_gate_up, int M, int I,
-                    int H, kvc_stream_t stream);
+                    int H, const int* dev_rows, kvc_stream_t stream);
 int kvc_rows_lm_head(float* logits, int* tokens, const void* x, const void* norm_w, float eps, const void* w, int M,
-                     int V, int H, void* workspace, size_t workspace_bytes, kvc_stream_t stream);
+                     int V, int H, const int* dev_rows, void* workspace, size_t workspace_bytes,
+                     kvc_stream_t stream);
 int kvc_rows_set_tuning(int splits, int groups_per_wg, int shape);
 
 /* ---- Qwen2-shaped decoder served with continuous batching (include/kvc/qwen_model.h;
@@ -288,11 +322,13 @@ typedef struct kvc_qwen_config {
     int block_size, num_blocks, max_batch, max_rows;  /* max_rows: longest prompt */
     uint64_t seed;                                      /* 0: default */
     int step_path;  /* 0: fused decode-step kernels when a step has <= 32 rows; 1: one kernel per op */
+    int graph;      /* 1: fused steps replay one captured HIP graph */
 } kvc_qwen_config;
 typedef struct kvc_qwen_stats {
     int steps, finished;
     long long tokens, prompt_tokens;
     double wall_us, prefill_us, decode_us;   /* host clock around the whole run / prefills / decode steps */
+    long long graph_steps;                   /* decode steps that replayed the captured graph */
 } kvc_qwen_stats;
 typedef struct kvc_qwen kvc_qwen;
 int  kvc_qwen_create(const kvc_qwen_config* cfg, kvc_qwen** out);
@@ -353,6 +389,7 @@ typedef struct kvc_engine_config {
     int prefill;       /* 1: admitted prompts run qk_write_kv + qk_paged_causal_attn per layer; the
                           GPU time advances the measured clock (the virtual clock ignores it) */
     uint64_t seed;     /* seed of the synthetic q/k/v fill */
+    int graph;         /* 1: planned decode steps replay one captured HIP graph (counts in device memory) */
 } kvc_engine_config;
 
 typedef struct kvc_engine_stats {     /* EngineStats (engine.h:33-45) + p50 + digest */

@@ -44,6 +44,7 @@ class EngineConfigC(C.Structure):
         ("num_blocks", i32), ("max_batch", i32), ("n_layers", i32), ("dtype", i32),
         ("kv_write", i32), ("clock_mode", i32), ("virt_c0", f64), ("virt_c1", f64),
         ("virt_c2", f64), ("device", i32), ("split_tokens", i32), ("decode_path", i32), ("prefill", i32), ("seed", u64),
+        ("graph", i32),
     ]
 
 
@@ -52,14 +53,14 @@ class QwenConfigC(C.Structure):
         ("layers", i32), ("hidden", i32), ("n_heads", i32), ("n_kv_heads", i32), ("head_dim", i32),
         ("inter", i32), ("vocab", i32), ("eps", C.c_float), ("theta", C.c_float), ("init_std", C.c_float),
         ("block_size", i32), ("num_blocks", i32), ("max_batch", i32), ("max_rows", i32), ("seed", u64),
-        ("step_path", i32),
+        ("step_path", i32), ("graph", i32),
     ]
 
 
 class QwenStatsC(C.Structure):
     _fields_ = [
         ("steps", i32), ("finished", i32), ("tokens", C.c_longlong), ("prompt_tokens", C.c_longlong),
-        ("wall_us", f64), ("prefill_us", f64), ("decode_us", f64),
+        ("wall_us", f64), ("prefill_us", f64), ("decode_us", f64), ("graph_steps", C.c_longlong),
     ]
 
 
@@ -134,10 +135,18 @@ _SIGS = {
     "kvc_argmax": (i32, [vp, i32, i32, vp, vp]),
     "kvc_linear": (i32, [vp, vp, vp, i32, i32, i32, i32, vp]),
     "kvc_rows_workspace_size": (sz, [i32, i32]),
-    "kvc_rows_linear": (i32, [vp, vp, vp, i32, i32, i32, vp, f32, i32, vp, sz, vp]),
-    "kvc_rows_qkv": (i32, [vp, vp, vp, vp, vp, f32, vp, vp, vp, i32, i32, i32, i32, i32, f32, vp]),
-    "kvc_rows_swiglu": (i32, [vp, vp, vp, f32, vp, i32, i32, i32, vp]),
-    "kvc_rows_lm_head": (i32, [vp, vp, vp, vp, f32, vp, i32, i32, i32, vp, sz, vp]),
+    "kvc_rows_linear": (i32, [vp, vp, vp, i32, i32, i32, vp, f32, i32, vp, vp, sz, vp]),
+    "kvc_rows_qkv": (i32, [vp, vp, vp, vp, vp, f32, vp, vp, vp, i32, i32, i32, i32, i32, f32, vp, vp]),
+    "kvc_rows_swiglu": (i32, [vp, vp, vp, f32, vp, i32, i32, i32, vp, vp]),
+    "kvc_rows_lm_head": (i32, [vp, vp, vp, vp, f32, vp, i32, i32, i32, vp, vp, sz, vp]),
+    "kvc_embed_gather_dev": (i32, [vp, vp, vp, vp, i32, i32, i32, vp]),
+    "kvc_batched_paged_decode_planned_dev": (
+        i32, [vp, vp, vp, vp, vp, vp, vp, i32, vp, i32, i32, i32, i32, i32, f32, i32, vp, i32, i32, vp, vp, sz, vp]),
+    "kvc_decode_plan_capacity": (i32, [i32, C.c_longlong, i32, i32, i32, i32, i32, ip]),
+    "kvc_graph_begin": (i32, [vp]),
+    "kvc_graph_end": (i32, [vp, C.POINTER(vp)]),
+    "kvc_graph_launch": (i32, [vp, vp]),
+    "kvc_graph_destroy": (i32, [vp]),
     "kvc_rows_set_tuning": (i32, [i32, i32, i32]),
     "kvc_flash_decode": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, f32, i32, i32, vp, sz, vp]),
     "kvc_flash_decode_workspace_size": (sz, [i32, i32, i32]),

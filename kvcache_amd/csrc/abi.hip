@@ -499,7 +499,7 @@ int run_causal_tile(const void* q, void* out, const void* k, const void* v, cons
 int run_planned(const void* q, const void* k_new, const void* v_new, const int* wpos, const void* k_pool,
                 const void* v_pool, const int* table_all, int table_len, void* out, int N, int Hq, int Hkv, int D,
                 int BLOCK, float scale, int dtype, const int* work, int n_units, int n_records, void* ws,
-                size_t ws_bytes, hipStream_t st) {
+                size_t ws_bytes, hipStream_t st, const int* dev_counts = nullptr) {
     {
         int rc = check_common(N, Hq, Hkv, D, dtype, q, k_pool, v_pool, out);
         if (rc || N == 0 || n_units == 0) return rc;
@@ -548,6 +548,7 @@ int run_planned(const void* q, const void* k_new, const void* v_new, const int* 
         L.need_merge = false;
         L.units = n_units;
         p.k_new = k_new; p.v_new = v_new; p.wpos = wpos;
+        p.dev_counts = dev_counts;  // (n_units, N, n_records are then capacities)
         return launch_decode(L, st);
     }
 }
@@ -640,6 +641,28 @@ int kvc_event_create(void** ev) {
     int rc = hip_check(hipEventCreate(&e), "hipEventCreate");
     *ev = e;
     return rc;
+}
+int kvc_graph_begin(kvc_stream_t st) {
+    return hip_check(hipStreamBeginCapture(S(st), hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+}
+int kvc_graph_end(kvc_stream_t st, void** exec) {
+    if (!exec) return set_error(KVC_ERR_ARG, "null out pointer");
+    *exec = nullptr;
+    hipGraph_t g = nullptr;
+    int rc = hip_check(hipStreamEndCapture(S(st), &g), "hipStreamEndCapture");
+    if (rc) return rc;
+    hipGraphExec_t e = nullptr;
+    rc = hip_check(hipGraphInstantiate(&e, g, nullptr, nullptr, 0), "hipGraphInstantiate");
+    (void)hipGraphDestroy(g);
+    if (rc == KVC_OK) *exec = e;
+    return rc;
+}
+int kvc_graph_launch(void* exec, kvc_stream_t st) {
+    if (!exec) return set_error(KVC_ERR_ARG, "null graph");
+    return hip_check(hipGraphLaunch((hipGraphExec_t)exec, S(st)), "hipGraphLaunch");
+}
+int kvc_graph_destroy(void* exec) {
+    return exec ? hip_check(hipGraphExecDestroy((hipGraphExec_t)exec), "hipGraphExecDestroy") : KVC_OK;
 }
 int kvc_event_destroy(void* ev) { return ev ? hip_check(hipEventDestroy((hipEvent_t)ev), "hipEventDestroy") : KVC_OK; }
 int kvc_event_record(void* ev, kvc_stream_t st) { return hip_check(hipEventRecord((hipEvent_t)ev, S(st)), "hipEventRecord"); }
@@ -842,6 +865,40 @@ int kvc_batched_paged_append_decode_planned(const void* q, const void* k_new, co
             return set_error(KVC_ERR_ARG, "k_new and v_new must be 16-byte aligned");
         return kvc::run_planned(q, k_new, v_new, wpos, k_pool, v_pool, table_all, table_len, out, N, Hq, Hkv, D,
                                 BLOCK, scale, dtype, work, n_units, n_records, ws, ws_bytes, S(st));
+    });
+}
+
+int kvc_batched_paged_decode_planned_dev(const void* q, const void* k_new, const void* v_new, const int* wpos,
+                                        void* k_pool, void* v_pool, const int* table_all, int table_len, void* out,
+                                        int N_cap, int Hq, int Hkv, int D, int BLOCK, float scale, int dtype,
+                                        const int* work, int units_cap, int records_cap, const int* dev_counts,
+                                        void* ws, size_t ws_bytes, kvc_stream_t st) {
+    return guarded([&]() -> int {
+        if (!dev_counts) return set_error(KVC_ERR_ARG, "null dev_counts");
+        const bool append = k_new != nullptr;
+        if (append && (!v_new || !wpos)) return set_error(KVC_ERR_ARG, "append needs k_new, v_new and wpos");
+        if (append && (!aligned16(k_new) || !aligned16(v_new)))
+            return set_error(KVC_ERR_ARG, "k_new and v_new must be 16-byte aligned");
+        if (records_cap > 0 && !ws) return set_error(KVC_ERR_ARG, "a graph-safe launch needs its workspace");
+        return kvc::run_planned(q, append ? k_new : nullptr, append ? v_new : nullptr, append ? wpos : nullptr,
+                                k_pool, v_pool, table_all, table_len, out, N_cap, Hq, Hkv, D, BLOCK, scale, dtype,
+                                work, units_cap, records_cap, ws, ws_bytes, S(st), dev_counts);
+    });
+}
+
+int kvc_decode_plan_capacity(int N, long long total_tokens, int Hq, int Hkv, int D, int BLOCK, int dtype,
+                             int* max_units) {
+    return guarded([&]() -> int {
+        if (!max_units) return set_error(KVC_ERR_ARG, "null out pointer");
+        *max_units = 0;
+        if (N < 0 || total_tokens < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || D <= 0 || BLOCK <= 0)
+            return set_error(KVC_ERR_ARG, "bad plan capacity arguments");
+        const kvc::PlanShape ps = kvc::plan_shape(Hq, Hkv, D, BLOCK, dtype);
+        // a sequence of L tokens is cut into at most L / min_chunk + 1 chunks per head slot
+        const long long units = (long long)ps.hks * ((long long)N + total_tokens / std::max(ps.min_chunk, 1) + 1);
+        if (units > INT_MAX) return set_error(KVC_ERR_ARG, "plan capacity too large");
+        *max_units = (int)units;
+        return KVC_OK;
     });
 }
 

@@ -285,6 +285,12 @@ struct Unit {
 template <bool PLANNED>
 __device__ __forceinline__ bool load_unit(const DecodeParams& p, int heads, Unit& u) {
     if constexpr (PLANNED) {
+        int N = p.N, n_records = p.n_records;
+        if (p.dev_counts) {  // fixed-capacity grid: the step's counts come from device memory
+            if ((int)blockIdx.x >= p.dev_counts[1]) return false;
+            N = min(p.dev_counts[0], p.N);
+            n_records = min(p.dev_counts[2], p.n_records);
+        }
         const int* w = p.work + (size_t)blockIdx.x * p.work_ints;
         u.s = w[0];
         const int hks = w[1] & 0xFFFF;
@@ -300,8 +306,8 @@ __device__ __forceinline__ bool load_unit(const DecodeParams& p, int heads, Unit
         u.ctr_idx = w[6] > 0 ? w[6] : 0;
         u.tab_start = w[7];
         // a unit outside the launch's shape (a stale or foreign plan) is skipped
-        if (u.s < 0 || u.s >= p.N || u.hk < 0 || u.hk >= p.Hkv || u.c < 0 || u.c >= u.nc) return false;
-        return u.nc == 1 || (w[5] >= 0 && (long long)w[5] + u.nc <= p.n_records && w[6] >= 0 && w[6] < p.n_records);
+        if (u.s < 0 || u.s >= N || u.hk < 0 || u.hk >= p.Hkv || u.c < 0 || u.c >= u.nc) return false;
+        return u.nc == 1 || (w[5] >= 0 && (long long)w[5] + u.nc <= n_records && w[6] >= 0 && w[6] < n_records);
     } else {
         int unit = blockIdx.x;
         u.sub = unit % p.nsub;  unit /= p.nsub;

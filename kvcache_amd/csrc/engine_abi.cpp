@@ -96,6 +96,7 @@ int kvc_engine_create(const kvc_engine_config* c, kvc_engine** out) {
             return kvc::set_error(KVC_ERR_ARG, "decode_path must be KVC_DECODE_PLANNED or KVC_DECODE_DEVICE_LENGTHS");
         ec.decode_path = c->decode_path;
         ec.prefill = c->prefill != 0;
+        ec.graph = c->graph != 0;
         if (c->seed) ec.seed = c->seed;
         if (c->max_batch <= 0) return kvc::set_error(KVC_ERR_ARG, "max_batch must be > 0");
         *out = new kvc_engine(ec);

@@ -55,6 +55,8 @@ struct DecodeParams {
     int work_ints;            // planned: ints per unit (8, or 64 with inline block ids)
     int table_len;            // planned: ints in table_all (bounds every block-id read)
     int n_records;            // planned: record groups of the plan (bounds partials and counters)
+    const int* dev_counts;    // planned, graph-safe launches: {N, units, records} of this step in device
+                              // memory (each clamped to the launch's N / grid / n_records capacities)
     // planned launches with a fused append: the step's new K/V rows [N][Hkv][D] and
     // their positions wpos[N]; the unit whose chunk holds wpos[s] uses the new row in
     // place of the pool's and (first head subgroup) writes it to the pool

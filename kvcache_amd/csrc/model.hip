@@ -31,8 +31,9 @@ __device__ __forceinline__ float wave_sum(float x) {
 
 // out[r, :] = table[ids[r], :]; ids outside [0, V) give a zero row.
 __global__ __launch_bounds__(kThreads) void embed_kernel(_Float16* out, const _Float16* table, const int* ids, int V,
-                                                         int H) {
+                                                         int H, const int* dev_rows) {
     const int r = blockIdx.x;
+    if (dev_rows && r >= *dev_rows) return;
     const int id = ids[r];
     const bool ok = id >= 0 && id < V;
     const f16x8* src = reinterpret_cast<const f16x8*>(table + (size_t)(ok ? id : 0) * H);
@@ -200,7 +201,19 @@ int kvc_embed_gather(void* out, const void* embed, const int* ids, int L, int H,
         if (L == 0) return KVC_OK;
         if (!out || !embed || !ids || !a16(out) || !a16(embed)) return set_error(KVC_ERR_ARG, "embed: bad pointers");
         hipLaunchKernelGGL(embed_kernel, dim3(L), dim3(kThreads), 0, (hipStream_t)st, (_Float16*)out,
-                           (const _Float16*)embed, ids, V, H);
+                           (const _Float16*)embed, ids, V, H, nullptr);
+        return hip_check(hipGetLastError(), "embed launch");
+    });
+}
+
+int kvc_embed_gather_dev(void* out, const void* embed, const int* ids, const int* dev_rows, int L_cap, int H, int V,
+                         kvc_stream_t st) {
+    return guard_model([&]() -> int {
+        if (L_cap <= 0 || H <= 0 || H % 8 || V <= 0) return set_error(KVC_ERR_ARG, "embed: L_cap > 0, H > 0 (multiple of 8), V > 0");
+        if (!out || !embed || !ids || !dev_rows || !a16(out) || !a16(embed))
+            return set_error(KVC_ERR_ARG, "embed: bad pointers");
+        hipLaunchKernelGGL(embed_kernel, dim3(L_cap), dim3(kThreads), 0, (hipStream_t)st, (_Float16*)out,
+                           (const _Float16*)embed, ids, V, H, dev_rows);
         return hip_check(hipGetLastError(), "embed launch");
     });
 }

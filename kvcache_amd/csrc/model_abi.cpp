@@ -45,6 +45,8 @@ int kvc_qwen_create(const kvc_qwen_config* cfg, kvc_qwen** out) {
         if (cfg->seed) c.seed = cfg->seed;
         if (cfg->step_path != 0 && cfg->step_path != 1) return kvc::set_error(KVC_ERR_ARG, "qwen config: step_path 0 or 1");
         c.step_path = cfg->step_path;
+        if (cfg->graph != 0 && cfg->graph != 1) return kvc::set_error(KVC_ERR_ARG, "qwen config: graph 0 or 1");
+        c.graph = cfg->graph;
         if (c.layers <= 0 || c.hidden <= 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 || c.head_dim <= 0 || c.inter <= 0 ||
             c.vocab <= 0 || c.block_size <= 0 || c.num_blocks <= 0 || c.max_batch <= 0 || c.max_rows <= 0)
             return kvc::set_error(KVC_ERR_ARG, "qwen config: sizes must be positive");
@@ -101,6 +103,7 @@ int kvc_qwen_serve(kvc_qwen* h, int n_req, const int* prompt_off, const int* pro
             stats->steps = st.steps; stats->finished = st.finished; stats->tokens = st.tokens;
             stats->prompt_tokens = st.prompt_tokens; stats->wall_us = st.wall_us; stats->prefill_us = st.prefill_us;
             stats->decode_us = st.decode_us;
+            stats->graph_steps = st.graph_steps;
         }
         return KVC_OK;
     });

@@ -67,6 +67,7 @@ struct RowsParams {
     const int* pos;          // qkv: rotary position of each row
     float log2_theta;
     int q_cols, kv_cols, head_dim;
+    const int* dev_rows;     // graph-safe launches: the step's row count in device memory (M is then a capacity)
     float* logits;           // logits: fp32 [M, N] or nullptr
     float* best_v;           // logits: [groups][kRows] per-group row maxima
     int* best_i;
@@ -171,7 +172,9 @@ __device__ __forceinline__ void epilogue(const RowsParams& p, int g, int m, int 
 // buffered, one barrier per group) and stored.  SPLIT: the K range is split across
 // workgroups (one group per workgroup) and the last to arrive finishes the group.
 template <int EPI, bool NORM, int MT, int WAVES, int S, bool SPLIT>
-__global__ __launch_bounds__(WAVES * 64) void rows_kernel(RowsParams p) {
+__global__ __launch_bounds__(WAVES * 64) void rows_kernel(RowsParams pin) {
+    RowsParams p = pin;
+    if (p.dev_rows) p.M = min(max(*p.dev_rows, 0), pin.M);
     constexpr int kThreads = WAVES * 64;
     constexpr int kItems = kRows * 16 / kThreads;  // (row, column pair) items per thread
     __shared__ float s_red[2][WAVES][kRows][kCols + 1];
@@ -371,10 +374,11 @@ __global__ __launch_bounds__(WAVES * 64) void rows_kernel(RowsParams p) {
 // tokens[m] = the column of the largest candidate over the groups (first index on ties).
 constexpr int kArgThreads = 256;
 __global__ __launch_bounds__(kArgThreads) void group_argmax_kernel(const float* best_v, const int* best_i, int groups,
-                                                                   int* tokens) {
+                                                                   int* tokens, const int* dev_rows) {
     __shared__ float sv[kArgThreads / 64];
     __shared__ int si[kArgThreads / 64];
     const int m = blockIdx.x;
+    if (dev_rows && m >= *dev_rows) return;
     float bv = -FLT_MAX;
     int bi = INT_MAX;
     for (int gi = threadIdx.x; gi < groups; gi += kArgThreads)
@@ -487,7 +491,7 @@ size_t kvc_rows_workspace_size(int N, int K) {
 }
 
 int kvc_rows_linear(void* y, const void* x, const void* w, int M, int N, int K, const void* norm_w, float eps,
-                    int residual, void* ws, size_t ws_bytes, kvc_stream_t st) {
+                    int residual, const int* dev_rows, void* ws, size_t ws_bytes, kvc_stream_t st) {
     try {
         int rc = check_rows(M, K, x, w);
         if (!rc) rc = check_norm(norm_w, eps, K);
@@ -507,6 +511,7 @@ int kvc_rows_linear(void* y, const void* x, const void* w, int M, int N, int K, 
         p.a = (const _Float16*)x; p.w = (const _Float16*)w; p.norm_w = (const _Float16*)norm_w; p.eps = eps;
         p.M = M; p.N = N; p.K = K;
         p.out = (_Float16*)y;
+        p.dev_rows = dev_rows;
         p.ctr = (unsigned*)ws;
         p.part = ws ? (float*)((char*)ws + kCtrBytes) : nullptr;
         const hipStream_t hs = (hipStream_t)st;
@@ -519,7 +524,7 @@ int kvc_rows_linear(void* y, const void* x, const void* w, int M, int N, int K, 
 
 int kvc_rows_qkv(void* q, void* k, void* v, const void* x, const void* norm_w, float eps, const void* w_qkv,
                  const void* b_qkv, const int* pos, int M, int H, int Hq, int Hkv, int D, float theta,
-                 kvc_stream_t st) {
+                 const int* dev_rows, kvc_stream_t st) {
     try {
         int rc = check_rows(M, H, x, w_qkv);
         if (!rc) rc = check_norm(norm_w, eps, H);
@@ -534,6 +539,7 @@ int kvc_rows_qkv(void* q, void* k, void* v, const void* x, const void* norm_w, f
         p.M = M; p.N = n; p.K = H;
         p.out = (_Float16*)q; p.k_out = (_Float16*)k; p.v_out = (_Float16*)v;
         p.bias = (const _Float16*)b_qkv; p.pos = pos; p.log2_theta = log2f(theta);
+        p.dev_rows = dev_rows;
         p.q_cols = Hq * D; p.kv_cols = Hkv * D; p.head_dim = D;
         const Shape s = plan_shape(n / kCols, H, norm_w != nullptr);
         if (s.splits > 1) return set_error(KVC_ERR_UNSUPPORTED, "rows qkv: K too large for one workgroup");
@@ -545,7 +551,7 @@ int kvc_rows_qkv(void* q, void* k, void* v, const void* x, const void* norm_w, f
 }
 
 int kvc_rows_swiglu(void* act, const void* x, const void* norm_w, float eps, const void* w_gate_up, int M, int I,
-                    int H, kvc_stream_t st) {
+                    int H, const int* dev_rows, kvc_stream_t st) {
     try {
         int rc = check_rows(M, H, x, w_gate_up);
         if (!rc) rc = check_norm(norm_w, eps, H);
@@ -558,6 +564,7 @@ int kvc_rows_swiglu(void* act, const void* x, const void* norm_w, float eps, con
         p.a = (const _Float16*)x; p.w = (const _Float16*)w_gate_up; p.norm_w = (const _Float16*)norm_w; p.eps = eps;
         p.M = M; p.N = I; p.K = H;
         p.out = (_Float16*)act;
+        p.dev_rows = dev_rows;
         const Shape s = plan_shape(I / 16, H, norm_w != nullptr);
         if (s.splits > 1) return set_error(KVC_ERR_UNSUPPORTED, "rows swiglu: K too large for one workgroup");
         return norm_w ? launch_rows<kEpiSwiglu, true>(p, s, (hipStream_t)st)
@@ -568,7 +575,7 @@ int kvc_rows_swiglu(void* act, const void* x, const void* norm_w, float eps, con
 }
 
 int kvc_rows_lm_head(float* logits, int* tokens, const void* x, const void* norm_w, float eps, const void* w, int M,
-                     int V, int H, void* ws, size_t ws_bytes, kvc_stream_t st) {
+                     int V, int H, const int* dev_rows, void* ws, size_t ws_bytes, kvc_stream_t st) {
     try {
         int rc = check_rows(M, H, x, w);
         if (!rc) rc = check_norm(norm_w, eps, H);
@@ -584,6 +591,7 @@ int kvc_rows_lm_head(float* logits, int* tokens, const void* x, const void* norm
         p.a = (const _Float16*)x; p.w = (const _Float16*)w; p.norm_w = (const _Float16*)norm_w; p.eps = eps;
         p.M = M; p.N = V; p.K = H;
         p.logits = logits;
+        p.dev_rows = dev_rows;
         p.best_v = (float*)((char*)ws + kCtrBytes);
         p.best_i = (int*)((char*)ws + kCtrBytes + (size_t)groups * kRows * 4);
         const Shape one = plan_shape(groups, H, true);  // candidates need whole rows: no K split
@@ -592,7 +600,7 @@ int kvc_rows_lm_head(float* logits, int* tokens, const void* x, const void* norm
                     : launch_rows<kEpiLogits, false>(p, one, (hipStream_t)st);
         if (rc) return rc;
         hipLaunchKernelGGL(group_argmax_kernel, dim3(M), dim3(kArgThreads), 0, (hipStream_t)st, p.best_v, p.best_i,
-                           groups, tokens);
+                           groups, tokens, dev_rows);
         return hip_check(hipGetLastError(), "argmax launch");
     } catch (...) {
         return set_error(KVC_ERR_STATE, "unexpected exception");

@@ -76,12 +76,13 @@ class EngineConfig:
     decode_path: int = 0         # 0 host-planned decode, 1 device-lengths path with split_tokens
     prefill: bool = False        # admitted prompts run K/V writes + causal attention (measured clock)
     seed: int = 0
+    graph: bool = False          # planned decode steps replay one captured HIP graph
 
     def to_c(self) -> EngineConfigC:
         return EngineConfigC(self.n_heads, self.n_kv_heads, self.head_dim, self.block_size, self.num_blocks,
                              self.max_batch, self.n_layers, self.dtype, int(self.kv_write), self.clock_mode,
                              self.virt_c0, self.virt_c1, self.virt_c2, int(self.device), self.split_tokens,
-                             self.decode_path, int(self.prefill), self.seed)
+                             self.decode_path, int(self.prefill), self.seed, int(self.graph))
 
 
 @dataclass

@@ -29,11 +29,12 @@ class QwenConfig:
     max_rows: int = 1024
     seed: int = 0
     step_path: int = 0  # 0: fused decode-step kernels for steps of <= 32 rows; 1: one kernel per op
+    graph: int = 1  # fused decode steps replay one captured HIP graph
 
     def to_c(self) -> QwenConfigC:
         return QwenConfigC(self.layers, self.hidden, self.n_heads, self.n_kv_heads, self.head_dim, self.inter,
                            self.vocab, self.eps, self.theta, self.init_std, self.block_size, self.num_blocks,
-                           self.max_batch, self.max_rows, self.seed, self.step_path)
+                           self.max_batch, self.max_rows, self.seed, self.step_path, self.graph)
 
 
 class QwenModel:
@@ -87,4 +88,4 @@ class QwenModel:
             o += n
         return res, {"steps": st.steps, "finished": st.finished, "tokens": st.tokens,
                      "prompt_tokens": st.prompt_tokens, "wall_us": st.wall_us, "prefill_us": st.prefill_us,
-                     "decode_us": st.decode_us}
+                     "decode_us": st.decode_us, "graph_steps": st.graph_steps}

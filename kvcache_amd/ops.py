@@ -197,27 +197,32 @@ def rows_workspace_size(N, K) -> int:
     return int(lib().kvc_rows_workspace_size(N, K))
 
 
-def rows_linear(y, x, w, M, N, K, *, norm_w=None, eps=1e-6, residual=False, workspace=None, stream=None):
+def rows_linear(y, x, w, M, N, K, *, norm_w=None, eps=1e-6, residual=False, dev_rows=None, workspace=None,
+                stream=None):
     """y[M,N] = A w^T, or y += A w^T (residual), A = x or RMSNorm(x) * norm_w."""
     ws, wsb = _ws(workspace)
-    check(lib().kvc_rows_linear(_p(y), _p(x), _p(w), M, N, K, _p(norm_w), eps, int(residual), ws, wsb, stream))
+    check(lib().kvc_rows_linear(_p(y), _p(x), _p(w), M, N, K, _p(norm_w), eps, int(residual), _p(dev_rows), ws, wsb,
+                                stream))
 
 
-def rows_qkv(q, k, v, x, w_qkv, b_qkv, pos, M, H, Hq, Hkv, D, theta, *, norm_w=None, eps=1e-6, stream=None):
+def rows_qkv(q, k, v, x, w_qkv, b_qkv, pos, M, H, Hq, Hkv, D, theta, *, norm_w=None, eps=1e-6, dev_rows=None,
+             stream=None):
     """q|k|v = RMSNorm(x) [wq;wk;wv]^T + bias, rotary on q and k at pos[r]."""
     check(lib().kvc_rows_qkv(_p(q), _p(k), _p(v), _p(x), _p(norm_w), eps, _p(w_qkv), _p(b_qkv), _p(pos), M, H, Hq,
-                             Hkv, D, theta, stream))
+                             Hkv, D, theta, _p(dev_rows), stream))
 
 
-def rows_swiglu(act, x, w_gate_up, M, I, H, *, norm_w=None, eps=1e-6, stream=None):
+def rows_swiglu(act, x, w_gate_up, M, I, H, *, norm_w=None, eps=1e-6, dev_rows=None, stream=None):
     """act = silu(A wg^T) * (A wu^T), w_gate_up = [wg; wu]."""
-    check(lib().kvc_rows_swiglu(_p(act), _p(x), _p(norm_w), eps, _p(w_gate_up), M, I, H, stream))
+    check(lib().kvc_rows_swiglu(_p(act), _p(x), _p(norm_w), eps, _p(w_gate_up), M, I, H, _p(dev_rows), stream))
 
 
-def rows_lm_head(logits, tokens, x, w, M, V, H, *, norm_w=None, eps=1e-6, workspace=None, stream=None):
+def rows_lm_head(logits, tokens, x, w, M, V, H, *, norm_w=None, eps=1e-6, dev_rows=None, workspace=None,
+                 stream=None):
     """fp32 logits (or None) and the greedy token of each row."""
     ws, wsb = _ws(workspace)
-    check(lib().kvc_rows_lm_head(_p(logits), _p(tokens), _p(x), _p(norm_w), eps, _p(w), M, V, H, ws, wsb, stream))
+    check(lib().kvc_rows_lm_head(_p(logits), _p(tokens), _p(x), _p(norm_w), eps, _p(w), M, V, H, _p(dev_rows), ws,
+                                 wsb, stream))
 
 
 def rows_set_tuning(splits: int = -1, groups_per_wg: int = -1, shape: int = -1) -> None:

@@ -7,7 +7,10 @@
 // kernels are checked against the CPU restatement elsewhere; this program checks
 // the runner's packing (offsets of tables and work list in the upload, the
 // workspace sizing, growth of the metadata buffers) on a ragged GQA batch with
-// sequences long enough to be split, over two layers with K/V writes.
+// sequences long enough to be split, over two layers with K/V writes.  Then the
+// graph-replayed planned step (one capture, counts and metadata in device memory)
+// against the eagerly launched one, step after step with different batches: the
+// same kernels on the same plans, so the outputs must be bit-identical.
 #include <cmath>
 #include <cstdio>
 #include <vector>
@@ -67,6 +70,28 @@ int main() {
                         planned.digest == split.digest ? "equal" : "DIFFER");
             if (!(err <= 2e-3) || !finite || planned.digest != split.digest) worst = 1;
         }
+    }
+    for (int kv_write = 0; kv_write <= 1; ++kv_write) {
+        RunnerOptions eo;
+        eo.n_kv_heads = Hkv; eo.n_layers = L; eo.dtype = KVC_F16; eo.kv_write = kv_write;
+        RunnerOptions go = eo;
+        go.graph = true;
+        ModelRunner eager(Hq, D, B, maxB, NB, eo), graph(Hq, D, B, maxB, NB, go);
+        for (int n : {maxB, 5, 17, 1, maxB}) {
+            std::vector<Sequence*> b(batch.begin() + (maxB - n) / 2, batch.begin() + (maxB - n) / 2 + n);
+            std::vector<int> wp(wpos.begin() + (maxB - n) / 2, wpos.begin() + (maxB - n) / 2 + n);
+            eager.decode_step(b, kvm, kv_write ? wp.data() : nullptr);
+            const auto a = fetch(eager, n);
+            graph.decode_step(b, kvm, kv_write ? wp.data() : nullptr);
+            const auto c = fetch(graph, n);
+            size_t diff = 0;
+            for (size_t i = 0; i < a.size(); ++i) diff += (a[i] != c[i]);
+            std::printf("graph kv_write=%d N=%d: %zu of %zu outputs differ from the eager step\n", kv_write, n, diff,
+                        a.size());
+            if (diff) worst = 1;
+        }
+        std::printf("graph steps replayed: %lld\n", graph.graph_steps);
+        if (graph.graph_steps != 5) worst = 1;
     }
     std::printf(worst ? "=== RUNNER PATHS MISMATCH ===\n" : "=== RUNNER PATHS OK ===\n");
     return worst;
