@@ -30,3 +30,56 @@ def test_rmsnorm_silu_argmax_properties():
     np.testing.assert_allclose(M.silu_mul(np.array([40.0]), np.array([1.0])), [40.0], rtol=1e-15)
     assert M.argmax(np.array([[1.0, 3.0, 3.0, 2.0]]))[0] == 1                     # first of tied maxima
     assert (M.embed_gather(np.eye(3), [2, -1, 5]) == np.array([[0, 0, 1], [0, 0, 0], [0, 0, 0]])).all()
+
+
+def _tiny(layers=2, Hq=4, Hkv=2, D=8, H=16, I=24, V=50, seed=3, zero=False):
+    from types import SimpleNamespace
+    cfg = SimpleNamespace(layers=layers, hidden=H, n_heads=Hq, n_kv_heads=Hkv, head_dim=D, inter=I, vocab=V,
+                          eps=1e-6, theta=1e4)
+    rng = np.random.default_rng(seed)
+    f = lambda *s: (0.0 if zero else 0.3) * rng.standard_normal(s).astype(np.float16)
+    W = {"embed": rng.standard_normal((V, H)).astype(np.float16).ravel(),
+         "norm": (1 + 0.1 * rng.standard_normal(H)).astype(np.float16)}
+    for l in range(layers):
+        W.update({f"ln1.{l}": np.ones(H, np.float16), f"ln2.{l}": np.ones(H, np.float16),
+                  f"wq.{l}": f(Hq * D, H), f"bq.{l}": f(Hq * D), f"wk.{l}": f(Hkv * D, H), f"bk.{l}": f(Hkv * D),
+                  f"wv.{l}": f(Hkv * D, H), f"bv.{l}": f(Hkv * D), f"wo.{l}": f(H, Hq * D),
+                  f"wg.{l}": f(I, H), f"wu.{l}": f(I, H), f"wd.{l}": f(H, I)})
+    return cfg, W
+
+
+def test_decoder_zero_layers_is_norm_and_tied_head():
+    """Zero projections leave the residual stream at the embedding: logits are the
+    final RMSNorm of the token's embedding against the tied embedding matrix."""
+    cfg, W = _tiny(zero=True)
+    tok = np.array([3, 7, 7, 41])
+    got = M.decoder_logits(W, cfg, tok)
+    E = W["embed"].reshape(cfg.vocab, cfg.hidden).astype(np.float64)
+    x = E[tok]
+    n = x / np.sqrt(np.mean(x * x, axis=1, keepdims=True) + cfg.eps) * W["norm"].astype(np.float64)
+    np.testing.assert_allclose(got, n.astype(np.float16).astype(np.float64) @ E.T, rtol=2e-3, atol=2e-3)
+
+
+def test_decoder_is_causal():
+    """Logits at position i depend on tokens 0..i only (the causal mask)."""
+    cfg, W = _tiny()
+    a = np.array([5, 9, 13, 2, 30, 11])
+    b = a.copy(); b[4:] = [44, 1]
+    la, lb = M.decoder_logits(W, cfg, a), M.decoder_logits(W, cfg, b)
+    np.testing.assert_array_equal(la[:4], lb[:4])
+    assert np.abs(la[4:] - lb[4:]).max() > 1e-3
+
+
+def test_decoder_grouped_query_equals_repeated_heads():
+    """Hq/Hkv = 2 query heads per KV head gives the same logits as MHA whose K/V
+    projections repeat each KV head for its query heads (head h uses KV head h // g)."""
+    cfg, W = _tiny(Hq=4, Hkv=2)
+    cfg_m, Wm = _tiny(Hq=4, Hkv=4)
+    Wm = dict(W)
+    D, H = cfg.head_dim, cfg.hidden
+    for l in range(cfg.layers):
+        for n, shape in (("wk", (2, D, H)), ("wv", (2, D, H)), ("bk", (2, D)), ("bv", (2, D))):
+            Wm[f"{n}.{l}"] = np.repeat(W[f"{n}.{l}"].reshape(shape), 2, axis=0).reshape(-1, *shape[2:]) \
+                if len(shape) == 3 else np.repeat(W[f"{n}.{l}"].reshape(shape), 2, axis=0).ravel()
+    tok = np.array([1, 2, 3, 4, 5])
+    np.testing.assert_allclose(M.decoder_logits(W, cfg, tok), M.decoder_logits(Wm, cfg_m, tok), rtol=0, atol=0)
