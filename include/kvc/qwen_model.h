@@ -19,9 +19,10 @@
 // captures its single-sequence decode step, qwen_infer.cu:135-214).
 //
 // Greedy serving (QwenModel::serve): requests are admitted FIFO up to max_batch
-// running sequences; an admitted request is prefilled (its first token comes from
-// the prompt's last position), then every step decodes one token for every running
-// sequence; a sequence retires after gen_len tokens.
+// running sequences; the prompts admitted together are prefilled together (their
+// rows stacked into one forward, up to prefill_rows rows; each request's first token
+// comes from its prompt's last position), then every step decodes one token for
+// every running sequence; a sequence retires after gen_len tokens.
 #pragma once
 #include <algorithm>
 #include <chrono>
@@ -41,6 +42,7 @@ struct QwenConfig {
     uint64_t seed = 0x71776e32ull;
     int step_path = 0;  // 0: fused kernels for steps of <= 32 rows; 1: one kernel per op
     int graph = 1;      // fused steps replay one captured HIP graph
+    int prefill_rows = 4096;  // prompt rows stacked into one prefill forward (a longer prompt runs alone)
 };
 
 struct QwenModel {
@@ -114,7 +116,7 @@ struct QwenModel {
             l.wd = param((size_t)H * I);
         }
         normf = param(H, true);
-        const size_t R = std::max(c.max_rows, c.max_batch);
+        const size_t R = std::max({c.max_rows, c.max_batch, c.prefill_rows});
         x = alloc(R * H * 2); nrm = alloc(R * H * 2); o = alloc(R * H * 2);
         q = alloc(R * QD * 2); att = alloc(R * QD * 2); k = alloc(R * KD * 2); v = alloc(R * KD * 2);
         gate = alloc(R * I * 2); up = alloc(R * I * 2);
@@ -239,8 +241,10 @@ struct QwenModel {
     // (optional on the fused path), argmax.  d_rows_head: the row count in device
     // memory (graph capture; `rows` is then the capacity).
     void head(int first, int rows, bool want_logits = true, const int* d_rows_head = nullptr) {
+        head_rows(static_cast<const char*>(x) + (size_t)first * c.hidden * 2, rows, want_logits, d_rows_head);
+    }
+    void head_rows(const void* xr, int rows, bool want_logits = true, const int* d_rows_head = nullptr) {
         const int H = c.hidden;
-        const void* xr = static_cast<const char*>(x) + (size_t)first * H * 2;
         if (rows_ok && rows <= kRowsMax) {
             kvc::check(kvc_rows_lm_head(want_logits ? logits : nullptr, d_tok, xr, normf, c.eps, embed, rows, c.vocab,
                                         H, d_rows_head, rws, rws_bytes, stream),
@@ -250,6 +254,74 @@ struct QwenModel {
         kvc::check(kvc_rmsnorm(nrm, xr, normf, rows, H, c.eps, stream), "final norm");
         kvc::check(kvc_linear(logits, nrm, embed, rows, c.vocab, H, KVC_F32, stream), "lm_head");
         kvc::check(kvc_argmax(logits, rows, c.vocab, d_tok, stream), "argmax");
+    }
+
+    // Prompt processing of several admitted sequences in one forward: their rows are
+    // stacked (row r of prompt i at position r), the K/V of every row go to its slot,
+    // each prompt attends causally over its own table, and the last row of each
+    // prompt gives its first token (first[i]).  Rows are independent in every op but
+    // attention, so each prompt's result is that of prefill() up to fp32 summation
+    // order in the linear layers.
+    void prefill_batch(const std::vector<Sequence*>& ss, const std::vector<const int*>& toks, int* first) {
+        const int n = (int)ss.size();
+        if (n == 0) return;
+        if (n > c.max_batch) throw kvc::Error(KVC_ERR_ARG, "prefill_batch: more prompts than max_batch");
+        std::vector<int> off(n + 1, 0), toff(n + 1, 0);
+        for (int i = 0; i < n; ++i) {
+            const int P = ss[i]->prompt_len;
+            if (P <= 0) throw kvc::Error(KVC_ERR_ARG, "prefill_batch: empty prompt");
+            off[i + 1] = off[i] + P;
+            toff[i + 1] = toff[i] + (int)ss[i]->block_table.size();
+        }
+        const int R = off[n];
+        if (R > std::max({c.max_rows, c.max_batch, c.prefill_rows}))
+            throw kvc::Error(KVC_ERR_ARG, "prefill_batch: more rows than the activation buffers hold");
+        // upload: [ids R | pos R | slot R | last n | tables]
+        const size_t ints = 3 * (size_t)R + n + toff[n];
+        ensure_meta(ints);
+        kvc::check(kvc_stream_synchronize(stream), "meta reuse");
+        int* h = h_meta;
+        size_t wsz = 0;
+        for (int i = 0; i < n; ++i) {
+            const Sequence& s = *ss[i];
+            const int P = s.prompt_len;
+            std::memcpy(h + off[i], toks[i], P * 4);
+            for (int r = 0; r < P; ++r) {
+                h[R + off[i] + r] = r;
+                h[2 * R + off[i] + r] = s.block_table[r / c.block_size] * c.block_size + r % c.block_size;
+            }
+            h[3 * R + i] = off[i + 1] - 1;
+            std::memcpy(h + 3 * R + n + toff[i], s.block_table.data(), s.block_table.size() * 4);
+            wsz = std::max(wsz, kvc_paged_causal_attn_workspace_size(0, P, c.n_heads, c.n_kv_heads, c.head_dim,
+                                                                     c.block_size, KVC_F16));
+        }
+        kvc::check(kvc_step_upload(d_meta, h, ints * 4, stream), "prefill upload");
+        const int* d_ids = d_meta;
+        const int* d_pos = d_meta + R;
+        const int* d_slot = d_meta + 2 * R;
+        const int* d_last = d_meta + 3 * R;
+        const int* d_tabs = d_meta + 3 * R + n;
+        ensure_ws(wsz);
+        kvc::check(kvc_embed_gather(x, embed, d_ids, R, c.hidden, c.vocab, stream), "embed");
+        const float scale = 1.0f / __builtin_sqrtf((float)c.head_dim);
+        const size_t QD = (size_t)c.n_heads * c.head_dim;
+        layers(R, d_pos, 0, [&](int l) {
+            kvc::check(kvc_write_kv_slots(k, v, kl(l), vl(l), d_slot, R, c.n_kv_heads, c.head_dim, c.block_size,
+                                          KVC_F16, stream),
+                       "prefill write_kv");
+            for (int i = 0; i < n; ++i)
+                kvc::check(kvc_paged_causal_attn(static_cast<const char*>(q) + off[i] * QD * 2,
+                                                 static_cast<char*>(att) + off[i] * QD * 2, kl(l), vl(l),
+                                                 d_tabs + toff[i], 0, off[i + 1] - off[i], c.n_heads, c.n_kv_heads,
+                                                 c.head_dim, c.block_size, scale, KVC_F16, ws, ws_bytes, stream),
+                           "prefill attention");
+        });
+        // the last row of every prompt, gathered, through the head
+        kvc::check(kvc_embed_gather(o, x, d_last, n, c.hidden, R, stream), "last rows");
+        head_rows(o, n, false);
+        kvc::check(kvc_memcpy_d2h(h_tok, d_tok, n * 4, stream), "tokens");
+        kvc::check(kvc_stream_synchronize(stream), "prefill");
+        std::memcpy(first, h_tok, n * 4);
     }
 
     // Prompt processing of one admitted sequence (kvm.allocate_prompt done): writes the
@@ -445,21 +517,42 @@ struct QwenModel {
                     ++r;
                 }
             }
-            while ((int)run.size() < c.max_batch && !waiting.empty()) {  // admit + prefill
+            std::vector<int> admitted;
+            while ((int)run.size() < c.max_batch && !waiting.empty()) {  // admit
                 const int i = waiting.front();
                 Sequence& s = seqs[i];
                 if (reqs[i].gen_len < 1 || s.prompt_len < 1) throw kvc::Error(KVC_ERR_ARG, "serve: empty request");
+                if (s.prompt_len > std::max(c.max_rows, c.prefill_rows))
+                    throw kvc::Error(KVC_ERR_ARG, "serve: prompt longer than max_rows");
                 if (reserved + worst(i) > c.num_blocks) break;
                 if (!kvm.allocate_prompt(s)) break;
                 reserved += worst(i);
                 waiting.pop_front();
-                const auto p0 = clk::now();
-                const int t = prefill(s, reqs[i].prompt.data());
-                st.prefill_us += std::chrono::duration<double, std::micro>(clk::now() - p0).count();
-                st.prompt_tokens += s.prompt_len;
-                out[i].push_back(t);
-                st.tokens++;
+                admitted.push_back(i);
                 run.push_back(i);
+            }
+            for (size_t a = 0; a < admitted.size();) {  // prefill the admitted prompts, stacked
+                std::vector<Sequence*> ps;
+                std::vector<const int*> pt;
+                int rows = 0;
+                size_t b = a;
+                for (; b < admitted.size(); ++b) {
+                    const int P = seqs[admitted[b]].prompt_len;
+                    if (!ps.empty() && rows + P > c.prefill_rows) break;
+                    ps.push_back(&seqs[admitted[b]]);
+                    pt.push_back(reqs[admitted[b]].prompt.data());
+                    rows += P;
+                }
+                std::vector<int> first(ps.size());
+                const auto p0 = clk::now();
+                prefill_batch(ps, pt, first.data());
+                st.prefill_us += std::chrono::duration<double, std::micro>(clk::now() - p0).count();
+                for (size_t j = 0; j < ps.size(); ++j) {
+                    out[admitted[a + j]].push_back(first[j]);
+                    st.prompt_tokens += ps[j]->prompt_len;
+                    st.tokens++;
+                }
+                a = b;
             }
             std::vector<Sequence*> batch;
             in.clear();

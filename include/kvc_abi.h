@@ -323,6 +323,7 @@ typedef struct kvc_qwen_config {
     uint64_t seed;                                      /* 0: default */
     int step_path;  /* 0: fused decode-step kernels when a step has <= 32 rows; 1: one kernel per op */
     int graph;      /* 1: fused steps replay one captured HIP graph */
+    int prefill_rows;  /* prompt rows stacked into one prefill forward (0: 4096) */
 } kvc_qwen_config;
 typedef struct kvc_qwen_stats {
     int steps, finished;

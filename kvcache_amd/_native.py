@@ -53,7 +53,7 @@ class QwenConfigC(C.Structure):
         ("layers", i32), ("hidden", i32), ("n_heads", i32), ("n_kv_heads", i32), ("head_dim", i32),
         ("inter", i32), ("vocab", i32), ("eps", C.c_float), ("theta", C.c_float), ("init_std", C.c_float),
         ("block_size", i32), ("num_blocks", i32), ("max_batch", i32), ("max_rows", i32), ("seed", u64),
-        ("step_path", i32), ("graph", i32),
+        ("step_path", i32), ("graph", i32), ("prefill_rows", i32),
     ]
 
 

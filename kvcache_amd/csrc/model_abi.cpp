@@ -47,6 +47,8 @@ int kvc_qwen_create(const kvc_qwen_config* cfg, kvc_qwen** out) {
         c.step_path = cfg->step_path;
         if (cfg->graph != 0 && cfg->graph != 1) return kvc::set_error(KVC_ERR_ARG, "qwen config: graph 0 or 1");
         c.graph = cfg->graph;
+        if (cfg->prefill_rows < 0) return kvc::set_error(KVC_ERR_ARG, "qwen config: prefill_rows >= 0");
+        if (cfg->prefill_rows > 0) c.prefill_rows = cfg->prefill_rows;
         if (c.layers <= 0 || c.hidden <= 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 || c.head_dim <= 0 || c.inter <= 0 ||
             c.vocab <= 0 || c.block_size <= 0 || c.num_blocks <= 0 || c.max_batch <= 0 || c.max_rows <= 0)
             return kvc::set_error(KVC_ERR_ARG, "qwen config: sizes must be positive");

@@ -30,11 +30,13 @@ class QwenConfig:
     seed: int = 0
     step_path: int = 0  # 0: fused decode-step kernels for steps of <= 32 rows; 1: one kernel per op
     graph: int = 1  # fused decode steps replay one captured HIP graph
+    prefill_rows: int = 4096  # prompt rows stacked into one prefill forward
 
     def to_c(self) -> QwenConfigC:
         return QwenConfigC(self.layers, self.hidden, self.n_heads, self.n_kv_heads, self.head_dim, self.inter,
                            self.vocab, self.eps, self.theta, self.init_std, self.block_size, self.num_blocks,
-                           self.max_batch, self.max_rows, self.seed, self.step_path, self.graph)
+                           self.max_batch, self.max_rows, self.seed, self.step_path, self.graph,
+                           self.prefill_rows)
 
 
 class QwenModel:
