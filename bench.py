@@ -283,14 +283,14 @@ def bench_prefill(steps, warmup):
     return res
 
 
-def bench_c5(n_req=64, gen=64, seed=5):
+def bench_c5(n_req=64, gen=64, seed=5, graph=True):
     """Config 5: the Qwen2-shaped decoder (24 layers, hidden 896, 14q/2kv, D 64, SwiGLU 4864, vocab 151936,
     random N(0, 0.02) fp16 weights) serving n_req requests greedily with continuous batching at batch 32;
     prompts of 16..256 random tokens, gen tokens each.  Throughput on the host clock around the whole run
     (each step ends with the sampled tokens on the host, as serving needs them)."""
     from kvcache_amd.model import QwenConfig, QwenModel
     rng = np.random.default_rng(seed)
-    cfg = QwenConfig(max_batch=32, max_rows=256, seed=seed)
+    cfg = QwenConfig(max_batch=32, max_rows=256, seed=seed, graph=int(graph))
     m = QwenModel(cfg)
     try:
         prompts = [rng.integers(0, cfg.vocab, int(n)) for n in rng.integers(16, 257, n_req)]
@@ -300,6 +300,7 @@ def bench_c5(n_req=64, gen=64, seed=5):
         m.close()
     return {"workload": f"C5 Qwen2-shaped decoder, {n_req} requests, prompts 16-256 tokens, {gen} generated each, "
                         "greedy, continuous batching width 32, random fp16 weights",
+            "graph_replay": bool(graph), "graph_steps": st["graph_steps"],
             "tokens": st["tokens"], "prompt_tokens": st["prompt_tokens"], "steps": st["steps"],
             "tokens_per_s": round(st["tokens"] / (st["wall_us"] * 1e-6), 1),
             "wall_ms": round(st["wall_us"] / 1e3, 2), "prefill_ms": round(st["prefill_us"] / 1e3, 2),
@@ -405,6 +406,7 @@ def main() -> int:
                     help="run only config 3 or config 4 and print its result (profiling)")
     ap.add_argument("--warm", action="store_true",
                     help="also time the planned path on one pool copy (Infinity-Cache resident)")
+    ap.add_argument("--no-graph", action="store_true", help="config 5: launch every decode step eagerly")
     ap.add_argument("--tune", action="append", default=[], metavar="KEY=VALUE",
                     help="set a library tuning knob (kvc_set_tuning), e.g. wg_per_cu=4")
     ap.add_argument("--fused", type=int, default=-1,
@@ -435,7 +437,7 @@ def main() -> int:
     if a.only:
         res = (bench_c3(a.steps, a.warmup, sweep_targets) if a.only == "c3" else
                bench_prefill(a.steps, a.warmup) if a.only == "prefill" else
-               bench_c5() if a.only == "c5" else bench_c4())
+               bench_c5(graph=not a.no_graph) if a.only == "c5" else bench_c4())
         print(json.dumps(res), flush=True)
         return 0
     if a.lengths == "reference":

@@ -108,57 +108,83 @@ __device__ __forceinline__ void st_f(__amdgpu_buffer_rsrc_t r, int byte_ofs, flo
     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, byte_ofs, 0, 0);
 }
 
+// Epilogue inputs that depend only on the group, the row and the column pair (the
+// residual row values; the q|k|v biases and the row's rotary position): loaded with
+// the group's weights, so the epilogue needs no further memory round trip.
+struct EpiIn {
+    _Float16 a0, a1;
+    int pos;
+};
+
+template <int EPI>
+__device__ __forceinline__ EpiIn epi_load(const RowsParams& p, int M, int g, int m, int c, bool ok) {
+    EpiIn e{};
+    const int c0 = tile_row<EPI>(p, g, 0) + c, c1 = tile_row<EPI>(p, g, 1) + c;
+    if constexpr (EPI == kEpiResidual) {
+        const auto r = rsrc(p.out, M * p.N * 2);
+        const int mm = ok ? m : kRows;
+        e.a0 = ld_h(r, (mm * p.N + c0) * 2);
+        e.a1 = ld_h(r, (mm * p.N + c1) * 2);
+    } else if constexpr (EPI == kEpiQkv) {
+        const auto rb = rsrc(p.bias, (p.q_cols + 2 * p.kv_cols) * 2);
+        e.a0 = ld_h(rb, c0 * 2);
+        e.a1 = ld_h(rb, c1 * 2);
+        e.pos = (int)__builtin_amdgcn_raw_buffer_load_b32(rsrc(p.pos, M * 4), m * 4, 0, 0);
+    }
+    return e;
+}
+
 // Epilogue of one (row m, lane column c) pair: v0 from tile 0, v1 from tile 1.  All
 // memory traffic goes through buffer descriptors bounded by the M valid rows, so
 // rows >= M (and invalid groups, `ok` false) drop their stores without a branch:
 // a branch around a store would make the compiler's load counters inexact and
 // force a full wait on the weight loads in flight.
 template <int EPI>
-__device__ __forceinline__ void epilogue(const RowsParams& p, int g, int m, int c, float v0, float v1, bool ok,
-                                         float& bv, int& bi) {
+__device__ __forceinline__ void epilogue(const RowsParams& p, int M, int g, int m, int c, float v0, float v1, bool ok,
+                                         const EpiIn& e, float& bv, int& bi) {
     const int c0 = tile_row<EPI>(p, g, 0) + c, c1 = tile_row<EPI>(p, g, 1) + c;
     const int mm = ok ? m : kRows;  // row index past the descriptors when the group is not valid
     if constexpr (EPI == kEpiStore) {
-        const auto r = rsrc(p.out, p.M * p.N * 2);
+        const auto r = rsrc(p.out, M * p.N * 2);
         st_h(r, (mm * p.N + c0) * 2, (_Float16)v0);
         st_h(r, (mm * p.N + c1) * 2, (_Float16)v1);
     } else if constexpr (EPI == kEpiResidual) {
-        const auto r = rsrc(p.out, p.M * p.N * 2);
-        const int o0 = (mm * p.N + c0) * 2, o1 = (mm * p.N + c1) * 2;
-        const float x0 = (float)ld_h(r, o0), x1 = (float)ld_h(r, o1);
-        st_h(r, o0, (_Float16)(x0 + (float)(_Float16)v0));
-        st_h(r, o1, (_Float16)(x1 + (float)(_Float16)v1));
+        const auto r = rsrc(p.out, M * p.N * 2);
+        st_h(r, (mm * p.N + c0) * 2, (_Float16)((float)e.a0 + (float)(_Float16)v0));
+        st_h(r, (mm * p.N + c1) * 2, (_Float16)((float)e.a1 + (float)(_Float16)v1));
     } else if constexpr (EPI == kEpiSwiglu) {
         const float gf = (float)(_Float16)v0, uf = (float)(_Float16)v1;
-        st_h(rsrc(p.out, p.M * p.N * 2), (mm * p.N + 16 * g + c) * 2, (_Float16)(gf / (1.0f + expf(-gf)) * uf));
+        st_h(rsrc(p.out, M * p.N * 2), (mm * p.N + 16 * g + c) * 2, (_Float16)(gf / (1.0f + expf(-gf)) * uf));
     } else if constexpr (EPI == kEpiQkv) {
         // q/k/v projection + bias (qwen_serve.cu:140-147), rotary on q and k (qwen_kernels.cu:64-79).
         // The group's columns lie in one head, so its region (q, k or v) is uniform.
-        _Float16 y0 = (_Float16)((float)(_Float16)v0 + (float)p.bias[c0]);
-        _Float16 y1 = (_Float16)((float)(_Float16)v1 + (float)p.bias[c1]);
+        _Float16 y0 = (_Float16)((float)(_Float16)v0 + (float)e.a0);
+        _Float16 y1 = (_Float16)((float)(_Float16)v1 + (float)e.a1);
         const int t = c0 % p.head_dim;  // < D/2: pair (t, t + D/2)
         const float inv = exp2f(-p.log2_theta * (2.0f * (float)t / (float)p.head_dim));
-        const int posm = (int)__builtin_amdgcn_raw_buffer_load_b32(rsrc(p.pos, p.M * 4), m * 4, 0, 0);
         float sn, co;
-        sincosf((float)posm * inv, &sn, &co);
+        sincosf((float)e.pos * inv, &sn, &co);
         const float x1 = (float)y0, x2 = (float)y1;
-        const bool rot = c0 < p.q_cols + p.kv_cols;
-        if (rot) {  // uniform
+        // region of the group from its first column, wave-uniform (every column of the
+        // group lies in one head), so the store descriptor is built once in scalars
+        const int cg = uniform(tile_row<EPI>(p, g, 0));
+        const bool rot = cg < p.q_cols + p.kv_cols;
+        if (rot) {
             y0 = (_Float16)(x1 * co - x2 * sn);
             y1 = (_Float16)(x2 * co + x1 * sn);
         }
-        const bool isq = c0 < p.q_cols;
+        const bool isq = cg < p.q_cols;
         _Float16* base = isq ? p.out : rot ? p.k_out : p.v_out;
         const int width = isq ? p.q_cols : p.kv_cols;
-        const int col = isq ? c0 : rot ? c0 - p.q_cols : c0 - p.q_cols - p.kv_cols;
-        const auto r = rsrc(base, p.M * width * 2);
+        const int col = c0 - (isq ? 0 : rot ? p.q_cols : p.q_cols + p.kv_cols);
+        const auto r = rsrc(base, M * width * 2);
         st_h(r, (mm * width + col) * 2, y0);
         st_h(r, (mm * width + col + (c1 - c0)) * 2, y1);
     } else {  // kEpiLogits
-        const auto r = rsrc(p.logits, p.logits ? p.M * p.N * 4 : 0);
+        const auto r = rsrc(p.logits, p.logits ? M * p.N * 4 : 0);
         st_f(r, (mm * p.N + c0) * 4, v0);
         st_f(r, (mm * p.N + c1) * 4, v1);
-        if (m < p.M) {  // (no memory access inside)
+        if (m < M) {  // (no memory access inside)
             better(bv, bi, v0, c0);
             better(bv, bi, v1, c1);
         }
@@ -172,9 +198,10 @@ __device__ __forceinline__ void epilogue(const RowsParams& p, int g, int m, int 
 // buffered, one barrier per group) and stored.  SPLIT: the K range is split across
 // workgroups (one group per workgroup) and the last to arrive finishes the group.
 template <int EPI, bool NORM, int MT, int WAVES, int S, bool SPLIT>
-__global__ __launch_bounds__(WAVES * 64) void rows_kernel(RowsParams pin) {
-    RowsParams p = pin;
-    if (p.dev_rows) p.M = min(max(*p.dev_rows, 0), pin.M);
+__global__ __launch_bounds__(WAVES * 64) void rows_kernel(RowsParams p) {
+    // the rows of this call (graph-safe launches read them from device memory);
+    // p itself is never copied: a modified copy of the parameters ends up in scratch
+    const int M = uniform(p.dev_rows ? min(max(*p.dev_rows, 0), p.M) : p.M);
     constexpr int kThreads = WAVES * 64;
     constexpr int kItems = kRows * 16 / kThreads;  // (row, column pair) items per thread
     __shared__ float s_red[2][WAVES][kRows][kCols + 1];
@@ -193,7 +220,7 @@ __global__ __launch_bounds__(WAVES * 64) void rows_kernel(RowsParams pin) {
     const int kbytes = p.K * 2;
 
     // A fragments of this wave's k range (rows >= M and steps past K read as zero)
-    const auto ar = rsrc(p.a, p.M * kbytes);
+    const auto ar = rsrc(p.a, M * kbytes);
     u4 af[S][MT];
     u4 nw[NORM ? S : 1];
 #pragma unroll
@@ -209,7 +236,12 @@ __global__ __launch_bounds__(WAVES * 64) void rows_kernel(RowsParams pin) {
     // group past the end reads zeros without touching memory), so the instruction
     // stream has no branches and the compiler's load counters stay exact: the waits
     // for one group leave the next group's loads in flight.
-    auto load_b = [&](u4 (&b)[S][2], int g, bool valid) {
+    auto load_b = [&](u4 (&b)[S][2], EpiIn (&e)[kItems], int g, bool valid) {
+#pragma unroll
+        for (int it = 0; it < kItems; ++it) {
+            const int item = threadIdx.x + it * kThreads;
+            e[it] = epi_load<EPI>(p, M, valid ? g : g0, item / 16, item % 16, valid);
+        }
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
             const auto br = rsrc(p.w + (size_t)tile_row<EPI>(p, valid ? g : g0, t) * p.K, 16 * kbytes);
@@ -220,7 +252,8 @@ __global__ __launch_bounds__(WAVES * 64) void rows_kernel(RowsParams pin) {
         }
     };
     u4 b0[S][2], b1[S][2];
-    load_b(b0, g0, true);
+    EpiIn e0[kItems], e1[kItems];
+    load_b(b0, e0, g0, true);
 
     if constexpr (NORM) {
         // RMSNorm of the rows (qwen_kernels.cu:24-40): sum of squares over this wave's
@@ -260,7 +293,7 @@ __global__ __launch_bounds__(WAVES * 64) void rows_kernel(RowsParams pin) {
     // One column group: MFMAs over this wave's k range, sum over the waves, epilogue.
     // `ok` false (a group past the end) runs the same code with every store dropped.
     // Returns false when this workgroup is not the last of a split group (it is done).
-    auto run_group = [&](const u4 (&b)[S][2], int j, bool ok) -> bool {
+    auto run_group = [&](const u4 (&b)[S][2], const EpiIn (&e)[kItems], int j, bool ok) -> bool {
         const int g = g0 + j;
         f4 acc[MT][2];
 #pragma unroll
@@ -302,7 +335,7 @@ __global__ __launch_bounds__(WAVES * 64) void rows_kernel(RowsParams pin) {
 #pragma unroll
             for (int it = 0; it < kItems; ++it) {
                 const int item = threadIdx.x + it * kThreads, m = item / 16, c = item % 16;
-                if (m < p.M) {
+                if (m < M) {
                     __hip_atomic_store(mine + m * kCols + c, v[it][0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     __hip_atomic_store(mine + m * kCols + c + 16, v[it][1], __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
@@ -323,7 +356,7 @@ __global__ __launch_bounds__(WAVES * 64) void rows_kernel(RowsParams pin) {
 #pragma unroll
             for (int it = 0; it < kItems; ++it) {
                 const int item = threadIdx.x + it * kThreads, m = item / 16, c = item % 16;
-                if (m < p.M) {
+                if (m < M) {
                     float a0 = 0.f, a1 = 0.f;
                     for (int s2 = 0; s2 < p.splits; ++s2) {
                         a0 += ld(all + (size_t)s2 * kRows * kCols + m * kCols + c);
@@ -340,7 +373,7 @@ __global__ __launch_bounds__(WAVES * 64) void rows_kernel(RowsParams pin) {
             const int item = threadIdx.x + it * kThreads, m = item / 16, c = item % 16;
             float bv = -FLT_MAX;
             int bi = INT_MAX;
-            epilogue<EPI>(p, ok ? g : g0, m, c, v[it][0], v[it][1], ok, bv, bi);
+            epilogue<EPI>(p, M, ok ? g : g0, m, c, v[it][0], v[it][1], ok, e[it], bv, bi);
             if constexpr (EPI == kEpiLogits) {
                 // the 16 column pairs of row m sit in 16 consecutive lanes
 #pragma unroll
@@ -359,14 +392,14 @@ __global__ __launch_bounds__(WAVES * 64) void rows_kernel(RowsParams pin) {
     };
 
     if constexpr (SPLIT) {
-        run_group(b0, 0, true);
+        run_group(b0, e0, 0, true);
     } else {
         // two groups per iteration so the buffers swap roles without register copies
         for (int j = 0; j < ng; j += 2) {
-            load_b(b1, g0 + j + 1, j + 1 < ng);
-            run_group(b0, j, true);
-            load_b(b0, g0 + j + 2, j + 2 < ng);
-            run_group(b1, j + 1, j + 1 < ng);
+            load_b(b1, e1, g0 + j + 1, j + 1 < ng);
+            run_group(b0, e0, j, true);
+            load_b(b0, e0, g0 + j + 2, j + 2 < ng);
+            run_group(b1, e1, j + 1, j + 1 < ng);
         }
     }
 }
@@ -423,8 +456,13 @@ Shape plan_shape(int groups, int K, bool norm) {
         s.splits = std::max(min_splits, g_tune_splits > 0 ? std::min(g_tune_splits, ks / 4 > 0 ? ks / 4 : 1) : 0);
     }
     if (s.splits == 1) {
-        const int slots = 2 * 256;  // resident workgroups the kernels are sized for
-        s.gpw = g_tune_gpw > 0 ? g_tune_gpw : std::max(1, (groups + slots - 1) / slots);
+        // groups per workgroup (measured at 32 rows): up to ~1024 groups, one workgroup
+        // per CU (256) running its groups back to back with the next one's loads in
+        // flight beats two co-resident single-group workgroups (gate/up, 304 groups:
+        // 8.7 vs 12.5 us); for many groups, about two workgroups per CU (lm_head, 4748
+        // groups: 10 per workgroup, 67-69 us, vs 78-88 us at 5-8 or 12-16)
+        const int per = groups <= 1024 ? 256 : 512;
+        s.gpw = g_tune_gpw > 0 ? g_tune_gpw : std::max(1, (groups + per - 1) / per);
     }
     return s;
 }
