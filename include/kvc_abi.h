@@ -297,8 +297,8 @@ int kvc_linear(void* y, const void* x, const void* w, int M, int N, int K, int o
  * dev_rows != NULL (graph-safe launches): the row count is read from device memory and
  *   M is its capacity (<= 32).
  * kvc_rows_set_tuning: overrides, -1 = automatic: K splits of layers with K > 1024,
- *   column groups (32 outputs) per workgroup, kernel shape 0..2 (4 waves x 7 k steps,
- *   8 waves x 4, 4 waves x 4 with K split).  The workspace size depends on them. */
+ *   column groups (32 outputs) per workgroup, kernel shape 0..3 (4 waves x 7 k steps,
+ *   8 waves x 4, 4 or 8 waves x 4 with K split).  The workspace size depends on them. */
 size_t kvc_rows_workspace_size(int N, int K);
 int kvc_rows_linear(void* y, const void* x, const void* w, int M, int N, int K, const void* norm_w, float eps,
                     int residual, const int* dev_rows, void* workspace, size_t workspace_bytes, kvc_stream_t stream);
