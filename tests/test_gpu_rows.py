@@ -146,3 +146,61 @@ def test_rows_rejects_bad_shapes():
         ops.rows_linear(x, x, w, 4, 896, 896)  # y aliases x
     with pytest.raises(KvcError):  # split layer without a workspace
         ops.rows_linear(y, x, DeviceBuffer(896 * 4864 * 2), 4, 896, 4864, residual=True)
+
+
+@pytest.mark.parametrize("n", [1, 7, 16, 17, 31])
+def test_rows_dev_rows_equal_plain_calls(n):
+    """The graph-safe form (row count read from device memory, M = 32 as capacity)
+    gives bit for bit the plain call's rows and leaves the rows past the count
+    untouched."""
+    say(f"rows dev_rows n={n}")
+    cap, H, I, QD, KD, V = 32, 896, 4864, 896, 128, 4096
+    rng = np.random.default_rng(350 + n)
+    x = rng.standard_normal((cap, H)).astype(np.float16)
+    a = rng.standard_normal((cap, I)).astype(np.float16)
+    nw = (1 + 0.1 * rng.standard_normal(H)).astype(np.float16)
+    w = (0.03 * rng.standard_normal((H, H))).astype(np.float16)
+    wd = (0.03 * rng.standard_normal((H, I))).astype(np.float16)
+    wqkv = (0.03 * rng.standard_normal((QD + 2 * KD, H))).astype(np.float16)
+    bqkv = (0.5 * rng.standard_normal(QD + 2 * KD)).astype(np.float16)
+    wgu = (0.03 * rng.standard_normal((2 * I, H))).astype(np.float16)
+    wl = (0.03 * rng.standard_normal((V, H))).astype(np.float16)
+    pos = rng.integers(0, 3000, cap).astype(np.int32)
+    dn = dev(np.array([n], np.int32))
+    ws = workspace(V, I)
+    sentinel = np.float16(7.25)
+
+    def both(shape, dtype, call):
+        """call(out, M, dev_rows) on a sentinel-filled buffer; returns (plain, graph-safe)."""
+        outs = []
+        for M_, d in ((n, None), (cap, dn)):
+            buf = dev(np.full(shape, sentinel, dtype))
+            call(buf, M_, d)
+            outs.append(host(buf, dtype, shape))
+        return outs
+
+    p_, g_ = both((cap, H), np.float16, lambda o, M_, d: ops.rows_linear(
+        o, dev(x), dev(w), M_, H, H, norm_w=dev(nw), eps=EPS, dev_rows=d, workspace=ws))
+    np.testing.assert_array_equal(g_[:n], p_[:n]); assert np.all(g_[n:] == sentinel)
+    # residual into x, K split across workgroups
+    p_, g_ = [], []
+    for M_, d in ((n, None), (cap, dn)):
+        xb = dev(x)
+        ops.rows_linear(xb, dev(a), dev(wd), M_, H, I, residual=True, dev_rows=d, workspace=ws)
+        (p_ if d is None else g_).append(host(xb, np.float16, (cap, H)))
+    np.testing.assert_array_equal(g_[0][:n], p_[0][:n]); np.testing.assert_array_equal(g_[0][n:], x[n:])
+    # q|k|v + rotary
+    res = []
+    for M_, d in ((n, None), (cap, dn)):
+        q, k, v = (dev(np.full((cap, c), sentinel, np.float16)) for c in (QD, KD, KD))
+        ops.rows_qkv(q, k, v, dev(x), dev(wqkv), dev(bqkv), dev(pos), M_, H, 14, 2, 64, 1e6, norm_w=dev(nw),
+                     eps=EPS, dev_rows=d)
+        res.append([host(t, np.float16, (cap, c)) for t, c in ((q, QD), (k, KD), (v, KD))])
+    for pt, gt in zip(*res):
+        np.testing.assert_array_equal(gt[:n], pt[:n]); assert np.all(gt[n:] == sentinel)
+    p_, g_ = both((cap, I), np.float16, lambda o, M_, d: ops.rows_swiglu(
+        o, dev(x), dev(wgu), M_, I, H, norm_w=dev(nw), eps=EPS, dev_rows=d))
+    np.testing.assert_array_equal(g_[:n], p_[:n]); assert np.all(g_[n:] == sentinel)
+    p_, g_ = both((cap,), np.int32, lambda o, M_, d: ops.rows_lm_head(
+        None, o, dev(x), dev(wl), M_, V, H, norm_w=dev(nw), eps=EPS, dev_rows=d, workspace=ws))
+    np.testing.assert_array_equal(g_[:n], p_[:n])

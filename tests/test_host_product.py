@@ -236,3 +236,36 @@ def test_decode_plan_covers_every_token_once(case):
     recs = sorted(v[0] + k for v in groups.values() for k in range(v[2]))
     assert recs == list(range(nr)), "record ids are dense and disjoint"
     assert sorted(v[1] for v in groups.values()) == list(range(len(groups)))
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,B,dtype", [(8, 8, 64, 16, 1), (14, 2, 64, 16, 1), (14, 2, 64, 16, 0),
+                                              (8, 8, 64, 4, 1), (32, 8, 128, 16, 1)])
+def test_decode_plan_capacity_bounds_every_plan(Hq, Hkv, D, B, dtype):
+    """The graph-safe launches are sized by kvc_decode_plan_capacity(N, tokens): no plan
+    of at most N sequences holding at most `tokens` tokens may need more units or
+    partial records than it returns, whatever the length mix."""
+    import ctypes as C
+
+    from kvcache_amd import ops
+    from kvcache_amd._native import lib
+    rng = np.random.default_rng(Hq * 100 + D + B + dtype)
+    N, tokens = 32, 32 * 2048
+    cap = C.c_int(0)
+    assert lib().kvc_decode_plan_capacity(N, tokens, Hq, Hkv, D, B, dtype, C.byref(cap)) == 0
+    mixes = [np.full(N, tokens // N), np.r_[[tokens - (N - 1)], np.ones(N - 1, int)], np.ones(N, int),
+             np.array([tokens // 2, tokens // 2]), np.array([tokens])]
+    for _ in range(20):
+        n = int(rng.integers(1, N + 1))
+        cut = np.sort(rng.choice(np.arange(1, tokens), n - 1, replace=False)) if n > 1 else np.array([], int)
+        mixes.append(np.diff(np.r_[0, cut, int(rng.integers(n, tokens + 1))]))
+    planned = 0
+    for lens in mixes:
+        lens = np.maximum(np.asarray(lens, np.int32), 0)
+        try:
+            _, nu, nr = ops.decode_plan(lens, Hq, Hkv, D, B, dtype=dtype)
+        except Exception as e:  # sequences too long for a path are refused by the planner itself
+            assert "too long" in str(e) or "unsupported" in str(e).lower(), e
+            continue
+        planned += 1
+        assert nu <= cap.value and nr <= cap.value, (lens.tolist()[:8], nu, nr, cap.value)
+    assert planned >= len(mixes) - 2
