@@ -258,10 +258,12 @@ struct QwenModel {
 
     // Prompt processing of several admitted sequences in one forward: their rows are
     // stacked (row r of prompt i at position r), the K/V of every row go to its slot,
-    // each prompt attends causally over its own table, and the last row of each
-    // prompt gives its first token (first[i]).  Rows are independent in every op but
-    // attention, so each prompt's result is that of prefill() up to fp32 summation
-    // order in the linear layers.
+    // and the last row of each prompt gives its first token (first[i]).  Causal
+    // attention over all prompts is one planned decode launch per layer: row r of
+    // prompt i is a query of length r + 1 over prompt i's table (the causal form of
+    // qwen_kernels.cu:146-181), planned once for the batch.  Rows are independent in
+    // every op but attention, so each prompt's result is that of prefill() up to fp32
+    // summation order.
     void prefill_batch(const std::vector<Sequence*>& ss, const std::vector<const int*>& toks, int* first) {
         const int n = (int)ss.size();
         if (n == 0) return;
@@ -276,12 +278,30 @@ struct QwenModel {
         const int R = off[n];
         if (R > std::max({c.max_rows, c.max_batch, c.prefill_rows}))
             throw kvc::Error(KVC_ERR_ARG, "prefill_batch: more rows than the activation buffers hold");
-        // upload: [ids R | pos R | slot R | last n | tables]
-        const size_t ints = 3 * (size_t)R + n + toff[n];
+        // the causal plan: row r of prompt i attends over r + 1 positions of table i
+        const int T = toff[n];
+        h_len.resize(R); h_off.resize(R); h_tab.resize(T);
+        for (int i = 0; i < n; ++i) {
+            std::memcpy(h_tab.data() + toff[i], ss[i]->block_table.data(), ss[i]->block_table.size() * 4);
+            for (int r = 0; r < ss[i]->prompt_len; ++r) {
+                h_len[off[i] + r] = r + 1;
+                h_off[off[i] + r] = toff[i];
+            }
+        }
+        int nu = 0, nr = 0;
+        kvc::check(kvc_decode_plan(h_len.data(), h_off.data(), h_tab.data(), T, R, c.n_heads, c.n_kv_heads,
+                                   c.head_dim, c.block_size, KVC_F16, 0, nullptr, 0, &nu, &nr),
+                   "prefill plan");
+        const int ipu = kvc_decode_plan_entry_ints(c.n_heads, c.n_kv_heads, c.head_dim, c.block_size, KVC_F16);
+        h_work.resize((size_t)nu * ipu);
+        kvc::check(kvc_decode_plan(h_len.data(), h_off.data(), h_tab.data(), T, R, c.n_heads, c.n_kv_heads,
+                                   c.head_dim, c.block_size, KVC_F16, 0, h_work.data(), nu, &nu, &nr),
+                   "prefill plan");
+        // upload: [ids R | pos R | slot R | last n | tables T | work]
+        const size_t ints = 3 * (size_t)R + n + T + h_work.size();
         ensure_meta(ints);
         kvc::check(kvc_stream_synchronize(stream), "meta reuse");
         int* h = h_meta;
-        size_t wsz = 0;
         for (int i = 0; i < n; ++i) {
             const Sequence& s = *ss[i];
             const int P = s.prompt_len;
@@ -291,30 +311,27 @@ struct QwenModel {
                 h[2 * R + off[i] + r] = s.block_table[r / c.block_size] * c.block_size + r % c.block_size;
             }
             h[3 * R + i] = off[i + 1] - 1;
-            std::memcpy(h + 3 * R + n + toff[i], s.block_table.data(), s.block_table.size() * 4);
-            wsz = std::max(wsz, kvc_paged_causal_attn_workspace_size(0, P, c.n_heads, c.n_kv_heads, c.head_dim,
-                                                                     c.block_size, KVC_F16));
         }
+        std::memcpy(h + 3 * R + n, h_tab.data(), (size_t)T * 4);
+        std::memcpy(h + 3 * R + n + T, h_work.data(), h_work.size() * 4);
         kvc::check(kvc_step_upload(d_meta, h, ints * 4, stream), "prefill upload");
         const int* d_ids = d_meta;
         const int* d_pos = d_meta + R;
         const int* d_slot = d_meta + 2 * R;
         const int* d_last = d_meta + 3 * R;
         const int* d_tabs = d_meta + 3 * R + n;
-        ensure_ws(wsz);
+        const int* d_work = d_tabs + T;
+        ensure_ws(kvc_decode_planned_workspace_size(c.n_heads, c.n_kv_heads, c.head_dim, c.block_size, KVC_F16, nr));
         kvc::check(kvc_embed_gather(x, embed, d_ids, R, c.hidden, c.vocab, stream), "embed");
         const float scale = 1.0f / __builtin_sqrtf((float)c.head_dim);
-        const size_t QD = (size_t)c.n_heads * c.head_dim;
         layers(R, d_pos, 0, [&](int l) {
             kvc::check(kvc_write_kv_slots(k, v, kl(l), vl(l), d_slot, R, c.n_kv_heads, c.head_dim, c.block_size,
                                           KVC_F16, stream),
                        "prefill write_kv");
-            for (int i = 0; i < n; ++i)
-                kvc::check(kvc_paged_causal_attn(static_cast<const char*>(q) + off[i] * QD * 2,
-                                                 static_cast<char*>(att) + off[i] * QD * 2, kl(l), vl(l),
-                                                 d_tabs + toff[i], 0, off[i + 1] - off[i], c.n_heads, c.n_kv_heads,
-                                                 c.head_dim, c.block_size, scale, KVC_F16, ws, ws_bytes, stream),
-                           "prefill attention");
+            kvc::check(kvc_batched_paged_decode_planned(q, kl(l), vl(l), d_tabs, T, att, R, c.n_heads, c.n_kv_heads,
+                                                        c.head_dim, c.block_size, scale, KVC_F16, d_work, nu, nr, ws,
+                                                        ws_bytes, stream),
+                       "prefill attention");
         });
         // the last row of every prompt, gathered, through the head
         kvc::check(kvc_embed_gather(o, x, d_last, n, c.hidden, R, stream), "last rows");
