@@ -104,6 +104,7 @@ struct Engine {
     std::vector<Sequence*> running;
     std::vector<double> latencies;
     std::vector<int> wpos;
+    std::vector<Sequence*> admitted;  // this step's admissions (prefilled together)
     int reserved_blocks = 0;
     double clock = 0;
     int next_id = 0;
@@ -154,6 +155,7 @@ struct Engine {
                 ++i;
             }
         }
+        admitted.clear();
         while ((int)running.size() < cfg.max_batch && !waiting.empty() &&  // 2) admit
                waiting.front()->arrival_us <= clock) {
             Sequence* s = waiting.front();
@@ -164,12 +166,13 @@ struct Engine {
             s->status = SeqStatus::Running;
             running.push_back(s);
             waiting.pop_front();
-            if (cfg.prefill) {  // the prompt is processed on admission
-                const double pu = runner.prefill(*s, kvm);
-                stats.prefill_us += pu;
-                stats.gpu_us += pu;
-                clock += pu;
-            }
+            admitted.push_back(s);
+        }
+        if (cfg.prefill && !admitted.empty()) {  // the step's admitted prompts are processed together
+            const double pu = runner.prefill_batch(admitted, kvm);
+            stats.prefill_us += pu;
+            stats.gpu_us += pu;
+            clock += pu;
         }
         if (running.empty()) {  // 3) idle or done
             if (waiting.empty()) return false;

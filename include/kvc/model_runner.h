@@ -78,6 +78,12 @@ struct ModelRunner {
     int* h_ptab = nullptr;
     void* h_ptab_ev = nullptr;
     int pf_cap = 0, ptab_cap = 0;
+    // batched prefill: causal plan and its upload [slot | tables | work]
+    std::vector<int> pf_len, pf_off, pf_tab, pf_work;
+    int* d_pf = nullptr;
+    int* h_pf = nullptr;
+    void* h_pf_ev = nullptr;
+    size_t pf_meta_cap = 0;
     double last_prefill_us = 0;
     uint64_t digest = 1469598103934665603ull;
     long long last_sum_len = 0;
@@ -129,6 +135,7 @@ struct ModelRunner {
         kvc_free(dq); kvc_free(dk); kvc_free(dv); kvc_free(dout); kvc_free(d_meta); kvc_free(ws);
         kvc_free(pq); kvc_free(pk); kvc_free(pv); kvc_free(pout); kvc_free(d_ptab); kvc_host_free(h_ptab);
         kvc_event_destroy(h_ptab_ev);
+        kvc_free(d_pf); kvc_host_free(h_pf); kvc_event_destroy(h_pf_ev);
         for (int i = 0; i < kRing; ++i) { kvc_host_free(h_meta[i]); kvc_event_destroy(h_ev[i]); }
         kvc_event_destroy(ev0); kvc_event_destroy(ev1);
         kvc_graph_destroy(gexec);
@@ -420,6 +427,98 @@ struct ModelRunner {
                        "prefill write_kv");
             kvc::check(kvc_paged_causal_attn(pq, pout, kvm.k_layer(l), kvm.v_layer(l), d_ptab, 0, P, n_heads,
                                              n_kv_heads, head_dim, block_size, scale, opt.dtype, ws, ws_bytes, stream),
+                       "prefill attention");
+        }
+        kvc::check(kvc_event_record(ev1, stream), "event");
+        if (opt.clock_mode != 0) return 0.0;
+        float ms = 0.f;
+        kvc::check(kvc_event_elapsed_ms(&ms, ev0, ev1), "event elapsed");
+        last_prefill_us = (double)ms * 1e3;
+        return last_prefill_us;
+    }
+
+    // Prompt processing of the sequences admitted in one step, together: per layer one
+    // slot-mapped write of every prompt row's K/V and ONE planned decode launch in
+    // which row r of a prompt is a query of length r + 1 over that prompt's table (the
+    // causal definition of qwen_kernels.cu:146-181).  A single prompt takes prefill().
+    // Returns the GPU time (us) on the measured clock, 0 on the virtual clock.
+    double prefill_batch(const std::vector<Sequence*>& ss, KVCacheManager& kvm) {
+        last_prefill_us = 0;
+        if (!opt.device || !opt.prefill || ss.empty()) return 0.0;
+        if (ss.size() == 1) return prefill(*ss[0], kvm);
+        if (!kvm.has_device()) throw kvc::Error(KVC_ERR_STATE, "prefill: KV manager has no device pools");
+        const size_t es = kvc::dtype_size(opt.dtype);
+        int R = 0, T = 0;
+        for (const Sequence* s : ss) { R += std::max(s->prompt_len, 0); T += (int)s->block_table.size(); }
+        if (R == 0) return 0.0;
+        if (R > pf_cap) {
+            kvc::check(kvc_stream_synchronize(stream), "prefill growth");
+            kvc_free(pq); kvc_free(pk); kvc_free(pv); kvc_free(pout);
+            pq = pk = pv = pout = nullptr;
+            pf_cap = 0;
+            const int cap = std::max(R, 256);
+            kvc::check(kvc_malloc(&pq, (size_t)cap * n_heads * head_dim * es), "prefill q");
+            kvc::check(kvc_malloc(&pout, (size_t)cap * n_heads * head_dim * es), "prefill out");
+            kvc::check(kvc_malloc(&pk, (size_t)cap * n_kv_heads * head_dim * es), "prefill k");
+            kvc::check(kvc_malloc(&pv, (size_t)cap * n_kv_heads * head_dim * es), "prefill v");
+            kvc::check(kvc_fill_normal(pq, (size_t)cap * n_heads * head_dim, opt.dtype, opt.seed + 3, 1.0f, stream), "fill");
+            kvc::check(kvc_fill_normal(pk, (size_t)cap * n_kv_heads * head_dim, opt.dtype, opt.seed + 4, 1.0f, stream), "fill");
+            kvc::check(kvc_fill_normal(pv, (size_t)cap * n_kv_heads * head_dim, opt.dtype, opt.seed + 5, 1.0f, stream), "fill");
+            pf_cap = cap;
+        }
+        // plan: rows of every prompt with causal lengths over their own tables
+        pf_len.resize(R); pf_off.resize(R); pf_tab.resize(T);
+        std::vector<int> slot(R);
+        int r0 = 0, t0 = 0;
+        for (const Sequence* s : ss) {
+            std::memcpy(pf_tab.data() + t0, s->block_table.data(), s->block_table.size() * sizeof(int));
+            for (int r = 0; r < s->prompt_len; ++r) {
+                pf_len[r0 + r] = r + 1;
+                pf_off[r0 + r] = t0;
+                slot[r0 + r] = s->block_table[r / block_size] * block_size + r % block_size;
+            }
+            r0 += s->prompt_len;
+            t0 += (int)s->block_table.size();
+        }
+        int nu = 0, nr = 0;
+        kvc::check(kvc_decode_plan(pf_len.data(), pf_off.data(), pf_tab.data(), T, R, n_heads, n_kv_heads, head_dim,
+                                   block_size, opt.dtype, opt.plan_target, nullptr, 0, &nu, &nr),
+                   "prefill plan");
+        const int ipu = kvc_decode_plan_entry_ints(n_heads, n_kv_heads, head_dim, block_size, opt.dtype);
+        pf_work.resize((size_t)nu * ipu);
+        kvc::check(kvc_decode_plan(pf_len.data(), pf_off.data(), pf_tab.data(), T, R, n_heads, n_kv_heads, head_dim,
+                                   block_size, opt.dtype, opt.plan_target, pf_work.data(), nu, &nu, &nr),
+                   "prefill plan");
+        // one upload: [slot R | tables T | work]
+        const size_t ints = (size_t)R + T + pf_work.size();
+        if (ints > pf_meta_cap) {
+            kvc::check(kvc_stream_synchronize(stream), "prefill metadata growth");
+            kvc_free(d_pf); kvc_host_free(h_pf);
+            d_pf = nullptr; h_pf = nullptr;
+            pf_meta_cap = std::max(ints, pf_meta_cap * 2);
+            kvc::check(kvc_malloc((void**)&d_pf, pf_meta_cap * sizeof(int)), "prefill metadata");
+            kvc::check(kvc_host_alloc((void**)&h_pf, pf_meta_cap * sizeof(int)), "pinned prefill metadata");
+            if (!h_pf_ev) kvc::check(kvc_event_create(&h_pf_ev), "prefill event");
+        } else if (h_pf_ev) {
+            kvc::check(kvc_event_synchronize(h_pf_ev), "prefill metadata wait");  // previous upload done
+        }
+        std::memcpy(h_pf, slot.data(), (size_t)R * sizeof(int));
+        std::memcpy(h_pf + R, pf_tab.data(), (size_t)T * sizeof(int));
+        std::memcpy(h_pf + R + T, pf_work.data(), pf_work.size() * sizeof(int));
+        kvc::check(kvc_step_upload(d_pf, h_pf, ints * sizeof(int), stream), "prefill upload");
+        kvc::check(kvc_event_record(h_pf_ev, stream), "prefill event");
+        const int* d_slot = d_pf;
+        const int* d_tab = d_pf + R;
+        const int* d_work = d_tab + T;
+        ensure_workspace(kvc_decode_planned_workspace_size(n_heads, n_kv_heads, head_dim, block_size, opt.dtype, nr));
+        kvc::check(kvc_event_record(ev0, stream), "event");
+        for (int l = 0; l < opt.n_layers; ++l) {
+            kvc::check(kvc_write_kv_slots(pk, pv, kvm.k_layer(l), kvm.v_layer(l), d_slot, R, n_kv_heads, head_dim,
+                                          block_size, opt.dtype, stream),
+                       "prefill write_kv");
+            kvc::check(kvc_batched_paged_decode_planned(pq, kvm.k_layer(l), kvm.v_layer(l), d_tab, T, pout, R,
+                                                        n_heads, n_kv_heads, head_dim, block_size, scale, opt.dtype,
+                                                        d_work, nu, nr, ws, ws_bytes, stream),
                        "prefill attention");
         }
         kvc::check(kvc_event_record(ev1, stream), "event");

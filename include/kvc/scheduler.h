@@ -54,16 +54,16 @@ inline EngineStats run_static(std::vector<Request> reqs, KVCacheManager& kvm, Mo
             if (reserved + fp > kvm.num_blocks) break;
             kvm.allocate_prompt(seqs[idx]);
             reserved += fp;
-            if (runner.opt.prefill) {  // the prompt is processed on admission
-                const double pu = runner.prefill(seqs[idx], kvm);
-                R.prefill_us += pu;
-                R.gpu_us += pu;
-                clock += pu;
-            }
             group.push_back(&seqs[idx]);
             ++idx;
         }
         if (group.empty()) break;  // not even one request fits the pool
+        if (runner.opt.prefill) {  // the group's prompts are processed together on admission
+            const double pu = runner.prefill_batch(group, kvm);
+            R.prefill_us += pu;
+            R.gpu_us += pu;
+            clock += pu;
+        }
         int active = (int)group.size();
         while (active > 0) {
             int still = 0;
