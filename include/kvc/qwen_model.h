@@ -28,7 +28,10 @@
 #include <chrono>
 #include <cstring>
 #include <deque>
+#include <fstream>
+#include <sstream>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 #include "../kvc_abi.h"
@@ -55,6 +58,8 @@ struct QwenModel {
     kvc_stream_t stream = nullptr;
     std::vector<void*> owned;
     void *embed = nullptr, *normf = nullptr;
+    void* lm_head = nullptr;  // nullptr: tied to the embedding
+    const void* lm_w() const { return lm_head ? lm_head : embed; }
     std::vector<Layer> L;
     // activations for up to max(max_rows, max_batch) rows
     void *x = nullptr, *nrm = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *o = nullptr,
@@ -246,13 +251,13 @@ struct QwenModel {
     void head_rows(const void* xr, int rows, bool want_logits = true, const int* d_rows_head = nullptr) {
         const int H = c.hidden;
         if (rows_ok && rows <= kRowsMax) {
-            kvc::check(kvc_rows_lm_head(want_logits ? logits : nullptr, d_tok, xr, normf, c.eps, embed, rows, c.vocab,
+            kvc::check(kvc_rows_lm_head(want_logits ? logits : nullptr, d_tok, xr, normf, c.eps, lm_w(), rows, c.vocab,
                                         H, d_rows_head, rws, rws_bytes, stream),
                        "final norm + lm_head + argmax");
             return;
         }
         kvc::check(kvc_rmsnorm(nrm, xr, normf, rows, H, c.eps, stream), "final norm");
-        kvc::check(kvc_linear(logits, nrm, embed, rows, c.vocab, H, KVC_F32, stream), "lm_head");
+        kvc::check(kvc_linear(logits, nrm, lm_w(), rows, c.vocab, H, KVC_F32, stream), "lm_head");
         kvc::check(kvc_argmax(logits, rows, c.vocab, d_tok, stream), "argmax");
     }
 
@@ -490,6 +495,143 @@ struct QwenModel {
         kvc::check(kvc_stream_synchronize(stream), "decode");
         std::memcpy(out, h_tok, n * 4);
         ++graph_steps;
+    }
+
+    // ---- weights in the reference's dump format (qwen_loader.h:21-76, written by
+    // tools/dump_weights.py:29-66): manifest.tsv lines "name<TAB>offset<TAB>nbytes<TAB>
+    // shape_csv" over weights.bin, fp16 row-major [out, in], Hugging Face names.
+    struct WeightRef {
+        std::string name;
+        void* dst;
+        std::vector<int> shape;
+    };
+    std::vector<WeightRef> weight_refs() {
+        const int H = c.hidden, QD = c.n_heads * c.head_dim, KD = c.n_kv_heads * c.head_dim, I = c.inter;
+        std::vector<WeightRef> w{{"model.embed_tokens.weight", embed, {c.vocab, H}}};
+        for (int l = 0; l < c.layers; ++l) {
+            const std::string p = "model.layers." + std::to_string(l) + ".";
+            const Layer& y = L[l];
+            w.push_back({p + "input_layernorm.weight", y.ln1, {H}});
+            w.push_back({p + "self_attn.q_proj.weight", y.wq, {QD, H}});
+            w.push_back({p + "self_attn.q_proj.bias", y.bq, {QD}});
+            w.push_back({p + "self_attn.k_proj.weight", y.wk, {KD, H}});
+            w.push_back({p + "self_attn.k_proj.bias", y.bk, {KD}});
+            w.push_back({p + "self_attn.v_proj.weight", y.wv, {KD, H}});
+            w.push_back({p + "self_attn.v_proj.bias", y.bv, {KD}});
+            w.push_back({p + "self_attn.o_proj.weight", y.wo, {H, QD}});
+            w.push_back({p + "post_attention_layernorm.weight", y.ln2, {H}});
+            w.push_back({p + "mlp.gate_proj.weight", y.wg, {I, H}});
+            w.push_back({p + "mlp.up_proj.weight", y.wu, {I, H}});
+            w.push_back({p + "mlp.down_proj.weight", y.wd, {H, I}});
+        }
+        w.push_back({"model.norm.weight", normf, {H}});
+        return w;
+    }
+    static size_t elems(const std::vector<int>& s) {
+        size_t n = 1;
+        for (int d : s) n *= (size_t)d;
+        return n;
+    }
+
+    // Loads every tensor of the model from `dir` (sizes and shapes must match the
+    // configuration; other entries are ignored).  lm_head.weight, when present and
+    // different from the embedding, becomes an untied output matrix.
+    void load_weights(const std::string& dir) {
+        struct Entry { size_t off, nbytes; std::vector<int> shape; };
+        std::unordered_map<std::string, Entry> man;
+        std::ifstream mf(dir + "/manifest.tsv");
+        if (!mf) throw kvc::Error(KVC_ERR_ARG, "load_weights: cannot open " + dir + "/manifest.tsv");
+        std::string line;
+        size_t end = 0;
+        while (std::getline(mf, line)) {
+            if (line.empty()) continue;
+            std::istringstream ss(line);
+            std::string name, off, nb, shape;
+            if (!std::getline(ss, name, '\t') || !std::getline(ss, off, '\t') || !std::getline(ss, nb, '\t'))
+                throw kvc::Error(KVC_ERR_ARG, "load_weights: malformed manifest line: " + line);
+            std::getline(ss, shape);
+            Entry e{std::stoull(off), std::stoull(nb), {}};
+            std::stringstream sc(shape);
+            for (std::string d; std::getline(sc, d, ',');)
+                if (!d.empty()) e.shape.push_back(std::stoi(d));
+            end = std::max(end, e.off + e.nbytes);
+            man[name] = e;
+        }
+        std::ifstream bf(dir + "/weights.bin", std::ios::binary | std::ios::ate);
+        if (!bf) throw kvc::Error(KVC_ERR_ARG, "load_weights: cannot open " + dir + "/weights.bin");
+        if ((size_t)bf.tellg() < end) throw kvc::Error(KVC_ERR_ARG, "load_weights: weights.bin shorter than the manifest");
+        const size_t chunk = (size_t)64 << 20;
+        char* stage = nullptr;
+        kvc::check(kvc_host_alloc((void**)&stage, chunk), "pinned staging");
+        auto read_into = [&](const Entry& e, void* dst) {
+            for (size_t done = 0; done < e.nbytes; done += chunk) {
+                const size_t n = std::min(chunk, e.nbytes - done);
+                bf.seekg((std::streamoff)(e.off + done));
+                bf.read(stage, (std::streamsize)n);
+                if (!bf) throw kvc::Error(KVC_ERR_ARG, "load_weights: read failed");
+                kvc::check(kvc_memcpy_h2d(static_cast<char*>(dst) + done, stage, n, stream), "weights upload");
+                kvc::check(kvc_stream_synchronize(stream), "weights upload");
+            }
+        };
+        try {
+            for (const WeightRef& w : weight_refs()) {
+                const auto it = man.find(w.name);
+                if (it == man.end()) throw kvc::Error(KVC_ERR_ARG, "load_weights: missing tensor " + w.name);
+                if (it->second.nbytes != elems(w.shape) * 2 || it->second.shape != w.shape)
+                    throw kvc::Error(KVC_ERR_ARG, "load_weights: " + w.name + " has the wrong size or shape");
+                read_into(it->second, w.dst);
+            }
+            const auto lh = man.find("lm_head.weight");
+            bool tied = true;
+            if (lh != man.end()) {
+                const auto& e = man["model.embed_tokens.weight"];
+                if (lh->second.nbytes != e.nbytes || lh->second.shape != e.shape)
+                    throw kvc::Error(KVC_ERR_ARG, "load_weights: lm_head.weight has the wrong size or shape");
+                // tied when the bytes equal the embedding's (the dump stores a copy)
+                std::vector<char> a(chunk), b(chunk);
+                for (size_t done = 0; done < e.nbytes && tied; done += chunk) {
+                    const size_t n = std::min(chunk, e.nbytes - done);
+                    bf.seekg((std::streamoff)(e.off + done)); bf.read(a.data(), (std::streamsize)n);
+                    bf.seekg((std::streamoff)(lh->second.off + done)); bf.read(b.data(), (std::streamsize)n);
+                    tied = std::memcmp(a.data(), b.data(), n) == 0;
+                }
+                if (!tied) {
+                    if (!lm_head) lm_head = alloc(lh->second.nbytes);
+                    read_into(lh->second, lm_head);
+                }
+            }
+            if (tied) lm_head = nullptr;  // (an untied matrix from an earlier load stays allocated, unused)
+        } catch (...) {
+            kvc_host_free(stage);
+            throw;
+        }
+        kvc_host_free(stage);
+        kvc_graph_destroy(gexec);  // the captured step holds the old output matrix
+        gexec = nullptr;
+    }
+
+    // Writes the model's tensors in the same format (lm_head.weight included, as the
+    // reference's dump does for the tied Qwen2.5 models).
+    void save_weights(const std::string& dir) {
+        std::ofstream bf(dir + "/weights.bin", std::ios::binary);
+        std::ofstream mf(dir + "/manifest.tsv");
+        if (!bf || !mf) throw kvc::Error(KVC_ERR_ARG, "save_weights: cannot write into " + dir);
+        auto refs = weight_refs();
+        refs.push_back({"lm_head.weight", const_cast<void*>(lm_w()), {c.vocab, c.hidden}});
+        size_t off = 0;
+        std::vector<char> host;
+        for (const WeightRef& w : refs) {
+            const size_t nb = elems(w.shape) * 2;
+            host.resize(nb);
+            kvc::check(kvc_memcpy_d2h(host.data(), w.dst, nb, stream), "weights download");
+            kvc::check(kvc_stream_synchronize(stream), "weights download");
+            bf.write(host.data(), (std::streamsize)nb);
+            std::string shape;
+            for (size_t i = 0; i < w.shape.size(); ++i) shape += (i ? "," : "") + std::to_string(w.shape[i]);
+            mf << w.name << '\t' << off << '\t' << nb << '\t' << shape << '\n';
+            off += nb;
+        }
+        if (!bf || !mf) throw kvc::Error(KVC_ERR_ARG, "save_weights: write failed");
     }
 
     struct Request {

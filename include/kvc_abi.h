@@ -342,6 +342,14 @@ int  kvc_qwen_tensor(kvc_qwen* h, const char* name, int layer, void** ptr, size_
  * request order (sum of gen_len ints). */
 int  kvc_qwen_serve(kvc_qwen* h, int n_req, const int* prompt_off, const int* prompt_tokens, const int* gen_len,
                     int* out_tokens, kvc_qwen_stats* stats);
+/* weights in the reference's dump format (QwenWeights::load, qwen_loader.h:21-76; written by
+ * tools/dump_weights.py:29-66): <dir>/manifest.tsv ("name\toffset\tnbytes\tshape_csv"
+ * per line, Hugging Face names) over <dir>/weights.bin (fp16, [out, in] row-major).
+ * Load: every tensor of the configured shape must be present (others are ignored);
+ * lm_head.weight, if it differs from the embedding, is used untied.  Save: writes all
+ * tensors, lm_head.weight included. */
+int  kvc_qwen_load_weights(kvc_qwen* h, const char* dir);
+int  kvc_qwen_save_weights(kvc_qwen* h, const char* dir);
 /* one prompt: its first generated token and the fp32 logits of its last position (vocab floats) */
 int  kvc_qwen_prefill_logits(kvc_qwen* h, const int* tokens, int P, float* logits_host, int* token);
 

@@ -165,6 +165,8 @@ _SIGS = {
     "kvc_qwen_tensor": (i32, [vp, C.c_char_p, i32, C.POINTER(vp), C.POINTER(sz)]),
     "kvc_qwen_serve": (i32, [vp, i32, vp, vp, vp, vp, C.POINTER(QwenStatsC)]),
     "kvc_qwen_prefill_logits": (i32, [vp, vp, i32, vp, vp]),
+    "kvc_qwen_load_weights": (i32, [vp, C.c_char_p]),
+    "kvc_qwen_save_weights": (i32, [vp, C.c_char_p]),
     "kvc_engine_destroy": (None, [vp]),
     "kvc_engine_reset": (i32, [vp]),
     "kvc_engine_add_request": (i32, [vp, i32, i32, f64]),

@@ -111,6 +111,22 @@ int kvc_qwen_serve(kvc_qwen* h, int n_req, const int* prompt_off, const int* pro
     });
 }
 
+int kvc_qwen_load_weights(kvc_qwen* h, const char* dir) {
+    if (!h || !dir) return kvc::set_error(KVC_ERR_ARG, "null argument");
+    return guard([&]() -> int {
+        h->m.load_weights(dir);
+        return KVC_OK;
+    });
+}
+
+int kvc_qwen_save_weights(kvc_qwen* h, const char* dir) {
+    if (!h || !dir) return kvc::set_error(KVC_ERR_ARG, "null argument");
+    return guard([&]() -> int {
+        h->m.save_weights(dir);
+        return KVC_OK;
+    });
+}
+
 int kvc_qwen_prefill_logits(kvc_qwen* h, const int* tokens, int P, float* logits_host, int* token) {
     if (!h || !tokens || P <= 0) return kvc::set_error(KVC_ERR_ARG, "bad argument");
     return guard([&]() -> int {

@@ -67,6 +67,13 @@ class QwenModel:
         check(lib().kvc_device_synchronize())
         return out
 
+    def load_weights(self, directory) -> None:
+        """Weights from the reference's dump format: manifest.tsv + weights.bin."""
+        check(lib().kvc_qwen_load_weights(self._h, str(directory).encode()))
+
+    def save_weights(self, directory) -> None:
+        check(lib().kvc_qwen_save_weights(self._h, str(directory).encode()))
+
     def prefill_logits(self, tokens) -> tuple[int, np.ndarray]:
         t = np.ascontiguousarray(np.asarray(tokens, np.int32))
         logits = np.empty(self.cfg.vocab, np.float32)

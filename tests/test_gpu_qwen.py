@@ -110,3 +110,56 @@ def test_config5_shape_prefill_and_generation():
         assert total_exact >= 0.9 * sum(gens)
     finally:
         m.close()
+
+
+def test_weights_round_trip_in_reference_format(tmp_path):
+    """save_weights writes the reference's dump format (manifest.tsv over weights.bin,
+    Hugging Face names, fp16 [out, in]); a model with other random weights that loads
+    it has the same tensors and generates the same tokens.  An lm_head.weight that
+    differs from the embedding is used untied; a missing or misshapen tensor is an
+    error."""
+    say("qwen: weights save / load")
+    from kvcache_amd import KvcError
+    kw = dict(layers=2, vocab=4096, num_blocks=512, max_batch=8, max_rows=256)
+    a, b = QwenModel(QwenConfig(seed=11, **kw)), QwenModel(QwenConfig(seed=99, **kw))
+    try:
+        a.save_weights(tmp_path)
+        lines = (tmp_path / "manifest.tsv").read_text().splitlines()
+        rows = [l.split("\t") for l in lines]
+        assert all(len(r) == 4 for r in rows) and rows[0][0] == "model.embed_tokens.weight"
+        assert rows[0][3] == "4096,896" and rows[-1][0] == "lm_head.weight"
+        assert "model.layers.1.self_attn.q_proj.bias" in [r[0] for r in rows]
+        ends = [int(r[1]) + int(r[2]) for r in rows]
+        assert ends[-1] == (tmp_path / "weights.bin").stat().st_size
+        assert not np.array_equal(b.tensor("wq", 1), a.tensor("wq", 1))
+        b.load_weights(tmp_path)
+        for n in ("embed", "norm"):
+            np.testing.assert_array_equal(b.tensor(n), a.tensor(n))
+        for l in range(2):
+            for n in NAMES:
+                np.testing.assert_array_equal(b.tensor(n, l), a.tensor(n, l))
+        rng = np.random.default_rng(4)
+        prompts = [rng.integers(0, 4096, n) for n in (9, 40, 17)]
+        oa, _ = a.serve(prompts, [6, 6, 6])
+        ob, _ = b.serve(prompts, [6, 6, 6])
+        for x, y in zip(oa, ob):
+            np.testing.assert_array_equal(x, y)
+        # an untied output matrix: zeros give zero logits and token 0
+        blob = bytearray((tmp_path / "weights.bin").read_bytes())
+        off, nb = int(rows[-1][1]), int(rows[-1][2])
+        blob[off:off + nb] = bytes(nb)
+        (tmp_path / "weights.bin").write_bytes(bytes(blob))
+        b.load_weights(tmp_path)
+        tok, lg = b.prefill_logits(prompts[0])
+        assert tok == 0 and not lg.any()
+        # errors
+        (tmp_path / "manifest.tsv").write_text("\n".join(l for l in lines if "layers.1.mlp.up_proj" not in l))
+        with pytest.raises(KvcError):
+            b.load_weights(tmp_path)
+        bad = [l.replace("\t896,896", "\t448,1792") if "o_proj" in l else l for l in lines]
+        (tmp_path / "manifest.tsv").write_text("\n".join(bad))
+        with pytest.raises(KvcError):
+            b.load_weights(tmp_path)
+    finally:
+        a.close()
+        b.close()
