@@ -283,7 +283,7 @@ def bench_prefill(steps, warmup):
     return res
 
 
-def bench_c5(n_req=64, gen=64, seed=5, graph=True):
+def bench_c5(n_req=64, gen=64, seed=5, graph=False):
     """Config 5: the Qwen2-shaped decoder (24 layers, hidden 896, 14q/2kv, D 64, SwiGLU 4864, vocab 151936,
     random N(0, 0.02) fp16 weights) serving n_req requests greedily with continuous batching at batch 32;
     prompts of 16..256 random tokens, gen tokens each.  Throughput on the host clock around the whole run
@@ -313,7 +313,7 @@ def lib_call(name, *args):
     return getattr(lib(), name)(*args)
 
 
-def bench_c4():
+def bench_c4(graph=False):
     """Config 4: 256 requests, width 32, 2048 MB pool, 24 layers of write + GQA decode
     per step (14q/2kv, D 64, fp16); continuous vs static, offline and Poisson 400/s."""
     from kvcache_amd import KVC_F16
@@ -325,16 +325,20 @@ def bench_c4():
                        n_layers=24, dtype=KVC_F16, kv_write=True, clock_mode=0)
     eng = Engine(cfg)
     import dataclasses
-    eng_g = Engine(dataclasses.replace(cfg, graph=True))  # the 24 launches of a step replayed as one HIP graph
+    # --graph: the 24 launches of a step also replayed as one HIP graph (measured equal to
+    # eager launches; off by default so the default command profiles cleanly)
+    eng_g = Engine(dataclasses.replace(cfg, graph=True)) if graph else None
     out = {"workload": "C4 256 requests, width 32, 2048 MB pool, 24 layers write+decode, 14q/2kv D64 fp16",
            "num_blocks": num_blocks}
     for name, trace in (("offline", Wl.baseline_trace(256, 0.0, 11)), ("poisson400", Wl.baseline_trace(256, 400.0, 11)),
                         ("ref_offline", Wl.ref_trace())):
         p, g, a = trace
         res = {}
-        for pol, fn in (("continuous", lambda: run_continuous(p, g, a, eng)),
-                        ("continuous_graph", lambda: run_continuous(p, g, a, eng_g)),
-                        ("static", lambda: run_static(p, g, a, eng, 32))):
+        pols = [("continuous", lambda: run_continuous(p, g, a, eng))]
+        if eng_g is not None:
+            pols.append(("continuous_graph", lambda: run_continuous(p, g, a, eng_g)))
+        pols.append(("static", lambda: run_static(p, g, a, eng, 32)))
+        for pol, fn in pols:
             st = fn()
             res[pol] = {"iters": st.iters, "tokens": st.tokens,
                         "tokens_per_s": round(st.tokens / (st.wall_us * 1e-6), 1) if st.wall_us else 0.0,
@@ -406,7 +410,8 @@ def main() -> int:
                     help="run only config 3 or config 4 and print its result (profiling)")
     ap.add_argument("--warm", action="store_true",
                     help="also time the planned path on one pool copy (Infinity-Cache resident)")
-    ap.add_argument("--no-graph", action="store_true", help="config 5: launch every decode step eagerly")
+    ap.add_argument("--graph", action="store_true",
+                    help="configs 4 and 5: replay each decode step as a captured HIP graph (default: eager launches)")
     ap.add_argument("--tune", action="append", default=[], metavar="KEY=VALUE",
                     help="set a library tuning knob (kvc_set_tuning), e.g. wg_per_cu=4")
     ap.add_argument("--fused", type=int, default=-1,
@@ -437,7 +442,7 @@ def main() -> int:
     if a.only:
         res = (bench_c3(a.steps, a.warmup, sweep_targets) if a.only == "c3" else
                bench_prefill(a.steps, a.warmup) if a.only == "prefill" else
-               bench_c5(graph=not a.no_graph) if a.only == "c5" else bench_c4())
+               bench_c5(graph=a.graph) if a.only == "c5" else bench_c4(graph=a.graph))
         print(json.dumps(res), flush=True)
         return 0
     if a.lengths == "reference":
@@ -511,12 +516,12 @@ def main() -> int:
         except Exception as e:  # noqa: BLE001
             extras["prefill"] = {"error": repr(e)}
         try:
-            extras["c5"] = bench_c5()
+            extras["c5"] = bench_c5(graph=a.graph)
             log(f"C5: {extras['c5']}")
         except Exception as e:  # noqa: BLE001
             extras["c5"] = {"error": repr(e)}
         try:
-            extras["c4"] = bench_c4()
+            extras["c4"] = bench_c4(graph=a.graph)
             log(f"C4: {json.dumps(extras['c4'])}")
         except Exception as e:  # noqa: BLE001
             extras["c4"] = {"error": repr(e)}
