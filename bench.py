@@ -308,6 +308,28 @@ def bench_c5(n_req=64, gen=64, seed=5, graph=False):
             "ms_per_decode_step": round(st["decode_us"] / 1e3 / max(st["steps"], 1), 3)}
 
 
+def memory_accounting(lens, H, D, B, lmax=2048):
+    """The memory report of bench_throughput.cu:73-80,135-139 for this batch: KV bytes
+    actually used, the paged pool (blocks + table ints) and the contiguous max-length
+    reservation, for the fp16 layout measured here and the reference's fp32 one (whose
+    numbers are the README's 325.0 / 328.7 / 1024 MB)."""
+    MB = 1048576.0
+    blocks = int(sum((int(x) + B - 1) // B for x in lens))
+    out = {"sequences": len(lens), "tokens": int(np.sum(lens)), "blocks": blocks, "lmax_reserved": lmax,
+           "table_bytes": blocks * 4}
+    for name, es in (("fp16", 2), ("fp32_reference_layout", 4)):
+        used = float(np.sum(lens)) * H * D * es * 2 / MB
+        paged = (blocks * H * B * D * es * 2 + blocks * 4) / MB
+        reserved = len(lens) * H * lmax * D * es * 2 / MB
+        budget = 4096 * MB
+        out[name] = {"used_mb": round(used, 1), "paged_mb": round(paged, 1), "contiguous_reserved_mb": round(reserved, 1),
+                     "contiguous_util_pct": round(100 * used / reserved, 1),
+                     "paged_overhead_pct": round(100 * (paged - used) / used, 2),
+                     "seqs_in_4096mb_contiguous": int(budget / (H * lmax * D * es * 2)),
+                     "seqs_in_4096mb_paged": int(budget / (((int(np.mean(lens)) + B - 1) // B) * H * B * D * es * 2))}
+    return out
+
+
 def lib_call(name, *args):
     from kvcache_amd._native import lib
     return getattr(lib(), name)(*args)
@@ -549,6 +571,7 @@ def main() -> int:
                      "algorithmic_bytes_per_launch": total, "kv_bytes_per_launch": kv,
                      "mean_launch_us": round(t_launch * 1e3, 3)},
         "warm_GBps": warm,
+        "memory": memory_accounting(lens, Hkv, D, B),
         "parity_max_abs_err": err,
         "cpu_baseline": cpu,
         "extras": extras,

@@ -203,3 +203,22 @@ def test_never_admissible_request_is_reported(orc):
     assert rc == 1
     rc, st, _ = orc.sim_static([50], [50], [0.0], 16, 5, 4)
     assert rc == 1 and st.finished == 0
+
+
+def test_bench_memory_report_matches_readme(orc):
+    """bench.py's memory report (bench_throughput.cu:73-80,135-139) gives the README's
+    numbers in the reference's fp32 layout for the config-2 batch."""
+    import sys
+    from pathlib import Path
+    sys.path.insert(0, str(Path(__file__).resolve().parent.parent))
+    import bench
+    m = bench.memory_accounting(orc.ref_lengths(128, 2048, 12345), 8, 64, 16)
+    r = m["fp32_reference_layout"]
+    assert m["blocks"] == 5259 and m["table_bytes"] == 5259 * 4
+    assert round(r["contiguous_reserved_mb"]) == pub("ragged_batch_reserved_mb_contiguous")
+    assert round(r["used_mb"]) == pub("ragged_batch_used_mb_contiguous")
+    assert round(r["paged_mb"]) == pub("ragged_batch_mb_paged")
+    assert r["contiguous_util_pct"] == pub("ragged_batch_util_pct_contiguous")
+    assert r["seqs_in_4096mb_contiguous"] == pub("budget_4096mb_max_seqs_contiguous")
+    assert r["seqs_in_4096mb_paged"] == pub("budget_4096mb_max_seqs_paged")
+    assert m["fp16"]["used_mb"] * 2 == pytest.approx(r["used_mb"], abs=0.1)
