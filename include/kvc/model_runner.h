@@ -91,7 +91,7 @@ struct ModelRunner {
     // graph replay: metadata at fixed places [N, units, records, 0 | wpos cap_n |
     // work cap_units*ipu | table cap_tab] in d_g, a pinned ring h_g of the same layout
     void* gexec = nullptr;
-    const KVCacheManager* g_kvm = nullptr;  // pools the graph was captured with
+    std::vector<const void*> g_pools;       // pools the graph was captured with (K and V of every layer)
     bool graph_failed = false;
     int* d_g = nullptr;
     int* h_g[kRing] = {};
@@ -308,8 +308,13 @@ struct ModelRunner {
     }
 
     // Captures the planned step (n_layers graph-safe launches) for these pools.
+    std::vector<const void*> pools_of(const KVCacheManager& kvm) const {
+        std::vector<const void*> p;
+        for (int l = 0; l < opt.n_layers; ++l) { p.push_back(kvm.k_layer(l)); p.push_back(kvm.v_layer(l)); }
+        return p;
+    }
     bool ensure_graph(const KVCacheManager& kvm) {
-        if (gexec && g_kvm == &kvm) return true;
+        if (gexec && g_pools == pools_of(kvm)) return true;
         if (graph_failed) return false;
         kvc_graph_destroy(gexec);
         gexec = nullptr;
@@ -349,7 +354,7 @@ struct ModelRunner {
             return false;
         }
         gexec = exec;
-        g_kvm = &kvm;
+        g_pools = pools_of(kvm);
         return true;
     }
 
