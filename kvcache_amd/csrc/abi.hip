@@ -72,7 +72,8 @@ constexpr int kMfmaMaxFusedChunks = 64;
 inline bool mfma_path(int group, int D, int dtype, int BLOCK, bool paged) {
     const int t = tuning().mfma;
     if (t == 0 || dtype != KVC_F16 || (D != 64 && D != 128) || group > 16 || group < (t == 1 ? 3 : 4)) return false;
-    return !paged || BLOCK % 16 == 0;
+    // paged: 16-token subtiles inside one block, block index and offset by shift and mask
+    return !paged || (BLOCK % 16 == 0 && (BLOCK & (BLOCK - 1)) == 0);
 }
 
 // Tokens covered by one wave-wide 16-byte load.
@@ -319,7 +320,7 @@ PlanShape plan_shape(int Hq, int Hkv, int D, int BLOCK, int dtype) {
         ps.wpb = (t == 4 || t == 8) ? t : 8;
         // a split costs the chunk tail a store, an arrival and a merge: below ~1024
         // tokens a sequence stays in one unit
-        ps.min_chunk = ((1024 + BLOCK - 1) / BLOCK) * BLOCK;
+        ps.min_chunk = ((tuning().mfma_min_chunk + BLOCK - 1) / BLOCK) * BLOCK;
         ps.max_chunk = kMfmaMaxChunkBlocksHost * BLOCK;
         ps.slots = 176;
         // the unit's first block ids travel in its entry: the kernel reads entry and
@@ -442,7 +443,9 @@ inline hipStream_t S(kvc_stream_t s) { return static_cast<hipStream_t>(s); }
 
 // ---- prompt attention on the matrix cores: 16 queries of one head per unit ----
 bool causal_tile_path(int Nq, int Hq, int Hkv, int D, int BLOCK, int dtype) {
-    if (tuning().mfma == 0 || dtype != KVC_F16 || (D != 64 && D != 128) || BLOCK <= 0 || BLOCK % 16) return false;
+    if (tuning().mfma == 0 || dtype != KVC_F16 || (D != 64 && D != 128) || BLOCK <= 0 || BLOCK % 16 ||
+        (BLOCK & (BLOCK - 1)))
+        return false;
     if (Hq <= 0 || Hkv <= 0 || Hq % Hkv) return false;
     return (long long)Nq * Hq * D * 2 < (1LL << 31);  // the q descriptor spans all queries
 }
@@ -932,6 +935,7 @@ int kvc_set_tuning(const char* key, int value) {
     else if (k == "mfma" && value >= -1 && value <= 1) tuning().mfma = value;
     else if (k == "wg_per_cu" && value >= -1 && value <= 32) tuning().wg_per_cu = value;
     else if (k == "split_first" && (value == 0 || value == 1)) tuning().split_first = value;
+    else if (k == "mfma_min_chunk" && value >= 16 && value <= 1 << 20) tuning().mfma_min_chunk = value;
     else return set_error(KVC_ERR_ARG, "unknown tuning key or bad value: " + k);
     return KVC_OK;
 }
@@ -948,6 +952,7 @@ int kvc_get_tuning(const char* key, int* value) {
     else if (k == "mfma") *value = tuning().mfma;
     else if (k == "wg_per_cu") *value = tuning().wg_per_cu;
     else if (k == "split_first") *value = tuning().split_first;
+    else if (k == "mfma_min_chunk") *value = tuning().mfma_min_chunk;
     else return set_error(KVC_ERR_ARG, "unknown tuning key: " + k);
     return KVC_OK;
 }

@@ -19,9 +19,9 @@
 //          16-dim column tile.  The A operand is the lane's own 8 probabilities
 //          (token order tau(g, i) = 4g+i for i < 4, 16+4g+i-4 otherwise); the B
 //          operand needs V transposed (8 tokens of one dim per lane), so each
-//          wave stages its 32-token V tile in LDS, row-major with the dword column
-//          XOR-swizzled by ((row >> 2) & 3) << 3, and reads it back with 16-bit
-//          loads: the four lane groups then hit disjoint banks.
+//          wave stages its 32-token V tile in LDS, row-major with 32-byte segments
+//          XOR-permuted by row, and reads it back with the transposing LDS read
+//          (two per 16-dim column tile).
 //
 // Unit decomposition, partial records, arrival counters and merge modes are those
 // of split_kernel (one unit = sequence x KV head x chunk, all query heads of the
@@ -38,6 +38,13 @@ constexpr int kMfmaMaxHeads = 16;         // query heads per KV head on this pat
 constexpr int kMaxFusedChunks = 64;       // chunks the fused merge combines (one per lane)
 
 typedef _Float16 f16x8v __attribute__((ext_vector_type(8)));
+typedef short s16x4v __attribute__((ext_vector_type(4)));
+
+// ds_read_b64_tr_b16 (gfx950) at an LDS address held in a generic pointer.
+__device__ __forceinline__ s16x4v ds_read_tr16(const char* p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s16x4v*)(__attribute__((address_space(3))) char*)(const_cast<char*>(p)));
+}
 
 template <int D, int MODE, int WPB>
 __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(DecodeParams p) {
@@ -117,7 +124,7 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(DecodeParams p) {
             vnew = *reinterpret_cast<const u32x4*>(vn + (lane * 16) % ROW);  // = bytes lane*16 for lane < ROW/16
             kst = *reinterpret_cast<const u32x4*>(kn + (lane * 16) % ROW);
             const int w = p.wpos[s];
-            wp = (w >= j0 && w < j1) ? w : -1;
+            wp = uniform((w >= j0 && w < j1) ? w : -1);
         }
     }
 
@@ -138,17 +145,26 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(DecodeParams p) {
             qb[j] = __builtin_bit_cast(f16x8v, buffer_load16(qr, n16 * ROW + g4 * 16 + j * 64));
     }
     const int qlast = CAUSAL ? p.fixed_len + q0 + n16 : INT_MAX;  // last key this column may see
+    // scores use |scale|: a negative scale negates q instead (exact in fp16)
+    const float sl2 = fabsf(p.scale_log2);
+    if (p.scale_log2 < 0.f) {
+#pragma unroll
+        for (int j = 0; j < KJ; ++j) qb[j] = -qb[j];
+    }
 
     const char* kb = static_cast<const char*>(p.k);
     const char* vb = static_cast<const char*>(p.v);
     size_t cbase = 0;
-    const int b0 = PAGED ? j0 / p.block : 0;
+    // paged: BLOCK is a power of two (host-checked), so block index and offset are
+    // a shift and a mask
+    const int bsh = PAGED ? __builtin_ctz((unsigned)p.block) : 0, bmask = p.block - 1;
+    const int b0 = PAGED ? j0 >> bsh : 0;
     int nblk = 0;
     bool inl = false;  // block ids from the entry (no table read, no LDS staging)
     if constexpr (MODE == kContiguous) {
         cbase = ((size_t)s * p.seq_stride + (size_t)hk * p.head_stride) * 2;
     } else {
-        nblk = min(j1 > j0 ? (j1 - 1) / p.block - b0 + 1 : 0, kMfmaMaxChunkBlocks);
+        nblk = min(j1 > j0 ? ((j1 - 1) >> bsh) - b0 + 1 : 0, kMfmaMaxChunkBlocks);
         inl = PLANNED && p.work_ints == kWave && u.n_inline >= nblk;
         if (!inl) {
             const int first = PLANNED ? u.tab_start : (p.tab_off ? p.tab_off[s] : 0) + b0;
@@ -160,14 +176,15 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(DecodeParams p) {
             __syncthreads();
         }
     }
-    // physical block of the chunk's rel-th block (rel uniform, < nblk)
+    // physical block of the chunk's rel-th block (rel uniform, < nblk), as a scalar
+    // from either source
     auto block_id = [&](int rel) -> int {
         if (inl) return __builtin_amdgcn_readlane(ev, 8 + min(rel, kWave - 9));
-        return s_tab[min(rel, kMfmaMaxChunkBlocks - 1)];
+        return uniform(s_tab[min(rel, kMfmaMaxChunkBlocks - 1)]);
     };
     if (PLANNED && wp >= 0 && u.sub == 0 && wave == 0 && lane < ROW / 16) {
-        const int phys = block_id(max(wp / p.block - b0, 0));
-        const size_t off = ((size_t)(phys * p.Hkv + hk) * p.block + wp % p.block) * ROW + lane * 16;
+        const int phys = block_id(max((wp >> bsh) - b0, 0));
+        const size_t off = ((size_t)(phys * p.Hkv + hk) * p.block + (wp & bmask)) * ROW + lane * 16;
         *reinterpret_cast<u32x4*>(const_cast<char*>(kb) + off) = kst;
         *reinterpret_cast<u32x4*>(const_cast<char*>(vb) + off) = vnew;
     }
@@ -176,14 +193,17 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(DecodeParams p) {
         u32x4 k[2][KJ];
         u32x4 v[2][VL];
     };
-    // Byte offset of the 16-row subtile starting at token t (inside one block).
+    // Byte offset of the 16-row subtile starting at token t (inside one block).  All
+    // of the tile addressing stays in scalar registers: a vector temporary here can
+    // land on a register whose load is still in flight and make the issue wait.
+    const unsigned blk_bytes = (unsigned)p.block * ROW;
     auto subtile = [&](int t) -> size_t {
         if constexpr (MODE == kContiguous) {
             return cbase + (size_t)t * ROW;
         } else {
-            const int rel = min(max(t / p.block - b0, 0), max(nblk - 1, 0));
-            const int phys = uniform(block_id(rel));
-            return ((size_t)(phys * p.Hkv + hk) * p.block + (t % p.block)) * ROW;
+            const int rel = min(max((t >> bsh) - b0, 0), max(nblk - 1, 0));
+            const unsigned slot = (unsigned)(block_id(rel) * p.Hkv + hk);
+            return (size_t)slot * blk_bytes + (unsigned)((t & bmask) * ROW);
         }
     };
     auto issue = [&](int k, Tile& T) {
@@ -191,10 +211,12 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(DecodeParams p) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const int t = t0 + 16 * h;
-            // valid rows, never past the end of the block holding the subtile
-            int rows = min(max(j1 - t, 0), 16);
-            if constexpr (PAGED) rows = min(rows, p.block - t % p.block);
-            rows = uniform(rows);
+            // valid rows, never past the end of the block holding the subtile (the
+            // empty asm keeps the clamp from turning into a vector med3)
+            int rows = max(j1 - t, 0);
+            asm("" : "+s"(rows));
+            rows = min(rows, 16);
+            if constexpr (PAGED) rows = min(rows, p.block - (t & bmask));
             const size_t off = rows > 0 ? subtile(t) : 0;
             const __amdgpu_buffer_rsrc_t kr = tile_rsrc(kb + off, rows * ROW);
             const __amdgpu_buffer_rsrc_t vr = tile_rsrc(vb + off, rows * ROW);
@@ -206,54 +228,62 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(DecodeParams p) {
     };
 
     char* vt = s_buf + wave * kTileBytes;   // this wave's V tile
+    // 32-byte segment of a V row in LDS: the sixteen rows one transposing read
+    // touches (4 g4 + r, same segment) spread over all banks
+    auto vseg = [](int r, int seg) { return seg ^ (D == 64 ? (r >> 1) & 3 : r & 7); };
     float m = -FLT_MAX, l = 0.f;            // per head n16 (identical in the four lane groups)
     f32x4 O[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) O[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    auto consume = [&](int k, const Tile& T) {
+    // FULL: every row of the tile is a valid key for every column and none is the
+    // step's new row, so the masks and the new-row selects drop out
+    auto consume = [&](int k, const Tile& T, auto full_tag) {
+        constexpr bool FULL = decltype(full_tag)::value;
         const int t0 = j0 + (wave + WPB * k) * kMfmaTile;
-        // V rows -> LDS, dword column swizzled by ((row >> 2) & 3) << 3
+        // V rows -> LDS, row-major with the row's 32-byte segments (16 dims each)
+        // permuted by vseg
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
             for (int q = 0; q < VL; ++q) {
                 const int off = q * 1024 + lane * 16;
                 const int r = 16 * h + off / ROW;
-                const int dw = ((off % ROW) >> 2) ^ (((r >> 2) & 3) << 3);
-                *reinterpret_cast<u32x4*>(vt + r * ROW + dw * 4) = t0 + r == wp ? vnew : T.v[h][q];
+                const int cb = off % ROW;
+                *reinterpret_cast<u32x4*>(vt + r * ROW + vseg(r, cb >> 5) * 32 + (cb & 31)) =
+                    !FULL && t0 + r == wp ? vnew : T.v[h][q];
             }
         // scores of the 32 tokens for all heads
         f32x4 S[2];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-            const bool nr = t0 + 16 * h + n16 == wp;   // this lane's K row is the new one
+            const bool nr = !FULL && t0 + 16 * h + n16 == wp;   // this lane's K row is the new one
 #pragma unroll
             for (int j = 0; j < KJ; ++j)
                 acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8v, nr ? knew[j] : T.k[h][j]), qb[j],
                                                              acc, 0, 0, 0);
             S[h] = acc;
         }
-        float sc[8];
+        // the scale is >= 0 here (q carries its sign), so the tile max is taken on
+        // the raw scores and each probability is one fma and one exp2
         bool ok[8];
         float mx = -FLT_MAX;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int h = i >> 2, r = i & 3;
-            ok[i] = t0 + 16 * h + 4 * g4 + r < j1 && t0 + 16 * h + 4 * g4 + r <= qlast;
-            sc[i] = S[h][r] * p.scale_log2;
-            mx = ok[i] ? fmaxf(mx, sc[i]) : mx;
+            ok[i] = FULL || (t0 + 16 * h + 4 * g4 + r < j1 && t0 + 16 * h + 4 * g4 + r <= qlast);
+            mx = ok[i] ? fmaxf(mx, S[h][r]) : mx;
         }
         mx = fmaxf(mx, shfl_xor(mx, 16));
         mx = fmaxf(mx, shfl_xor(mx, 32));
-        const float mn = fmaxf(m, mx);
+        const float mn = fmaxf(m, mx * sl2);
         const float corr = fast_exp2(m - mn);
         float ps = 0.f;
         f16x8v pa;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const float pi = ok[i] ? fast_exp2(sc[i] - mn) : 0.f;
+            const float pi = ok[i] ? fast_exp2(__builtin_fmaf(S[i >> 2][i & 3], sl2, -mn)) : 0.f;
             ps += pi;
             pa[i] = (_Float16)pi;
         }
@@ -269,33 +299,40 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(DecodeParams p) {
         }
         __builtin_amdgcn_wave_barrier();
         asm volatile("" ::: "memory");
-        // V^T operand: 8 tokens tau(g4, i) of dim n16 + 16 nt
-        const _Float16* vh = reinterpret_cast<const _Float16*>(vt);
+        // V^T operand: 8 tokens tau(g4, i) of dim n16 + 16 nt, by two transposing
+        // reads.  ds_read_b64_tr_b16 over a group of 16 lanes: lane i receives element
+        // i % 4 of the 8 bytes addressed by lane 4j + i/4, for j = 0..3.  Lane 4r + c
+        // of group g4 addresses dims 16 nt + 4c .. +3 of token 4 g4 + r (then of token
+        // 16 + 4 g4 + r), so lane n16 receives dim 16 nt + n16 of those four tokens.
+        const int vr0 = 4 * g4 + (n16 >> 2);
+        const int vcb = 8 * (n16 & 3);
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
-            f16x8v vbv;
-            const int dw = ((n16 + 16 * nt) >> 1) ^ (g4 << 3);
-            const int col = dw * 2 + (n16 & 1);   // in halfs
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int r = (i < 4) ? 4 * g4 + i : 16 + 4 * g4 + (i - 4);
-                vbv[i] = vh[r * D + col];
-            }
+            const s16x4v lo = ds_read_tr16(vt + vr0 * ROW + vseg(vr0, nt) * 32 + vcb);
+            const s16x4v hi = ds_read_tr16(vt + (vr0 + 16) * ROW + vseg(vr0 + 16, nt) * 32 + vcb);
+            const f16x8v vbv = __builtin_bit_cast(f16x8v, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
             O[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vbv, O[nt], 0, 0, 0);
         }
         __builtin_amdgcn_wave_barrier();
         asm volatile("" ::: "memory");
     };
 
+    auto step = [&](int k, const Tile& T) {
+        const int t0 = j0 + (wave + WPB * k) * kMfmaTile;
+        const bool full = t0 + kMfmaTile <= j1 && (!CAUSAL || t0 + kMfmaTile - 1 <= p.fixed_len + q0) &&
+                          (wp < t0 || wp >= t0 + kMfmaTile);
+        if (full) consume(k, T, std::true_type{});
+        else consume(k, T, std::false_type{});
+    };
     if (kmax > 0) {
         Tile A, B;
         issue(0, A);
         for (int k = 0;; k += 2) {
             issue(k + 1, B);
-            consume(k, A);
+            step(k, A);
             if (k + 1 >= kmax) break;
             issue(k + 2, A);
-            consume(k + 1, B);
+            step(k + 1, B);
             if (k + 2 >= kmax) break;
         }
     }

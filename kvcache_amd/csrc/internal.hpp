@@ -108,6 +108,7 @@ struct Tuning {
     int wg_per_cu = -1;         // >0: reserve LDS so at most this many decode workgroups share a CU;
                                 // 0: no cap; -1: automatic (4 on the planned one/two-head path)
     int split_first = 1;        // planner: chunks of split sequences before whole sequences
+    int mfma_min_chunk = 1024;  // planner, grouped-query path: tokens below which a sequence stays in one unit
 };
 // Dynamic LDS that caps decode workgroups per CU at wg_per_cu (0: none).
 size_t occupancy_lds(size_t static_lds, int wg_per_cu);

@@ -255,15 +255,30 @@ def test_c3_long_context_split_k(orc):
 
 
 # ---- planned path (host-known lengths; the serving scheduler's path) ----------------
-def run_planned(q, K, V, lens, Hkv, block, dtype, perm=None, target=0, workspace=None, inline=True):
+def run_planned(q, K, V, lens, Hkv, block, dtype, perm=None, target=0, workspace=None, inline=True, scale=None):
     N, Hq, D = q.shape
+    scale = float(1.0 / np.sqrt(D)) if scale is None else float(scale)
     kp, vp, table, tab_off = paged_layout(K, V, lens, block, perm)
     work, nu, nr = ops.decode_plan(lens, Hq, Hkv, D, block, tab_off=tab_off, table=table if inline else None,
                                    dtype=dtype, target_tokens=target)
     out = DeviceBuffer(q.nbytes)
     ops.launch_batched_paged_planned(dev(q), dev(kp), dev(vp), dev(table), len(table), out, N, Hq, Hkv, D, block,
-                                     float(1.0 / np.sqrt(D)), dev(work), nu, nr, dtype=dtype, workspace=workspace)
+                                     scale, dev(work), nu, nr, dtype=dtype, workspace=workspace)
     return host(out, q.dtype, q.shape).astype(np.float64)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("scale", [-0.2, 0.0, 0.5])
+def test_planned_grouped_scale_sign(orc, D, scale):
+    # the matrix-core kernel takes the tile max on raw scores and carries the sign of
+    # the scale in q; a zero scale gives the plain mean of V
+    say(f"planned grouped D={D} scale={scale}")
+    lens = np.array([1, 17, 300, 1000], np.int32)
+    N, Hq, Hkv, B = len(lens), 14, 2, 16
+    q, K, V = normal((N, Hq, D), 190, np.float16), normal((N, Hkv, 1000, D), 191, np.float16), normal((N, Hkv, 1000, D), 192, np.float16)
+    ref = orc.batched_contig(q, K, V, lens, float(scale))
+    got = run_planned(q, K, V, lens, Hkv, B, KVC_F16, perm=np.random.default_rng(11).permutation(200), scale=scale)
+    assert np.abs(got - ref).max() <= 2e-3
 
 
 @pytest.mark.parametrize("lengths", ["reference", "loguniform"])
@@ -345,9 +360,10 @@ def test_mfma_gqa_matches_valu_and_oracle(orc, Hq, Hkv, D):
     np.testing.assert_array_equal(pl, pn)
 
 
-@pytest.mark.parametrize("block", [8, 32, 64])
+@pytest.mark.parametrize("block", [8, 32, 48, 64])
 def test_mfma_block_sizes(orc, block):
-    # BLOCK 8 holds no whole 16-token subtile: the grouped path falls back to the VALU kernel
+    # BLOCK 8 holds no whole 16-token subtile and BLOCK 48 is no power of two: the
+    # grouped path falls back to the VALU kernel for both
     say(f"mfma block={block}")
     lens = np.array([3, 64, 100, 1000], np.int32)
     N, Hq, Hkv, D = len(lens), 14, 2, 64
