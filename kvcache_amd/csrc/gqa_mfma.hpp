@@ -59,7 +59,7 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(DecodeParams p) {
     // the heads of one query); query q attends to positions 0 .. fixed_len + q
     constexpr bool CAUSAL = MODE == kCausalTile;
     constexpr int kTileBytes = kMfmaTile * ROW;
-    constexpr int kMainBytes = WPB * kTileBytes;
+    constexpr int kMainBytes = 2 * WPB * kTileBytes;   // per wave: V tile, then K tile
     constexpr int kEpiBytes = WPB * kMfmaMaxHeads * (D + 2) * 4;
     __shared__ __attribute__((aligned(16))) char s_buf[kMainBytes > kEpiBytes ? kMainBytes : kEpiBytes];
     __shared__ int s_tab[PAGED ? kMfmaMaxChunkBlocks : 1];
@@ -112,16 +112,12 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(DecodeParams p) {
     // ahead of the table), and the unit of the first head subgroup stores the row
     // in the pool once the block ids are staged.
     int wp = -1;
-    u32x4 knew[KJ], vnew = {0, 0, 0, 0}, kst = {0, 0, 0, 0};
-#pragma unroll
-    for (int j = 0; j < KJ; ++j) knew[j] = u32x4{0, 0, 0, 0};
+    u32x4 vnew = {0, 0, 0, 0}, kst = {0, 0, 0, 0};  // bytes (lane*16) % ROW of the new V and K rows
     if constexpr (PLANNED) {
         if (p.wpos != nullptr) {
             const char* kn = static_cast<const char*>(p.k_new) + ((size_t)s * p.Hkv + hk) * ROW;
             const char* vn = static_cast<const char*>(p.v_new) + ((size_t)s * p.Hkv + hk) * ROW;
-#pragma unroll
-            for (int j = 0; j < KJ; ++j) knew[j] = *reinterpret_cast<const u32x4*>(kn + g4 * 16 + j * 64);
-            vnew = *reinterpret_cast<const u32x4*>(vn + (lane * 16) % ROW);  // = bytes lane*16 for lane < ROW/16
+            vnew = *reinterpret_cast<const u32x4*>(vn + (lane * 16) % ROW);
             kst = *reinterpret_cast<const u32x4*>(kn + (lane * 16) % ROW);
             const int w = p.wpos[s];
             wp = uniform((w >= j0 && w < j1) ? w : -1);
@@ -190,7 +186,7 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(DecodeParams p) {
     }
 
     struct Tile {
-        u32x4 k[2][KJ];
+        u32x4 k[2][VL];   // both: 1 KiB of whole rows per wave load
         u32x4 v[2][VL];
     };
     // Byte offset of the 16-row subtile starting at token t (inside one block).  All
@@ -221,16 +217,20 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(DecodeParams p) {
             const __amdgpu_buffer_rsrc_t kr = tile_rsrc(kb + off, rows * ROW);
             const __amdgpu_buffer_rsrc_t vr = tile_rsrc(vb + off, rows * ROW);
 #pragma unroll
-            for (int j = 0; j < KJ; ++j) T.k[h][j] = buffer_load16(kr, n16 * ROW + g4 * 16 + j * 64);
+            for (int q = 0; q < VL; ++q) T.k[h][q] = buffer_load16(kr, q * 1024 + lane * 16);
 #pragma unroll
             for (int q = 0; q < VL; ++q) T.v[h][q] = buffer_load16(vr, q * 1024 + lane * 16);
         }
     };
 
-    char* vt = s_buf + wave * kTileBytes;   // this wave's V tile
+    char* vt = s_buf + wave * kTileBytes;           // this wave's V tile
+    char* kt = s_buf + (WPB + wave) * kTileBytes;   // and K tile
     // 32-byte segment of a V row in LDS: the sixteen rows one transposing read
     // touches (4 g4 + r, same segment) spread over all banks
     auto vseg = [](int r, int seg) { return seg ^ (D == 64 ? (r >> 1) & 3 : r & 7); };
+    // 16-byte chunk of a K row in LDS: the sixteen rows one operand read touches
+    // (same chunk) spread over the banks
+    auto kchunk = [](int r, int c) { return c ^ (r & 7); };
     float m = -FLT_MAX, l = 0.f;            // per head n16 (identical in the four lane groups)
     f32x4 O[NT];
 #pragma unroll
@@ -252,17 +252,22 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(DecodeParams p) {
                 const int cb = off % ROW;
                 *reinterpret_cast<u32x4*>(vt + r * ROW + vseg(r, cb >> 5) * 32 + (cb & 31)) =
                     !FULL && t0 + r == wp ? vnew : T.v[h][q];
+                *reinterpret_cast<u32x4*>(kt + r * ROW + kchunk(r, cb >> 4) * 16) = !FULL && t0 + r == wp ? kst : T.k[h][q];
             }
-        // scores of the 32 tokens for all heads
+        __builtin_amdgcn_wave_barrier();
+        asm volatile("" ::: "memory");
+        // scores of the 32 tokens for all heads; A operand from the K tile: row
+        // 16h + n16, dims 8*g4 + 32j .. +7 (16-byte chunk g4 + 4j)
         f32x4 S[2];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-            const bool nr = !FULL && t0 + 16 * h + n16 == wp;   // this lane's K row is the new one
+            const int r = 16 * h + n16;
+            f16x8v ka[KJ];
 #pragma unroll
-            for (int j = 0; j < KJ; ++j)
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8v, nr ? knew[j] : T.k[h][j]), qb[j],
-                                                             acc, 0, 0, 0);
+            for (int j = 0; j < KJ; ++j) ka[j] = *reinterpret_cast<const f16x8v*>(kt + r * ROW + kchunk(r, g4 + 4 * j) * 16);
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < KJ; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[j], qb[j], acc, 0, 0, 0);
             S[h] = acc;
         }
         // the scale is >= 0 here (q carries its sign), so the tile max is taken on
