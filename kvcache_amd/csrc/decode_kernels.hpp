@@ -460,8 +460,13 @@ __global__ __launch_bounds__(WPB * kWave) void split_kernel(DecodeParams p) {
                 b.k[u] = kk;
                 b.v[u] = ok ? vv : u32x4{0, 0, 0, 0};
             } else {
-                // valid rows of this wave-load (kept scalar: the descriptor must live in SGPRs)
-                const int rows = uniform(min(max(j1 - t0, 0), TPW));
+                // valid rows of this wave-load, kept in scalar registers (the descriptor
+                // lives in SGPRs; the empty asm stops the clamp from becoming a vector
+                // med3, whose temporary could land on a register with a load in flight
+                // and make the issue wait)
+                int rows = max(j1 - t0, 0);
+                asm("" : "+s"(rows));
+                rows = min(rows, TPW);
                 size_t tile;
                 if constexpr (MODE == kContiguous) {
                     tile = cbase + (size_t)max(t0, 0) * ROW;

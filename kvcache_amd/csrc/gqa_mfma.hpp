@@ -8,9 +8,13 @@
 // group at once with v_mfma_f32_16x16x32_f16 (heads padded to 16):
 //
 //   QK^T : S[16 tok][16 heads] = K[16 tok][32 dims] x Q^T[32 dims][16 heads],
-//          D/32 MFMAs per 16-token subtile.  The A operand is the K rows exactly as
-//          loaded (lane l: row l%16, 16 contiguous bytes at dim 8*(l/16) + 32j);
-//          the B operand is q in the same lane layout (loaded once per unit).
+//          D/32 MFMAs per 16-token subtile.  The A operand (lane l: row l%16, 16
+//          bytes at dim 8*(l/16) + 32j) would read half of 16 cache lines per load
+//          instruction, which streams at about half the rate of whole lines when a
+//          launch occupies few CUs; so K is loaded like V, 1 KiB of whole rows per
+//          wave load, staged in LDS (16-byte chunks XOR-permuted by row & 7) and
+//          read back in the operand layout.  The B operand is q in that layout
+//          (loaded once per unit).
 //   softmax: the result layout gives lane l the scores of head l%16 for tokens
 //          4*(l/16)+r (r = 0..3) of each subtile, i.e. 8 scores per lane for a
 //          32-token tile; the tile max per head needs two lane exchanges (xor 16,
