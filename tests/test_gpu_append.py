@@ -93,13 +93,16 @@ def test_fill_normal_is_deterministic_and_normal():
 def test_fused_append_decode_equals_write_then_decode(orc, dtype, Hq, Hkv, block):
     """The step's write (qk_batched_write_kv) followed by the decode equals the fused
     launch bit for bit: the same outputs and the same pools afterwards; rows with
-    wpos = -1 or outside the attended length are not written."""
+    wpos = -1 or outside the attended length are not written.  Write positions at the
+    end of the context, inside it and at a tile's first row."""
     say(f"fused append+decode dtype={dtype} Hq={Hq} Hkv={Hkv} block={block}")
     D = 64
     nt = as_np(dtype)
     lens = np.array([1, 17, 300, 1200, 33, 0, 640, 2000], np.int32)
     wpos = lens - 1
     wpos[4] = -1                      # an idle slot: nothing written
+    wpos[3] = 517                     # inside the context: row 5 of a full 32-token tile
+    wpos[6] = 64                      # first row of a tile
     N = len(lens)
     nb = [(int(L) + block - 1) // block for L in lens]
     tab_off = np.concatenate([[0], np.cumsum(nb)]).astype(np.int32)
