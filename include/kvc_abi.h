@@ -63,7 +63,11 @@ int         kvc_device_count(int* count);
  * "mfma" (grouped-query heads on the matrix cores: -1 automatic, 0 off, 1 on),
  * "wg_per_cu" (cap on decode workgroups per CU through reserved LDS: -1
  * automatic, 0 none, n), "split_first" (planner: chunks of split sequences
- * before whole sequences). */
+ * before whole sequences), "mfma_min_chunk" (planner, grouped-query heads on the
+ * matrix cores: tokens below which a sequence stays in one unit, default 1024).
+ * The matrix-core path takes fp16 K/V, head_dim 64 or 128, 3..16 query heads per
+ * KV head and, paged, a power-of-two BLOCK >= 16; other shapes use the VALU
+ * kernels. */
 int         kvc_set_tuning(const char* key, int value);
 int         kvc_get_tuning(const char* key, int* value);
 
@@ -194,7 +198,7 @@ int kvc_decode_auto_split(int N, int Hq, int Hkv, int D, int BLOCK, int cap, int
  * runs kvc_batched_paged_decode_planned with the same shape and tables; every
  * block-id read is bounded by table_len (ints in table_all).  Partials of split
  * sequences are merged by the last chunk to finish, inside the same kernel.
- * A plan depends on the tuning knobs ("mfma", "waves_per_block"): plan and launch
+ * A plan depends on the tuning knobs ("mfma", "waves_per_block", "mfma_min_chunk"): plan and launch
  * under the same settings.  Units naming a sequence or KV head outside N / Hkv
  * are skipped. */
 int kvc_decode_plan_entry_ints(int Hq, int Hkv, int D, int BLOCK, int dtype);
