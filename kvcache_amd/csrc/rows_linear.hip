@@ -13,11 +13,15 @@
 //    gate/up tile pair, or one rotary pair of q/k half-heads); one workgroup of
 //    WAVES waves per (column group, K split);
 //  * each wave owns a range of 32-wide k steps and issues every load of its range
-//    at once (two weight tiles + the A rows per step, 16 bytes per lane with
-//    buffer loads whose descriptors bound the weight tile and the M valid rows, so
-//    the tail steps and the rows >= M read as zero with no branches), then runs the
-//    16x16x32 fp16 MFMAs: A lane l = row l%16, B lane l = W row l%16, both with the
-//    8 k values at 8*(l/16) of the step;
+//    at once (two weight tiles + the A rows, with buffer loads whose descriptors
+//    bound the weight tile and the M valid rows, so the tail steps and the rows >= M
+//    read as zero with no branches), then runs the 16x16x32 fp16 MFMAs: A lane l =
+//    row l%16, B lane l = W row l%16, both with the 8 k values at 8*(l/16) of the
+//    step.  That operand layout read straight from memory touches half of 16 cache
+//    lines per load instruction, which streams at about half the rate of whole
+//    lines when a launch occupies few CUs; so the loads read whole 128-byte lines
+//    (a step pair of 8 rows per instruction) and each wave transposes them through
+//    a 4 KiB LDS area, a step pair at a time, into the operand layout;
 //  * waves are summed through LDS; when K is split across workgroups, each writes
 //    its 32x32 partial and the last to arrive (agent-scope counter, reset by it)
 //    sums the partials in split order -- deterministic -- and runs the epilogue.
@@ -207,6 +211,9 @@ __global__ __launch_bounds__(WAVES * 64) void rows_kernel(RowsParams p) {
     __shared__ float s_red[2][WAVES][kRows][kCols + 1];
     __shared__ float s_ss[WAVES][kRows];
     __shared__ unsigned s_last;
+    // per wave: two 16-row x 128-byte blocks (a step pair of two A tiles or of the
+    // two weight tiles), 16-byte chunk c of row r at chunk c ^ (r & 7)
+    __shared__ __attribute__((aligned(16))) char s_stage[WAVES][2][16 * 128];
 
     const int lane = threadIdx.x & 63;
     const int wave = uniform(threadIdx.x >> 6);
@@ -218,25 +225,54 @@ __global__ __launch_bounds__(WAVES * 64) void rows_kernel(RowsParams p) {
     const int nsteps = max(0, min(S, ksteps - first));
     const int r16 = lane & 15, q4 = lane >> 4;
     const int kbytes = p.K * 2;
+    // whole-line loads: step pair pp, half h = rows 8h .. 8h+7 of a 16-row tile; lane l
+    // reads row 8h + l/8, 16-byte chunk l%8 of the 128 bytes at k step first + 2pp
+    // (chunks 0-3 belong to the pair's first step, 4-7 to its second)
+    constexpr int NP = (S + 1) / 2;
+    const int lrow = lane >> 3, lch = lane & 7;
+    auto pair_ofs = [&](int pp, int h, bool ok) {
+        return ok && 2 * pp + (lch >> 2) < nsteps ? (8 * h + lrow) * kbytes + (first + 2 * pp) * 64 + lch * 16 : kOob;
+    };
+    char(*stg)[16 * 128] = s_stage[wave];
+    auto swz = [](int r, int c) { return r * 128 + ((c ^ (r & 7)) << 4); };
+    // block b (0/1) of the wave's area <- the lane's two whole-line chunks
+    auto stage = [&](int b, u4 lo, u4 hi) {
+        *reinterpret_cast<u4*>(stg[b] + swz(lrow, lch)) = lo;
+        *reinterpret_cast<u4*>(stg[b] + swz(8 + lrow, lch)) = hi;
+    };
+    // operand fragment of step j (0/1) of the pair in block b: row r16, chunk 4j + q4
+    auto unstage = [&](int b, int j) { return *reinterpret_cast<const u4*>(stg[b] + swz(r16, 4 * j + q4)); };
+    auto lds_fence = []() {
+        __builtin_amdgcn_wave_barrier();
+        asm volatile("" ::: "memory");
+    };
 
-    // A fragments of this wave's k range (rows >= M and steps past K read as zero)
+    // A rows of this wave's k range (rows >= M and steps past K read as zero), loaded
+    // as whole lines
     const auto ar = rsrc(p.a, M * kbytes);
-    u4 af[S][MT];
+    u4 al[NP][MT][2];
     u4 nw[NORM ? S : 1];
 #pragma unroll
-    for (int i = 0; i < S; ++i) {
-        const int kofs = (first + i) * 64 + q4 * 16;  // byte offset of the lane's 8 k values
-        const bool in = i < nsteps;
+    for (int pp = 0; pp < NP; ++pp)
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
-            af[i][mt] = __builtin_amdgcn_raw_buffer_load_b128(ar, in ? (mt * 16 + r16) * kbytes + kofs : kOob, 0, 0);
-        if constexpr (NORM) nw[i] = __builtin_amdgcn_raw_buffer_load_b128(rsrc(p.norm_w, kbytes), in ? kofs : kOob, 0, 0);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int o = pair_ofs(pp, h, true);
+                al[pp][mt][h] = __builtin_amdgcn_raw_buffer_load_b128(ar, o == kOob ? kOob : mt * 16 * kbytes + o, 0, 0);
+            }
+    if constexpr (NORM) {
+#pragma unroll
+        for (int i = 0; i < S; ++i) {
+            const int kofs = (first + i) * 64 + q4 * 16;  // byte offset of the lane's 8 k values
+            nw[i] = __builtin_amdgcn_raw_buffer_load_b128(rsrc(p.norm_w, kbytes), i < nsteps ? kofs : kOob, 0, 0);
+        }
     }
     // Weight tiles of group g: two 16-row tiles, S steps each.  Always issued (a
     // group past the end reads zeros without touching memory), so the instruction
     // stream has no branches and the compiler's load counters stay exact: the waits
     // for one group leave the next group's loads in flight.
-    auto load_b = [&](u4 (&b)[S][2], EpiIn (&e)[kItems], int g, bool valid) {
+    auto load_b = [&](u4 (&b)[NP][2][2], EpiIn (&e)[kItems], int g, bool valid) {
 #pragma unroll
         for (int it = 0; it < kItems; ++it) {
             const int item = threadIdx.x + it * kThreads;
@@ -246,14 +282,30 @@ __global__ __launch_bounds__(WAVES * 64) void rows_kernel(RowsParams p) {
         for (int t = 0; t < 2; ++t) {
             const auto br = rsrc(p.w + (size_t)tile_row<EPI>(p, valid ? g : g0, t) * p.K, 16 * kbytes);
 #pragma unroll
-            for (int i = 0; i < S; ++i)
-                b[i][t] = __builtin_amdgcn_raw_buffer_load_b128(
-                    br, valid && i < nsteps ? r16 * kbytes + (first + i) * 64 + q4 * 16 : kOob, 0, 0);
+            for (int pp = 0; pp < NP; ++pp)
+#pragma unroll
+                for (int h = 0; h < 2; ++h) b[pp][t][h] = __builtin_amdgcn_raw_buffer_load_b128(br, pair_ofs(pp, h, valid), 0, 0);
         }
     };
-    u4 b0[S][2], b1[S][2];
+    u4 b0[NP][2][2], b1[NP][2][2];
     EpiIn e0[kItems], e1[kItems];
     load_b(b0, e0, g0, true);
+
+    // A into the operand layout, a step pair at a time through the wave's LDS area
+    u4 af[S][MT];
+#pragma unroll
+    for (int pp = 0; pp < NP; ++pp) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) stage(mt, al[pp][mt][0], al[pp][mt][1]);
+        lds_fence();
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            if (2 * pp + j < S) {
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) af[2 * pp + j][mt] = unstage(mt, j);
+            }
+        lds_fence();
+    }
 
     if constexpr (NORM) {
         // RMSNorm of the rows (qwen_kernels.cu:24-40): sum of squares over this wave's
@@ -293,22 +345,36 @@ __global__ __launch_bounds__(WAVES * 64) void rows_kernel(RowsParams p) {
     // One column group: MFMAs over this wave's k range, sum over the waves, epilogue.
     // `ok` false (a group past the end) runs the same code with every store dropped.
     // Returns false when this workgroup is not the last of a split group (it is done).
-    auto run_group = [&](const u4 (&b)[S][2], const EpiIn (&e)[kItems], int j, bool ok) -> bool {
+    auto run_group = [&](const u4 (&b)[NP][2][2], const EpiIn (&e)[kItems], int j, bool ok) -> bool {
         const int g = g0 + j;
         f4 acc[MT][2];
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
             for (int t = 0; t < 2; ++t) acc[mt][t] = f4{0.f, 0.f, 0.f, 0.f};
-        // (steps past this wave's range hold zeros: no guard, no branch)
+        // (steps past this wave's range hold zeros: no guard, no branch); the weight
+        // tiles go to the operand layout a step pair at a time through the LDS area
 #pragma unroll
-        for (int i = 0; i < S; ++i)
+        for (int pp = 0; pp < NP; ++pp) {
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
+            for (int t = 0; t < 2; ++t) stage(t, b[pp][t][0], b[pp][t][1]);
+            lds_fence();
 #pragma unroll
-                for (int t = 0; t < 2; ++t)
-                    acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(af[i][mt]), as_h8(b[i][t]), acc[mt][t],
-                                                                        0, 0, 0);
+            for (int jj = 0; jj < 2; ++jj)
+                if (2 * pp + jj < S) {
+                    const int i = 2 * pp + jj;
+                    u4 bw[2];
+#pragma unroll
+                    for (int t = 0; t < 2; ++t) bw[t] = unstage(t, jj);
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                        for (int t = 0; t < 2; ++t)
+                            acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(af[i][mt]), as_h8(bw[t]),
+                                                                                acc[mt][t], 0, 0, 0);
+                }
+            lds_fence();
+        }
         // C lane layout: rows 4*(l/16) + r of the 16-row tile, column l%16.
         float(*red)[kRows][kCols + 1] = s_red[j & 1];
 #pragma unroll
