@@ -510,9 +510,10 @@ Shape plan_shape(int groups, int K, bool norm) {
     const int ks = K / 32;
     Shape s{groups, 1, 4, 7, 1};
     int shape = g_tune_shape;
-    // automatic: 4x7 for many groups, 8x4 for few, 8x4 with K split past 32 steps
-    // (down_proj K 4864 at 32 rows: 8.7 us over 5 splits, vs 12.3 us for 4x4 over 10)
-    if (shape < 0) shape = ks <= 28 && groups >= 128 ? 0 : ks <= 32 ? 1 : 3;
+    // automatic: 4x7 for very many groups (lm_head, 4748 groups: 49 us vs 51 us at
+    // 8x4), 8x4 otherwise (gate|up at I 4864, 304 groups: 7.1 us vs 7.8 us at 4x7),
+    // 8x4 with K split past 32 steps (down_proj K 4864 at 32 rows: 5 splits)
+    if (shape < 0) shape = ks <= 28 && groups >= 1024 ? 0 : ks <= 32 ? 1 : 3;
     if (shape == 0 && ks > 28) shape = 1;
     if (shape == 1 && ks > 32) shape = 2;
     if (norm && shape >= 2) shape = 1;  // callers reject normalised K above 1024
