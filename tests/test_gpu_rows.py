@@ -50,6 +50,22 @@ def test_rows_linear_store(M_, norm):
     close(host(y, np.float16, (M_, N)), ref)
 
 
+@pytest.mark.parametrize("M_,K", [(3, 32), (32, 96), (17, 160), (32, 1024)])
+@pytest.mark.parametrize("norm", [False, True])
+def test_rows_linear_short_k(M_, K, norm):
+    # K of 1, 3, 5 and 32 k steps: the whole-line loads read k steps in pairs, so a
+    # wave whose range ends inside a pair masks the pair's second half
+    say(f"rows linear store M={M_} K={K} norm={norm}")
+    N = 64
+    x, nw = inputs(M_, K, 320 + K)
+    w = (0.1 * normal((N, K), 321)).astype(np.float16)
+    y = DeviceBuffer(M_ * N * 2)
+    ops.rows_linear(y, dev(x), dev(w), M_, N, K, norm_w=dev(nw) if norm else None, eps=EPS,
+                    workspace=workspace(N, K))
+    a = _r16(M.rmsnorm(x, nw, EPS)) if norm else x.astype(np.float32)
+    close(host(y, np.float16, (M_, N)), M.linear(a, w))
+
+
 @pytest.mark.parametrize("M_,K,splits", [(32, 896, -1), (7, 896, 1), (32, 4864, -1), (20, 4864, 7), (3, 4864, 40),
                                          (16, 4864, 5)])
 def test_rows_linear_residual_splits(M_, K, splits):
