@@ -29,9 +29,10 @@
 //
 // Unit decomposition, partial records, arrival counters and merge modes are those
 // of split_kernel (one unit = sequence x KV head x chunk, all query heads of the
-// group).  The chunk's block ids are staged in LDS, so chunks may span up to
-// kMfmaMaxChunkBlocks blocks; BLOCK must be a multiple of 16 (each 16-token
-// subtile lies inside one block and is read through one buffer descriptor whose
+// group).  The chunk's block ids come with a planned entry (up to 56, read with
+// it) or are staged in LDS, so chunks may span up to kMfmaMaxChunkBlocks blocks;
+// BLOCK must be a power of two >= 16 (each 16-token subtile lies inside one block,
+// located by a shift and a mask, and is read through one buffer descriptor whose
 // size admits only the valid rows).  The fused cross-chunk merge runs on every
 // thread of the last-arriving workgroup (weights per chunk in LDS, then each
 // thread accumulates one (head, dim) over the chunks with independent loads).
