@@ -58,6 +58,27 @@ __device__ __forceinline__ float shfl_xor(float x, int mask) {
     return __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, __float_as_int(x)));
 }
 
+// Lane exchanges across the 16-lane rows and the 32-lane halves in registers
+// (gfx950 v_permlane16_swap / v_permlane32_swap): swapping a value with itself
+// leaves x[l] in one result and x[l ^ 16] (x[l ^ 32]) in the other, so the pair
+// gives max / sum with that partner lane without an LDS round trip.
+__device__ __forceinline__ float max_xor16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Sum over each aligned group of LPT consecutive lanes, result in every lane.
 // quad_perm[1,0,3,2] / [2,3,0,1] give the 4-lane sum; row_half_mirror (lane i
 // reads 7-i) then adds the other quad of the 8-lane half row, row_mirror (lane i

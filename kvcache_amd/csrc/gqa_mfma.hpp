@@ -18,7 +18,10 @@
 //   softmax: the result layout gives lane l the scores of head l%16 for tokens
 //          4*(l/16)+r (r = 0..3) of each subtile, i.e. 8 scores per lane for a
 //          32-token tile; the tile max per head needs two lane exchanges (xor 16,
-//          xor 32); online (max, sum) per head in log2 units.
+//          xor 32, in registers with the permlane swaps); online (max, sum) per head
+//          in log2 units.  Each tile's P V goes into a fresh accumulator, folded into
+//          O with the rows' rescale factors afterwards, so the MFMAs do not wait for
+//          the factors' lane gather.
 //   PV   : O[16 heads][16 dims] += P[16 heads][32 tok] x V[32 tok][16 dims] per
 //          16-dim column tile.  The A operand is the lane's own 8 probabilities
 //          (token order tau(g, i) = 4g+i for i < 4, 16+4g+i-4 otherwise); the B
@@ -285,8 +288,7 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(DecodeParams p) {
             ok[i] = FULL || (t0 + 16 * h + 4 * g4 + r < j1 && t0 + 16 * h + 4 * g4 + r <= qlast);
             mx = ok[i] ? fmaxf(mx, S[h][r]) : mx;
         }
-        mx = fmaxf(mx, shfl_xor(mx, 16));
-        mx = fmaxf(mx, shfl_xor(mx, 32));
+        mx = max_xor32(max_xor16(mx));
         const float mn = fmaxf(m, mx * sl2);
         const float corr = fast_exp2(m - mn);
         float ps = 0.f;
@@ -299,14 +301,13 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(DecodeParams p) {
         }
         l = __builtin_fmaf(l, corr, ps);
         m = mn;
-        // rescale O: row 4*g4 + r of the output tile belongs to head 4*g4 + r,
-        // whose factor is held by lane 4*g4 + r
+        // rescale factors of the output rows: row 4*g4 + r belongs to head 4*g4 + r,
+        // whose factor is held by lane 4*g4 + r (applied after this tile's P V, which
+        // is computed into its own accumulator and so does not wait for them)
+        float cr[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const float cr = __int_as_float(__builtin_amdgcn_ds_bpermute((4 * g4 + r) << 2, __float_as_int(corr)));
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) O[nt][r] *= cr;
-        }
+        for (int r = 0; r < 4; ++r)
+            cr[r] = __int_as_float(__builtin_amdgcn_ds_bpermute((4 * g4 + r) << 2, __float_as_int(corr)));
         __builtin_amdgcn_wave_barrier();
         asm volatile("" ::: "memory");
         // V^T operand: 8 tokens tau(g4, i) of dim n16 + 16 nt, by two transposing
@@ -321,7 +322,9 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(DecodeParams p) {
             const s16x4v lo = ds_read_tr16(vt + vr0 * ROW + vseg(vr0, nt) * 32 + vcb);
             const s16x4v hi = ds_read_tr16(vt + (vr0 + 16) * ROW + vseg(vr0 + 16, nt) * 32 + vcb);
             const f16x8v vbv = __builtin_bit_cast(f16x8v, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-            O[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vbv, O[nt], 0, 0, 0);
+            const f32x4 pv = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vbv, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) O[nt][r] = __builtin_fmaf(O[nt][r], cr[r], pv[r]);
         }
         __builtin_amdgcn_wave_barrier();
         asm volatile("" ::: "memory");
@@ -346,8 +349,7 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(DecodeParams p) {
             if (k + 2 >= kmax) break;
         }
     }
-    l += shfl_xor(l, 16);
-    l += shfl_xor(l, 32);
+    l = sum_xor32(sum_xor16(l));
 
     // Combine the waves: per-wave (m, l) per head and O through LDS.
     __syncthreads();  // every wave is done with its V tile
