@@ -28,8 +28,12 @@ TESTS_CPP = ROOT / "tests" / "cpp"
 ARCH = os.environ.get("KVC_OFFLOAD_ARCH", "gfx950")
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 # -packed-fp32-ops: keep the compiler from emitting packed fp32 VALU ops.
+# kernarg preload: the first two kernel arguments arrive in scalar registers at wave
+# start (the decode kernels take their work list there, so the entry is read without
+# waiting for the parameter block); the compiler keeps a fallback that loads them.
 DEVICE_FLAGS = [f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",
-                "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+                "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+                "-mllvm", "-amdgpu-kernarg-preload-count=2"]
 HOST_FLAGS = ["-x", "c++", "-O2", "-std=c++17", "-fPIC", "-Wall"]
 
 

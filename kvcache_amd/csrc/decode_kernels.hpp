@@ -303,8 +303,19 @@ struct Unit {
     size_t rec0, cstride, ctr_idx;
 };
 
+// The 8-int header of this workgroup's planned entry.  The kernels take the work
+// list as their first, register-preloaded arguments and read the header before
+// anything else, so it is in flight alongside the fetch of the parameter block; the
+// grid never exceeds the entries allocated, so it is read before the device-count
+// check.
+__device__ __forceinline__ void read_header(const int* work, int work_ints, int (&h)[8]) {
+    const int* w = work + (size_t)blockIdx.x * work_ints;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) h[i] = w[i];
+}
+
 template <bool PLANNED>
-__device__ __forceinline__ bool load_unit(const DecodeParams& p, int heads, Unit& u) {
+__device__ __forceinline__ bool load_unit(const DecodeParams& p, const int (&h)[8], int heads, Unit& u) {
     if constexpr (PLANNED) {
         int N = p.N, n_records = p.n_records;
         if (p.dev_counts) {  // fixed-capacity grid: the step's counts come from device memory
@@ -312,23 +323,22 @@ __device__ __forceinline__ bool load_unit(const DecodeParams& p, int heads, Unit
             N = min(p.dev_counts[0], p.N);
             n_records = min(p.dev_counts[2], p.n_records);
         }
-        const int* w = p.work + (size_t)blockIdx.x * p.work_ints;
-        u.s = w[0];
-        const int hks = w[1] & 0xFFFF;
-        u.c = w[1] >> 16;
+        u.s = h[0];
+        const int hks = h[1] & 0xFFFF;
+        u.c = h[1] >> 16;
         u.hk = hks / p.nsub;
         u.sub = hks % p.nsub;
-        u.j0 = max(w[2], 0);
-        u.j1 = max(w[3], u.j0);
-        u.nc = max(w[4] & 0xFFFF, 1);
-        u.n_inline = (unsigned)w[4] >> 16;
-        u.rec0 = ((size_t)(w[5] > 0 ? w[5] : 0) + (size_t)u.c) * heads;
+        u.j0 = max(h[2], 0);
+        u.j1 = max(h[3], u.j0);
+        u.nc = max(h[4] & 0xFFFF, 1);
+        u.n_inline = (unsigned)h[4] >> 16;
+        u.rec0 = ((size_t)(h[5] > 0 ? h[5] : 0) + (size_t)u.c) * heads;
         u.cstride = heads;
-        u.ctr_idx = w[6] > 0 ? w[6] : 0;
-        u.tab_start = w[7];
+        u.ctr_idx = h[6] > 0 ? h[6] : 0;
+        u.tab_start = h[7];
         // a unit outside the launch's shape (a stale or foreign plan) is skipped
         if (u.s < 0 || u.s >= N || u.hk < 0 || u.hk >= p.Hkv || u.c < 0 || u.c >= u.nc) return false;
-        return u.nc == 1 || (w[5] >= 0 && (long long)w[5] + u.nc <= n_records && w[6] >= 0 && w[6] < n_records);
+        return u.nc == 1 || (h[5] >= 0 && (long long)h[5] + u.nc <= n_records && h[6] >= 0 && h[6] < n_records);
     } else {
         int unit = blockIdx.x;
         u.sub = unit % p.nsub;  unit /= p.nsub;
@@ -360,7 +370,7 @@ constexpr int kMaxChunkBlocks = 4096;
 // writes either the normalised output (single-chunk sequence) or the chunk
 // partial, optionally followed by the fused cross-chunk merge.
 template <typename T, int D, int G, int MODE, int WPB, int U>
-__global__ __launch_bounds__(WPB * kWave) void split_kernel(DecodeParams p) {
+__global__ __launch_bounds__(WPB * kWave) void split_kernel(const int* __restrict__ work, int work_ints, DecodeParams p) {
     using Tr = Traits<T>;
     constexpr int EPL = Tr::EPL;
     constexpr int LPT = D / EPL;      // lanes per K/V row
@@ -384,10 +394,12 @@ __global__ __launch_bounds__(WPB * kWave) void split_kernel(DecodeParams p) {
     // loads does not wait for the table
     int ev = 0;
     if constexpr (PLANNED && UNIFORM) {
-        if (p.work_ints > 8 && lane < p.work_ints) ev = p.work[(size_t)blockIdx.x * p.work_ints + lane];
+        if (work_ints > 8 && lane < work_ints) ev = work[(size_t)blockIdx.x * work_ints + lane];
     }
+    int hdr[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if constexpr (PLANNED) read_header(work, work_ints, hdr);
     Unit u;
-    if (!load_unit<PLANNED>(p, G, u)) return;
+    if (!load_unit<PLANNED>(p, hdr, G, u)) return;
     const int s = u.s, hk = u.hk, sub = u.sub, c = u.c, nc = u.nc, j0 = u.j0, j1 = u.j1;
     const int tab_start = u.tab_start;
     const int n_inl = u.n_inline;  // block ids carried by the planned entry
@@ -744,11 +756,11 @@ template <typename T, int D, int G, int WPB, int U>
 int launch_split_mode(DecodeLaunch L, dim3 grid, hipStream_t st) {
     const dim3 block(WPB * kWave);
     switch (L.mode) {
-        case kContiguous:   L.lds_pad = lds_pad(split_kernel<T, D, G, kContiguous, WPB, U>, L.wg_per_cu); hipLaunchKernelGGL((split_kernel<T, D, G, kContiguous, WPB, U>), grid, block, L.lds_pad, st, L.p); break;
-        case kPagedUniform: L.lds_pad = lds_pad(split_kernel<T, D, G, kPagedUniform, WPB, U>, L.wg_per_cu); hipLaunchKernelGGL((split_kernel<T, D, G, kPagedUniform, WPB, U>), grid, block, L.lds_pad, st, L.p); break;
-        case kPagedPerLane: L.lds_pad = lds_pad(split_kernel<T, D, G, kPagedPerLane, WPB, U>, L.wg_per_cu); hipLaunchKernelGGL((split_kernel<T, D, G, kPagedPerLane, WPB, U>), grid, block, L.lds_pad, st, L.p); break;
-        case kPlannedUniform: L.lds_pad = lds_pad(split_kernel<T, D, G, kPlannedUniform, WPB, U>, L.wg_per_cu); hipLaunchKernelGGL((split_kernel<T, D, G, kPlannedUniform, WPB, U>), grid, block, L.lds_pad, st, L.p); break;
-        case kPlannedPerLane: L.lds_pad = lds_pad(split_kernel<T, D, G, kPlannedPerLane, WPB, U>, L.wg_per_cu); hipLaunchKernelGGL((split_kernel<T, D, G, kPlannedPerLane, WPB, U>), grid, block, L.lds_pad, st, L.p); break;
+        case kContiguous:   L.lds_pad = lds_pad(split_kernel<T, D, G, kContiguous, WPB, U>, L.wg_per_cu); hipLaunchKernelGGL((split_kernel<T, D, G, kContiguous, WPB, U>), grid, block, L.lds_pad, st, L.p.work, L.p.work_ints, L.p); break;
+        case kPagedUniform: L.lds_pad = lds_pad(split_kernel<T, D, G, kPagedUniform, WPB, U>, L.wg_per_cu); hipLaunchKernelGGL((split_kernel<T, D, G, kPagedUniform, WPB, U>), grid, block, L.lds_pad, st, L.p.work, L.p.work_ints, L.p); break;
+        case kPagedPerLane: L.lds_pad = lds_pad(split_kernel<T, D, G, kPagedPerLane, WPB, U>, L.wg_per_cu); hipLaunchKernelGGL((split_kernel<T, D, G, kPagedPerLane, WPB, U>), grid, block, L.lds_pad, st, L.p.work, L.p.work_ints, L.p); break;
+        case kPlannedUniform: L.lds_pad = lds_pad(split_kernel<T, D, G, kPlannedUniform, WPB, U>, L.wg_per_cu); hipLaunchKernelGGL((split_kernel<T, D, G, kPlannedUniform, WPB, U>), grid, block, L.lds_pad, st, L.p.work, L.p.work_ints, L.p); break;
+        case kPlannedPerLane: L.lds_pad = lds_pad(split_kernel<T, D, G, kPlannedPerLane, WPB, U>, L.wg_per_cu); hipLaunchKernelGGL((split_kernel<T, D, G, kPlannedPerLane, WPB, U>), grid, block, L.lds_pad, st, L.p.work, L.p.work_ints, L.p); break;
         default: return set_error(KVC_ERR_ARG, "unknown decode mode");
     }
     return KVC_OK;
@@ -797,10 +809,10 @@ template <int D, int WPB>
 int launch_gqa_mode(DecodeLaunch L, dim3 grid, hipStream_t st) {
     const dim3 block(WPB * kWave);
     switch (L.mode) {
-        case kContiguous:     L.lds_pad = lds_pad(gqa_mfma_kernel<D, kContiguous, WPB>, L.wg_per_cu); hipLaunchKernelGGL((gqa_mfma_kernel<D, kContiguous, WPB>), grid, block, L.lds_pad, st, L.p); break;
-        case kPagedUniform:   L.lds_pad = lds_pad(gqa_mfma_kernel<D, kPagedUniform, WPB>, L.wg_per_cu); hipLaunchKernelGGL((gqa_mfma_kernel<D, kPagedUniform, WPB>), grid, block, L.lds_pad, st, L.p); break;
-        case kPlannedUniform: L.lds_pad = lds_pad(gqa_mfma_kernel<D, kPlannedUniform, WPB>, L.wg_per_cu); hipLaunchKernelGGL((gqa_mfma_kernel<D, kPlannedUniform, WPB>), grid, block, L.lds_pad, st, L.p); break;
-        case kCausalTile:     hipLaunchKernelGGL((gqa_mfma_kernel<D, kCausalTile, WPB>), grid, block, 0, st, L.p); break;
+        case kContiguous:     L.lds_pad = lds_pad(gqa_mfma_kernel<D, kContiguous, WPB>, L.wg_per_cu); hipLaunchKernelGGL((gqa_mfma_kernel<D, kContiguous, WPB>), grid, block, L.lds_pad, st, L.p.work, L.p.work_ints, L.p); break;
+        case kPagedUniform:   L.lds_pad = lds_pad(gqa_mfma_kernel<D, kPagedUniform, WPB>, L.wg_per_cu); hipLaunchKernelGGL((gqa_mfma_kernel<D, kPagedUniform, WPB>), grid, block, L.lds_pad, st, L.p.work, L.p.work_ints, L.p); break;
+        case kPlannedUniform: L.lds_pad = lds_pad(gqa_mfma_kernel<D, kPlannedUniform, WPB>, L.wg_per_cu); hipLaunchKernelGGL((gqa_mfma_kernel<D, kPlannedUniform, WPB>), grid, block, L.lds_pad, st, L.p.work, L.p.work_ints, L.p); break;
+        case kCausalTile:     hipLaunchKernelGGL((gqa_mfma_kernel<D, kCausalTile, WPB>), grid, block, 0, st, L.p.work, L.p.work_ints, L.p); break;
         default: return set_error(KVC_ERR_ARG, "matrix-core decode: unsupported addressing mode");
     }
     return KVC_OK;

@@ -55,7 +55,7 @@ __device__ __forceinline__ s16x4v ds_read_tr16(const char* p) {
 }
 
 template <int D, int MODE, int WPB>
-__global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(DecodeParams p) {
+__global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(const int* __restrict__ work, int work_ints, DecodeParams p) {
     static_assert(D == 64 || D == 128, "MFMA decode is built for head_dim 64 and 128");
     constexpr int ROW = D * 2;                 // bytes per fp16 K/V row
     constexpr int KJ = D / 32;                 // MFMA k-steps over the head dimension
@@ -77,17 +77,18 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(DecodeParams p) {
 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
+    // planned entries carry the unit's block ids after the 8-int header (one int per
+    // lane): entry and header are read first, from the preloaded arguments
+    int ev = 0;
+    int hdr[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if constexpr (PLANNED) {
+        if (work_ints == kWave) ev = work[(size_t)blockIdx.x * kWave + lane];
+        read_header(work, work_ints, hdr);
+    }
     const int wave = uniform(tid >> 6);
     const int n16 = lane & 15;   // head (S layout) / output column within a tile
     const int g4 = lane >> 4;    // lane group
     const int heads = p.group;   // query heads of the KV group, <= 16 (host-checked)
-
-    // planned entries may carry the unit's block ids after the 8-int header: one
-    // int per lane, read together with the header
-    int ev = 0;
-    if constexpr (PLANNED) {
-        if (p.work_ints == kWave) ev = p.work[(size_t)blockIdx.x * kWave + lane];
-    }
     Unit u;
     int qh = 0, q0 = 0;  // causal: query head and first query of the tile
     if constexpr (CAUSAL) {
@@ -107,7 +108,7 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(DecodeParams p) {
         u.nc = (lmax + p.chunk_tokens - 1) / p.chunk_tokens;  // chunks of the tile's last query
         u.rec0 = 0; u.cstride = 0; u.ctr_idx = 0;
     } else {
-        if (!load_unit<PLANNED>(p, heads, u)) return;
+        if (!load_unit<PLANNED>(p, hdr, heads, u)) return;
     }
     const int s = u.s, hk = u.hk, j0 = u.j0, j1 = u.j1, nc = u.nc;
     const int hq0 = hk * p.group;
