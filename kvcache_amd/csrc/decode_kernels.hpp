@@ -655,71 +655,92 @@ __global__ __launch_bounds__(WPB * kWave) void split_kernel(const int* __restric
 }
 
 // Standalone log-sum-exp merge: one 512-thread workgroup per (sequence, query
-// head).  All chunk maxima are loaded at once and reduced; then MG = 512/D chunk
-// groups x D dims accumulate 2^(m_c-M) * (acc_c, l_c) with independent loads
-// (unrolled), and the groups are summed through LDS.  Sequences with a single
-// chunk were finished by the split kernel and exit at once.
+// head); MG = 512/D chunk groups x D dims.  The sequence's length and the first
+// kMergeBatch records of every chunk group are loaded in ONE round: the record
+// loads run ahead of the chunk count (indices clamped below max_chunks, inside
+// the workspace) and records at or past the count are dropped by selects, so
+// stale workspace contents never reach the sum.  Each thread reduces its records
+// with its own maximum, later batches (more than kMergeBatch * MG chunks) are
+// folded in with a rescale, and the groups combine through LDS:
+//   M = max_g M_g,  out = sum_g 2^(M_g-M) acc_g / sum_g 2^(M_g-M) l_g.
+// Sequences with a single chunk were finished by the split kernel.
 constexpr int kMergeThreads = 512;
+constexpr int kMergeBatch = 8;
 
 template <typename T, int D>
 __global__ __launch_bounds__(kMergeThreads) void merge_kernel(DecodeParams p) {
     constexpr int MG = kMergeThreads / D;  // chunk groups
-    __shared__ float s_red[kMergeThreads / kWave];
     __shared__ float s_acc[MG][D];
-    __shared__ float s_l[MG];
+    __shared__ float s_ml[MG][2];
     const int t = threadIdx.x;
-    const int lane = t & (kWave - 1), wave = t >> 6;
     const int s = blockIdx.x / p.Hq, hq = blockIdx.x % p.Hq;
+    const int cg = t / D, d = t % D;
+    const size_t rec0 = (size_t)s * p.max_chunks * p.Hq + hq;
+    const size_t cstride = (size_t)p.Hq;  // records between consecutive chunks
+    const int cmax = p.max_chunks;
+
+    float mm[kMergeBatch], ll[kMergeBatch], aa[kMergeBatch];
+#pragma unroll
+    for (int u = 0; u < kMergeBatch; ++u) {  // unconditional loads: no branch waits between them
+        const size_t rec = rec0 + (size_t)min(cg + u * MG, cmax - 1) * cstride;
+        const float2 ml = *reinterpret_cast<const float2*>(p.part_ml + rec * 2);
+        mm[u] = ml.x; ll[u] = ml.y;
+        aa[u] = p.part_acc[rec * D + d];
+    }
     int nc, j0, j1;
     chunk_range(p, s, 0, nc, j0, j1);
     if (nc <= 1) return;
-    const size_t rec0 = (size_t)s * p.max_chunks * p.Hq + hq;
-    const size_t cstride = (size_t)p.Hq;  // records between consecutive chunks
 
-    float mx = -FLT_MAX;
-    for (int c = t; c < nc; c += kMergeThreads) mx = fmaxf(mx, p.part_ml[(rec0 + c * cstride) * 2]);
+    float M = -FLT_MAX;
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, shfl_xor(mx, o));
-    if (lane == 0) s_red[wave] = mx;
-    __syncthreads();
-    float M = s_red[0];
-#pragma unroll
-    for (int w = 1; w < kMergeThreads / kWave; ++w) M = fmaxf(M, s_red[w]);
-
-    const int cg = t / D, d = t % D;
+    for (int u = 0; u < kMergeBatch; ++u) M = cg + u * MG < nc ? fmaxf(M, mm[u]) : M;
     float at = 0.f, lt = 0.f;
-    int c = cg;
-    for (; c + 3 * MG < nc; c += 4 * MG) {
-        float w4[4], a4[4], l4[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const size_t rec = rec0 + (size_t)(c + u * MG) * cstride;
-            w4[u] = p.part_ml[rec * 2];
-            l4[u] = p.part_ml[rec * 2 + 1];
-            a4[u] = p.part_acc[rec * D + d];
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const float w = fast_exp2(w4[u] - M);
-            lt = __builtin_fmaf(w, l4[u], lt);
-            at = __builtin_fmaf(w, a4[u], at);
-        }
+    for (int u = 0; u < kMergeBatch; ++u) {
+        const bool ok = cg + u * MG < nc;
+        const float w = fast_exp2(mm[u] - M);
+        lt = ok ? __builtin_fmaf(w, ll[u], lt) : lt;
+        at = ok ? __builtin_fmaf(w, aa[u], at) : at;
     }
-    for (; c < nc; c += MG) {
-        const size_t rec = rec0 + (size_t)c * cstride;
-        const float w = fast_exp2(p.part_ml[rec * 2] - M);
-        lt = __builtin_fmaf(w, p.part_ml[rec * 2 + 1], lt);
-        at = __builtin_fmaf(w, p.part_acc[rec * D + d], at);
+    for (int c0 = kMergeBatch * MG; c0 < nc; c0 += kMergeBatch * MG) {
+#pragma unroll
+        for (int u = 0; u < kMergeBatch; ++u) {
+            const size_t rec = rec0 + (size_t)min(c0 + cg + u * MG, nc - 1) * cstride;
+            const float2 ml = *reinterpret_cast<const float2*>(p.part_ml + rec * 2);
+            mm[u] = ml.x; ll[u] = ml.y;
+            aa[u] = p.part_acc[rec * D + d];
+        }
+        float Mb = M;
+#pragma unroll
+        for (int u = 0; u < kMergeBatch; ++u) Mb = c0 + cg + u * MG < nc ? fmaxf(Mb, mm[u]) : Mb;
+        const float r = fast_exp2(M - Mb);
+        at *= r;
+        lt *= r;
+#pragma unroll
+        for (int u = 0; u < kMergeBatch; ++u) {
+            const bool ok = c0 + cg + u * MG < nc;
+            const float w = fast_exp2(mm[u] - Mb);
+            lt = ok ? __builtin_fmaf(w, ll[u], lt) : lt;
+            at = ok ? __builtin_fmaf(w, aa[u], at) : at;
+        }
+        M = Mb;
     }
     s_acc[cg][d] = at;
-    if (d == 0) s_l[cg] = lt;
+    if (d == 0) {
+        s_ml[cg][0] = M;
+        s_ml[cg][1] = lt;
+    }
     __syncthreads();
     if (t < D) {
+        float Mx = s_ml[0][0];
+#pragma unroll
+        for (int g = 1; g < MG; ++g) Mx = fmaxf(Mx, s_ml[g][0]);
         float a = 0.f, l = 0.f;
 #pragma unroll
         for (int g = 0; g < MG; ++g) {
-            a += s_acc[g][t];
-            l += s_l[g];
+            const float w = fast_exp2(s_ml[g][0] - Mx);
+            a = __builtin_fmaf(w, s_acc[g][t], a);
+            l = __builtin_fmaf(w, s_ml[g][1], l);
         }
         static_cast<T*>(p.out)[((size_t)s * p.Hq + hq) * D + t] = (T)(l > 0.f ? a * (1.0f / l) : 0.f);
     }
