@@ -146,22 +146,31 @@ __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirs
 
 // Length and chunk range of unit chunk c of sequence s.  Returns false when the
 // unit has no chunk (beyond the sequence's chunk count).
-__device__ __forceinline__ bool chunk_range(const DecodeParams& p, int s, int c, int& nc, int& j0, int& j1) {
-    int L = p.cur_len ? p.cur_len[s] : (p.causal ? p.fixed_len + s + 1 : p.fixed_len);
+// Attended length of sequence s (device lengths, or the fixed/causal length).
+__device__ __forceinline__ int seq_len(const DecodeParams& p, int s) {
+    return p.cur_len ? p.cur_len[s] : (p.causal ? p.fixed_len + s + 1 : p.fixed_len);
+}
+
+// Chunk c of a sequence of L tokens.
+__device__ __forceinline__ bool chunk_range_of(const DecodeParams& p, int L, int c, int& nc, int& j0, int& j1) {
     L = min(max(L, 0), p.cap);  // a length above the stated cap never reads past the caches
     if (p.num_splits > 0) {
         nc = p.num_splits;
         const int ch = (L + nc - 1) / nc;
         j0 = min(c * ch, L);
         j1 = min(j0 + ch, L);
-        return c < nc;
+        return (unsigned)c < (unsigned)nc;  // c in [0, nc)
     }
     const int ch = p.chunk_tokens;
     L = min(L, ch * p.max_chunks);  // lengths beyond cap stay inside grid and workspace
     nc = max(1, (L + ch - 1) / ch);
     j0 = c * ch;
     j1 = min(j0 + ch, L);
-    return c < nc;
+    return (unsigned)c < (unsigned)nc;  // c in [0, nc)
+}
+
+__device__ __forceinline__ bool chunk_range(const DecodeParams& p, int s, int c, int& nc, int& j0, int& j1) {
+    return chunk_range_of(p, seq_len(p, s), c, nc, j0, j1);
 }
 
 // Log-sum-exp merge of the nc chunk partials of one query head: chunk c's
@@ -314,7 +323,27 @@ __device__ __forceinline__ void read_header(const int* work, int work_ints, int 
     for (int i = 0; i < 8; ++i) h[i] = w[i];
 }
 
-template <bool PLANNED>
+// Device-length decomposition: the length and table offset of this workgroup's
+// sequence, read at kernel entry (h[0], h[1]) so both are in flight together
+// with the rest of the parameter block.  Branch-free: s < N for every workgroup
+// of the grid, and a missing array is a zero-size descriptor that reads 0.
+template <bool PAGED>
+__device__ __forceinline__ void read_seq(const DecodeParams& p, int (&h)[8]) {
+    // the scalars load_unit needs come with the first fetch of the parameter block
+    // (left to itself the compiler fetches them in a second round, after this one)
+    asm volatile("" ::"s"(p.max_chunks), "s"(p.fixed_len), "s"(p.causal), "s"(p.cap), "s"(p.last_chunk_first));
+    const int s = (int)(blockIdx.x / (unsigned)(p.nsub * p.Hkv)) % p.N;
+    h[0] = (int)__builtin_amdgcn_raw_buffer_load_b32(tile_rsrc(p.cur_len, p.cur_len ? p.N * 4 : 0), s * 4, 0, 0);
+    h[1] = (int)__builtin_amdgcn_raw_buffer_load_b32(tile_rsrc(p.tab_off, PAGED && p.tab_off ? p.N * 4 : 0),
+                                                     s * 4, 0, 0);
+    // keep the scheduler from sinking the loads below work that waits for the
+    // rest of the parameter block
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// h: the planned entry's header, or read_seq's values for the device-length
+// decomposition.
+template <bool PLANNED, bool PAGED = true>
 __device__ __forceinline__ bool load_unit(const DecodeParams& p, const int (&h)[8], int heads, Unit& u) {
     if constexpr (PLANNED) {
         int N = p.N, n_records = p.n_records;
@@ -345,9 +374,12 @@ __device__ __forceinline__ bool load_unit(const DecodeParams& p, const int (&h)[
         u.hk = unit % p.Hkv;    unit /= p.Hkv;
         u.s = unit % p.N;
         u.c = p.last_chunk_first ? p.max_chunks - 1 - unit / p.N : unit / p.N;
-        u.tab_start = 0;
-        if (u.c >= p.max_chunks) return false;
-        if (!chunk_range(p, u.s, u.c, u.nc, u.j0, u.j1)) return false;
+        // length and table offset: read_seq (c >= max_chunks needs no test of its
+        // own: nc <= max_chunks, so chunk_range_of rejects it)
+        const int lu = uniform(h[0]);
+        const int L = p.cur_len ? lu : (p.causal ? p.fixed_len + u.s + 1 : p.fixed_len);
+        u.tab_start = uniform(h[1]);
+        if (!chunk_range_of(p, L, u.c, u.nc, u.j0, u.j1)) return false;
         u.rec0 = ((size_t)u.s * p.max_chunks + u.c) * p.Hq + u.hk * p.group + u.sub * heads;
         u.cstride = p.Hq;
         u.ctr_idx = ((size_t)u.s * p.Hkv + u.hk) * p.nsub + u.sub;
@@ -398,8 +430,9 @@ __global__ __launch_bounds__(WPB * kWave) void split_kernel(const int* __restric
     }
     int hdr[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     if constexpr (PLANNED) read_header(work, work_ints, hdr);
+    else read_seq<MODE != kContiguous>(p, hdr);
     Unit u;
-    if (!load_unit<PLANNED>(p, hdr, G, u)) return;
+    if (!load_unit<PLANNED, MODE != kContiguous>(p, hdr, G, u)) return;
     const int s = u.s, hk = u.hk, sub = u.sub, c = u.c, nc = u.nc, j0 = u.j0, j1 = u.j1;
     const int tab_start = u.tab_start;
     const int n_inl = u.n_inline;  // block ids carried by the planned entry
@@ -450,7 +483,7 @@ __global__ __launch_bounds__(WPB * kWave) void split_kernel(const int* __restric
         // The block ids are read through a descriptor: on the planned path the
         // descriptor spans table_all (table_len ints), so any plan reads inside it;
         // otherwise it spans this chunk's nblk entries.
-        const int first = PLANNED ? tab_start : (p.tab_off ? p.tab_off[s] : 0) + b0;
+        const int first = tab_start + (PLANNED ? 0 : b0);
         const __amdgpu_buffer_rsrc_t trs =
             PLANNED ? tile_rsrc(p.table_all, p.table_len * 4) : tile_rsrc(p.table_all + first, nblk * 4);
         const int tb = PLANNED ? first * 4 : 0;  // byte offset of the chunk's first entry

@@ -84,6 +84,8 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(const int* __rest
     if constexpr (PLANNED) {
         if (work_ints == kWave) ev = work[(size_t)blockIdx.x * kWave + lane];
         read_header(work, work_ints, hdr);
+    } else if constexpr (!CAUSAL) {
+        read_seq<PAGED>(p, hdr);
     }
     const int wave = uniform(tid >> 6);
     const int n16 = lane & 15;   // head (S layout) / output column within a tile
@@ -100,7 +102,7 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(const int* __rest
         u.s = 0;
         u.sub = 0;
         u.hk = qh / p.group;
-        u.tab_start = 0;
+        u.tab_start = PAGED && p.tab_off ? p.tab_off[0] : 0;
         const int lmax = min(p.fixed_len + min(q0 + 16, p.N), p.cap);  // keys of the tile's last query
         u.j0 = u.c * p.chunk_tokens;
         u.j1 = min(u.j0 + p.chunk_tokens, lmax);
@@ -108,7 +110,7 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(const int* __rest
         u.nc = (lmax + p.chunk_tokens - 1) / p.chunk_tokens;  // chunks of the tile's last query
         u.rec0 = 0; u.cstride = 0; u.ctr_idx = 0;
     } else {
-        if (!load_unit<PLANNED>(p, hdr, heads, u)) return;
+        if (!load_unit<PLANNED, PAGED>(p, hdr, heads, u)) return;
     }
     const int s = u.s, hk = u.hk, j0 = u.j0, j1 = u.j1, nc = u.nc;
     const int hq0 = hk * p.group;
@@ -172,7 +174,7 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(const int* __rest
         nblk = min(j1 > j0 ? ((j1 - 1) >> bsh) - b0 + 1 : 0, kMfmaMaxChunkBlocks);
         inl = PLANNED && p.work_ints == kWave && u.n_inline >= nblk;
         if (!inl) {
-            const int first = PLANNED ? u.tab_start : (p.tab_off ? p.tab_off[s] : 0) + b0;
+            const int first = u.tab_start + (PLANNED ? 0 : b0);
             const __amdgpu_buffer_rsrc_t trs =
                 PLANNED ? tile_rsrc(p.table_all, p.table_len * 4) : tile_rsrc(p.table_all + first, nblk * 4);
             const int tb = PLANNED ? first * 4 : 0;

@@ -25,18 +25,8 @@ enum DecodeMode { kContiguous = 0, kPagedUniform = 1, kPagedPerLane = 2, kPlanne
                   kCausalTile = 5 };
 
 struct DecodeParams {
-    const void* q;
-    const void* k;
-    const void* v;
-    void* out;
-    const int* table_all;     // paged only
-    const int* tab_off;       // paged only (nullptr: single table starting at table_all)
-    const int* cur_len;       // device lengths (nullptr: use fixed_len)
-    float* part_acc;          // [N*max_chunks*Hq, D] fp32 partial accumulators
-    float* part_ml;           // [N*max_chunks*Hq, 2] (running max in log2 units, running sum)
-    unsigned long long* counters;  // [N*Hkv*nsub] arrival counters (fused merge), or nullptr
-    long long seq_stride;     // contiguous: elements between sequences
-    long long head_stride;    // contiguous: elements between KV heads
+    // scalars first: everything a workgroup needs to locate its unit lies in the
+    // first lines of the parameter block, fetched in one round at wave start
     int N, Hq, Hkv, block;
     int group;                // Hq / Hkv
     int nsub;                 // query-head subgroups per KV head (group / G)
@@ -51,6 +41,18 @@ struct DecodeParams {
     unsigned epoch;           // per-call tag of the arrival counters
     int merge_mode;           // MergeMode
     int last_chunk_first;     // 1: dispatch the highest chunk index first
+    const void* q;
+    const void* k;
+    const void* v;
+    void* out;
+    const int* table_all;     // paged only
+    const int* tab_off;       // paged only (nullptr: single table starting at table_all)
+    const int* cur_len;       // device lengths (nullptr: use fixed_len)
+    float* part_acc;          // [N*max_chunks*Hq, D] fp32 partial accumulators
+    float* part_ml;           // [N*max_chunks*Hq, 2] (running max in log2 units, running sum)
+    unsigned long long* counters;  // [N*Hkv*nsub] arrival counters (fused merge), or nullptr
+    long long seq_stride;     // contiguous: elements between sequences
+    long long head_stride;    // contiguous: elements between KV heads
     const int* work;          // planned units (work_ints ints each, see kvc_decode_plan), or nullptr
     int work_ints;            // planned: ints per unit (8, or 64 with inline block ids)
     int table_len;            // planned: ints in table_all (bounds every block-id read)
