@@ -236,6 +236,28 @@ def test_caller_workspace_reuse_and_errors(orc):
     assert e.value.status == KVC_ERR_WORKSPACE
 
 
+@pytest.mark.parametrize("D,dtype,Hq,Hkv,split", [(32, KVC_F32, 8, 2, 16), (64, KVC_F32, 8, 8, 16),
+                                                   (128, KVC_F32, 4, 2, 16), (256, KVC_F32, 2, 2, 16),
+                                                   (64, KVC_F16, 14, 2, 32), (128, KVC_F16, 14, 2, 32)])
+def test_merge_kernel_chunk_batches_dirty_workspace(orc, D, dtype, Hq, Hkv, split):
+    # The merge kernel reads 8 records per chunk group (512/D groups) ahead of the chunk
+    # count, then folds later batches in with a rescale: 0, 1, 3, 19 and 132 chunks per
+    # sequence cover the early exit, a partial first batch and (for every D) several
+    # later batches; records past each sequence's count hold random bytes.
+    say(f"merge kernel batches D={D} dtype={dtype} Hq={Hq} Hkv={Hkv} split={split}")
+    lens = np.array([0, 1, 40, 300, 2100], np.int32)
+    npdt = np.float32 if dtype == KVC_F32 else np.float16
+    q = normal((5, Hq, D), 110 + D, npdt)
+    K, V = normal((5, Hkv, 2100, D), 111 + D, npdt), normal((5, Hkv, 2100, D), 112 + D, npdt)
+    need = ops.decode_workspace_size(5, Hq, Hkv, D, 16, 2100, split, dtype)
+    ws = DeviceBuffer(need)
+    ws.upload(np.random.default_rng(D).integers(0, 256, need, dtype=np.uint8))
+    with tuning("fused_merge", 0):  # the standalone merge kernel
+        got = run_batched(q, K, V, lens, Hkv, 16, dtype, split=split, workspace=ws)
+    assert np.all(got[0] == 0)
+    assert np.abs(got - oracle_out(orc, q, K, V, lens)).max() <= (1e-5 if dtype == KVC_F32 else 2e-3)
+
+
 # ---- config 3: long-context split-K, Qwen2.5-0.5B attention shape --------------------
 def test_c3_long_context_split_k(orc):
     lens = np.array([8192, 16384, 32768, 32768], np.int32)
