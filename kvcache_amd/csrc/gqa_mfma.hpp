@@ -38,7 +38,7 @@
 // located by a shift and a mask, and is read through one buffer descriptor whose
 // size admits only the valid rows).  The fused cross-chunk merge runs on every
 // thread of the last-arriving workgroup (weights per chunk in LDS, then each
-// thread accumulates one (head, dim) over the chunks with independent loads).
+// thread accumulates one (head, dim) over up to 32 chunks per round of loads).
 
 constexpr int kMfmaTile = 32;             // tokens per wave tile (two 16-row subtiles)
 constexpr int kMfmaMaxChunkBlocks = 1024; // block ids staged per unit
@@ -454,38 +454,50 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(const int* __rest
     };
     const size_t first = u.rec0 - (size_t)u.c * u.cstride;  // record of chunk 0, head 0
     const int ncm = min(nc, kMaxFusedChunks);                // the host keeps nc within this
-    // per head: chunk weights 2^(m_c - M) (one chunk per lane) and the total sum
+    // per head: chunk weights 2^(m_c - M) (one chunk per lane) and the total sum; m and
+    // l are read together, unconditionally (lanes past the count re-read the last chunk
+    // and drop out by select)
     for (int g = wave; g < heads; g += WPB) {
         const bool in = lane < ncm;
-        const size_t rec = first + (size_t)(in ? lane : 0) * u.cstride + g;
-        const float mc = in ? ld(p.part_ml + rec * 2) : -FLT_MAX;
+        const size_t rec = first + (size_t)min(lane, ncm - 1) * u.cstride + g;
+        const float mraw = ld(p.part_ml + rec * 2), lraw = ld(p.part_ml + rec * 2 + 1);
+        const float mc = in ? mraw : -FLT_MAX;
         float M = mc;
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, shfl_xor(M, o));
         const float w = in ? fast_exp2(mc - M) : 0.f;
-        float lw = in ? w * ld(p.part_ml + rec * 2 + 1) : 0.f;
+        float lw = in ? w * lraw : 0.f;
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) lw += shfl_xor(lw, o);
         s_w[g][lane] = w;
         if (lane == 0) s_L[g] = lw;
     }
     __syncthreads();
-    // each thread owns one (head, dim) and keeps 16 chunk partials in flight
-    constexpr int E = 16;
-    for (int idx = tid; idx < heads * D; idx += WPB * kWave) {
-        const int g = idx / D, d = idx % D;
-        float acc[4] = {0.f, 0.f, 0.f, 0.f};
-        for (int c = 0; c < ncm; c += E) {
-            float a[E];
+    // each thread owns one (head, dim) and reads its chunk partials E at a time (one
+    // round for up to 32 chunks): loads unconditional (indices clamped to the last
+    // chunk, weights of chunks past the count are 0), E fixed per variant so that no
+    // branch sits between the loads
+    auto merge_out = [&](auto e_tag) {
+        constexpr int E = decltype(e_tag)::value;
+        for (int idx = tid; idx < heads * D; idx += WPB * kWave) {
+            const int g = idx / D, d = idx % D;
+            float acc[4] = {0.f, 0.f, 0.f, 0.f};
+            for (int c0 = 0; c0 < ncm; c0 += E) {
+                float a[E];
 #pragma unroll
-            for (int e = 0; e < E; ++e)
-                a[e] = c + e < ncm ? ld(p.part_acc + (first + (size_t)(c + e) * u.cstride + g) * D + d) : 0.f;
+                for (int e = 0; e < E; ++e)
+                    a[e] = ld(p.part_acc + (first + (size_t)min(c0 + e, ncm - 1) * u.cstride + g) * D + d);
 #pragma unroll
-            for (int e = 0; e < E; ++e) acc[e & 3] = __builtin_fmaf(c + e < ncm ? s_w[g][c + e] : 0.f, a[e], acc[e & 3]);
+                for (int e = 0; e < E; ++e)
+                    acc[e & 3] = __builtin_fmaf(c0 + e < ncm ? s_w[g][c0 + e] : 0.f, a[e], acc[e & 3]);
+            }
+            const float sum = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+            const float L = s_L[g];
+            ob[(size_t)g * D + d] = (_Float16)(L > 0.f ? sum * (1.0f / L) : 0.f);
         }
-        const float a = (acc[0] + acc[1]) + (acc[2] + acc[3]);
-        const float L = s_L[g];
-        ob[(size_t)g * D + d] = (_Float16)(L > 0.f ? a * (1.0f / L) : 0.f);
-    }
+    };
+    // (head_dim 128 keeps 16-chunk rounds: its main loop already fills the registers)
+    if (D == 128 || ncm <= 16) merge_out(std::integral_constant<int, 16>{});
+    else merge_out(std::integral_constant<int, 32>{});
     if (tid == 0) __hip_atomic_store(ctr, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
