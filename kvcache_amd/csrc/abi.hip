@@ -245,6 +245,8 @@ int check_common(int N, int Hq, int Hkv, int D, int dtype, const void* q, const 
                  const void* out) {
     if (!dtype_ok(dtype)) return set_error(KVC_ERR_ARG, "dtype must be KVC_F32 (0) or KVC_F16 (1)");
     if (N < 0 || Hq <= 0 || Hkv <= 0) return set_error(KVC_ERR_ARG, "N must be >= 0 and head counts > 0");
+    // the kernels read lengths and table offsets through 32-bit byte-sized descriptors
+    if (N >= (1 << 28)) return set_error(KVC_ERR_UNSUPPORTED, "N must be below 2^28 sequences per launch");
     if (Hq % Hkv) return set_error(KVC_ERR_ARG, "Hq must be a multiple of Hkv");
     if (!d_ok(D)) return set_error(KVC_ERR_UNSUPPORTED, "head_dim must be 32, 64, 128 or 256");
     if (N == 0) return KVC_OK;

@@ -50,6 +50,14 @@ def test_unsupported_head_dim(D, status):
     assert e.value.status == status and "head_dim" in str(e.value)
 
 
+def test_batch_beyond_descriptor_range_rejected():
+    # lengths and table offsets are read through 32-bit byte-sized descriptors
+    p = _fake()
+    with pytest.raises(N.KvcError) as e:
+        ops.launch_batched_paged(p, p, p, p, p, p, p, 1 << 28, 8, 64, 16, 100, 0.1, dtype=N.KVC_F16)
+    assert e.value.status == N.KVC_ERR_UNSUPPORTED and "2^28" in str(e.value)
+
+
 def test_bad_arguments_rejected():
     p = _fake()
     with pytest.raises(N.KvcError) as e:  # Hq not a multiple of Hkv
