@@ -302,6 +302,7 @@ constexpr int kPlanIntsInline = 64;   // grouped-query units: header + up to 56 
 
 struct PlanShape {
     int G, nsub, hks, tpw, wpb, min_chunk, max_chunk, slots, entry_ints;
+    int target_cap = INT_MAX;  // largest automatic chunk target (tokens)
     bool uniform, mfma;
 };
 
@@ -343,6 +344,10 @@ PlanShape plan_shape(int Hq, int Hkv, int D, int BLOCK, int dtype) {
     // units to aim for per CU: ~3.5 for one or two heads per wave (about 1.3 rounds
     // of the 4 units a CU runs at once), ~3 for larger groups
     ps.slots = ps.G <= 2 ? 256 * 7 / 2 : 256 * 3;
+    // and, for one or two heads, chunks of at most 640 tokens: on config 2 (N=128 ragged
+    // MHA) 640 beat the 752 the slot count gives (33.9 vs 34.5 us), and 576-640 was the
+    // best range for log-uniform lengths as well
+    if (ps.G <= 2) ps.target_cap = 640;
     // uniform paging: the first 8 block ids ride in the entry (the first batch of
     // every wave of a 4-wave unit touches at most 8 blocks for 16-token blocks)
     ps.entry_ints = ps.uniform ? kPlanInts + 8 : kPlanInts;
@@ -356,7 +361,9 @@ int make_plan(const int* lens, const int* tab_off, const int* table, int table_l
     long long total = 0;
     for (int i = 0; i < N; ++i) total += std::max(lens[i], 1);
     total *= ps.hks;
-    if (target <= 0) target = (int)std::min<long long>((total + ps.slots - 1) / ps.slots, INT_MAX / 2);
+    if (target <= 0)
+        target = (int)std::min<long long>(std::min<long long>((total + ps.slots - 1) / ps.slots, ps.target_cap),
+                                          INT_MAX / 2);
     int T = std::max(target, ps.min_chunk);
     T = (T + BLOCK - 1) / BLOCK * BLOCK;
     T = std::min(T, ps.max_chunk);
