@@ -289,6 +289,27 @@ def run_planned(q, K, V, lens, Hkv, block, dtype, perm=None, target=0, workspace
     return host(out, q.dtype, q.shape).astype(np.float64)
 
 
+@pytest.mark.parametrize("Hq,Hkv,D,dtype", [(8, 8, 64, KVC_F16), (14, 2, 64, KVC_F16), (4, 2, 128, KVC_F32)])
+def test_planned_many_chunks_fused_merge(orc, Hq, Hkv, D, dtype):
+    # contexts of up to 20k tokens split into 20-31 chunks per (sequence, KV head),
+    # merged by the last chunk to arrive; two launches on one workspace (arrival
+    # counters left by the first, random bytes before) give identical outputs
+    say(f"planned many chunks Hq={Hq} Hkv={Hkv} D={D} dtype={dtype}")
+    lens = np.array([3000, 9000, 40, 20000], np.int32)
+    npdt = np.float32 if dtype == KVC_F32 else np.float16
+    q = normal((4, Hq, D), 200, npdt)
+    K, V = normal((4, Hkv, 20000, D), 201, npdt), normal((4, Hkv, 20000, D), 202, npdt)
+    work, nu, nr = ops.decode_plan(lens, Hq, Hkv, D, 16, dtype=dtype)
+    assert nr > 8 * 2 * Hkv, "the plan splits the long contexts into more than 8 chunks"
+    ws = DeviceBuffer(ops.planned_workspace_size(Hq, Hkv, D, nr, BLOCK=16, dtype=dtype))
+    ws.upload(np.random.default_rng(9).integers(0, 256, ws.nbytes, dtype=np.uint8))
+    perm = np.random.default_rng(12).permutation(sum((int(x) + 15) // 16 for x in lens))
+    first = run_planned(q, K, V, lens, Hkv, 16, dtype, perm=perm, workspace=ws)
+    second = run_planned(q, K, V, lens, Hkv, 16, dtype, perm=perm, workspace=ws)
+    np.testing.assert_array_equal(first, second)
+    assert np.abs(first - oracle_out(orc, q, K, V, lens)).max() <= (1e-5 if dtype == KVC_F32 else 2e-3)
+
+
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("scale", [-0.2, 0.0, 0.5])
 def test_planned_grouped_scale_sign(orc, D, scale):
