@@ -554,7 +554,7 @@ int run_planned(const void* q, const void* k_new, const void* v_new, const int* 
         L.dtype = dtype; L.D = D; L.G = ps.G; L.mode = ps.uniform ? kPlannedUniform : kPlannedPerLane;
         L.mfma = ps.mfma;
         // a cap on co-resident units lets the longest-first order work as a queue
-        L.wg_per_cu = tuning().wg_per_cu >= 0 ? tuning().wg_per_cu : (!ps.mfma && ps.G <= 2 ? 4 : 0);
+        L.wg_per_cu = tuning().wg_per_cu >= 0 ? tuning().wg_per_cu : (!ps.mfma && ps.G <= 2 ? 6 : 0);
         L.wpb = tuning().waves_per_block ? tuning().waves_per_block : ps.wpb;
         L.batch = tuning().batch;
         L.need_merge = false;
