@@ -269,3 +269,16 @@ def test_decode_plan_capacity_bounds_every_plan(Hq, Hkv, D, B, dtype):
         planned += 1
         assert nu <= cap.value and nr <= cap.value, (lens.tolist()[:8], nu, nr, cap.value)
     assert planned >= len(mixes) - 2
+
+
+def test_decode_plan_chunk_sizing():
+    # one or two heads per unit: the automatic target is the batch's tokens per unit
+    # slot capped at 640, and a sequence stays whole up to 1.5 targets; grouped-query
+    # plans cut long contexts into ~1024-token units (planner rules of abi.hip)
+    from kvcache_amd import ops
+    for lens, Hq, Hkv, units, biggest in ((W.ref_lengths(), 8, 8, 1408, 960),
+                                         (W.loguniform_lengths(128, 16, 2048, 7), 8, 8, 1392, 720),
+                                         (np.array([8192, 16384, 32768, 32768], np.int32), 14, 2, 176, 1024)):
+        work, nu, nr = ops.decode_plan(lens, Hq, Hkv, 64, 16, dtype=KVC_F16)
+        sizes = work[:, 3] - work[:, 2]
+        assert nu == units and sizes.max() <= biggest, (nu, int(sizes.max()))
