@@ -6,8 +6,14 @@ r = (s >> 9) / 2^23 in float32):
   * ref_trace    -- bench_continuous.cu:38-50, prompt 16+(int)(240*rp*rp),
                     gen 8+(int)(504*rg*rg), Poisson gaps -log(u)/rate*1e6 drawn only
                     when rate > 0 (so the online trace differs from the offline one)
+  * fill_rand    -- bench_paged.cu:19-24, values 2r - 1 in [-1, 1) from the same LCG
   * hval         -- bench_throughput.cu:21-25 deterministic K/V values in [-1, 1)
   * shuffle_perm -- main_paged.cu:28-37 seeded block-table shuffle
+  * demo_trace   -- demo_engine.cu:18-28, prompt 8 + rand() % 120 then gen
+                    16 + rand() % 200 after srand(123), with glibc's rand()
+                    (GlibcRand: the TYPE_3 additive feedback generator)
+These are input generators: every parity check holds for whatever inputs they
+produce (outputs are compared with the CPU oracle on the same inputs).
 BASELINE distributions (seeded numpy PCG64; no reference counterpart):
   * loguniform_lengths -- lengths log-uniform in [lo, hi]
   * baseline_trace     -- prompts uniform [1, 256], generation geometric (mean
@@ -70,6 +76,68 @@ def hval(s, h, pos, d, salt) -> np.ndarray:
     x = (x * u(0x9E3779B1)) & u(_M)
     x = x ^ (x >> u(16))
     return (np.asarray(x >> u(9)).astype(np.float32) / np.float32(8388608.0)) * np.float32(2.0) - np.float32(1.0)
+
+
+def fill_rand(n: int, seed: int) -> np.ndarray:
+    """bench_paged.cu:19-24: x = r * 2 - 1 per element, r from the LCG above (float32)."""
+    out = np.empty(n, dtype=np.float32)
+    s = seed
+    for i in range(n):
+        s, r = _lcg01(s)
+        out[i] = r * np.float32(2.0) - np.float32(1.0)
+    return out
+
+
+class GlibcRand:
+    """glibc's rand() (random() with the default 128-byte TYPE_3 state): an additive
+    lagged-Fibonacci generator r[i] = r[i-3] + r[i-31] (mod 2^32) seeded through the
+    Park-Miller recurrence r[i] = 16807 r[i-1] mod (2^31 - 1) for i < 31, r[i] =
+    r[i-31] for 31 <= i < 34, with the first 310 outputs discarded; rand() returns
+    r[i] >> 1.  (Published description of glibc's random_r.c; demo_engine.cu draws
+    its trace with srand/rand.)"""
+
+    def __init__(self, seed: int = 1):
+        seed &= _M
+        if seed == 0:
+            seed = 1
+        r = [0] * 34
+        r[0] = seed
+        for i in range(1, 31):
+            hi, lo = divmod(r[i - 1] if r[i - 1] < 2**31 else r[i - 1] - 2**32, 127773)
+            # C division truncates toward zero
+            if r[i - 1] >= 2**31 and lo != 0:
+                hi, lo = hi + 1, lo - 127773
+            word = 16807 * lo - 2836 * hi
+            if word < 0:
+                word += 2147483647
+            r[i] = word & _M
+        for i in range(31, 34):
+            r[i] = r[i - 31]
+        self._r = r
+        for _ in range(310):
+            self._next()
+
+    def _next(self) -> int:
+        r = self._r
+        v = (r[-3] + r[-31]) & _M
+        r.append(v)
+        del r[0]
+        return v
+
+    def rand(self) -> int:
+        return self._next() >> 1
+
+
+def demo_trace(nreq: int = 256, seed: int = 123) -> tuple[np.ndarray, np.ndarray]:
+    """demo_engine.cu:18-28: srand(seed); per request prompt = 8 + rand() % 120,
+    then gen = 16 + rand() % 200."""
+    g = GlibcRand(seed)
+    prompt = np.empty(nreq, dtype=np.int32)
+    gen = np.empty(nreq, dtype=np.int32)
+    for i in range(nreq):
+        prompt[i] = 8 + g.rand() % 120
+        gen[i] = 16 + g.rand() % 200
+    return prompt, gen
 
 
 def shuffle_perm(nb: int, seed: int = 42) -> np.ndarray:

@@ -36,11 +36,7 @@ _SIGS = {
     "orc_flash_merge": (None, [vp, vp, vp, vp, i32, i32, i32]),
     "orc_flash_decode": (None, [vp, vp, vp, vp, i32, i32, i32, C.c_longlong, f64, i32, i32]),
     "orc_ref_lengths": (None, [i32, i32, u32, vp]),
-    "orc_hval": (C.c_float, [u32, u32, u32, u32, u32]),
-    "orc_fill_rand": (None, [vp, C.c_longlong, u32]),
-    "orc_shuffle_perm": (None, [i32, u32, vp]),
     "orc_ref_trace": (None, [i32, i32, i32, f64, u32, vp, vp, vp]),
-    "orc_demo_trace": (None, [i32, u32, vp, vp]),
     "orc_kvm_new": (vp, [i32, i32, i32, i32]),
     "orc_kvm_delete": (None, [vp]),
     "orc_kvm_free_blocks": (i32, [vp]),
@@ -151,28 +147,6 @@ def ref_trace(nreq=256, prompt_max=256, gen_max=512, rate=0.0, seed=2024):
     p = np.zeros(nreq, np.int32); g = np.zeros(nreq, np.int32); a = np.zeros(nreq, np.float64)
     lib().orc_ref_trace(nreq, prompt_max, gen_max, rate, seed, _p(p), _p(g), _p(a))
     return p, g, a
-
-
-def demo_trace(nreq=256, seed=123):
-    p = np.zeros(nreq, np.int32); g = np.zeros(nreq, np.int32)
-    lib().orc_demo_trace(nreq, seed, _p(p), _p(g))
-    return p, g
-
-
-def hval(s, h, pos, d, salt):
-    return lib().orc_hval(s, h, pos, d, salt)
-
-
-def shuffle_perm(nb, seed=42):
-    out = np.zeros(nb, np.int32)
-    lib().orc_shuffle_perm(nb, seed, _p(out))
-    return out
-
-
-def fill_rand(n, seed):
-    out = np.zeros(n, np.float32)
-    lib().orc_fill_rand(_p(out), n, seed)
-    return out
 
 
 # ---- scheduling ------------------------------------------------------------------

@@ -56,7 +56,7 @@ def test_c1_single_sequence_contiguous_vs_paged(orc, dtype):
     oc = host(out_c, nt, q.shape)
     ref = orc.batched_contig(q[None], K[None], V[None], np.array([S], np.int32), scale)[0]
     assert np.abs(oc - ref).max() <= tol(dtype)
-    for perm in (None, orc.shuffle_perm(S // B, 42)):     # identity and main_paged.cu's shuffled table
+    for perm in (None, W.shuffle_perm(S // B, 42)):     # identity and main_paged.cu's shuffled table
         kp, vp, table, _ = paged_layout(K[None], V[None], [S], B, perm)
         out_p = DeviceBuffer(q.nbytes)
         ops.launch_paged(dev(q), dev(kp), dev(vp), dev(table), out_p, S, H, D, B, scale, dtype=dtype)

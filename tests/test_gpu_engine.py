@@ -52,7 +52,7 @@ def test_config4_shape_24_layers_gqa_fp16(orc):
 
 def test_measured_clock_invariants(orc):
     say("engine measured clock")
-    p, g = orc.demo_trace(256, 123)
+    p, g = W.demo_trace(256, 123)
     eng = Engine(EngineConfig(n_heads=8, head_dim=64, block_size=16, num_blocks=512, max_batch=32))
     st = run_continuous(p, g, np.zeros(256), eng)
     assert st.tokens == g.sum() and st.finished == 256 and st.peak_blocks <= 512

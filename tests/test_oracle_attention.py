@@ -16,6 +16,8 @@ import numpy as np
 import pytest
 from scipy.special import expit, softmax
 
+from kvcache_amd import workloads as W
+
 
 def rng(seed=0):
     return np.random.default_rng(seed)
@@ -130,7 +132,7 @@ def test_paged_shuffled_equals_contiguous(orc, tmp_path):
     K = r.standard_normal((N, H, S, D)).astype(np.float32)
     V = r.standard_normal((N, H, S, D)).astype(np.float32)
     nb = [(int(L) + B - 1) // B for L in lens]
-    perm = orc.shuffle_perm(sum(nb), 42)
+    perm = W.shuffle_perm(sum(nb), 42)
     kp = np.zeros((sum(nb), H, B, D), np.float32)
     vp = np.zeros_like(kp)
     tab_off = np.concatenate([[0], np.cumsum(nb)]).astype(np.int32)

@@ -50,14 +50,51 @@ def test_continuous_trace_known_answers(orc):
     assert abs(a2[-1] / 1e6 - 256 / 400) < 0.25      # ~256 arrivals at 400/s
 
 
-def test_hval_and_shuffle(orc):
+def test_fill_rand_stream_gives_the_ragged_lengths():
+    """bench_paged.cu:19-24 fills with x = 2r - 1 from the same LCG as the ragged lengths of
+    bench_throughput.cu:50-57, so mapping its stream back through r = (x + 1) / 2 (exact in
+    float32: r = k / 2^23) and L = 16 + (int)(2032 r^2) must give the README's batch
+    (sum 83,212, max 2,022, 5,259 blocks of 16)."""
     from kvcache_amd import workloads as W
-    for args in [(0, 0, 0, 0, 1), (5, 3, 100, 63, 2), (127, 7, 2021, 0, 3)]:
-        assert orc.hval(*args) == W.hval(*args)
-        assert -1.0 <= orc.hval(*args) < 1.0
-    perm = orc.shuffle_perm(64, 42)
-    assert sorted(perm.tolist()) == list(range(64)) and perm.tolist() != list(range(64))
-    np.testing.assert_array_equal(perm, W.shuffle_perm(64, 42))
+    x = W.fill_rand(128, 12345)
+    assert x.dtype == np.float32 and -1.0 <= x.min() and x.max() < 1.0
+    r = (x + np.float32(1.0)) / np.float32(2.0)
+    L = np.array([16 + int(np.float32(2032.0) * ri * ri) for ri in r])
+    assert L.sum() == 83212 and L.max() == 2022 and sum((int(v) + 15) // 16 for v in L) == 5259
+    np.testing.assert_array_equal(L, W.ref_lengths(128, 2048, 12345))
+
+
+def test_demo_trace_draws_glibc_rand():
+    """demo_engine.cu:18-28 draws with srand(123)/rand(): the restated glibc generator must
+    give the C library's own sequence (called through ctypes), and the trace takes the
+    prompt draw before the generation draw of each request."""
+    import ctypes
+    import ctypes.util
+    from kvcache_amd import workloads as W
+    libc = ctypes.CDLL(ctypes.util.find_library("c"))
+    if not hasattr(libc, "gnu_get_libc_version"):
+        pytest.skip("C library is not glibc")
+    for seed in (123, 0, 1, 2024, 0x80000005, 0xFFFFFFFF):
+        libc.srand(ctypes.c_uint(seed))
+        want = [libc.rand() for _ in range(600)]
+        g = W.GlibcRand(seed)
+        assert [g.rand() for _ in range(600)] == want, seed
+    libc.srand(ctypes.c_uint(123))
+    draws = [libc.rand() for _ in range(2 * 256)]
+    p, g = W.demo_trace(256, 123)
+    np.testing.assert_array_equal(p, [8 + d % 120 for d in draws[0::2]])
+    np.testing.assert_array_equal(g, [16 + d % 200 for d in draws[1::2]])
+    assert 8 <= p.min() and p.max() <= 127 and 16 <= g.min() and g.max() <= 215
+
+
+def test_shuffle_perm_is_a_permutation():
+    """main_paged.cu:28-37's table shuffle is an input generator: the paged == contiguous
+    checks hold for any permutation, so only that it is one (and not the identity) matters."""
+    from kvcache_amd import workloads as W
+    for nb in (1, 2, 64, 5259):
+        perm = W.shuffle_perm(nb, 42)
+        assert sorted(perm.tolist()) == list(range(nb))
+        assert nb < 64 or perm.tolist() != list(range(nb))
 
 
 # ---- allocator / manager ---------------------------------------------------------
@@ -191,7 +228,8 @@ def test_isolated_poisson_arrivals(orc):
 
 def test_demo_engine_invariants(orc):
     # demo_engine.cu:14-42: 8 heads, D 64, BLOCK 16, 512 blocks, width 32, srand(123)
-    p, g = orc.demo_trace(256, 123)
+    from kvcache_amd import workloads as W
+    p, g = W.demo_trace(256, 123)
     assert 8 <= p.min() and p.max() <= 127 and 16 <= g.min() and g.max() <= 215
     rc, st = orc.sim_engine(p, g, np.zeros(256), 16, 512, 32)
     assert rc == 0 and st.tokens == g.sum() and st.finished == 256 and st.peak_blocks <= 512
