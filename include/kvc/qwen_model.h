@@ -44,7 +44,7 @@ struct QwenConfig {
     int block_size = 16, num_blocks = 10922, max_batch = 32, max_rows = 1024;  // max_rows: prompt rows per prefill
     uint64_t seed = 0x71776e32ull;
     int step_path = 0;  // 0: fused kernels for steps of <= 32 rows; 1: one kernel per op
-    int graph = 1;      // fused steps replay one captured HIP graph
+    int graph = 0;      // 1: fused steps replay one captured HIP graph (measured no faster than eager)
     int prefill_rows = 4096;  // prompt rows stacked into one prefill forward (a longer prompt runs alone)
 };
 
@@ -79,11 +79,13 @@ struct QwenModel {
     // [n, units, records, 0 | ids B | pos B | work cap_units*ipu | table cap_tab]
     void* gexec = nullptr;
     bool graph_failed = false;
+    const void* g_ws = nullptr;  // the workspace and pools the captured graph holds
+    const void* g_pools[2] = {nullptr, nullptr};
     int* d_g = nullptr;
     int* h_g = nullptr;
     int g_cap_units = 0, g_cap_tab = 0, g_ipu = 0;
     size_t g_off_work = 0, g_off_tab = 0;
-    long long graph_steps = 0;
+    long long graph_steps = 0, graph_captures = 0;
     std::vector<int> h_work, h_tab, h_off, h_len;
 
     explicit QwenModel(const QwenConfig& cfg)
@@ -170,9 +172,16 @@ struct QwenModel {
         kvc::check(kvc_malloc((void**)&d_meta, meta_cap * 4), "meta");
         kvc::check(kvc_host_alloc((void**)&h_meta, meta_cap * 4), "pinned meta");
     }
+    // Grows the split-K workspace.  A captured step graph holds the old address, so
+    // it is destroyed here and captured again by the next decode step.
     void ensure_ws(size_t need) {
         if (need <= ws_bytes) return;
         kvc::check(kvc_stream_synchronize(stream), "workspace growth");
+        if (gexec) {
+            kvc_graph_destroy(gexec);
+            gexec = nullptr;
+            g_ws = nullptr;
+        }
         kvc_free(ws);
         ws = nullptr;
         ws_bytes = std::max(need, (size_t)1 << 20) * 2;
@@ -453,8 +462,10 @@ struct QwenModel {
         g_off_work = 4 + 2 * (size_t)B;
         g_off_tab = g_off_work + (size_t)g_cap_units * g_ipu;
         const size_t ints = g_off_tab + g_cap_tab;
-        kvc::check(kvc_malloc((void**)&d_g, ints * 4), "graph metadata");
-        kvc::check(kvc_host_alloc((void**)&h_g, ints * 4), "pinned graph metadata");
+        if (!d_g) {  // kept across captures (a workspace growth makes the next step capture again)
+            kvc::check(kvc_malloc((void**)&d_g, ints * 4), "graph metadata");
+            kvc::check(kvc_host_alloc((void**)&h_g, ints * 4), "pinned graph metadata");
+        }
         kvc::check(kvc_memset(d_g, 0, ints * 4, stream), "graph metadata");  // zero counts: an idle replay
         ensure_ws(kvc_decode_planned_workspace_size(c.n_heads, c.n_kv_heads, c.head_dim, c.block_size, KVC_F16,
                                                     g_cap_units));
@@ -477,10 +488,16 @@ struct QwenModel {
             throw;
         }
         kvc::check(kvc_graph_end(stream, &gexec), "graph instantiate");
+        ++graph_captures;
+        g_ws = ws;
+        g_pools[0] = kl(0);
+        g_pools[1] = vl(0);
         return true;
     }
 
     void decode_graph(int n, const int* in, int T, int nu, int nr, int ipu, int* out) {
+        if (ws != g_ws || kl(0) != g_pools[0] || vl(0) != g_pools[1])
+            throw kvc::Error(KVC_ERR_STATE, "decode_graph: workspace or pools differ from those the graph captured");
         const int B = c.max_batch;
         int* h = h_g;
         h[0] = n; h[1] = nu; h[2] = nr; h[3] = 0;
@@ -640,7 +657,7 @@ struct QwenModel {
     };
     struct ServeStats {
         int steps = 0, finished = 0;
-        long long tokens = 0, prompt_tokens = 0, graph_steps = 0;
+        long long tokens = 0, prompt_tokens = 0, graph_steps = 0, graph_captures = 0;
         double wall_us = 0, prefill_us = 0, decode_us = 0;
     };
 
@@ -648,7 +665,7 @@ struct QwenModel {
     ServeStats serve(const std::vector<Request>& reqs, std::vector<std::vector<int>>& out) {
         using clk = std::chrono::steady_clock;
         ServeStats st;
-        const long long graph_steps0 = graph_steps;
+        const long long graph_steps0 = graph_steps, graph_captures0 = graph_captures;
         kvm.reset();
         out.assign(reqs.size(), {});
         std::vector<Sequence> seqs(reqs.size());
@@ -738,6 +755,7 @@ struct QwenModel {
         }
         st.wall_us = std::chrono::duration<double, std::micro>(clk::now() - t0).count();
         st.graph_steps = graph_steps - graph_steps0;
+        st.graph_captures = graph_captures - graph_captures0;
         return st;
     }
 };

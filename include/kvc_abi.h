@@ -7,7 +7,9 @@
  *   - separate query / KV head counts (Hq, Hkv) for grouped-query attention,
  *   - an explicit HIP stream (`stream` is a hipStream_t; NULL = null stream),
  *   - caller-provided workspace for split-K partials (NULL = a grow-only buffer
- *     owned by the library, allocated on first need),
+ *     owned by the library, one per (device, stream), allocated on first need;
+ *     calls on one stream are ordered by it, calls on different streams never
+ *     share partials; refused with KVC_ERR_STATE while the stream is capturing),
  *   - an int status instead of void: 0 = KVC_OK, otherwise a KVC_ERR_* code,
  *     with a readable message from kvc_last_error().
  * No function throws across this boundary.  All launches are asynchronous on
@@ -326,7 +328,7 @@ typedef struct kvc_qwen_config {
     int block_size, num_blocks, max_batch, max_rows;  /* max_rows: longest prompt */
     uint64_t seed;                                      /* 0: default */
     int step_path;  /* 0: fused decode-step kernels when a step has <= 32 rows; 1: one kernel per op */
-    int graph;      /* 1: fused steps replay one captured HIP graph */
+    int graph;      /* 1: fused steps replay one captured HIP graph (0: eager launches) */
     int prefill_rows;  /* prompt rows stacked into one prefill forward (0: 4096) */
 } kvc_qwen_config;
 typedef struct kvc_qwen_stats {
@@ -334,6 +336,7 @@ typedef struct kvc_qwen_stats {
     long long tokens, prompt_tokens;
     double wall_us, prefill_us, decode_us;   /* host clock around the whole run / prefills / decode steps */
     long long graph_steps;                   /* decode steps that replayed the captured graph */
+    long long graph_captures;                /* step graphs captured (again after a workspace growth) */
 } kvc_qwen_stats;
 typedef struct kvc_qwen kvc_qwen;
 int  kvc_qwen_create(const kvc_qwen_config* cfg, kvc_qwen** out);

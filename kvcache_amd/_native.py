@@ -61,6 +61,7 @@ class QwenStatsC(C.Structure):
     _fields_ = [
         ("steps", i32), ("finished", i32), ("tokens", C.c_longlong), ("prompt_tokens", C.c_longlong),
         ("wall_us", f64), ("prefill_us", f64), ("decode_us", f64), ("graph_steps", C.c_longlong),
+        ("graph_captures", C.c_longlong),
     ]
 
 

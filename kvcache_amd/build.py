@@ -5,7 +5,10 @@
 
 Sources: kvcache_amd/csrc/*.hip (device + ABI) and *.cpp (host-only C++).
 Objects go to kvcache_amd/_build/, the library to kvcache_amd/libkvcache_amd.so,
-test programs (tests/cpp/*.cpp) to kvcache_amd/_build/bin/.
+test programs (tests/cpp/*.cpp) to kvcache_amd/_build/bin/.  When the reference
+tree is present, its test programs that use only the API this library replaces
+(tests/test_kv_manager.cu) are compiled unchanged against include/kvc into
+kvcache_amd/_build/bin/ref_<name>: the drop-in check (built, never committed).
 """
 from __future__ import annotations
 
@@ -24,6 +27,9 @@ BUILD = PKG / "_build"
 LIB = PKG / "libkvcache_amd.so"
 INCLUDE = ROOT / "include"
 TESTS_CPP = ROOT / "tests" / "cpp"
+REFERENCE = Path(os.environ.get("KVC_REFERENCE", "/root/reference"))
+# reference test programs whose only includes are headers this library replaces
+REFERENCE_TESTS = ["tests/test_kv_manager.cu"]
 
 ARCH = os.environ.get("KVC_OFFLOAD_ARCH", "gfx950")
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
@@ -79,6 +85,22 @@ def build_cpp_tests() -> list[Path]:
     return built
 
 
+def build_reference_tests() -> list[Path]:
+    """The reference's own test programs, source unchanged, against include/kvc."""
+    out_dir = BUILD / "bin"
+    out_dir.mkdir(parents=True, exist_ok=True)
+    built = []
+    for rel in REFERENCE_TESTS:
+        src = REFERENCE / rel
+        if not src.exists():
+            continue
+        exe = out_dir / ("ref_" + src.stem)
+        _run([HIPCC, "-x", "c++", "-O2", "-std=c++17", f"-I{INCLUDE / 'kvc'}", str(src), "-o", str(exe), f"-L{PKG}",
+              "-lkvcache_amd", "-Wl,-rpath,$ORIGIN/../..", "-Wl,-rpath,/opt/rocm/lib"])
+        built.append(exe)
+    return built
+
+
 def main(argv: list[str] | None = None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--lib-only", action="store_true")
@@ -86,7 +108,7 @@ def main(argv: list[str] | None = None) -> int:
     a = ap.parse_args(argv)
     print(f"built {build_library(a.jobs)}")
     if not a.lib_only:
-        for exe in build_cpp_tests():
+        for exe in build_cpp_tests() + build_reference_tests():
             print(f"built {exe}")
     return 0
 

@@ -12,6 +12,7 @@
 #include <atomic>
 #include <cmath>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -191,21 +192,31 @@ unsigned next_epoch() {
     return e ? e : g_epoch.fetch_add(1u, std::memory_order_relaxed) + 1u;
 }
 
-// Library-owned grow-only workspace per device (used when the caller passes none).
+// Library-owned grow-only workspace per (device, stream), used when the caller passes
+// none.  Launches on one stream run in order, so they can share a buffer; launches on
+// different streams get different buffers, so overlapping split-K calls never write
+// each other's partials or arrival counters.  Refused under stream capture: a graph
+// would keep the address of a buffer that a later growth frees.
 std::mutex g_ws_mu;
-std::vector<std::pair<void*, size_t>> g_ws;
+std::map<std::pair<int, hipStream_t>, std::pair<void*, size_t>> g_ws;
 
-int default_workspace(size_t bytes, void** out) {
+int default_workspace(size_t bytes, hipStream_t st, void** out) {
+    if (st != nullptr) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        int rc = hip_check(hipStreamIsCapturing(st, &cs), "hipStreamIsCapturing");
+        if (rc) return rc;
+        if (cs != hipStreamCaptureStatusNone)
+            return set_error(KVC_ERR_STATE, "a launch under stream capture must pass its own workspace");
+    }
     std::lock_guard<std::mutex> lk(g_ws_mu);
     int dev = 0;
     int rc = hip_check(hipGetDevice(&dev), "hipGetDevice");
     if (rc) return rc;
-    if ((int)g_ws.size() <= dev) g_ws.resize(dev + 1, {nullptr, 0});
-    auto& slot = g_ws[dev];
+    auto& slot = g_ws[{dev, st}];
     if (slot.second < bytes) {
         if (slot.first) {
-            // queued kernels may still read the old buffer
-            rc = hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize (workspace growth)");
+            // kernels queued on this stream may still read the old buffer
+            rc = hip_check(hipStreamSynchronize(st), "hipStreamSynchronize (workspace growth)");
             if (rc) return rc;
             (void)hipFree(slot.first);
             slot = {nullptr, 0};
@@ -219,10 +230,10 @@ int default_workspace(size_t bytes, void** out) {
     return KVC_OK;
 }
 
-int resolve_workspace(const Plan& pl, void* ws, size_t ws_bytes, DecodeParams& p) {
+int resolve_workspace(const Plan& pl, void* ws, size_t ws_bytes, DecodeParams& p, hipStream_t st) {
     if (pl.max_chunks <= 1) return KVC_OK;
     if (!ws) {
-        int rc = default_workspace(pl.ws_bytes, &ws);
+        int rc = default_workspace(pl.ws_bytes, st, &ws);
         if (rc) return rc;
     } else if (ws_bytes < pl.ws_bytes) {
         return set_error(KVC_ERR_WORKSPACE, "workspace too small: need " + std::to_string(pl.ws_bytes) +
@@ -280,7 +291,7 @@ int run_batched(const void* q, const void* k, const void* v, const int* table_al
     p.group = Hq / Hkv; p.nsub = pl.nsub;
     p.chunk_tokens = pl.chunk; p.num_splits = 0; p.max_chunks = pl.max_chunks;
     p.scale_log2 = scale * 1.4426950408889634f;
-    rc = resolve_workspace(pl, ws, ws_bytes, p);
+    rc = resolve_workspace(pl, ws, ws_bytes, p, st);
     if (rc) return rc;
     p.lpb_shift = pl.lpb_shift;
     p.last_chunk_first = tuning().last_chunk_first;
@@ -499,7 +510,7 @@ int run_causal_tile(const void* q, void* out, const void* k, const void* v, cons
     p.chunk_tokens = pl.chunk; p.max_chunks = pl.max_chunks;
     p.fixed_len = base; p.cap = base + Nq; p.causal = 1;
     p.scale_log2 = scale * 1.4426950408889634f;
-    rc = resolve_workspace(pl, ws, ws_bytes, p);
+    rc = resolve_workspace(pl, ws, ws_bytes, p, st);
     if (rc) return rc;
     p.merge_mode = kMergeKernel;
     L.dtype = KVC_F16; L.D = D; L.G = pl.G; L.mode = kCausalTile; L.wpb = pl.wpb; L.batch = tuning().batch;
@@ -534,7 +545,7 @@ int run_planned(const void* q, const void* k_new, const void* v_new, const int* 
         if (n_records > 0) {
             const size_t need = planned_workspace(Hq, Hkv, D, BLOCK, dtype, n_records);
             if (!ws) {
-                rc = default_workspace(need, &ws);
+                rc = default_workspace(need, st, &ws);
                 if (rc) return rc;
             } else if (ws_bytes < need) {
                 return set_error(KVC_ERR_WORKSPACE, "workspace too small: need " + std::to_string(need) +
@@ -987,7 +998,7 @@ int kvc_flash_decode(const void* q, const void* k_cache, const void* v_cache, vo
         p.N = 1; p.Hq = H; p.Hkv = H; p.block = 1; p.group = 1; p.nsub = 1;
         p.chunk_tokens = 0; p.num_splits = ns; p.max_chunks = ns;
         p.scale_log2 = scale * 1.4426950408889634f;
-        rc = resolve_workspace(pl, ws, ws_bytes, p);
+        rc = resolve_workspace(pl, ws, ws_bytes, p, S(st));
         if (rc) return rc;
         p.last_chunk_first = tuning().last_chunk_first;
         L.dtype = dtype; L.D = D; L.G = 1; L.mode = kContiguous; L.wpb = choose_wpb((long long)ns * H);

@@ -106,6 +106,7 @@ int kvc_qwen_serve(kvc_qwen* h, int n_req, const int* prompt_off, const int* pro
             stats->prompt_tokens = st.prompt_tokens; stats->wall_us = st.wall_us; stats->prefill_us = st.prefill_us;
             stats->decode_us = st.decode_us;
             stats->graph_steps = st.graph_steps;
+            stats->graph_captures = st.graph_captures;
         }
         return KVC_OK;
     });

@@ -29,7 +29,7 @@ class QwenConfig:
     max_rows: int = 1024
     seed: int = 0
     step_path: int = 0  # 0: fused decode-step kernels for steps of <= 32 rows; 1: one kernel per op
-    graph: int = 1  # fused decode steps replay one captured HIP graph
+    graph: int = 0  # 1: fused decode steps replay one captured HIP graph
     prefill_rows: int = 4096  # prompt rows stacked into one prefill forward
 
     def to_c(self) -> QwenConfigC:
@@ -97,4 +97,5 @@ class QwenModel:
             o += n
         return res, {"steps": st.steps, "finished": st.finished, "tokens": st.tokens,
                      "prompt_tokens": st.prompt_tokens, "wall_us": st.wall_us, "prefill_us": st.prefill_us,
-                     "decode_us": st.decode_us, "graph_steps": st.graph_steps}
+                     "decode_us": st.decode_us, "graph_steps": st.graph_steps,
+                     "graph_captures": st.graph_captures}

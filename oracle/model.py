@@ -61,13 +61,14 @@ def _r16(a):
     return np.asarray(a, np.float32).astype(np.float16).astype(np.float32)
 
 
-def decoder_logits(W, cfg, tokens):
+def decoder_logits(W, cfg, tokens, logits_from=0):
     """Teacher-forced forward of one token sequence through the Qwen2-shaped decoder
     (qwen_serve.cu:97-121 for every position at once: causal attention over the
     prefix), returning float64 logits [T, vocab].  W maps names to fp16 arrays
     (kvcache_amd.model.QwenModel.tensor layout: [out, in] row-major); fp16 rounding is
     applied where the GPU stores a kernel's output, arithmetic is float32 (GEMMs) and
-    float64 (norms, softmax)."""
+    float64 (norms, softmax).  Rows before `logits_from` are left out of the lm_head
+    (the returned array still has T rows; those are zero)."""
     H, Hq, Hkv, D = cfg.hidden, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim
     I, V = cfg.inter, cfg.vocab
     tok = np.asarray(tokens)
@@ -98,8 +99,10 @@ def decoder_logits(W, cfg, tokens):
         n = _r16(rmsnorm(x, w("ln2", (H,)), cfg.eps))
         a = _r16(silu_mul(_r16(n @ w("wg", (I, H)).T), _r16(n @ w("wu", (I, H)).T)))
         x = _r16(x + _r16(a @ w("wd", (H, I)).T))
-    n = _r16(rmsnorm(x, f32(W["norm"]), cfg.eps))
-    return (n @ f32(embed).T).astype(np.float64)
+    out = np.zeros((T, V), np.float64)
+    n = _r16(rmsnorm(x[logits_from:], f32(W["norm"]), cfg.eps))
+    out[logits_from:] = n @ f32(embed).T
+    return out
 
 
 def teacher_forced_check(logits_cpu, prompt_len, generated, margin):

@@ -18,8 +18,8 @@ def run(name, *args):
     return r
 
 
-def test_kv_manager_host():
-    assert run("test_kv_manager", "--host").returncode == 0
+def test_kv_manager_scenario_host():
+    assert run("kv_manager_scenario", "--host").returncode == 0
 
 
 def test_demo_engine_host():
@@ -27,8 +27,24 @@ def test_demo_engine_host():
 
 
 @pytest.mark.gpu
-def test_kv_manager_device():
-    assert run("test_kv_manager").returncode == 0
+def test_kv_manager_scenario_device():
+    assert run("kv_manager_scenario").returncode == 0
+
+
+@pytest.mark.gpu
+def test_reference_kv_manager_test_unchanged_against_dropin_headers():
+    """The reference's tests/test_kv_manager.cu, source unchanged, compiled against
+    include/kvc by kvcache_amd.build (only where the reference tree was present at build
+    time; the binary travels with the built library)."""
+    if not (BIN / "ref_test_kv_manager").exists():
+        pytest.skip("reference test program not built (reference tree absent at build time)")
+    r = run("ref_test_kv_manager")
+    assert r.returncode == 0 and "[FAIL]" not in r.stdout
+
+
+@pytest.mark.gpu
+def test_qwen_graph_recaptured_after_workspace_growth():
+    assert run("test_qwen_graph_regrow").returncode == 0
 
 
 @pytest.mark.gpu

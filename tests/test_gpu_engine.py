@@ -21,6 +21,7 @@ def _same(ours, ref):
     assert (ours.iters, ours.tokens, ours.slot_steps, ours.useful_steps, ours.peak_blocks, ours.finished) == (
         ref.iters, ref.tokens, ref.slot_steps, ref.useful_steps, ref.peak_blocks, ref.finished)
     assert ours.wall_us == ref.wall_us and ours.p99_latency_us == ref.p99_latency_us
+    assert ours.p50_latency_us == ref.p50_latency_us and ours.avg_latency_us == ref.avg_latency_us
     assert ours.step_digest == ref.digest
 
 
@@ -48,6 +49,44 @@ def test_config4_shape_24_layers_gqa_fp16(orc):
     eng = Engine(cfg)
     rc, ref = orc.sim_engine(p, g, a, 16, num_blocks, 32, True, COST)
     _same(run_continuous(p, g, a, eng), ref)
+
+
+C4_BLOCKS = (2048 * 1024 * 1024) // (24 * 2 * 16 * 64 * 2 * 2)   # 2048 MB pool of 24 fp16 layer slices
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("trace", ["baseline", "reference"])
+@pytest.mark.parametrize("rate", [0.0, 400.0], ids=["offline", "poisson400"])
+def test_config4_full_trace(orc, trace, rate):
+    """Configuration 4 as stated: 256 requests, batch width 32, a 2048 MB pool of 24 fp16
+    layer slices, 14q/2kv heads, D 64, 24 layers of K/V write + grouped-query decode per
+    step on the GPU, offline and Poisson 400/s arrivals (bench_continuous.cu:25-107,
+    engine.h:100-148).  On the virtual clock continuous and static batching must make
+    the oracle's decisions step for step: iterations, tokens, slot steps, peak blocks,
+    average / p50 / p99 latency and the digest of every step's uploaded tables; the
+    reference trace offline gives the known 1801 / 3898 iterations."""
+    say(f"engine config 4: {trace} trace, rate {rate}")
+    if trace == "baseline":
+        p, g, a = W.baseline_trace(256, rate, 11)
+    else:
+        p, g, a = W.ref_trace(256, 256, 512, rate, 2024)
+    cfg = EngineConfig(n_heads=14, n_kv_heads=2, head_dim=64, block_size=16, num_blocks=C4_BLOCKS, max_batch=32,
+                       n_layers=24, dtype=KVC_F16, kv_write=True, clock_mode=1, virt_c0=COST[0],
+                       virt_c1=COST[1], virt_c2=COST[2])
+    eng = Engine(cfg)
+    co = run_continuous(p, g, a, eng)
+    rc, ref = orc.sim_engine(p, g, a, 16, C4_BLOCKS, 32, True, COST)
+    assert rc == 0
+    _same(co, ref)
+    st = run_static(p, g, a, eng, 32)
+    rc, ref_s, _ = orc.sim_static(p, g, a, 16, C4_BLOCKS, 32, True, COST)
+    assert rc == 0
+    _same(st, ref_s)
+    assert co.tokens == st.tokens == g.sum() and co.finished == st.finished == 256
+    print(f"continuous {co.iters} iters, peak {co.peak_blocks} blocks, p50/p99 {co.p50_latency_us:.0f}/"
+          f"{co.p99_latency_us:.0f} us; static {st.iters} iters, slot util {st.slot_util:.3f}")
+    if trace == "reference" and rate == 0.0:
+        assert co.iters == 1801 and st.iters == 3898 and round(100 * st.slot_util, 1) == 38.9
 
 
 def test_measured_clock_invariants(orc):
