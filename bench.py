@@ -474,7 +474,8 @@ def main() -> int:
     else:
         lens = np.full(128, int(round(Wl.ref_lengths().mean())), np.int32)
     N, Hq, Hkv, D, B = 128, 8, 8, 64, 16
-    split = a.split or ops.decode_auto_split(N, Hq, Hkv, D, B, int(lens.max()))
+    # device-lengths path: split 0 = the kernel plans its own chunks from the device lengths
+    split = a.split
     log(f"C2: N={N} sum_len={int(lens.sum())} max={int(lens.max())} split={split} rotate={a.rotate}")
     W = build_c2(lens, Hq, Hkv, D, B, a.rotate, seed=12345, shuffle=not a.no_shuffle)
     err, host_data = check_c2(W, lens, Hq, Hkv, D, B, split)
@@ -501,7 +502,8 @@ def main() -> int:
 
     t_raw, _ = time_decode(W, lens, Hq, Hkv, D, B, split, a.steps, a.warmup)   # ms per launch
     raw = total / (t_raw * 1e-3) / 1e9
-    log(f"C2 cold, device-lengths path (split {split}): {t_raw * 1e3:.2f} us/launch, {raw:.1f} GB/s")
+    log(f"C2 cold, device-lengths path ({'self-planned' if split == 0 else f'split {split}'}): "
+        f"{t_raw * 1e3:.2f} us/launch, {raw:.1f} GB/s")
     for tgt in [int(x) for x in a.plan_sweep.split(",") if x]:
         tp, nu, nr, _ = time_planned(W, lens, Hq, Hkv, D, B, 30, 5, target=tgt)
         sweep[f"plan{tgt}"] = round(tp * 1e3, 2)

@@ -6,8 +6,9 @@
 // unchanged.  Differences a caller can see:
 //   * each launcher returns the kvc_status (0 = ok) instead of void; the last
 //     failure message is kvc_last_error();
-//   * launch_batched_paged and launch_batched_paged_flash run the same kernel
-//     (online fp32 softmax with split-K), so they agree bit for bit;
+//   * launch_batched_paged and launch_batched_paged_flash are one entry point: the
+//     online fp32 softmax with split-K is the only implementation; the kernel plans
+//     its chunks from the device lengths, so `cap` only sizes the launch;
 //   * launch_flash_decode allocates nothing per call: its partials live in a
 //     grow-only library workspace (pass your own through kvc_flash_decode).
 // Optional trailing arguments select a stream (hipStream_t as void*).
@@ -77,13 +78,12 @@ inline int qk_paged_causal_attn(const half* q, half* out, const half* k_pool, co
                                  KVC_F16, nullptr, 0, stream);
 }
 
-// The reference sizes nothing by the longest sequence here; the split-K plan
-// needs an upper bound, so `cap` (max cur_len) is an extra trailing argument
-// with a generous default.
+// As the reference, no length bound: the kernel plans its own chunks from the
+// device lengths (cap 0 = unknown), so every sequence is attended over its whole
+// length.
 inline int qk_batched_paged_decode_attn(const half* q, half* out, const half* k_pool, const half* v_pool,
                                         const int* table_all, const int* tab_off, const int* cur_len, int N, int Hq,
-                                        int Hkv, int D, int BLOCK, float scale, int cap = 32768,
-                                        kvc_stream_t stream = nullptr) {
-    return kvc_batched_paged_decode(q, k_pool, v_pool, table_all, tab_off, cur_len, out, N, Hq, Hkv, D, BLOCK, cap,
+                                        int Hkv, int D, int BLOCK, float scale, kvc_stream_t stream = nullptr) {
+    return kvc_batched_paged_decode(q, k_pool, v_pool, table_all, tab_off, cur_len, out, N, Hq, Hkv, D, BLOCK, 0,
                                     scale, KVC_F16, nullptr, 0, stream);
 }

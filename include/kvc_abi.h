@@ -66,7 +66,11 @@ int         kvc_device_count(int* count);
  * "wg_per_cu" (cap on decode workgroups per CU through reserved LDS: -1
  * automatic, 0 none, n), "split_first" (planner: chunks of split sequences
  * before whole sequences), "mfma_min_chunk" (planner, grouped-query heads on the
- * matrix cores: tokens below which a sequence stays in one unit, default 1024).
+ * matrix cores: tokens below which a sequence stays in one unit, default 1024),
+ * "self_plan" (device-length decode with the automatic split: 1 = the kernel
+ * derives the planner's units from the device lengths, 0 = a chunk x sequence x
+ * head grid sized by cap), "self_grid" (self-planned launches: 0 = one workgroup
+ * per resident slot, n = at most n workgroups, each then serving several units).
  * The matrix-core path takes fp16 K/V, head_dim 64 or 128, 3..16 query heads per
  * KV head and, paged, a power-of-two BLOCK >= 16; other shapes use the VALU
  * kernels. */
@@ -120,6 +124,13 @@ int kvc_append(const void* k_new, const void* v_new, void* k_cache, void* v_cach
 int kvc_write_kv(const void* k, const void* v, void* k_pool, void* v_pool,
                  const int* block_table, int start_pos, int L, int Hkv, int D, int BLOCK,
                  int dtype, kvc_stream_t stream);
+
+/* qkcuda_write_kv (qwen_kernels.h:43-44, qwen_kernels.cu:128-143): kvc_write_kv with the
+ * start position read from device memory (*dev_start_pos), so a captured graph can be
+ * replayed at advancing positions.  Rows whose position is negative are skipped. */
+int kvc_write_kv_dev(const void* k, const void* v, void* k_pool, void* v_pool,
+                     const int* block_table, const int* dev_start_pos, int L, int Hkv, int D, int BLOCK,
+                     int dtype, kvc_stream_t stream);
 
 /* qk_batched_write_kv (qwen_kernels.h:30-32, qwen_kernels.cu:270-290): one token per
  * sequence, k/v [N,Hkv,D] -> pool at position wpos[r] of table table_all+tab_off[r].
@@ -257,6 +268,17 @@ int kvc_paged_causal_attn(const void* q, void* out, const void* k_pool, const vo
                           void* workspace, size_t workspace_bytes, kvc_stream_t stream);
 size_t kvc_paged_causal_attn_workspace_size(int q_pos_base, int Nq, int Hq, int Hkv, int D, int BLOCK, int dtype);
 
+/* qkcuda_paged_causal_attn (qwen_kernels.h:45-47, qwen_kernels.cu:187-226): as
+ * kvc_paged_causal_attn with the first query's position read from device memory
+ * (*dev_q_pos_base), for captured graphs.  The kernel plans its own chunks from that
+ * position (no host-side length); Nq <= 512 on the matrix-core path, 1024 otherwise,
+ * and BLOCK a power of two. */
+int kvc_paged_causal_attn_dev(const void* q, void* out, const void* k_pool, const void* v_pool,
+                              const int* block_table, const int* dev_q_pos_base, int Nq, int Hq, int Hkv, int D,
+                              int BLOCK, float scale, int dtype, void* workspace, size_t workspace_bytes,
+                              kvc_stream_t stream);
+size_t kvc_paged_causal_attn_dev_workspace_size(int Nq, int Hq, int Hkv, int D, int BLOCK, int dtype);
+
 /* ---- decoder-step operations around the attention path (a Qwen2-shaped layer) ----
  * fp16 activations and weights, fp32 arithmetic; row widths multiples of 8.
  * qk_embed_gather (qwen_kernels.h:7): out[L,H] = embed[ids[r]] (ids outside [0,V) give zeros).
@@ -277,6 +299,8 @@ int kvc_add_bias(void* x, const void* bias, int L, int N, kvc_stream_t stream);
 int kvc_add_residual(void* x, const void* y, size_t n, kvc_stream_t stream);
 int kvc_silu_mul(void* out, const void* gate, const void* up, size_t n, kvc_stream_t stream);
 int kvc_rope(void* x, const int* pos, int pos_base, int L, int n_heads, int D, float theta, kvc_stream_t stream);
+/* qkcuda_rope (qwen_kernels.h:42, qwen_kernels.cu:83-99): positions *dev_pos_base + r. */
+int kvc_rope_dev(void* x, const int* dev_pos_base, int L, int n_heads, int D, float theta, kvc_stream_t stream);
 int kvc_argmax(const float* logits, int L, int V, int* out, kvc_stream_t stream);
 int kvc_linear(void* y, const void* x, const void* w, int M, int N, int K, int out_dtype, kvc_stream_t stream);
 

@@ -107,6 +107,7 @@ _SIGS = {
     "kvc_fill_normal": (i32, [vp, sz, i32, u64, f32, vp]),
     "kvc_append": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, i32, vp]),
     "kvc_write_kv": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp]),
+    "kvc_write_kv_dev": (i32, [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp]),
     "kvc_batched_write_kv": (i32, [vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp]),
     "kvc_write_kv_slots": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp]),
     "kvc_decode": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, f32, i32, vp]),
@@ -127,12 +128,15 @@ _SIGS = {
         i32, [vp, vp, vp, vp, vp, vp, vp, i32, vp, i32, i32, i32, i32, i32, f32, i32, vp, i32, i32, vp, sz, vp]),
     "kvc_paged_causal_attn": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, f32, i32, vp, sz, vp]),
     "kvc_paged_causal_attn_workspace_size": (sz, [i32, i32, i32, i32, i32, i32, i32]),
+    "kvc_paged_causal_attn_dev": (i32, [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, f32, i32, vp, sz, vp]),
+    "kvc_paged_causal_attn_dev_workspace_size": (sz, [i32, i32, i32, i32, i32, i32]),
     "kvc_embed_gather": (i32, [vp, vp, vp, i32, i32, i32, vp]),
     "kvc_rmsnorm": (i32, [vp, vp, vp, i32, i32, f32, vp]),
     "kvc_add_bias": (i32, [vp, vp, i32, i32, vp]),
     "kvc_add_residual": (i32, [vp, vp, sz, vp]),
     "kvc_silu_mul": (i32, [vp, vp, vp, sz, vp]),
     "kvc_rope": (i32, [vp, vp, i32, i32, i32, i32, f32, vp]),
+    "kvc_rope_dev": (i32, [vp, vp, i32, i32, i32, f32, vp]),
     "kvc_argmax": (i32, [vp, i32, i32, vp, vp]),
     "kvc_linear": (i32, [vp, vp, vp, i32, i32, i32, i32, vp]),
     "kvc_rows_workspace_size": (sz, [i32, i32]),

@@ -576,6 +576,101 @@ int run_planned(const void* q, const void* k_new, const void* v_new, const int* 
     }
 }
 
+// ---- self-planned decode (device lengths, no host plan) -------------------
+// Every workgroup of a persistent grid derives the host planner's units from the
+// lengths in device memory (selfplan.hpp).  Available when the planner's shape pages
+// uniformly and the batch's lengths fit in LDS.
+constexpr int kSelfMaxNValuHost = 1024, kSelfMaxNMfmaHost = 512, kSelfRecordsPerHeadHost = 64;
+
+bool self_plan_ok(int N, int Hq, int Hkv, int D, int BLOCK, int dtype) {
+    if (N <= 0 || BLOCK <= 0 || (BLOCK & (BLOCK - 1)) || Hq <= 0 || Hkv <= 0 || Hq % Hkv || !d_ok(D) ||
+        !dtype_ok(dtype))
+        return false;
+    const PlanShape ps = plan_shape(Hq, Hkv, D, BLOCK, dtype);
+    if (!ps.uniform || ps.hks > 0xFFFF) return false;
+    if (N > (ps.mfma ? kSelfMaxNMfmaHost : kSelfMaxNValuHost)) return false;
+    // the units' record numbering stays inside int
+    return (long long)kSelfRecordsPerHeadHost * ps.hks * N + 1 < (1LL << 30);
+}
+
+// Records of a self-planned launch (64 per sequence and head).
+long long self_plan_records(int N, int Hq, int Hkv, int D, int BLOCK, int dtype) {
+    return (long long)kSelfRecordsPerHeadHost * plan_shape(Hq, Hkv, D, BLOCK, dtype).hks * N;
+}
+
+size_t self_plan_workspace(int N, int Hq, int Hkv, int D, int BLOCK, int dtype) {
+    return planned_workspace(Hq, Hkv, D, BLOCK, dtype, (int)self_plan_records(N, Hq, Hkv, D, BLOCK, dtype));
+}
+
+// Contiguous caches are planned with chunks cut at this granularity, the paged
+// path's usual block, so a paged batch with 16-token blocks and the same batch in
+// contiguous caches run the same chunks (bit-identical outputs).
+constexpr int kSelfContigBlock = 16;
+
+// cur_len: device lengths; or (cur_len == NULL) causal prompt queries, query s
+// attending to *dev_base + s + 1 keys of the one table at table_all.  cap > 0 only
+// sizes the grid (the units of lengths up to cap); 0: unknown.  contig: caches
+// [N, Hkv, MAXS, D] addressed by seq_stride / head_stride (BLOCK ignored).
+int run_self_planned(const void* q, const void* k, const void* v, const int* table_all, const int* tab_off,
+                     const int* cur_len, const int* dev_base, void* out, int N, int Hq, int Hkv, int D, int BLOCK,
+                     int cap, float scale, int dtype, void* ws, size_t ws_bytes, hipStream_t st, bool contig = false,
+                     long long seq_stride = 0, long long head_stride = 0) {
+    int rc = check_common(N, Hq, Hkv, D, dtype, q, k, v, out);
+    if (rc || N == 0) return rc;
+    if (contig) BLOCK = kSelfContigBlock;
+    if (!contig && !table_all) return set_error(KVC_ERR_ARG, "null block table");
+    if (!std::isfinite(scale)) return set_error(KVC_ERR_ARG, "scale must be finite");
+    const PlanShape ps = plan_shape(Hq, Hkv, D, BLOCK, dtype);
+    const long long recs = self_plan_records(N, Hq, Hkv, D, BLOCK, dtype);
+    const size_t need = self_plan_workspace(N, Hq, Hkv, D, BLOCK, dtype);
+    if (!ws) {
+        rc = default_workspace(need, st, &ws);
+        if (rc) return rc;
+    } else if (ws_bytes < need) {
+        return set_error(KVC_ERR_WORKSPACE, "workspace too small: need " + std::to_string(need) + " bytes, got " +
+                                                std::to_string(ws_bytes));
+    } else if (((uintptr_t)ws & 15u) != 0) {
+        return set_error(KVC_ERR_ARG, "workspace must be 16-byte aligned");
+    }
+    DecodeLaunch L{};
+    DecodeParams& p = L.p;
+    p.q = q; p.k = k; p.v = v; p.out = out;
+    p.table_all = contig ? nullptr : table_all; p.tab_off = contig ? nullptr : tab_off;
+    p.cur_len = cur_len; p.dev_base = dev_base;
+    p.causal = cur_len ? 0 : 1;
+    p.seq_stride = seq_stride; p.head_stride = head_stride;
+    p.table_len = 0x1FFFFFFF;  // the reference's signature carries no table length
+    p.N = N; p.Hq = Hq; p.Hkv = Hkv; p.block = BLOCK;
+    p.group = Hq / Hkv; p.nsub = ps.nsub;
+    p.chunk_tokens = 1; p.max_chunks = 1;
+    p.cap = contig ? (int)(head_stride / D) : INT_MAX;  // contiguous: a longer sequence would leave its cache
+    p.scale_log2 = scale * 1.4426950408889634f;
+    p.work = nullptr; p.work_ints = kPlanInts;
+    p.n_records = (int)recs;
+    p.lpb_shift = ilog2_exact(BLOCK / ps.tpw);  // uniform paging (self_plan_ok)
+    p.sp_slots = ps.slots; p.sp_min_chunk = ps.min_chunk; p.sp_max_chunk = ps.max_chunk;
+    p.sp_target_cap = ps.target_cap; p.sp_nc_max = ps.mfma ? kMfmaMaxFusedChunks : 0;
+    const size_t rall = (size_t)recs;
+    const size_t acc = align_up(rall * ps.G * D * sizeof(float), kAlign), ml = align_up(rall * ps.G * 2 * sizeof(float), kAlign);
+    p.part_acc = static_cast<float*>(ws);
+    p.part_ml = reinterpret_cast<float*>(static_cast<char*>(ws) + acc);
+    p.counters = reinterpret_cast<unsigned long long*>(static_cast<char*>(ws) + acc + ml);
+    p.epoch = next_epoch();
+    p.merge_mode = kMergeAtomic;
+    L.dtype = dtype; L.D = D; L.G = ps.G; L.mode = contig ? kSelfContig : kSelfPlanned; L.mfma = ps.mfma;
+    L.wg_per_cu = tuning().wg_per_cu >= 0 ? tuning().wg_per_cu : (!ps.mfma && ps.G <= 2 ? 6 : 0);
+    L.wpb = tuning().waves_per_block ? tuning().waves_per_block : ps.wpb;
+    L.batch = tuning().batch;
+    L.need_merge = false;
+    // grid: the units lengths up to cap can need (the planner's bound), else the
+    // record budget; the launch caps it at the resident workgroups
+    long long upper = recs;
+    if (cap > 0) upper = std::min(upper, (long long)ps.hks * N * ((long long)cap / std::max(ps.min_chunk, 1) + 2));
+    if (tuning().self_grid > 0) upper = std::min(upper, (long long)tuning().self_grid);
+    L.units = (int)std::min<long long>(std::max(upper, 1LL), INT_MAX);
+    return launch_decode(L, st);
+}
+
 }  // namespace
 }  // namespace kvc
 
@@ -740,6 +835,19 @@ int kvc_write_kv(const void* k, const void* v, void* k_pool, void* v_pool, const
     });
 }
 
+int kvc_write_kv_dev(const void* k, const void* v, void* k_pool, void* v_pool, const int* block_table,
+                     const int* dev_start_pos, int L, int Hkv, int D, int BLOCK, int dtype, kvc_stream_t st) {
+    return guarded([&]() -> int {
+        int rc = write_common(dtype, Hkv, D, k, v, k_pool, v_pool);
+        if (rc) return rc;
+        if (L < 0 || BLOCK <= 0) return set_error(KVC_ERR_ARG, "bad L / BLOCK");
+        if (L > 0 && (!block_table || !dev_start_pos)) return set_error(KVC_ERR_ARG, "null block table / start");
+        WriteParams p{k, v, k_pool, v_pool, block_table, nullptr, nullptr, L, Hkv, D, BLOCK, 0, 0, kWriteTable,
+                      dev_start_pos};
+        return launch_write(p, dtype, S(st));
+    });
+}
+
 int kvc_batched_write_kv(const void* k, const void* v, void* k_pool, void* v_pool, const int* table_all,
                          const int* tab_off, const int* wpos, int N, int Hkv, int D, int BLOCK, int dtype,
                          kvc_stream_t st) {
@@ -794,8 +902,14 @@ int kvc_batched_decode_split(const void* q, const void* k_cache, const void* v_c
                              int N, int Hq, int Hkv, int D, int MAXS, int cap, float scale, int dtype, int split,
                              void* ws, size_t ws_bytes, kvc_stream_t st) {
     return guarded([&]() -> int {
-        if (MAXS < 0 || cap > MAXS) return set_error(KVC_ERR_ARG, "cap must be <= MAXS");
+        if (MAXS < 0 || cap < 0 || cap > MAXS) return set_error(KVC_ERR_ARG, "cap must be in [0, MAXS]");
         if (N > 0 && !cur_len) return set_error(KVC_ERR_ARG, "null cur_len");
+        // automatic split: the kernel plans from the device lengths, with the chunks of
+        // the paged path (so paged and contiguous batches agree bit for bit)
+        if (split == 0 && tuning().self_plan != 0 && self_plan_ok(N, Hq, Hkv, D, kSelfContigBlock, dtype))
+            return run_self_planned(q, k_cache, v_cache, nullptr, nullptr, cur_len, nullptr, out, N, Hq, Hkv, D, 0,
+                                    cap, scale, dtype, ws, ws_bytes, S(st), true, (long long)Hkv * MAXS * D,
+                                    (long long)MAXS * D);
         return run_batched(q, k_cache, v_cache, nullptr, nullptr, cur_len, 0, out, N, Hq, Hkv, D, 0,
                            (long long)Hkv * MAXS * D, (long long)MAXS * D, cap, scale, dtype, split, false, ws,
                            ws_bytes, S(st));
@@ -815,6 +929,13 @@ int kvc_batched_paged_decode_split(const void* q, const void* k_pool, const void
                                    kvc_stream_t st) {
     return guarded([&]() -> int {
         if (N > 0 && (!tab_off || !cur_len)) return set_error(KVC_ERR_ARG, "null tab_off / cur_len");
+        if (cap < 0) return set_error(KVC_ERR_ARG, "cap must be >= 0");
+        // automatic split: the kernel plans from the device lengths (cap only a hint)
+        if (split == 0 && tuning().self_plan != 0 && self_plan_ok(N, Hq, Hkv, D, BLOCK, dtype))
+            return run_self_planned(q, k_pool, v_pool, table_all, tab_off, cur_len, nullptr, out, N, Hq, Hkv, D,
+                                    BLOCK, cap, scale, dtype, ws, ws_bytes, S(st));
+        if (cap == 0 && N > 0)
+            return set_error(KVC_ERR_ARG, "this shape needs cap, the longest length (no self-planned path for it)");
         return run_batched(q, k_pool, v_pool, table_all, tab_off, cur_len, 0, out, N, Hq, Hkv, D, BLOCK, 0, 0, cap,
                            scale, dtype, split, true, ws, ws_bytes, S(st));
     });
@@ -833,6 +954,25 @@ int kvc_paged_causal_attn(const void* q, void* out, const void* k_pool, const vo
         return run_batched(q, k_pool, v_pool, block_table, nullptr, nullptr, q_pos_base, out, Nq, Hq, Hkv, D, BLOCK,
                            0, 0, q_pos_base + Nq, scale, dtype, 0, true, ws, ws_bytes, S(st), 1);
     });
+}
+
+int kvc_paged_causal_attn_dev(const void* q, void* out, const void* k_pool, const void* v_pool, const int* block_table,
+                              const int* dev_q_pos_base, int Nq, int Hq, int Hkv, int D, int BLOCK, float scale,
+                              int dtype, void* ws, size_t ws_bytes, kvc_stream_t st) {
+    return guarded([&]() -> int {
+        if (Nq < 0) return set_error(KVC_ERR_ARG, "Nq must be >= 0");
+        if (Nq > 0 && !dev_q_pos_base) return set_error(KVC_ERR_ARG, "null q_pos_base pointer");
+        if (Nq > 0 && !self_plan_ok(Nq, Hq, Hkv, D, BLOCK, dtype))
+            return set_error(KVC_ERR_UNSUPPORTED, "device-position prompt attention needs a power-of-two BLOCK the "
+                                                  "kernels page uniformly and at most 512 queries");
+        return run_self_planned(q, k_pool, v_pool, block_table, nullptr, nullptr, dev_q_pos_base, out, Nq, Hq, Hkv,
+                                D, BLOCK, 0, scale, dtype, ws, ws_bytes, S(st));
+    });
+}
+
+size_t kvc_paged_causal_attn_dev_workspace_size(int Nq, int Hq, int Hkv, int D, int BLOCK, int dtype) {
+    if (!self_plan_ok(Nq, Hq, Hkv, D, BLOCK, dtype)) return 0;
+    return self_plan_workspace(Nq, Hq, Hkv, D, BLOCK, dtype);
 }
 
 size_t kvc_paged_causal_attn_workspace_size(int q_pos_base, int Nq, int Hq, int Hkv, int D, int BLOCK, int dtype) {
@@ -927,6 +1067,10 @@ int kvc_decode_plan_capacity(int N, long long total_tokens, int Hq, int Hkv, int
 
 size_t kvc_decode_workspace_size(int N, int Hq, int Hkv, int D, int BLOCK, int cap, int split, int dtype) {
     if (N <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || !d_ok(D) || cap < 0 || split < 0 || !dtype_ok(dtype)) return 0;
+    if (split == 0 && tuning().self_plan != 0) {
+        const int b = BLOCK > 0 ? BLOCK : kSelfContigBlock;
+        if (self_plan_ok(N, Hq, Hkv, D, b, dtype)) return self_plan_workspace(N, Hq, Hkv, D, b, dtype);
+    }
     return plan_batched(N, Hq, Hkv, D, BLOCK, cap, dtype, split, BLOCK > 0).ws_bytes;
 }
 
@@ -956,6 +1100,8 @@ int kvc_set_tuning(const char* key, int value) {
     else if (k == "wg_per_cu" && value >= -1 && value <= 32) tuning().wg_per_cu = value;
     else if (k == "split_first" && (value == 0 || value == 1)) tuning().split_first = value;
     else if (k == "mfma_min_chunk" && value >= 16 && value <= 1 << 20) tuning().mfma_min_chunk = value;
+    else if (k == "self_plan" && (value == 0 || value == 1)) tuning().self_plan = value;
+    else if (k == "self_grid" && value >= 0) tuning().self_grid = value;
     else return set_error(KVC_ERR_ARG, "unknown tuning key or bad value: " + k);
     return KVC_OK;
 }
@@ -973,6 +1119,8 @@ int kvc_get_tuning(const char* key, int* value) {
     else if (k == "wg_per_cu") *value = tuning().wg_per_cu;
     else if (k == "split_first") *value = tuning().split_first;
     else if (k == "mfma_min_chunk") *value = tuning().mfma_min_chunk;
+    else if (k == "self_plan") *value = tuning().self_plan;
+    else if (k == "self_grid") *value = tuning().self_grid;
     else return set_error(KVC_ERR_ARG, "unknown tuning key: " + k);
     return KVC_OK;
 }

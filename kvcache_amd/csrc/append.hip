@@ -7,7 +7,8 @@
 // wave64 moves eight 128-byte fp16 D=64 rows per instruction, K and V together.
 // Destination row per mode:
 //   kWriteAppend  : cache[h, start_pos, :] of [H, S, D]            (kv_cache.cu:5-13)
-//   kWriteTable   : pool row of position start_pos + r via table    (qwen_kernels.cu:111-122)
+//   kWriteTable   : pool row of position start_pos + r via table    (qwen_kernels.cu:111-122;
+//                   start_pos from device memory: kcuda_write_kv, qwen_kernels.cu:128-143)
 //   kWriteBatched : pool row of position wpos[r] via table_all+tab_off[r] (qwen_kernels.cu:270-285)
 //   kWriteSlots   : pool row of slot_map[r] = phys*BLOCK + in        (slot-mapped form)
 // Rows whose position / slot is negative are skipped.
@@ -42,7 +43,8 @@ __global__ __launch_bounds__(256) void write_kernel(WriteParams p, int vpr) {
             int pos;
             const int* table = p.table;
             if (p.mode == kWriteTable) {
-                pos = p.start_pos + r;
+                pos = (p.dev_start ? *p.dev_start : p.start_pos) + r;
+                if (pos < 0) return;
             } else {
                 pos = p.idx[r];
                 if (pos < 0) return;

@@ -153,7 +153,7 @@ __device__ __forceinline__ int seq_len(const DecodeParams& p, int s) {
 
 // Chunk c of a sequence of L tokens.
 __device__ __forceinline__ bool chunk_range_of(const DecodeParams& p, int L, int c, int& nc, int& j0, int& j1) {
-    L = min(max(L, 0), p.cap);  // a length above the stated cap never reads past the caches
+    L = min(max(L, 0), p.cap);  // (longer sequences never get here: their units write NaN)
     if (p.num_splits > 0) {
         nc = p.num_splits;
         const int ch = (L + nc - 1) / nc;
@@ -309,8 +309,18 @@ __device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, int vof
 struct Unit {
     int s, hk, sub, c, nc, j0, j1, tab_start;
     int n_inline = 0;  // planned grouped-query units: block ids carried in the entry
+    bool over_cap = false;  // device-length grid: the sequence is longer than the stated cap
     size_t rec0, cstride, ctr_idx;
 };
+
+// NaN in the output rows of `heads` query heads from hq0 of sequence s: what a
+// sequence longer than the launch's stated cap gets instead of a silently
+// truncated attention.
+template <typename T, int D, int NT>
+__device__ void nan_rows(const DecodeParams& p, int s, int hq0, int heads) {
+    T* ob = static_cast<T*>(p.out) + ((size_t)s * p.Hq + hq0) * D;
+    for (int e = threadIdx.x; e < heads * D; e += NT) ob[e] = (T)__builtin_nanf("");
+}
 
 // The 8-int header of this workgroup's planned entry.  The kernels take the work
 // list as their first, register-preloaded arguments and read the header before
@@ -379,6 +389,10 @@ __device__ __forceinline__ bool load_unit(const DecodeParams& p, const int (&h)[
         const int lu = uniform(h[0]);
         const int L = p.cur_len ? lu : (p.causal ? p.fixed_len + u.s + 1 : p.fixed_len);
         u.tab_start = uniform(h[1]);
+        if (L > p.cap) {  // the grid and workspace do not cover it: chunk 0's unit writes NaN
+            u.over_cap = u.c == 0;
+            return false;
+        }
         if (!chunk_range_of(p, L, u.c, u.nc, u.j0, u.j1)) return false;
         u.rec0 = ((size_t)u.s * p.max_chunks + u.c) * p.Hq + u.hk * p.group + u.sub * heads;
         u.cstride = p.Hq;
@@ -386,6 +400,8 @@ __device__ __forceinline__ bool load_unit(const DecodeParams& p, const int (&h)[
         return true;
     }
 }
+
+#include "selfplan.hpp"
 
 // Largest chunk, in blocks, the per-lane paged path stages in LDS.
 constexpr int kMaxChunkBlocks = 4096;
@@ -409,30 +425,34 @@ __global__ __launch_bounds__(WPB * kWave) void split_kernel(const int* __restric
     constexpr int TPW = kWave / LPT;  // rows (tokens) per wave-wide load
     constexpr int ROW = D * (int)sizeof(T);  // bytes per K/V row
     static_assert(LPT >= 1 && LPT <= kWave && D % EPL == 0, "unsupported head_dim");
-    constexpr bool PLANNED = MODE == kPlannedUniform || MODE == kPlannedPerLane;
-    constexpr bool UNIFORM = MODE == kPagedUniform || MODE == kPlannedUniform;
+    constexpr bool SELF = MODE == kSelfPlanned || MODE == kSelfContig;
+    constexpr bool CONTIG = MODE == kContiguous || MODE == kSelfContig;
+    constexpr bool PLANNED = MODE == kPlannedUniform || MODE == kPlannedPerLane || SELF;
+    constexpr bool UNIFORM = MODE == kPagedUniform || MODE == kPlannedUniform || SELF;
     constexpr bool PER_LANE = MODE == kPagedPerLane || MODE == kPlannedPerLane;
     __shared__ float s_acc[WPB][G][D];
     __shared__ float s_m[WPB][G], s_l[WPB][G];
     __shared__ int s_tab[PER_LANE ? kMaxChunkBlocks : 1];
+    __shared__ std::conditional_t<SELF, SelfPlanLds<kSelfMaxNValu>, char> s_plan;
 
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = uniform(threadIdx.x >> 6);
+
+    // One unit, given its entry header (hdr) and, on the host-planned path, the
+    // entry's block ids (ev: one int per lane after the 8-int header).
+    auto run_unit = [&](const int (&hdr)[8], const int ev) {
+    // per-lane indices derived anew in every unit: in the persistent loop they would
+    // otherwise be hoisted out of it and held in registers across the whole loop
+    int tid_u = threadIdx.x;
+    if constexpr (SELF) asm volatile("" : "+v"(tid_u));
+    const int lane = tid_u & (kWave - 1);
     const int tslot = lane / LPT;
     const int dl = lane % LPT;
-
-    // planned entries may carry the chunk's first block ids after the 8-int header
-    // (one int per lane, read together with the header), so the first batch of
-    // loads does not wait for the table
-    int ev = 0;
-    if constexpr (PLANNED && UNIFORM) {
-        if (work_ints > 8 && lane < work_ints) ev = work[(size_t)blockIdx.x * work_ints + lane];
-    }
-    int hdr[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    if constexpr (PLANNED) read_header(work, work_ints, hdr);
-    else read_seq<MODE != kContiguous>(p, hdr);
     Unit u;
-    if (!load_unit<PLANNED, MODE != kContiguous>(p, hdr, G, u)) return;
+    if (!load_unit<PLANNED, !CONTIG>(p, hdr, G, u)) {
+        if (u.over_cap) nan_rows<T, D, WPB * kWave>(p, u.s, u.hk * p.group + u.sub * G, G);
+        return;
+    }
     const int s = u.s, hk = u.hk, sub = u.sub, c = u.c, nc = u.nc, j0 = u.j0, j1 = u.j1;
     const int tab_start = u.tab_start;
     const int n_inl = u.n_inline;  // block ids carried by the planned entry
@@ -474,7 +494,7 @@ __global__ __launch_bounds__(WPB * kWave) void split_kernel(const int* __restric
             wp = (w >= j0 && w < j1) ? w : -1;
         }
     }
-    if constexpr (MODE == kContiguous) {
+    if constexpr (CONTIG) {
         cbase = ((size_t)s * p.seq_stride + (size_t)hk * p.head_stride) * sizeof(T);
     } else {
         // blocks the chunk touches (0 for an empty chunk); the planner keeps this
@@ -534,7 +554,7 @@ __global__ __launch_bounds__(WPB * kWave) void split_kernel(const int* __restric
                 asm("" : "+s"(rows));
                 rows = min(rows, TPW);
                 size_t tile;
-                if constexpr (MODE == kContiguous) {
+                if constexpr (CONTIG) {
                     tile = cbase + (size_t)max(t0, 0) * ROW;
                 } else {
                     const int rel = i >> p.lpb_shift;           // block of the chunk
@@ -685,6 +705,27 @@ __global__ __launch_bounds__(WPB * kWave) void split_kernel(const int* __restric
         for (int g = 0; g < G; ++g) merge_head<T, D, false>(p, first + g, cstride, nc, ob + (size_t)g * D, lane);
     }
     if (lane == 0) __hip_atomic_store(ctr, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };  // run_unit
+
+    if constexpr (SELF) {
+        self_plan_setup<WPB * kWave>(p, s_plan);
+        for (int k = 0, r = self_plan_rank(0); r < s_plan.units; r = self_plan_rank(++k)) {
+            int hdr[8];
+            if (self_plan_unit<T, D, WPB * kWave>(p, s_plan, r, G, hdr)) run_unit(hdr, 0);
+        }
+    } else {
+        // planned entries may carry the chunk's first block ids after the 8-int
+        // header (one int per lane, read together with the header), so the first
+        // batch of loads does not wait for the table
+        int ev = 0;
+        if constexpr (PLANNED && UNIFORM) {
+            if (work_ints > 8 && lane < work_ints) ev = work[(size_t)blockIdx.x * work_ints + lane];
+        }
+        int hdr[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        if constexpr (PLANNED) read_header(work, work_ints, hdr);
+        else read_seq<!CONTIG>(p, hdr);
+        run_unit(hdr, ev);
+    }
 }
 
 // Standalone log-sum-exp merge: one 512-thread workgroup per (sequence, query
@@ -722,7 +763,7 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(DecodeParams p) {
     }
     int nc, j0, j1;
     chunk_range(p, s, 0, nc, j0, j1);
-    if (nc <= 1) return;
+    if (nc <= 1 || seq_len(p, s) > p.cap) return;  // one chunk, or NaN rows from the split kernel
 
     float M = -FLT_MAX;
 #pragma unroll
@@ -806,6 +847,31 @@ unsigned lds_pad(K kernel, int wg_per_cu) {
     return wg_per_cu > 0 ? lds_pad_for(reinterpret_cast<const void*>(kernel), wg_per_cu) : 0u;
 }
 
+// Workgroups of `kernel` resident on the whole device at once (block threads,
+// `lds` bytes of dynamic LDS): the size of a persistent grid.
+inline long long resident_blocks_for(const void* kernel, int block, unsigned lds) {
+    static std::mutex mu;
+    static std::unordered_map<const void*, std::unordered_map<unsigned, long long>> cache;
+    std::lock_guard<std::mutex> lk(mu);
+    auto& per = cache[kernel];
+    auto it = per.find(lds);
+    if (it != per.end()) return it->second;
+    int dev = 0, cus = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        cus = 256;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, block, lds) != hipSuccess || n <= 0) n = 1;
+    return per[lds] = (long long)n * cus;
+}
+
+// Grid of a self-planned launch: at most the units it can have, at most one
+// workgroup per resident slot.
+template <typename K>
+dim3 self_grid(K kernel, int block, unsigned lds, dim3 upper) {
+    const long long r = resident_blocks_for(reinterpret_cast<const void*>(kernel), block, lds);
+    return dim3((unsigned)std::max(1LL, std::min((long long)upper.x, r)));
+}
+
 template <typename T, int D, int G, int WPB, int U>
 int launch_split_mode(DecodeLaunch L, dim3 grid, hipStream_t st) {
     const dim3 block(WPB * kWave);
@@ -815,6 +881,18 @@ int launch_split_mode(DecodeLaunch L, dim3 grid, hipStream_t st) {
         case kPagedPerLane: L.lds_pad = lds_pad(split_kernel<T, D, G, kPagedPerLane, WPB, U>, L.wg_per_cu); hipLaunchKernelGGL((split_kernel<T, D, G, kPagedPerLane, WPB, U>), grid, block, L.lds_pad, st, L.p.work, L.p.work_ints, L.p); break;
         case kPlannedUniform: L.lds_pad = lds_pad(split_kernel<T, D, G, kPlannedUniform, WPB, U>, L.wg_per_cu); hipLaunchKernelGGL((split_kernel<T, D, G, kPlannedUniform, WPB, U>), grid, block, L.lds_pad, st, L.p.work, L.p.work_ints, L.p); break;
         case kPlannedPerLane: L.lds_pad = lds_pad(split_kernel<T, D, G, kPlannedPerLane, WPB, U>, L.wg_per_cu); hipLaunchKernelGGL((split_kernel<T, D, G, kPlannedPerLane, WPB, U>), grid, block, L.lds_pad, st, L.p.work, L.p.work_ints, L.p); break;
+        case kSelfPlanned:
+            L.lds_pad = lds_pad(split_kernel<T, D, G, kSelfPlanned, WPB, U>, L.wg_per_cu);
+            hipLaunchKernelGGL((split_kernel<T, D, G, kSelfPlanned, WPB, U>),
+                               self_grid(split_kernel<T, D, G, kSelfPlanned, WPB, U>, block.x, L.lds_pad, grid), block,
+                               L.lds_pad, st, L.p.work, L.p.work_ints, L.p);
+            break;
+        case kSelfContig:
+            L.lds_pad = lds_pad(split_kernel<T, D, G, kSelfContig, WPB, U>, L.wg_per_cu);
+            hipLaunchKernelGGL((split_kernel<T, D, G, kSelfContig, WPB, U>),
+                               self_grid(split_kernel<T, D, G, kSelfContig, WPB, U>, block.x, L.lds_pad, grid), block,
+                               L.lds_pad, st, L.p.work, L.p.work_ints, L.p);
+            break;
         default: return set_error(KVC_ERR_ARG, "unknown decode mode");
     }
     return KVC_OK;
@@ -867,6 +945,18 @@ int launch_gqa_mode(DecodeLaunch L, dim3 grid, hipStream_t st) {
         case kPagedUniform:   L.lds_pad = lds_pad(gqa_mfma_kernel<D, kPagedUniform, WPB>, L.wg_per_cu); hipLaunchKernelGGL((gqa_mfma_kernel<D, kPagedUniform, WPB>), grid, block, L.lds_pad, st, L.p.work, L.p.work_ints, L.p); break;
         case kPlannedUniform: L.lds_pad = lds_pad(gqa_mfma_kernel<D, kPlannedUniform, WPB>, L.wg_per_cu); hipLaunchKernelGGL((gqa_mfma_kernel<D, kPlannedUniform, WPB>), grid, block, L.lds_pad, st, L.p.work, L.p.work_ints, L.p); break;
         case kCausalTile:     hipLaunchKernelGGL((gqa_mfma_kernel<D, kCausalTile, WPB>), grid, block, 0, st, L.p.work, L.p.work_ints, L.p); break;
+        case kSelfPlanned:
+            L.lds_pad = lds_pad(gqa_mfma_kernel<D, kSelfPlanned, WPB>, L.wg_per_cu);
+            hipLaunchKernelGGL((gqa_mfma_kernel<D, kSelfPlanned, WPB>),
+                               self_grid(gqa_mfma_kernel<D, kSelfPlanned, WPB>, block.x, L.lds_pad, grid), block,
+                               L.lds_pad, st, L.p.work, L.p.work_ints, L.p);
+            break;
+        case kSelfContig:
+            L.lds_pad = lds_pad(gqa_mfma_kernel<D, kSelfContig, WPB>, L.wg_per_cu);
+            hipLaunchKernelGGL((gqa_mfma_kernel<D, kSelfContig, WPB>),
+                               self_grid(gqa_mfma_kernel<D, kSelfContig, WPB>, block.x, L.lds_pad, grid), block,
+                               L.lds_pad, st, L.p.work, L.p.work_ints, L.p);
+            break;
         default: return set_error(KVC_ERR_ARG, "matrix-core decode: unsupported addressing mode");
     }
     return KVC_OK;
@@ -889,7 +979,9 @@ int launch_gqa(const DecodeLaunch& L, dim3 grid, hipStream_t st) {
 
 template <typename T, int D>
 int launch_decode_d(const DecodeLaunch& L, hipStream_t st) {
-    const bool planned = L.mode == kPlannedUniform || L.mode == kPlannedPerLane;
+    // planned: the work list's units; self-planned: an upper bound of its units
+    const bool planned = L.mode == kPlannedUniform || L.mode == kPlannedPerLane || L.mode == kSelfPlanned ||
+                         L.mode == kSelfContig;
     const long long units = planned ? (long long)L.units
                           : L.mode == kCausalTile ? (long long)L.p.max_chunks * ((L.p.N + 15) / 16) * L.p.Hq
                                                   : (long long)L.p.max_chunks * L.p.N * L.p.Hkv * L.p.nsub;

@@ -61,8 +61,10 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(const int* __rest
     constexpr int KJ = D / 32;                 // MFMA k-steps over the head dimension
     constexpr int NT = D / 16;                 // 16-dim output column tiles
     constexpr int VL = 16 * ROW / 1024;        // 1 KiB wave loads per 16-row V subtile
-    constexpr bool PLANNED = MODE == kPlannedUniform;
-    constexpr bool PAGED = MODE != kContiguous;
+    constexpr bool SELF = MODE == kSelfPlanned || MODE == kSelfContig;
+    constexpr bool PLANNED = MODE == kPlannedUniform || SELF;
+    constexpr bool CONTIG = MODE == kContiguous || MODE == kSelfContig;
+    constexpr bool PAGED = !CONTIG;
     // prompt attention: the 16 columns are 16 consecutive queries of one head (not
     // the heads of one query); query q attends to positions 0 .. fixed_len + q
     constexpr bool CAUSAL = MODE == kCausalTile;
@@ -74,23 +76,23 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(const int* __rest
     __shared__ float s_w[kMfmaMaxHeads][kMaxFusedChunks];
     __shared__ float s_L[kMfmaMaxHeads];
     __shared__ int s_last;
+    __shared__ std::conditional_t<SELF, SelfPlanLds<kSelfMaxNMfma>, char> s_plan;
 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
-    // planned entries carry the unit's block ids after the 8-int header (one int per
-    // lane): entry and header are read first, from the preloaded arguments
-    int ev = 0;
-    int hdr[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    if constexpr (PLANNED) {
-        if (work_ints == kWave) ev = work[(size_t)blockIdx.x * kWave + lane];
-        read_header(work, work_ints, hdr);
-    } else if constexpr (!CAUSAL) {
-        read_seq<PAGED>(p, hdr);
-    }
     const int wave = uniform(tid >> 6);
+    const int heads = p.group;   // query heads of the KV group, <= 16 (host-checked)
+
+    // One unit, given its entry header (hdr) and, on the host-planned path, the
+    // entry's block ids (ev: one int per lane after the 8-int header).
+    auto run_unit = [&](const int (&hdr)[8], const int ev) {
+    // per-lane indices derived anew in every unit (not hoisted out of the persistent
+    // loop and held across it)
+    int tid_u = tid;
+    if constexpr (SELF) asm volatile("" : "+v"(tid_u));
+    const int lane = tid_u & (kWave - 1);
     const int n16 = lane & 15;   // head (S layout) / output column within a tile
     const int g4 = lane >> 4;    // lane group
-    const int heads = p.group;   // query heads of the KV group, <= 16 (host-checked)
     Unit u;
     int qh = 0, q0 = 0;  // causal: query head and first query of the tile
     if constexpr (CAUSAL) {
@@ -110,7 +112,10 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(const int* __rest
         u.nc = (lmax + p.chunk_tokens - 1) / p.chunk_tokens;  // chunks of the tile's last query
         u.rec0 = 0; u.cstride = 0; u.ctr_idx = 0;
     } else {
-        if (!load_unit<PLANNED, PAGED>(p, hdr, heads, u)) return;
+        if (!load_unit<PLANNED, PAGED>(p, hdr, heads, u)) {
+            if (u.over_cap) nan_rows<_Float16, D, WPB * kWave>(p, u.s, u.hk * p.group, heads);
+            return;
+        }
     }
     const int s = u.s, hk = u.hk, j0 = u.j0, j1 = u.j1, nc = u.nc;
     const int hq0 = hk * p.group;
@@ -168,7 +173,7 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(const int* __rest
     const int b0 = PAGED ? j0 >> bsh : 0;
     int nblk = 0;
     bool inl = false;  // block ids from the entry (no table read, no LDS staging)
-    if constexpr (MODE == kContiguous) {
+    if constexpr (CONTIG) {
         cbase = ((size_t)s * p.seq_stride + (size_t)hk * p.head_stride) * 2;
     } else {
         nblk = min(j1 > j0 ? ((j1 - 1) >> bsh) - b0 + 1 : 0, kMfmaMaxChunkBlocks);
@@ -205,7 +210,7 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(const int* __rest
     // land on a register whose load is still in flight and make the issue wait.
     const unsigned blk_bytes = (unsigned)p.block * ROW;
     auto subtile = [&](int t) -> size_t {
-        if constexpr (MODE == kContiguous) {
+        if constexpr (CONTIG) {
             return cbase + (size_t)t * ROW;
         } else {
             const int rel = min(max((t >> bsh) - b0, 0), max(nblk - 1, 0));
@@ -500,4 +505,25 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(const int* __rest
     if (D == 128 || ncm <= 16) merge_out(std::integral_constant<int, 16>{});
     else merge_out(std::integral_constant<int, 32>{});
     if (tid == 0) __hip_atomic_store(ctr, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };  // run_unit
+
+    if constexpr (SELF) {
+        self_plan_setup<WPB * kWave>(p, s_plan);
+        for (int k = 0, r = self_plan_rank(0); r < s_plan.units; r = self_plan_rank(++k)) {
+            int hdr[8];
+            if (self_plan_unit<_Float16, D, WPB * kWave>(p, s_plan, r, heads, hdr)) run_unit(hdr, 0);
+        }
+    } else {
+        // planned entries carry the unit's block ids after the 8-int header (one int
+        // per lane): entry and header are read first, from the preloaded arguments
+        int ev = 0;
+        int hdr[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        if constexpr (PLANNED) {
+            if (work_ints == kWave) ev = work[(size_t)blockIdx.x * kWave + lane];
+            read_header(work, work_ints, hdr);
+        } else if constexpr (!CAUSAL) {
+            read_seq<PAGED>(p, hdr);
+        }
+        run_unit(hdr, ev);
+    }
 }

@@ -21,8 +21,14 @@ int hip_check(hipError_t e, const char* what);
 // (chunk, sequence, head) decomposition; otherwise as kPaged*.
 // kCausalTile (matrix-core kernel only): prompt attention, a unit is 16 consecutive
 // queries of one query head over one chunk of keys of the shared block table.
+// kSelfPlanned: lengths in device memory; every workgroup of a persistent grid
+// derives the host planner's units itself (selfplan.hpp) and serves ranks
+// blockIdx.x, blockIdx.x + gridDim.x, ... (uniform paging, as kPlannedUniform).
+// kSelfContig: the same over contiguous caches [N, Hkv, MAXS, D], with chunks cut at
+// the paged path's 16-token block granularity, so paged and contiguous batches run
+// the same chunks and agree bit for bit.
 enum DecodeMode { kContiguous = 0, kPagedUniform = 1, kPagedPerLane = 2, kPlannedUniform = 3, kPlannedPerLane = 4,
-                  kCausalTile = 5 };
+                  kCausalTile = 5, kSelfPlanned = 6, kSelfContig = 7 };
 
 struct DecodeParams {
     // scalars first: everything a workgroup needs to locate its unit lies in the
@@ -35,7 +41,7 @@ struct DecodeParams {
     int max_chunks;           // chunks per sequence covered by the grid
     int fixed_len;            // length used when cur_len == nullptr
     int causal;               // 1: sequence s has length fixed_len + s + 1 (prompt queries, causal mask)
-    int cap;                  // lengths are clamped to cap (the caller's stated maximum)
+    int cap;                  // the caller's stated maximum length: a longer sequence gets NaN outputs
     int lpb_shift;            // kPagedUniform: log2(wave-loads per block)
     float scale_log2;         // softmax scale * log2(e)
     unsigned epoch;           // per-call tag of the arrival counters
@@ -65,6 +71,12 @@ struct DecodeParams {
     const void* k_new;
     const void* v_new;
     const int* wpos;
+    // kSelfPlanned: the planner's shape (plan_shape in abi.hip) and, for prompt
+    // queries whose first position lives in device memory, that position (query s
+    // then attends to *dev_base + s + 1 keys; causal must be 1)
+    int sp_slots, sp_min_chunk, sp_max_chunk, sp_target_cap;
+    int sp_nc_max;            // chunks per sequence the merge can combine (0: any)
+    const int* dev_base;
 };
 
 // How the chunk partials of a split sequence are combined.
@@ -113,6 +125,10 @@ struct Tuning {
                                 // 0: no cap; -1: automatic (4 on the planned one/two-head path)
     int split_first = 1;        // planner: chunks of split sequences before whole sequences
     int mfma_min_chunk = 1024;  // planner, grouped-query path: tokens below which a sequence stays in one unit
+    int self_plan = 1;          // device-length decode with an automatic split: 1 the kernel plans its own
+                                // units (selfplan.hpp), 0 the chunk x sequence x head grid
+    int self_grid = 0;          // self-planned launches: 0 automatic (resident workgroups), n: at most n
+                                // workgroups (each then serves several ranks, in rounds)
 };
 // Dynamic LDS that caps decode workgroups per CU at wg_per_cu (0: none).
 size_t occupancy_lds(size_t static_lds, int wg_per_cu);
@@ -131,6 +147,7 @@ struct WriteParams {
     const int* tab_off;  // kWriteBatched
     const int* idx;      // kWriteBatched: wpos[rows]; kWriteSlots: slot_map[rows]
     int rows, heads, D, block, start_pos, S, mode;
+    const int* dev_start = nullptr;  // kWriteTable: start position read from device memory
 };
 int launch_write(const WriteParams& p, int dtype, hipStream_t stream);
 

@@ -114,14 +114,15 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(_Float16* out, const
 // row r sits at position pos[r] (or pos_base + r); for t < D/2 the pair
 // (x_t, x_{t+D/2}) turns by angle pos * theta^(-2t/D).
 __global__ __launch_bounds__(kThreads) void rope_kernel(_Float16* x, const int* pos, int pos_base, size_t pairs,
-                                                        int heads, int D, float log2_theta) {
+                                                        int heads, int D, float log2_theta,
+                                                        const int* dev_base = nullptr) {
     const size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x;
     if (i >= pairs) return;
     const int hd = D / 2;
     const int t = (int)(i % hd);
     const size_t rh = i / hd;  // row * heads + head
     const int r = (int)(rh / heads);
-    const float p = (float)(pos ? pos[r] : pos_base + r);
+    const float p = (float)(pos ? pos[r] : (dev_base ? *dev_base : pos_base) + r);
     const float inv = exp2f(-log2_theta * (2.0f * (float)t / (float)D));
     float s, c;
     sincosf(p * inv, &s, &c);
@@ -272,6 +273,18 @@ int kvc_rope(void* x, const int* pos, int pos_base, int L, int n_heads, int D, f
         const size_t pairs = (size_t)L * n_heads * (D / 2);
         hipLaunchKernelGGL(rope_kernel, dim3(blocks_for(pairs)), dim3(kThreads), 0, (hipStream_t)st, (_Float16*)x, pos,
                            pos_base, pairs, n_heads, D, log2f(theta));
+        return hip_check(hipGetLastError(), "rope launch");
+    });
+}
+
+int kvc_rope_dev(void* x, const int* dev_pos_base, int L, int n_heads, int D, float theta, kvc_stream_t st) {
+    return guard_model([&]() -> int {
+        if (L < 0 || n_heads <= 0 || D <= 0 || D % 2 || !(theta > 1.f)) return set_error(KVC_ERR_ARG, "rope: bad shape");
+        if (L == 0) return KVC_OK;
+        if (!x || !dev_pos_base) return set_error(KVC_ERR_ARG, "rope: null pointer");
+        const size_t pairs = (size_t)L * n_heads * (D / 2);
+        hipLaunchKernelGGL(rope_kernel, dim3(blocks_for(pairs)), dim3(kThreads), 0, (hipStream_t)st, (_Float16*)x,
+                           nullptr, 0, pairs, n_heads, D, log2f(theta), dev_pos_base);
         return hip_check(hipGetLastError(), "rope launch");
     });
 }

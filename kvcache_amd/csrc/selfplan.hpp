@@ -1,0 +1,299 @@
+// selfplan.hpp -- decode units planned by the kernel from lengths in device memory.
+//
+// Included by decode_kernels.hpp inside namespace kvc::{anonymous}; uses its helpers.
+//
+// The reference's launchers take the lengths as a device array
+// (launch_batched_paged, batched.cu:140-147; qk_batched_paged_decode_attn,
+// qwen_kernels.cu:293-326), so the host cannot plan the launch without a copy and
+// a synchronisation.  Instead every workgroup of a persistent grid derives the
+// host planner's work (kvc_decode_plan: the same chunk target, the same chunks,
+// the same partial-record and counter numbering) from the lengths, orders the units
+// as the planner does -- chunks of split sequences first, then by length, longest
+// first (64 length buckets relative to the chunk target) -- and serves ranks in
+// rounds of gridDim.x (self_plan_rank).  Every workgroup computes the same order
+// from the same data, so each unit runs exactly once.  Per workgroup: one round of
+// loads (lengths, table offsets) into LDS, two reductions and a key histogram; per
+// rank, one block-wide scan over the sequences.  Outputs equal the host-planned
+// launch's on the same lengths bit for bit (same chunks, same merge order); only the
+// order in which units run differs within a length bucket.
+//
+// Budget: every (sequence, KV head) may use up to 64 partial records, and on the
+// matrix-core path a sequence has at most 64 chunks; the chunk target is raised
+// when the lengths need it (mean length / 63, longest length / 63).  A batch that
+// cannot fit even at the largest chunk (mean context above 63 largest chunks), or
+// with a length past its contiguous cache (p.cap), gets NaN outputs: never a
+// silent partial attention.
+
+constexpr int kSelfMaxNValu = 1024;    // sequences per launch (their plan rows live in LDS)
+constexpr int kSelfMaxNMfma = 512;     // (keeps two matrix-core workgroups per CU)
+constexpr int kSelfBuckets = 64;       // length buckets per split flag
+constexpr int kSelfKeys = 2 * kSelfBuckets;
+constexpr int kSelfRecordsPerHead = 64;
+constexpr int kSelfMaxChunks = 0xFFFF;  // chunks of one sequence (16-bit plan field)
+
+template <int NMAX>
+struct SelfPlanLds {
+    int len[NMAX];             // attended length of each sequence (>= 0)
+    int to[NMAX];              // first table entry of each sequence
+    int cut[NMAX];             // chunks | chunk length in blocks << 16
+    int keys[NMAX];            // key of chunks 0..nc-2 | key of the last chunk << 8
+    int count[kSelfKeys];      // units per order key
+    int base[kSelfKeys];       // rank of the first unit of each key (descending keys)
+    int part[3][16];           // per-wave partial sums of the block scans
+    double tot[16];            // per-wave sums of max(L, 1)
+    int lmax[16];
+    int hdr[8];                // the current rank's unit
+    int T, units, overflow;
+};
+
+__device__ __forceinline__ int wave_incl_scan(int x) {
+    const int lane = __lane_id();
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+        const int y = __builtin_amdgcn_ds_bpermute((lane - o) << 2, x);
+        x += lane >= o ? y : 0;
+    }
+    return x;
+}
+
+// ceil(a / b) for 0 <= a < 2^53, 0 < b < 2^31 (uniform operands: a double quotient
+// corrected to the exact integer, instead of a 64-bit integer division)
+__device__ __forceinline__ long long ceil_div_u(long long a, long long b) {
+    long long q = (long long)((double)a / (double)b);
+    while (q * b < a) ++q;
+    while (q > 0 && (q - 1) * b >= a) --q;
+    return q;
+}
+
+// Chunks of a sequence of L tokens at chunk target T (make_plan in abi.hip), in
+// 32-bit unsigned arithmetic (L < 2^31, T < 2^30).  BLOCK is a power of two.
+__device__ __forceinline__ void self_split(const DecodeParams& p, int L, int T, int bsh, int& nc, int& chunk) {
+    nc = 1;
+    chunk = max(L, 1);
+    const unsigned uL = (unsigned)L, uT = (unsigned)T, mc = (unsigned)p.sp_max_chunk;
+    if (uL > mc || uL > uT + uT / 2) {
+        unsigned n = max(2u, (uL + uT / 2) / uT);
+        n = max(n, (uL + mc - 1) / mc);
+        if (p.sp_nc_max) n = min(n, (unsigned)p.sp_nc_max);
+        unsigned ch = (uL + n - 1) / n;
+        ch = ((ch + (1u << bsh) - 1) >> bsh) << bsh;
+        chunk = (int)ch;
+        nc = (int)((uL + ch - 1) / ch);
+    }
+}
+
+// Order key of a unit of `len` tokens: split units above whole ones, longer above shorter.
+__device__ __forceinline__ int self_key(bool split, int len, int T) {
+    const unsigned b = min((unsigned)kSelfBuckets - 1, (unsigned)len * 42u / (unsigned)T);
+    return (split ? kSelfBuckets : 0) + (int)b;
+}
+
+// Units of a sequence in key `key`: run A = chunks 0..nc-2 of every head (nc > 1),
+// run B = the last chunk of every head.
+__device__ __forceinline__ void self_runs(int nc, int keys, int key, int hks, int& ca, int& cb) {
+    ca = nc > 1 && (keys & 0xFF) == key ? hks * (nc - 1) : 0;
+    cb = (keys >> 8) == key ? hks : 0;
+}
+
+// Block-wide exclusive scan of three ints per thread; NT threads.
+template <int NT, typename Lds>
+__device__ __forceinline__ void block_excl_scan3(Lds& S, int (&v)[3]) {
+    constexpr int NW = NT / kWave;
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
+    int incl[3];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        incl[k] = wave_incl_scan(v[k]);
+        if (lane == kWave - 1) S.part[k][wave] = incl[k];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        int pre = 0;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) pre += w < wave ? S.part[k][w] : 0;
+        v[k] = pre + incl[k] - v[k];
+    }
+}
+
+// Reads the lengths and table offsets, picks the chunk target, cuts every sequence
+// into chunks and counts the units per order key.  Every thread of the workgroup
+// calls it.
+template <int NT, typename Lds>
+__device__ void self_plan_setup(const DecodeParams& p, Lds& S) {
+    constexpr int NW = NT / kWave;
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+    const int N = p.N, B = p.block, hks = p.Hkv * p.nsub;
+    const int bsh = __builtin_ctz((unsigned)B);
+    const int spt = (N + NT - 1) / NT;  // consecutive sequences per thread
+    const int i0 = min(tid * spt, N), i1 = min(i0 + spt, N);
+    const int first = p.dev_base ? *p.dev_base : p.fixed_len;  // causal prompt queries
+    double tot = 0.0;
+    int lmax = 0, nb = 0;
+    for (int i = i0; i < i1; ++i) {
+        const int L = max(p.cur_len ? p.cur_len[i] : (p.causal ? first + i + 1 : p.fixed_len), 0);
+        S.len[i] = L;
+        if (p.tab_off) S.to[i] = p.tab_off[i];
+        tot += (double)max(L, 1);
+        lmax = max(lmax, L);
+        nb += (int)(((unsigned)L + B - 1) >> bsh);
+    }
+#pragma unroll
+    for (int o = kWave / 2; o >= 1; o >>= 1) {
+        tot += __shfl_xor(tot, o);
+        lmax = max(lmax, __shfl_xor(lmax, o));
+    }
+    const int nb_incl = wave_incl_scan(nb);
+    if (lane == kWave - 1) {
+        S.tot[wave] = tot;
+        S.lmax[wave] = lmax;
+        S.part[0][wave] = nb_incl;
+    }
+    if (tid < kSelfKeys) S.count[tid] = 0;
+    __syncthreads();
+    double tall = 0.0;
+    int lall = 0, nb_pre = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+        tall += S.tot[w];
+        lall = max(lall, S.lmax[w]);
+        nb_pre += w < wave ? S.part[0][w] : 0;
+    }
+    // chunk target: the host planner's (make_plan, target 0) ...
+    const long long tokens = (long long)tall;
+    long long target = ceil_div_u(tokens * hks, p.sp_slots);
+    target = min(target, (long long)p.sp_target_cap);
+    target = min(target, (long long)(INT_MAX / 2));
+    long long T = max(target, (long long)p.sp_min_chunk);
+    T = (T + B - 1) >> bsh << bsh;
+    T = min(T, (long long)p.sp_max_chunk);
+    // ... raised to the record budget (and the 64-chunk merge of the matrix-core path)
+    long long fit = ceil_div_u(tokens, 63LL * N);
+    if (p.sp_nc_max) fit = max(fit, ((long long)lall + 62) / 63);
+    fit = (fit + B - 1) >> bsh << bsh;
+    bool overflow = fit > p.sp_max_chunk;
+    if (fit > T) T = min(fit, (long long)p.sp_max_chunk);
+    const int Ti = uniform((int)T);
+    int run = nb_pre + nb_incl - nb;  // packed tables: first entry of sequence i0
+    bool over = false;
+    for (int i = i0; i < i1; ++i) {
+        const int L = S.len[i];
+        if (p.causal) {
+            S.to[i] = 0;  // prompt queries: one shared table
+        } else if (!p.tab_off) {
+            S.to[i] = run;
+            run += (int)(((unsigned)L + B - 1) >> bsh);
+        }
+        int nc, chunk;
+        self_split(p, L, Ti, bsh, nc, chunk);
+        over |= nc > kSelfMaxChunks || L > p.cap;
+        const int ka = self_key(nc > 1, chunk, Ti);
+        const int kb = self_key(nc > 1, nc > 1 ? L - (nc - 1) * chunk : L, Ti);
+        S.cut[i] = min(nc, kSelfMaxChunks) | ((chunk >> bsh) << 16);
+        S.keys[i] = ka | (kb << 8);
+        if (nc > 1) atomicAdd(&S.count[ka], hks * (nc - 1));
+        atomicAdd(&S.count[kb], hks);
+    }
+    overflow |= __syncthreads_or(over);
+    if (wave == 0) {
+        // descending keys: lane l holds keys 127 - 2l and 126 - 2l
+        const int ka = kSelfKeys - 1 - 2 * lane, kb = ka - 1;
+        const int ca = S.count[ka], cb = S.count[kb];
+        const int incl = wave_incl_scan(ca + cb);
+        S.base[ka] = incl - ca - cb;
+        S.base[kb] = incl - cb;
+        if (lane == kWave - 1) {
+            S.units = overflow ? N * hks : incl;
+            S.T = Ti;
+            S.overflow = overflow;
+        }
+    }
+    __syncthreads();
+}
+
+// The unit of rank r (r < S.units) as a planned-entry header.  Every thread of the
+// workgroup calls it with the same r.  Returns false (after writing NaN to the
+// unit's output rows) when the batch overflowed the plan's budget.
+template <typename E, int D, int NT, typename Lds>
+__device__ bool self_plan_unit(const DecodeParams& p, Lds& S, int r, int heads, int (&hdr)[8]) {
+    const int tid = threadIdx.x, lane = tid & (kWave - 1);
+    const int N = p.N, hks = p.Hkv * p.nsub;
+    if (S.overflow) {
+        const int s = r / hks, h = r % hks;
+        const int hq0 = (h / p.nsub) * p.group + (h % p.nsub) * heads;
+        E* ob = static_cast<E*>(p.out) + ((size_t)s * p.Hq + hq0) * D;
+        for (int e = tid; e < heads * D; e += NT) ob[e] = (E)__builtin_nanf("");
+        return false;
+    }
+    // the key holding rank r (every wave finds it; no barrier)
+    int key;
+    {
+        const int ka = 2 * lane, kb = ka + 1;
+        const bool ha = r >= S.base[ka] && r < S.base[ka] + S.count[ka];
+        const bool hb = r >= S.base[kb] && r < S.base[kb] + S.count[kb];
+        const unsigned long long ma = __ballot(ha), mb = __ballot(hb);
+        key = ma ? 2 * (__ffsll((long long)ma) - 1) : 2 * (__ffsll((long long)mb) - 1) + 1;
+    }
+    const int q = r - S.base[key];
+    const int spt = (N + NT - 1) / NT;
+    const int i0 = min(tid * spt, N), i1 = min(i0 + spt, N);
+    int v[3] = {0, 0, 0};  // units in `key`, records, counters of this thread's sequences
+    for (int i = i0; i < i1; ++i) {
+        const int nc = S.cut[i] & 0xFFFF;
+        int ca, cb;
+        self_runs(nc, S.keys[i], key, hks, ca, cb);
+        v[0] += ca + cb;
+        v[1] += nc > 1 ? nc : 0;
+        v[2] += nc > 1 ? 1 : 0;
+    }
+    const int own = v[0];
+    block_excl_scan3<NT>(S, v);
+    if (q >= v[0] && q < v[0] + own) {  // exactly one thread
+        int base = v[0], rec = v[1], ctr = v[2];
+        for (int i = i0; i < i1; ++i) {
+            const int nc = S.cut[i] & 0xFFFF;
+            int ca, cb;
+            self_runs(nc, S.keys[i], key, hks, ca, cb);
+            if (q < base + ca + cb) {
+                const int x = q - base;
+                int h, c;
+                if (x < ca) {
+                    h = x / (nc - 1);
+                    c = x - h * (nc - 1);
+                } else {
+                    h = x - ca;
+                    c = nc - 1;
+                }
+                const int L = S.len[i];
+                const int cblk = S.cut[i] >> 16;
+                const int j0 = c * cblk * p.block;
+                S.hdr[0] = i;
+                S.hdr[1] = h | (c << 16);
+                S.hdr[2] = nc > 1 ? j0 : 0;
+                S.hdr[3] = nc > 1 ? min(j0 + cblk * p.block, L) : L;
+                S.hdr[4] = nc;
+                S.hdr[5] = nc > 1 ? hks * rec + h * nc : -1;
+                S.hdr[6] = nc > 1 ? hks * ctr + h : -1;
+                S.hdr[7] = S.to[i] + (nc > 1 ? c * cblk : 0);
+                break;
+            }
+            base += ca + cb;
+            rec += nc > 1 ? nc : 0;
+            ctr += nc > 1 ? 1 : 0;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 8; ++k) hdr[k] = uniform(S.hdr[k]);
+    return true;
+}
+
+// The k-th rank workgroup b serves: the grid walks the ranks in rounds of gridDim.x,
+// in alternating direction (ranks run longest first, so the workgroup with the
+// longest unit of one round gets the shortest of the next).  Each rank is served
+// once; no counter, no atomics (a shared counter serialised ~1000 arrivals into tens
+// of microseconds).
+__device__ __forceinline__ int self_plan_rank(int k) {
+    const int G = (int)gridDim.x, b = (int)blockIdx.x;
+    return k * G + ((k & 1) ? G - 1 - b : b);
+}

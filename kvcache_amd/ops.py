@@ -18,7 +18,8 @@ __all__ = [
     "launch_batched_paged_flash", "launch_flash_decode", "qk_write_kv", "qk_batched_write_kv",
     "qk_batched_paged_decode_attn", "write_kv_slots", "decode_workspace_size", "decode_auto_split",
     "decode_plan", "planned_workspace_size", "launch_batched_paged_planned", "launch_batched_paged_append_planned",
-    "flash_decode_workspace_size", "qk_paged_causal_attn", "KVC_F16", "KVC_F32",
+    "flash_decode_workspace_size", "qk_paged_causal_attn", "qkcuda_paged_causal_attn", "qkcuda_write_kv",
+    "qkcuda_rope", "KVC_F16", "KVC_F32",
 ]
 
 
@@ -90,7 +91,9 @@ def qk_batched_write_kv(k, v, k_pool, v_pool, table_all, tab_off, wpos, N, Hkv, 
 
 
 def qk_batched_paged_decode_attn(q, out, k_pool, v_pool, table_all, tab_off, cur_len, N, Hq, Hkv, D, BLOCK, scale,
-                                 *, cap, dtype=KVC_F16, split=0, workspace=None, stream=None):
+                                 *, cap=0, dtype=KVC_F16, split=0, workspace=None, stream=None):
+    """qwen_kernels.h:35-37: no length bound is needed (cap = 0: the kernel plans its
+    own chunks from the device lengths); a cap > 0 only sizes the launch."""
     ws, wsb = _ws(workspace)
     check(lib().kvc_batched_paged_decode_split(_p(q), _p(k_pool), _p(v_pool), _p(table_all), _p(tab_off),
                                                _p(cur_len), _p(out), N, Hq, Hkv, D, BLOCK, cap, scale, dtype, split,
@@ -152,6 +155,26 @@ def qk_paged_causal_attn(q, out, k_pool, v_pool, block_table, q_pos_base, Nq, Hq
     ws, wsb = _ws(workspace)
     check(lib().kvc_paged_causal_attn(_p(q), _p(out), _p(k_pool), _p(v_pool), _p(block_table), q_pos_base, Nq, Hq,
                                       Hkv, D, BLOCK, scale, dtype, ws, wsb, stream))
+
+
+def qkcuda_paged_causal_attn(q, out, k_pool, v_pool, block_table, dev_q_pos_base, Nq, Hq, Hkv, D, BLOCK, scale, *,
+                             dtype=KVC_F16, workspace=None, stream=None):
+    """qwen_kernels.h:45-47: qk_paged_causal_attn with q_pos_base in device memory."""
+    ws, wsb = _ws(workspace)
+    check(lib().kvc_paged_causal_attn_dev(_p(q), _p(out), _p(k_pool), _p(v_pool), _p(block_table),
+                                          _p(dev_q_pos_base), Nq, Hq, Hkv, D, BLOCK, scale, dtype, ws, wsb, stream))
+
+
+def qkcuda_write_kv(k, v, k_pool, v_pool, block_table_dev, dev_start_pos, L, Hkv, D, BLOCK, *, dtype=KVC_F16,
+                    stream=None):
+    """qwen_kernels.h:43-44: qk_write_kv with start_pos in device memory."""
+    check(lib().kvc_write_kv_dev(_p(k), _p(v), _p(k_pool), _p(v_pool), _p(block_table_dev), _p(dev_start_pos), L,
+                                 Hkv, D, BLOCK, dtype, stream))
+
+
+def qkcuda_rope(x, L, n_heads, D, dev_pos_base, theta, *, stream=None):
+    """qwen_kernels.h:42: qk_rope with pos_base in device memory."""
+    check(lib().kvc_rope_dev(_p(x), _p(dev_pos_base), L, n_heads, D, theta, stream))
 
 
 # ---- decoder-step operations (qwen_kernels.h:7-13,22-24) -----------------------------
