@@ -75,10 +75,12 @@ inline int qkcuda_write_kv(const half* k, const half* v, half* k_pool, half* v_p
 }
 
 // qwen_kernels.h:45-47 -- qk_paged_causal_attn with the first query at *q_pos_base
-// (device memory); the kernel plans its chunks from that position.
+// (device memory); the kernel plans its chunks from that position.  The reference
+// calls it under graph capture, so it takes the allocation-free entry point (its
+// partials live in a static device array; calls overlapping on one GPU race).
 inline int qkcuda_paged_causal_attn(const half* q, half* out, const half* k_pool, const half* v_pool,
                                     const int* block_table_dev, int* q_pos_base, int Nq, int Hq, int Hkv, int D,
                                     int BLOCK, float scale, kvc_stream_t stream = nullptr) {
-    return kvc_paged_causal_attn_dev(q, out, k_pool, v_pool, block_table_dev, q_pos_base, Nq, Hq, Hkv, D, BLOCK, scale,
-                                     KVC_F16, nullptr, 0, stream);
+    return kvc_paged_causal_attn_dev_noalloc(q, out, k_pool, v_pool, block_table_dev, q_pos_base, Nq, Hq, Hkv, D,
+                                             BLOCK, scale, KVC_F16, stream);
 }

@@ -279,6 +279,19 @@ int kvc_paged_causal_attn_dev(const void* q, void* out, const void* k_pool, cons
                               kvc_stream_t stream);
 size_t kvc_paged_causal_attn_dev_workspace_size(int Nq, int Hq, int Hkv, int D, int BLOCK, int dtype);
 
+/* No counterpart in the reference: kvc_paged_causal_attn_dev for callers that cannot
+ * allocate (code under HIP graph capture -- the reference captures
+ * qkcuda_paged_causal_attn, qwen_infer.cu:145-162 --, tight serving loops, harnesses
+ * that forbid allocation).  It allocates nothing: its split-K partials and counters
+ * live in a static device array of 4 MiB per GPU (kvc_paged_causal_attn_dev_workspace_size
+ * must not exceed it: about 17 queries of the 14q/2kv, D 64 shape; larger sizes are
+ * refused with KVC_ERR_UNSUPPORTED).  Every call on a GPU shares that GPU's array,
+ * so calls that overlap on one GPU (other streams, other threads) race.  The array's
+ * device address is resolved on the first call on each GPU. */
+int kvc_paged_causal_attn_dev_noalloc(const void* q, void* out, const void* k_pool, const void* v_pool,
+                                      const int* block_table, const int* dev_q_pos_base, int Nq, int Hq, int Hkv,
+                                      int D, int BLOCK, float scale, int dtype, kvc_stream_t stream);
+
 /* ---- decoder-step operations around the attention path (a Qwen2-shaped layer) ----
  * fp16 activations and weights, fp32 arithmetic; row widths multiples of 8.
  * qk_embed_gather (qwen_kernels.h:7): out[L,H] = embed[ids[r]] (ids outside [0,V) give zeros).

@@ -130,6 +130,7 @@ _SIGS = {
     "kvc_paged_causal_attn_workspace_size": (sz, [i32, i32, i32, i32, i32, i32, i32]),
     "kvc_paged_causal_attn_dev": (i32, [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, f32, i32, vp, sz, vp]),
     "kvc_paged_causal_attn_dev_workspace_size": (sz, [i32, i32, i32, i32, i32, i32]),
+    "kvc_paged_causal_attn_dev_noalloc": (i32, [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, f32, i32, vp]),
     "kvc_embed_gather": (i32, [vp, vp, vp, i32, i32, i32, vp]),
     "kvc_rmsnorm": (i32, [vp, vp, vp, i32, i32, f32, vp]),
     "kvc_add_bias": (i32, [vp, vp, i32, i32, vp]),

@@ -671,6 +671,36 @@ int run_self_planned(const void* q, const void* k, const void* v, const int* tab
     return launch_decode(L, st);
 }
 
+// ---- allocation-free prompt attention (graph capture, callers that cannot allocate) ----
+// kvc_paged_causal_attn_dev_noalloc keeps its split-K partials and arrival counters
+// in this file-scope device array instead of a workspace.  Each GPU holds its own
+// copy at its own address, resolved once per device with hipGetSymbolAddress (the
+// array's name is only a host-side stand-in); every call on a GPU shares that GPU's
+// copy, so calls that overlap on one GPU race.  Nothing in it needs clearing: the
+// arrival counters carry each call's epoch and partials are written before they are
+// read.
+constexpr size_t kScratchBytes = (size_t)4 << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+std::mutex g_scratch_mu;
+std::vector<void*> g_scratch;  // device address of `scratch`, per GPU
+
+int scratch_address(void** out) {
+    int dev = 0;
+    int rc = hip_check(hipGetDevice(&dev), "hipGetDevice");
+    if (rc) return rc;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if ((int)g_scratch.size() <= dev) g_scratch.resize(dev + 1, nullptr);
+    if (!g_scratch[dev]) {
+        void* ptr = nullptr;
+        rc = hip_check(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+        if (rc) return rc;
+        g_scratch[dev] = ptr;
+    }
+    *out = g_scratch[dev];
+    return KVC_OK;
+}
+
 }  // namespace
 }  // namespace kvc
 
@@ -973,6 +1003,30 @@ int kvc_paged_causal_attn_dev(const void* q, void* out, const void* k_pool, cons
 size_t kvc_paged_causal_attn_dev_workspace_size(int Nq, int Hq, int Hkv, int D, int BLOCK, int dtype) {
     if (!self_plan_ok(Nq, Hq, Hkv, D, BLOCK, dtype)) return 0;
     return self_plan_workspace(Nq, Hq, Hkv, D, BLOCK, dtype);
+}
+
+int kvc_paged_causal_attn_dev_noalloc(const void* q, void* out, const void* k_pool, const void* v_pool,
+                                      const int* block_table, const int* dev_q_pos_base, int Nq, int Hq, int Hkv,
+                                      int D, int BLOCK, float scale, int dtype, kvc_stream_t st) {
+    return guarded([&]() -> int {
+        if (Nq < 0) return set_error(KVC_ERR_ARG, "Nq must be >= 0");
+        if (Nq == 0) return KVC_OK;
+        if (!dev_q_pos_base) return set_error(KVC_ERR_ARG, "null q_pos_base pointer");
+        if (!self_plan_ok(Nq, Hq, Hkv, D, BLOCK, dtype))
+            return set_error(KVC_ERR_UNSUPPORTED, "device-position prompt attention needs a power-of-two BLOCK the "
+                                                  "kernels page uniformly and at most 512 queries");
+        const size_t need = self_plan_workspace(Nq, Hq, Hkv, D, BLOCK, dtype);
+        if (need > kScratchBytes)
+            return set_error(KVC_ERR_UNSUPPORTED, "allocation-free prompt attention of " + std::to_string(Nq) +
+                                                      " queries needs " + std::to_string(need) +
+                                                      " bytes of scratch; the static scratch holds " +
+                                                      std::to_string(kScratchBytes));
+        void* ws = nullptr;
+        int rc = scratch_address(&ws);
+        if (rc) return rc;
+        return run_self_planned(q, k_pool, v_pool, block_table, nullptr, nullptr, dev_q_pos_base, out, Nq, Hq, Hkv,
+                                D, BLOCK, 0, scale, dtype, ws, kScratchBytes, S(st));
+    });
 }
 
 size_t kvc_paged_causal_attn_workspace_size(int q_pos_base, int Nq, int Hq, int Hkv, int D, int BLOCK, int dtype) {
