@@ -227,6 +227,90 @@ def cpu_baseline(host_data, W, lens, Hkv, B, D, budget_s, kv_bytes):
             "host_cpus": os.cpu_count()}
 
 
+def host_plan_cost(W, lens, Hq, Hkv, D, B, reps=500):
+    """Mean host time of one kvc_decode_plan (size query + fill, through ctypes) for this
+    batch, the work list's bytes (what the step's upload carries) and the chunk target."""
+    import ctypes as C
+
+    from kvcache_amd import KVC_F16, ops
+    from kvcache_amd._native import lib
+    L = lib()
+    lens = np.ascontiguousarray(lens, np.int32)
+    toff, tab = W["tab_off_host"], W["table_host"]
+    nu, nr = C.c_int(0), C.c_int(0)
+    ipu = int(L.kvc_decode_plan_entry_ints(Hq, Hkv, D, B, KVC_F16))
+    L.kvc_decode_plan(lens.ctypes.data, toff.ctypes.data, tab.ctypes.data, len(tab), len(lens), Hq, Hkv, D, B,
+                      KVC_F16, 0, None, 0, C.byref(nu), C.byref(nr))
+    work = np.zeros((nu.value, ipu), np.int32)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        L.kvc_decode_plan(lens.ctypes.data, toff.ctypes.data, tab.ctypes.data, len(tab), len(lens), Hq, Hkv, D, B,
+                          KVC_F16, 0, None, 0, C.byref(nu), C.byref(nr))
+        L.kvc_decode_plan(lens.ctypes.data, toff.ctypes.data, tab.ctypes.data, len(tab), len(lens), Hq, Hkv, D, B,
+                          KVC_F16, 0, work.ctypes.data, nu.value, C.byref(nu), C.byref(nr))
+    us = (time.perf_counter() - t0) / reps * 1e6
+    return {"us_per_plan": round(us, 2), "work_list_bytes": int(work.nbytes), "units": nu.value,
+            "chunk_tokens": ops.decode_plan_chunk(lens, Hq, Hkv, D, B)}
+
+
+def c2_variant(lens, steps, warmup, rotate):
+    """A C2 batch of other lengths: planned and self-planned (device-lengths) paths."""
+    N, Hq, Hkv, D, B = len(lens), 8, 8, 64, 16
+    W = build_c2(lens, Hq, Hkv, D, B, rotate, seed=777)
+    err, _ = check_c2(W, lens, Hq, Hkv, D, B, 0)
+    kv, total = alg_bytes(lens, Hq, Hkv, D, B)
+    t_self, _ = time_decode(W, lens, Hq, Hkv, D, B, 0, steps, warmup)
+    t_plan, nu, _, launch = time_planned(W, lens, Hq, Hkv, D, B, steps, warmup)
+    return {"sum_len": int(np.sum(lens)), "algorithmic_bytes": total, "parity_max_abs_err": err,
+            "planned": {"us_per_step": round(t_plan * 1e3, 3), "GBps": round(total / (t_plan * 1e-3) / 1e9, 1),
+                        "frac_hbm_peak": round(total / (t_plan * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "units": nu},
+            "device_lengths_self_planned": {"us_per_step": round(t_self * 1e3, 3),
+                                            "GBps": round(total / (t_self * 1e-3) / 1e9, 1),
+                                            "frac_hbm_peak": round(total / (t_self * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}}
+
+
+def bench_c4_layer(steps, warmup):
+    """The config-4 per-layer kernel at the trace's typical step: 32 running sequences of
+    the BASELINE trace halfway through their generation (prompt + gen/2 tokens), one
+    planned grouped-query launch with the new token's K/V appended (14q/2kv, D 64, fp16)."""
+    from kvcache_amd import KVC_F16, ops
+    from kvcache_amd import workloads as Wl
+    from kvcache_amd.device import DeviceBuffer, Event, fill_normal, synchronize
+    p, g, _ = Wl.baseline_trace(256, 0.0, 11)
+    lens = (p[:32] + g[:32] // 2).astype(np.int32)
+    Hq, Hkv, D, B = 14, 2, 64, 16
+    W = build_c2(lens, Hq, Hkv, D, B, rotate=8, seed=44)
+    N = len(lens)
+    kv, total = alg_bytes(lens, Hq, Hkv, D, B)
+    work, nu, nr = ops.decode_plan(lens, Hq, Hkv, D, B, tab_off=W["tab_off_host"], table=W["table_host"])
+    wdev = DeviceBuffer.from_numpy(work)
+    ws = DeviceBuffer(max(ops.planned_workspace_size(Hq, Hkv, D, nr, BLOCK=B, dtype=KVC_F16), 256))
+    knew, vnew = DeviceBuffer(N * Hkv * D * 2), DeviceBuffer(N * Hkv * D * 2)
+    fill_normal(knew, N * Hkv * D, KVC_F16, 45)
+    fill_normal(vnew, N * Hkv * D, KVC_F16, 46)
+    wpos = DeviceBuffer.from_numpy(lens - 1)
+
+    def launch(i):
+        k, v = W["pools"][i % len(W["pools"])]
+        ops.launch_batched_paged_append_planned(W["q"], knew, vnew, wpos, k, v, W["table"], len(W["table_host"]),
+                                                W["out"], N, Hq, Hkv, D, B, 1.0 / np.sqrt(D), wdev, nu, nr,
+                                                dtype=KVC_F16, workspace=ws)
+    for i in range(warmup):
+        launch(i)
+    synchronize()
+    e0, e1 = Event(), Event()
+    e0.record()
+    for i in range(steps):
+        launch(i)
+    e1.record()
+    synchronize()
+    t = e0.elapsed_ms(e1) / steps
+    return {"workload": "config-4 layer step: 32 sequences of the BASELINE trace at prompt + gen/2 tokens "
+                        f"(sum {int(lens.sum())}), planned grouped-query decode with fused append",
+            "units": nu, "algorithmic_bytes": total, "us_per_launch": round(t * 1e3, 3),
+            "GBps": round(total / (t * 1e-3) / 1e9, 1), "frac_hbm_peak": round(total / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def bench_c3(steps, warmup, plan_sweep=()):
     """Config 3: Hq 14 / Hkv 2, D 64, lengths {8192,16384,32768,32768}: 512-token splits on the
     device-lengths path (the configuration as stated) and the planned path (host-chosen chunks)."""
@@ -237,7 +321,15 @@ def bench_c3(steps, warmup, plan_sweep=()):
     kv, total = alg_bytes(lens, Hq, Hkv, D, B)
     res = {"workload": "C3 long-context split-K 14q/2kv D64 ctx {8k,16k,32k,32k} fp16 split 512",
            "us_per_step": round(t * 1e3, 2), "GBps": round(total / (t * 1e-3) / 1e9, 1),
-           "frac_hbm_peak": round(total / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "kv_bytes": kv}
+           "frac_hbm_peak": round(total / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "kv_bytes": kv,
+           "algorithmic_bytes": total}
+    t2, _ = time_decode(W, lens, Hq, Hkv, D, B, 1024, steps, warmup)
+    res["split_1024"] = {"us_per_step": round(t2 * 1e3, 2), "GBps": round(total / (t2 * 1e-3) / 1e9, 1),
+                         "frac_hbm_peak": round(total / (t2 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    ts, _ = time_decode(W, lens, Hq, Hkv, D, B, 0, steps, warmup)
+    res["device_lengths_self_planned"] = {"us_per_step": round(ts * 1e3, 2),
+                                          "GBps": round(total / (ts * 1e-3) / 1e9, 1),
+                                          "frac_hbm_peak": round(total / (ts * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     for tgt in plan_sweep:
         tp, nu, nr, _ = time_planned(W, lens, Hq, Hkv, D, B, 30, 5, target=tgt)
         log(f"C3 sweep planned target={tgt}: {tp * 1e3:.2f} us ({nu} units, {nr} records)")
@@ -526,9 +618,25 @@ def main() -> int:
         warm = round(total / (t_warm * 1e-3) / 1e9, 1)
         log(f"C2 warm (one pool, Infinity-Cache resident): {t_warm * 1e3:.2f} us, {warm} GB/s")
 
+    plan_cost = host_plan_cost(W, lens, Hq, Hkv, D, B)
+    plan_cost["plan_plus_kernel_us"] = round(plan_cost["us_per_plan"] + t_launch * 1e3, 2)
+    plan_cost["plan_plus_kernel_frac"] = round(total / ((plan_cost["us_per_plan"] + t_launch * 1e3) * 1e-6) / 1e9 /
+                                               HBM_PEAK_GBS, 4)
+    log(f"host plan: {plan_cost}")
+
     extras = {}
     if not a.no_extras:
         del W["pools"]
+        try:
+            extras["c2_loguniform"] = c2_variant(Wl.loguniform_lengths(128, 16, 2048, 7), a.steps, a.warmup, a.rotate)
+            log(f"C2 log-uniform: {extras['c2_loguniform']}")
+        except Exception as e:  # noqa: BLE001 -- extras never hide the headline
+            extras["c2_loguniform"] = {"error": repr(e)}
+        try:
+            extras["c4_layer"] = bench_c4_layer(a.steps, a.warmup)
+            log(f"C4 layer kernel: {extras['c4_layer']}")
+        except Exception as e:  # noqa: BLE001
+            extras["c4_layer"] = {"error": repr(e)}
         try:
             extras["c3"] = bench_c3(a.steps, a.warmup)
             log(f"C3: {extras['c3']}")
@@ -563,7 +671,11 @@ def main() -> int:
                                "max 2022), H=8 (MHA), D=64, BLOCK=16, fp16 KV, fp32 accumulate, shuffled free list",
                    "lengths": a.lengths, "path": "planned (host plan resident, one kernel per step)",
                    "planned_units": n_units, "rotating_pool_copies": a.rotate, "parallelism": "single GPU"},
-        "device_lengths_path": {"split_tokens": split, "us_per_step": round(t_raw * 1e3, 3), "GBps": round(raw, 1)},
+        "device_lengths_path": {"path": "self-planned (launch_batched_paged: the kernel plans from the device "
+                                        "lengths, no host plan)" if split == 0 else f"split {split}",
+                                "us_per_step": round(t_raw * 1e3, 3), "GBps": round(raw, 1),
+                                "frac_hbm_peak": round(raw / HBM_PEAK_GBS, 4)},
+        "host_plan": plan_cost,
         "pct_hbm_peak": round(100 * achieved / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,

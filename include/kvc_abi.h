@@ -238,6 +238,13 @@ int kvc_batched_paged_append_decode_planned(const void* q, const void* k_new, co
                                             int dtype, const int* work, int n_units, int n_records,
                                             void* workspace, size_t workspace_bytes, kvc_stream_t stream);
 
+/* The chunk target (tokens) kvc_decode_plan uses for these lengths and target_tokens:
+ * sequences up to 1.5x this length stay whole, longer ones are cut into near-equal
+ * block-aligned chunks of about this length.  Units run split chunks first, then
+ * longest first in 64 length buckets of target/42 tokens each. */
+int kvc_decode_plan_chunk(const int* host_lens, int N, int Hq, int Hkv, int D, int BLOCK, int dtype,
+                          int target_tokens, int* chunk_tokens);
+
 /* Upper bound on the units (and partial records) of any plan of N sequences holding
  * at most total_tokens tokens: the capacity a graph-safe launch is sized for. */
 int kvc_decode_plan_capacity(int N, long long total_tokens, int Hq, int Hkv, int D, int BLOCK, int dtype,

@@ -365,10 +365,21 @@ PlanShape plan_shape(int Hq, int Hkv, int D, int BLOCK, int dtype) {
     return ps;
 }
 
-int make_plan(const int* lens, const int* tab_off, const int* table, int table_len, int N, int Hq, int Hkv, int D,
-              int BLOCK, int dtype, int target, int* work, int capacity, int* n_units, int* n_records) {
-    const PlanShape ps = plan_shape(Hq, Hkv, D, BLOCK, dtype);
-    if (ps.hks > 0xFFFF) return set_error(KVC_ERR_UNSUPPORTED, "too many KV heads for the plan encoding");
+// Order key of a unit of `len` tokens at chunk target T: with split_first, chunks of
+// split sequences above whole sequences; then 64 length buckets, longer above
+// shorter.  The kernel's own planner (selfplan.hpp) orders units by the same keys.
+inline int plan_key(bool split, long long len, int T, bool split_first) {
+    const int b = (int)std::min<long long>(63, len * 42 / T);
+    return (split && split_first ? 64 : 0) + b;
+}
+
+// Two passes, no sort: the first cuts every sequence into chunks and counts the
+// units per order key (all a size query needs), the second writes each unit at its
+// key's next slot (a counting sort; within a key in generation order: sequence, then
+// chunks 0..nc-2 of every head, then the last chunk of every head).
+// The chunk target (tokens) of a plan: `target`, or automatically enough units to
+// fill the machine's slots about once, at least min_chunk, a multiple of BLOCK.
+int plan_chunk_target(const int* lens, int N, const PlanShape& ps, int BLOCK, int target) {
     long long total = 0;
     for (int i = 0; i < N; ++i) total += std::max(lens[i], 1);
     total *= ps.hks;
@@ -377,10 +388,21 @@ int make_plan(const int* lens, const int* tab_off, const int* table, int table_l
                                           INT_MAX / 2);
     int T = std::max(target, ps.min_chunk);
     T = (T + BLOCK - 1) / BLOCK * BLOCK;
-    T = std::min(T, ps.max_chunk);
-    struct U { int len, s, hks, j0, j1, c, nc, rec, ctr, tab; };
-    std::vector<U> units;
-    int rec = 0, ctr = 0;
+    return std::min(T, ps.max_chunk);
+}
+
+int make_plan(const int* lens, const int* tab_off, const int* table, int table_len, int N, int Hq, int Hkv, int D,
+              int BLOCK, int dtype, int target, int* work, int capacity, int* n_units, int* n_records) {
+    const PlanShape ps = plan_shape(Hq, Hkv, D, BLOCK, dtype);
+    if (ps.hks > 0xFFFF) return set_error(KVC_ERR_UNSUPPORTED, "too many KV heads for the plan encoding");
+    const int T = plan_chunk_target(lens, N, ps, BLOCK, target);
+    const bool split_first = tuning().split_first != 0;
+    // pass 1: chunks per sequence, units per key
+    thread_local std::vector<int> s_nc, s_chunk;
+    s_nc.resize(N);
+    s_chunk.resize(N);
+    long long count[128] = {0};
+    long long units = 0, rec = 0;
     long long off = 0;  // table start of sequence i when tab_off is not given: tables packed in order
     for (int i = 0; i < N; ++i) {
         const int L = std::max(lens[i], 0);
@@ -389,51 +411,76 @@ int make_plan(const int* lens, const int* tab_off, const int* table, int table_l
         if (t0 > INT_MAX - (L + BLOCK - 1) / BLOCK) return set_error(KVC_ERR_ARG, "block tables too long");
         int nc = 1, chunk = std::max(L, 1);
         if (L > ps.max_chunk || L > T + T / 2) {
-            nc = std::max(2, (L + T / 2) / T);                      // nearest whole number of chunks
-            nc = std::max(nc, (L + ps.max_chunk - 1) / ps.max_chunk);
-            if (ps.mfma) nc = std::min(nc, kMfmaMaxFusedChunks);  // the fused merge holds 64 chunks
-            chunk = (L + nc - 1) / nc;
-            chunk = (chunk + BLOCK - 1) / BLOCK * BLOCK;            // block-aligned chunk starts
-            nc = (L + chunk - 1) / chunk;
+            long long n = std::max(2LL, ((long long)L + T / 2) / T);  // nearest whole number of chunks
+            n = std::max(n, ((long long)L + ps.max_chunk - 1) / ps.max_chunk);
+            if (ps.mfma) n = std::min<long long>(n, kMfmaMaxFusedChunks);  // the fused merge holds 64 chunks
+            chunk = (int)(((long long)L + n - 1) / n);
+            chunk = (chunk + BLOCK - 1) / BLOCK * BLOCK;  // block-aligned chunk starts
+            nc = (int)(((long long)L + chunk - 1) / chunk);
         }
         if (nc > 0x7FFF) return set_error(KVC_ERR_UNSUPPORTED, "too many chunks per sequence for the plan encoding");
         if (ps.mfma && (nc > kMfmaMaxFusedChunks || (chunk + BLOCK - 1) / BLOCK + 1 > kMfmaMaxChunkBlocksHost))
             return set_error(KVC_ERR_UNSUPPORTED, "sequence too long for the grouped-query planned path");
-        for (int h = 0; h < ps.hks; ++h) {
-            const int r = nc > 1 ? rec : -1, k = nc > 1 ? ctr : -1;
-            for (int c = 0; c < nc; ++c) {
-                const int j0 = std::min(c * chunk, L), j1 = std::min(j0 + chunk, L);
-                units.push_back(U{j1 - j0, i, h, j0, j1, c, nc, r, k, (int)t0 + j0 / BLOCK});
-            }
-            if (nc > 1) { rec += nc; ++ctr; }
+        s_nc[i] = nc;
+        s_chunk[i] = chunk;
+        if (nc > 1) {
+            count[plan_key(true, chunk, T, split_first)] += (long long)ps.hks * (nc - 1);
+            count[plan_key(true, L - (long long)(nc - 1) * chunk, T, split_first)] += ps.hks;
+            rec += (long long)nc * ps.hks;
+        } else {
+            count[plan_key(false, L, T, split_first)] += ps.hks;
         }
+        units += (long long)ps.hks * nc;
     }
-    // longest first; with split_first the chunks of split sequences go before every
-    // whole sequence, so their cross-chunk merges overlap later units' streaming
-    const bool split_first = tuning().split_first != 0;
-    std::stable_sort(units.begin(), units.end(), [&](const U& a, const U& b) {
-        if (split_first && (a.nc > 1) != (b.nc > 1)) return a.nc > 1;
-        return a.len > b.len;
-    });
-    *n_units = (int)units.size();
-    *n_records = rec;
+    if (units > INT_MAX / 2 || rec > INT_MAX / 2) return set_error(KVC_ERR_UNSUPPORTED, "plan too large");
+    *n_units = (int)units;
+    *n_records = (int)rec;
     if (!work) return KVC_OK;  // size query
-    if (capacity < (int)units.size())
+    if (capacity < units)
         return set_error(KVC_ERR_WORKSPACE, "plan capacity " + std::to_string(capacity) + " < " +
-                                                std::to_string(units.size()) + " units");
+                                                std::to_string(units) + " units");
+    // pass 2: each unit at its key's next slot, keys in descending order
+    long long next[128];
+    long long acc = 0;
+    for (int k = 127; k >= 0; --k) {
+        next[k] = acc;
+        acc += count[k];
+    }
     const int inline_max = ps.entry_ints - kPlanInts;
-    for (size_t u = 0; u < units.size(); ++u) {
-        int* w = work + u * (size_t)ps.entry_ints;
-        const U& x = units[u];
+    auto put = [&](int key, int s, int h, int c, int j0, int j1, int nc, int r, int k, int tab) {
+        int* w = work + next[key]++ * (size_t)ps.entry_ints;
         int n_inl = 0;
         if (inline_max > 0) {
-            const int nblk = x.j1 > x.j0 ? (x.j1 - 1) / BLOCK - x.j0 / BLOCK + 1 : 0;
-            if (table && x.tab >= 0 && (long long)x.tab + std::min(nblk, inline_max) <= table_len)
+            const int nblk = j1 > j0 ? (j1 - 1) / BLOCK - j0 / BLOCK + 1 : 0;
+            if (table && tab >= 0 && (long long)tab + std::min(nblk, inline_max) <= table_len)
                 n_inl = std::min(nblk, inline_max);
-            for (int b = 0; b < inline_max; ++b) w[kPlanInts + b] = b < n_inl ? table[x.tab + b] : 0;
+            for (int b = 0; b < n_inl; ++b) w[kPlanInts + b] = table[tab + b];
+            for (int b = n_inl; b < inline_max; ++b) w[kPlanInts + b] = 0;
         }
-        w[0] = x.s; w[1] = x.hks | (x.c << 16); w[2] = x.j0; w[3] = x.j1;
-        w[4] = x.nc | (n_inl << 16); w[5] = x.rec; w[6] = x.ctr; w[7] = x.tab;
+        w[0] = s; w[1] = h | (c << 16); w[2] = j0; w[3] = j1;
+        w[4] = nc | (n_inl << 16); w[5] = r; w[6] = k; w[7] = tab;
+    };
+    int r0 = 0, k0 = 0;
+    off = 0;
+    for (int i = 0; i < N; ++i) {
+        const int L = std::max(lens[i], 0), nc = s_nc[i], chunk = s_chunk[i];
+        const int t0 = tab_off ? tab_off[i] : (int)off;
+        off += (L + BLOCK - 1) / BLOCK;
+        if (nc > 1) {
+            const int ka = plan_key(true, chunk, T, split_first);
+            const int kb = plan_key(true, L - (long long)(nc - 1) * chunk, T, split_first);
+            for (int h = 0; h < ps.hks; ++h)
+                for (int c = 0; c < nc - 1; ++c)
+                    put(ka, i, h, c, c * chunk, c * chunk + chunk, nc, r0 + h * nc, k0 + h, t0 + c * chunk / BLOCK);
+            const int jl = (nc - 1) * chunk;
+            for (int h = 0; h < ps.hks; ++h)
+                put(kb, i, h, nc - 1, jl, L, nc, r0 + h * nc, k0 + h, t0 + jl / BLOCK);
+            r0 += nc * ps.hks;
+            k0 += ps.hks;
+        } else {
+            const int kb = plan_key(false, L, T, split_first);
+            for (int h = 0; h < ps.hks; ++h) put(kb, i, h, 0, 0, L, 1, -1, -1, t0);
+        }
     }
     return KVC_OK;
 }
@@ -1100,6 +1147,20 @@ int kvc_batched_paged_decode_planned_dev(const void* q, const void* k_new, const
         return kvc::run_planned(q, append ? k_new : nullptr, append ? v_new : nullptr, append ? wpos : nullptr,
                                 k_pool, v_pool, table_all, table_len, out, N_cap, Hq, Hkv, D, BLOCK, scale, dtype,
                                 work, units_cap, records_cap, ws, ws_bytes, S(st), dev_counts);
+    });
+}
+
+int kvc_decode_plan_chunk(const int* host_lens, int N, int Hq, int Hkv, int D, int BLOCK, int dtype,
+                          int target_tokens, int* chunk_tokens) {
+    return guarded([&]() -> int {
+        if (!chunk_tokens) return set_error(KVC_ERR_ARG, "null out pointer");
+        *chunk_tokens = 0;
+        if (N < 0 || (N > 0 && !host_lens) || Hq <= 0 || Hkv <= 0 || Hq % Hkv || BLOCK <= 0 || !d_ok(D) ||
+            !dtype_ok(dtype))
+            return set_error(KVC_ERR_ARG, "bad plan arguments");
+        *chunk_tokens = kvc::plan_chunk_target(host_lens, N, kvc::plan_shape(Hq, Hkv, D, BLOCK, dtype), BLOCK,
+                                               target_tokens);
+        return KVC_OK;
     });
 }
 

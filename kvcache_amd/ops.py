@@ -125,6 +125,18 @@ def decode_plan(lens, Hq, Hkv, D, BLOCK, *, tab_off=None, table=None, dtype=KVC_
     return work[: nu.value], nu.value, nr.value
 
 
+def decode_plan_chunk(lens, Hq, Hkv, D, BLOCK, *, dtype=KVC_F16, target_tokens=0) -> int:
+    """The chunk target (tokens) kvc_decode_plan uses for these lengths."""
+    import ctypes as C
+
+    import numpy as np
+    lens = np.ascontiguousarray(np.asarray(lens, dtype=np.int32))
+    out = C.c_int(0)
+    check(lib().kvc_decode_plan_chunk(lens.ctypes.data, len(lens), Hq, Hkv, D, BLOCK, dtype, target_tokens,
+                                      C.byref(out)))
+    return out.value
+
+
 def planned_workspace_size(Hq, Hkv, D, n_records, *, BLOCK=16, dtype=KVC_F16) -> int:
     return int(lib().kvc_decode_planned_workspace_size(Hq, Hkv, D, BLOCK, dtype, n_records))
 

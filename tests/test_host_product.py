@@ -211,8 +211,12 @@ def test_decode_plan_covers_every_token_once(case):
     sizes = work[:, 3] - work[:, 2]
     split = work[:, 4] > 1
     # chunks of split sequences first (their merges overlap later units), each group longest first
+    # in length buckets of a 42nd of the chunk target
     assert not np.any(np.diff(split.astype(int)) > 0), "split chunks precede whole sequences"
-    assert np.all(np.diff(sizes[split]) <= 0) and np.all(np.diff(sizes[~split]) <= 0), "longest first"
+    T = ops.decode_plan_chunk(lens, Hq, Hkv, D, B)
+    buckets = np.minimum(63, sizes.astype(np.int64) * 42 // T)
+    assert np.all(np.diff(buckets[split]) <= 0) and np.all(np.diff(buckets[~split]) <= 0), "longest first"
+    assert np.all(np.diff(sizes[split]) <= T // 42 + 1) and np.all(np.diff(sizes[~split]) <= T // 42 + 1)
     nsub = Hq // Hkv // (7 if Hq // Hkv == 7 else Hq // Hkv)
     hks = Hkv * nsub
     cover = {}
