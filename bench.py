@@ -53,6 +53,21 @@ def measured_traffic():
         return None, None
 
 
+STATS_SUMMARY = ROOT / "profiles" / "split_kernel_planned_c2_stats.txt"
+
+
+def profiled_launch_us():
+    """Mean duration (us) of the headline kernel's timed dispatches in the committed
+    rocprofv3 kernel-trace summary of the default command, or None."""
+    try:
+        for line in STATS_SUMMARY.read_text().splitlines():
+            if line.startswith("headline_timed_mean_us:"):
+                return float(line.split(":", 1)[1])
+    except (OSError, ValueError):
+        pass
+    return None
+
+
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -608,6 +623,7 @@ def main() -> int:
         return 1
     ms_per_step = t_launch
     traffic, sym = measured_traffic()
+    prof_us = profiled_launch_us()
     traffic_src = (f"rocprofv3 --pmc FETCH_SIZE x2.0 + WRITE_SIZE x1.0 per dispatch of {sym} "
                    f"({TRAFFIC_SUMMARY.relative_to(ROOT)})") if traffic else None
     achieved = total / (t_launch * 1e-3) / 1e9
@@ -683,7 +699,12 @@ def main() -> int:
                      "kernel": "split_kernel<_Float16, D=64, G=1, kPlannedUniform, ...> (planned paged decode, "
                                "fused LSE merge)",
                      "algorithmic_bytes_per_launch": total, "kv_bytes_per_launch": kv,
-                     "mean_launch_us": round(t_launch * 1e3, 3)},
+                     "mean_launch_us": round(t_launch * 1e3, 3),
+                     "profile": ({"file": str(STATS_SUMMARY.relative_to(ROOT)), "mean_launch_us": prof_us,
+                                  "frac": round(total / (prof_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                                  "note": "rocprofv3 kernel trace of the default command on an earlier box; "
+                                          "achieved/frac above come from this run's HIP events"}
+                                 if prof_us else None)},
         "warm_GBps": warm,
         "memory": memory_accounting(lens, Hkv, D, B),
         "parity_max_abs_err": err,

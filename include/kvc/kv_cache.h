@@ -8,7 +8,9 @@
 //     failure message is kvc_last_error();
 //   * launch_batched_paged and launch_batched_paged_flash are one entry point: the
 //     online fp32 softmax with split-K is the only implementation; the kernel plans
-//     its chunks from the device lengths, so `cap` only sizes the launch;
+//     its chunks from the device lengths, so `cap` is not needed there (shapes
+//     without that path give a sequence longer than `cap` NaN outputs, never a
+//     partial attention);
 //   * launch_flash_decode allocates nothing per call: its partials live in a
 //     grow-only library workspace (pass your own through kvc_flash_decode).
 // Optional trailing arguments select a stream (hipStream_t as void*).

@@ -166,7 +166,13 @@ int kvc_batched_decode(const void* q, const void* k_cache, const void* v_cache,
 /* launch_batched_paged / launch_batched_paged_flash (kv_cache.h:20-27,
  * batched.cu:97-147,157-207) and qk_batched_paged_decode_attn (qwen_kernels.h:35-37,
  * qwen_kernels.cu:293-335): one query per sequence over its pages [0,cur_len[s]).
- * Bit-identical to kvc_batched_decode on the same logical data. */
+ * Bit-identical to kvc_batched_decode on the same logical data.
+ * cap: the caller's bound on every cur_len.  Shapes with a self-planned path
+ * (tuning "self_plan", at most 1024 sequences, 512 on the matrix cores; a
+ * power-of-two BLOCK of at least 1024 / (D * element bytes) tokens) plan from the
+ * device lengths and ignore it (0 allowed): every sequence is
+ * attended over its whole length.  Other shapes need cap > 0 and give a sequence
+ * longer than cap NaN outputs: never a silent partial attention. */
 int kvc_batched_paged_decode(const void* q, const void* k_pool, const void* v_pool,
                              const int* table_all, const int* tab_off, const int* cur_len,
                              void* out, int N, int Hq, int Hkv, int D, int BLOCK, int cap,

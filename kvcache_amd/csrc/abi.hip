@@ -629,7 +629,16 @@ int run_planned(const void* q, const void* k_new, const void* v_new, const int* 
 // uniformly and the batch's lengths fit in LDS.
 constexpr int kSelfMaxNValuHost = 1024, kSelfMaxNMfmaHost = 512, kSelfRecordsPerHeadHost = 64;
 
-bool self_plan_ok(int N, int Hq, int Hkv, int D, int BLOCK, int dtype) {
+// Partial records per (sequence, head) of a self-planned launch: 64, or enough for
+// a mean length of `bound` tokens (the caller's cap) at the largest chunk, so a
+// batch within its stated bound never overflows the record budget.
+int self_plan_budget(const PlanShape& ps, long long bound) {
+    long long r = kSelfRecordsPerHeadHost;
+    if (bound > 0) r = std::max(r, (bound + ps.max_chunk - 1) / ps.max_chunk + 1);
+    return (int)std::min<long long>(r, 1 << 24);
+}
+
+bool self_plan_ok(int N, int Hq, int Hkv, int D, int BLOCK, int dtype, long long bound = 0) {
     if (N <= 0 || BLOCK <= 0 || (BLOCK & (BLOCK - 1)) || Hq <= 0 || Hkv <= 0 || Hq % Hkv || !d_ok(D) ||
         !dtype_ok(dtype))
         return false;
@@ -637,16 +646,17 @@ bool self_plan_ok(int N, int Hq, int Hkv, int D, int BLOCK, int dtype) {
     if (!ps.uniform || ps.hks > 0xFFFF) return false;
     if (N > (ps.mfma ? kSelfMaxNMfmaHost : kSelfMaxNValuHost)) return false;
     // the units' record numbering stays inside int
-    return (long long)kSelfRecordsPerHeadHost * ps.hks * N + 1 < (1LL << 30);
+    return (long long)self_plan_budget(ps, bound) * ps.hks * N + 1 < (1LL << 30);
 }
 
-// Records of a self-planned launch (64 per sequence and head).
-long long self_plan_records(int N, int Hq, int Hkv, int D, int BLOCK, int dtype) {
-    return (long long)kSelfRecordsPerHeadHost * plan_shape(Hq, Hkv, D, BLOCK, dtype).hks * N;
+// Records of a self-planned launch (the budget per sequence and head).
+long long self_plan_records(int N, int Hq, int Hkv, int D, int BLOCK, int dtype, long long bound = 0) {
+    const PlanShape ps = plan_shape(Hq, Hkv, D, BLOCK, dtype);
+    return (long long)self_plan_budget(ps, bound) * ps.hks * N;
 }
 
-size_t self_plan_workspace(int N, int Hq, int Hkv, int D, int BLOCK, int dtype) {
-    return planned_workspace(Hq, Hkv, D, BLOCK, dtype, (int)self_plan_records(N, Hq, Hkv, D, BLOCK, dtype));
+size_t self_plan_workspace(int N, int Hq, int Hkv, int D, int BLOCK, int dtype, long long bound = 0) {
+    return planned_workspace(Hq, Hkv, D, BLOCK, dtype, (int)self_plan_records(N, Hq, Hkv, D, BLOCK, dtype, bound));
 }
 
 // Contiguous caches are planned with chunks cut at this granularity, the paged
@@ -668,8 +678,9 @@ int run_self_planned(const void* q, const void* k, const void* v, const int* tab
     if (!contig && !table_all) return set_error(KVC_ERR_ARG, "null block table");
     if (!std::isfinite(scale)) return set_error(KVC_ERR_ARG, "scale must be finite");
     const PlanShape ps = plan_shape(Hq, Hkv, D, BLOCK, dtype);
-    const long long recs = self_plan_records(N, Hq, Hkv, D, BLOCK, dtype);
-    const size_t need = self_plan_workspace(N, Hq, Hkv, D, BLOCK, dtype);
+    const long long bound = cap;  // the record budget follows the caller's stated bound
+    const long long recs = self_plan_records(N, Hq, Hkv, D, BLOCK, dtype, bound);
+    const size_t need = self_plan_workspace(N, Hq, Hkv, D, BLOCK, dtype, bound);
     if (!ws) {
         rc = default_workspace(need, st, &ws);
         if (rc) return rc;
@@ -697,6 +708,7 @@ int run_self_planned(const void* q, const void* k, const void* v, const int* tab
     p.lpb_shift = ilog2_exact(BLOCK / ps.tpw);  // uniform paging (self_plan_ok)
     p.sp_slots = ps.slots; p.sp_min_chunk = ps.min_chunk; p.sp_max_chunk = ps.max_chunk;
     p.sp_target_cap = ps.target_cap; p.sp_nc_max = ps.mfma ? kMfmaMaxFusedChunks : 0;
+    p.sp_records = self_plan_budget(ps, bound);
     const size_t rall = (size_t)recs;
     const size_t acc = align_up(rall * ps.G * D * sizeof(float), kAlign), ml = align_up(rall * ps.G * 2 * sizeof(float), kAlign);
     p.part_acc = static_cast<float*>(ws);
@@ -983,7 +995,7 @@ int kvc_batched_decode_split(const void* q, const void* k_cache, const void* v_c
         if (N > 0 && !cur_len) return set_error(KVC_ERR_ARG, "null cur_len");
         // automatic split: the kernel plans from the device lengths, with the chunks of
         // the paged path (so paged and contiguous batches agree bit for bit)
-        if (split == 0 && tuning().self_plan != 0 && self_plan_ok(N, Hq, Hkv, D, kSelfContigBlock, dtype))
+        if (split == 0 && tuning().self_plan != 0 && self_plan_ok(N, Hq, Hkv, D, kSelfContigBlock, dtype, cap))
             return run_self_planned(q, k_cache, v_cache, nullptr, nullptr, cur_len, nullptr, out, N, Hq, Hkv, D, 0,
                                     cap, scale, dtype, ws, ws_bytes, S(st), true, (long long)Hkv * MAXS * D,
                                     (long long)MAXS * D);
@@ -1008,7 +1020,7 @@ int kvc_batched_paged_decode_split(const void* q, const void* k_pool, const void
         if (N > 0 && (!tab_off || !cur_len)) return set_error(KVC_ERR_ARG, "null tab_off / cur_len");
         if (cap < 0) return set_error(KVC_ERR_ARG, "cap must be >= 0");
         // automatic split: the kernel plans from the device lengths (cap only a hint)
-        if (split == 0 && tuning().self_plan != 0 && self_plan_ok(N, Hq, Hkv, D, BLOCK, dtype))
+        if (split == 0 && tuning().self_plan != 0 && self_plan_ok(N, Hq, Hkv, D, BLOCK, dtype, cap))
             return run_self_planned(q, k_pool, v_pool, table_all, tab_off, cur_len, nullptr, out, N, Hq, Hkv, D,
                                     BLOCK, cap, scale, dtype, ws, ws_bytes, S(st));
         if (cap == 0 && N > 0)
@@ -1184,7 +1196,7 @@ size_t kvc_decode_workspace_size(int N, int Hq, int Hkv, int D, int BLOCK, int c
     if (N <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || !d_ok(D) || cap < 0 || split < 0 || !dtype_ok(dtype)) return 0;
     if (split == 0 && tuning().self_plan != 0) {
         const int b = BLOCK > 0 ? BLOCK : kSelfContigBlock;
-        if (self_plan_ok(N, Hq, Hkv, D, b, dtype)) return self_plan_workspace(N, Hq, Hkv, D, b, dtype);
+        if (self_plan_ok(N, Hq, Hkv, D, b, dtype, cap)) return self_plan_workspace(N, Hq, Hkv, D, b, dtype, cap);
     }
     return plan_batched(N, Hq, Hkv, D, BLOCK, cap, dtype, split, BLOCK > 0).ws_bytes;
 }

@@ -76,6 +76,7 @@ struct DecodeParams {
     // then attends to *dev_base + s + 1 keys; causal must be 1)
     int sp_slots, sp_min_chunk, sp_max_chunk, sp_target_cap;
     int sp_nc_max;            // chunks per sequence the merge can combine (0: any)
+    int sp_records;           // partial records per (sequence, head) in the workspace
     const int* dev_base;
 };
 

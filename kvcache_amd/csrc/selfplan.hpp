@@ -17,18 +17,17 @@
 // launch's on the same lengths bit for bit (same chunks, same merge order); only the
 // order in which units run differs within a length bucket.
 //
-// Budget: every (sequence, KV head) may use up to 64 partial records, and on the
-// matrix-core path a sequence has at most 64 chunks; the chunk target is raised
-// when the lengths need it (mean length / 63, longest length / 63).  A batch that
-// cannot fit even at the largest chunk (mean context above 63 largest chunks), or
-// with a length past its contiguous cache (p.cap), gets NaN outputs: never a
-// silent partial attention.
+// Budget: every (sequence, KV head) may use up to p.sp_records partial records (64,
+// or more when the caller states a long bound), and on the matrix-core path a
+// sequence has at most 64 chunks; the chunk target is raised when the lengths need
+// it (mean length / (sp_records - 1), longest length / 63).  A batch that cannot fit
+// even at the largest chunk, or with a length past its contiguous cache (p.cap),
+// gets NaN outputs: never a silent partial attention.
 
 constexpr int kSelfMaxNValu = 1024;    // sequences per launch (their plan rows live in LDS)
 constexpr int kSelfMaxNMfma = 512;     // (keeps two matrix-core workgroups per CU)
 constexpr int kSelfBuckets = 64;       // length buckets per split flag
 constexpr int kSelfKeys = 2 * kSelfBuckets;
-constexpr int kSelfRecordsPerHead = 64;
 constexpr int kSelfMaxChunks = 0xFFFF;  // chunks of one sequence (16-bit plan field)
 
 template <int NMAX>
@@ -168,7 +167,7 @@ __device__ void self_plan_setup(const DecodeParams& p, Lds& S) {
     T = (T + B - 1) >> bsh << bsh;
     T = min(T, (long long)p.sp_max_chunk);
     // ... raised to the record budget (and the 64-chunk merge of the matrix-core path)
-    long long fit = ceil_div_u(tokens, 63LL * N);
+    long long fit = ceil_div_u(tokens, (long long)(p.sp_records - 1) * N);
     if (p.sp_nc_max) fit = max(fit, ((long long)lall + 62) / 63);
     fit = (fit + B - 1) >> bsh << bsh;
     bool overflow = fit > p.sp_max_chunk;

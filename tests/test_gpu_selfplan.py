@@ -136,6 +136,24 @@ def test_lengths_past_the_stated_cap_are_attended_whole(orc):
     assert np.abs(cut[0] - ref[0]).max() > 1e-2
 
 
+def test_long_mean_context_within_the_stated_cap(orc):
+    """One- and two-head units take chunks of at most 64 blocks and 64 partial records
+    per (sequence, head) by default, so a batch whose mean context passes 63 x 1024
+    tokens (BLOCK 16) cannot be planned without a bound: it gets NaN rows.  With the
+    reference's own cap argument stated the record budget grows with it and the batch
+    is attended whole."""
+    say("mean context above the default record budget, MHA fp16")
+    lens = np.array([70000, 75000], np.int32)
+    Hq = Hkv = 2
+    D = 64
+    q, K, V = inputs(lens, Hq, Hkv, D, KVC_F16, 345)
+    kp, vp, table, tab_off = paged_layout(K, V, lens, 16)
+    got = self_planned(q, kp, vp, table, tab_off, lens, Hkv, 16, KVC_F16, cap=int(lens.max()))
+    assert np.abs(got - oracle(orc, q, K, V, lens)).max() <= 2e-3
+    unbounded = self_planned(q, kp, vp, table, tab_off, lens, Hkv, 16, KVC_F16, cap=0)
+    assert np.all(np.isnan(unbounded))
+
+
 def test_explicit_split_past_cap_gives_nan_rows(orc):
     """The explicit-split path sizes its grid by cap: a longer sequence gets NaN rows
     (loud), the others their attention."""
