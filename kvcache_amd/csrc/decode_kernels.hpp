@@ -433,7 +433,7 @@ __global__ __launch_bounds__(WPB * kWave) void split_kernel(const int* __restric
     __shared__ float s_acc[WPB][G][D];
     __shared__ float s_m[WPB][G], s_l[WPB][G];
     __shared__ int s_tab[PER_LANE ? kMaxChunkBlocks : 1];
-    __shared__ std::conditional_t<SELF, SelfPlanLds<kSelfMaxNValu>, char> s_plan;
+    __shared__ std::conditional_t<SELF, SelfPlanLds<kSelfMaxNValu, WPB>, char> s_plan;
 
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = uniform(threadIdx.x >> 6);
@@ -708,10 +708,11 @@ __global__ __launch_bounds__(WPB * kWave) void split_kernel(const int* __restric
     };  // run_unit
 
     if constexpr (SELF) {
-        self_plan_setup<WPB * kWave>(p, s_plan);
-        for (int k = 0, r = self_plan_rank(0); r < s_plan.units; r = self_plan_rank(++k)) {
+        // self-planned launches pass the device lengths as the (preloaded) first argument
+        const SelfPlan sp = self_plan_setup<WPB * kWave>(work, p, s_plan);
+        for (int k = 0, r = self_plan_rank(0); r < sp.units; r = self_plan_rank(++k)) {
             int hdr[8];
-            if (self_plan_unit<T, D, WPB * kWave>(p, s_plan, r, G, hdr)) run_unit(hdr, 0);
+            if (self_plan_unit<T, D, WPB * kWave>(p, s_plan, sp, r, G, hdr)) run_unit(hdr, 0);
         }
     } else {
         // planned entries may carry the chunk's first block ids after the 8-int
@@ -885,13 +886,13 @@ int launch_split_mode(DecodeLaunch L, dim3 grid, hipStream_t st) {
             L.lds_pad = lds_pad(split_kernel<T, D, G, kSelfPlanned, WPB, U>, L.wg_per_cu);
             hipLaunchKernelGGL((split_kernel<T, D, G, kSelfPlanned, WPB, U>),
                                self_grid(split_kernel<T, D, G, kSelfPlanned, WPB, U>, block.x, L.lds_pad, grid), block,
-                               L.lds_pad, st, L.p.work, L.p.work_ints, L.p);
+                               L.lds_pad, st, L.p.cur_len, L.p.N, L.p);
             break;
         case kSelfContig:
             L.lds_pad = lds_pad(split_kernel<T, D, G, kSelfContig, WPB, U>, L.wg_per_cu);
             hipLaunchKernelGGL((split_kernel<T, D, G, kSelfContig, WPB, U>),
                                self_grid(split_kernel<T, D, G, kSelfContig, WPB, U>, block.x, L.lds_pad, grid), block,
-                               L.lds_pad, st, L.p.work, L.p.work_ints, L.p);
+                               L.lds_pad, st, L.p.cur_len, L.p.N, L.p);
             break;
         default: return set_error(KVC_ERR_ARG, "unknown decode mode");
     }
@@ -949,13 +950,13 @@ int launch_gqa_mode(DecodeLaunch L, dim3 grid, hipStream_t st) {
             L.lds_pad = lds_pad(gqa_mfma_kernel<D, kSelfPlanned, WPB>, L.wg_per_cu);
             hipLaunchKernelGGL((gqa_mfma_kernel<D, kSelfPlanned, WPB>),
                                self_grid(gqa_mfma_kernel<D, kSelfPlanned, WPB>, block.x, L.lds_pad, grid), block,
-                               L.lds_pad, st, L.p.work, L.p.work_ints, L.p);
+                               L.lds_pad, st, L.p.cur_len, L.p.N, L.p);
             break;
         case kSelfContig:
             L.lds_pad = lds_pad(gqa_mfma_kernel<D, kSelfContig, WPB>, L.wg_per_cu);
             hipLaunchKernelGGL((gqa_mfma_kernel<D, kSelfContig, WPB>),
                                self_grid(gqa_mfma_kernel<D, kSelfContig, WPB>, block.x, L.lds_pad, grid), block,
-                               L.lds_pad, st, L.p.work, L.p.work_ints, L.p);
+                               L.lds_pad, st, L.p.cur_len, L.p.N, L.p);
             break;
         default: return set_error(KVC_ERR_ARG, "matrix-core decode: unsupported addressing mode");
     }

@@ -76,7 +76,7 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(const int* __rest
     __shared__ float s_w[kMfmaMaxHeads][kMaxFusedChunks];
     __shared__ float s_L[kMfmaMaxHeads];
     __shared__ int s_last;
-    __shared__ std::conditional_t<SELF, SelfPlanLds<kSelfMaxNMfma>, char> s_plan;
+    __shared__ std::conditional_t<SELF, SelfPlanLds<kSelfMaxNMfma, WPB>, char> s_plan;
 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
@@ -508,10 +508,11 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(const int* __rest
     };  // run_unit
 
     if constexpr (SELF) {
-        self_plan_setup<WPB * kWave>(p, s_plan);
-        for (int k = 0, r = self_plan_rank(0); r < s_plan.units; r = self_plan_rank(++k)) {
+        // self-planned launches pass the device lengths as the (preloaded) first argument
+        const SelfPlan sp = self_plan_setup<WPB * kWave>(work, p, s_plan);
+        for (int k = 0, r = self_plan_rank(0); r < sp.units; r = self_plan_rank(++k)) {
             int hdr[8];
-            if (self_plan_unit<_Float16, D, WPB * kWave>(p, s_plan, r, heads, hdr)) run_unit(hdr, 0);
+            if (self_plan_unit<_Float16, D, WPB * kWave>(p, s_plan, sp, r, heads, hdr)) run_unit(hdr, 0);
         }
     } else {
         // planned entries carry the unit's block ids after the 8-int header (one int

@@ -13,7 +13,7 @@
 // rounds of gridDim.x (self_plan_rank).  Every workgroup computes the same order
 // from the same data, so each unit runs exactly once.  Per workgroup: one round of
 // loads (lengths, table offsets) into LDS, two reductions and a key histogram; per
-// rank, one block-wide scan over the sequences.  Outputs equal the host-planned
+// rank, one wave-wide scan over the sequences.  Outputs equal the host-planned
 // launch's on the same lengths bit for bit (same chunks, same merge order); only the
 // order in which units run differs within a length bucket.
 //
@@ -23,6 +23,12 @@
 // it (mean length / (sp_records - 1), longest length / 63).  A batch that cannot fit
 // even at the largest chunk, or with a length past its contiguous cache (p.cap),
 // gets NaN outputs: never a silent partial attention.
+//
+// Cost structure: the lengths pointer arrives as the kernel's first (preloaded)
+// argument, so their loads issue at wave start, beside the parameter block's; the
+// setup then needs two barriers.  Finding a rank's unit is wave-local: every wave
+// holds the key table in registers and scans the plan rows with lane shuffles, so
+// the persistent loop has no barrier and no LDS broadcast between units.
 
 constexpr int kSelfMaxNValu = 1024;    // sequences per launch (their plan rows live in LDS)
 constexpr int kSelfMaxNMfma = 512;     // (keeps two matrix-core workgroups per CU)
@@ -30,19 +36,25 @@ constexpr int kSelfBuckets = 64;       // length buckets per split flag
 constexpr int kSelfKeys = 2 * kSelfBuckets;
 constexpr int kSelfMaxChunks = 0xFFFF;  // chunks of one sequence (16-bit plan field)
 
-template <int NMAX>
+template <int NMAX, int NW>
 struct SelfPlanLds {
     int len[NMAX];             // attended length of each sequence (>= 0)
     int to[NMAX];              // first table entry of each sequence
     int cut[NMAX];             // chunks | chunk length in blocks << 16
     int keys[NMAX];            // key of chunks 0..nc-2 | key of the last chunk << 8
-    int count[kSelfKeys];      // units per order key
-    int base[kSelfKeys];       // rank of the first unit of each key (descending keys)
-    int part[3][16];           // per-wave partial sums of the block scans
-    double tot[16];            // per-wave sums of max(L, 1)
-    int lmax[16];
-    int hdr[8];                // the current rank's unit
+    int hist[NW][kSelfKeys + 1];  // per-wave units per order key; [kSelfKeys]: sequences past the limits
+    double tot[NW];            // per-wave sums of max(L, 1)
+    int lmax[NW];
+    int nb[NW];                // per-wave blocks (packed tables)
+};
+
+// The plan as every wave holds it after self_plan_setup: the chunk target, the
+// number of ranks and, per lane, the first rank and the unit count of keys
+// kSelfKeys-1-2*lane (a) and kSelfKeys-2-2*lane (b); ranks run over the keys in
+// descending order.
+struct SelfPlan {
     int T, units, overflow;
+    int base_a, cnt_a, base_b, cnt_b;
 };
 
 __device__ __forceinline__ int wave_incl_scan(int x) {
@@ -94,43 +106,25 @@ __device__ __forceinline__ void self_runs(int nc, int keys, int key, int hks, in
     cb = (keys >> 8) == key ? hks : 0;
 }
 
-// Block-wide exclusive scan of three ints per thread; NT threads.
+// Reads the lengths (`lens`, device memory; NULL: causal prompt queries) and table
+// offsets, picks the chunk target, cuts every sequence into chunks and counts the
+// units per order key.  Every thread of the workgroup calls it; every wave returns
+// the same plan.
 template <int NT, typename Lds>
-__device__ __forceinline__ void block_excl_scan3(Lds& S, int (&v)[3]) {
+__device__ SelfPlan self_plan_setup(const int* lens, const DecodeParams& p, Lds& S) {
     constexpr int NW = NT / kWave;
-    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
-    int incl[3];
-#pragma unroll
-    for (int k = 0; k < 3; ++k) {
-        incl[k] = wave_incl_scan(v[k]);
-        if (lane == kWave - 1) S.part[k][wave] = incl[k];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < 3; ++k) {
-        int pre = 0;
-#pragma unroll
-        for (int w = 0; w < NW; ++w) pre += w < wave ? S.part[k][w] : 0;
-        v[k] = pre + incl[k] - v[k];
-    }
-}
-
-// Reads the lengths and table offsets, picks the chunk target, cuts every sequence
-// into chunks and counts the units per order key.  Every thread of the workgroup
-// calls it.
-template <int NT, typename Lds>
-__device__ void self_plan_setup(const DecodeParams& p, Lds& S) {
-    constexpr int NW = NT / kWave;
-    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = uniform(tid >> 6);
     const int N = p.N, B = p.block, hks = p.Hkv * p.nsub;
     const int bsh = __builtin_ctz((unsigned)B);
     const int spt = (N + NT - 1) / NT;  // consecutive sequences per thread
     const int i0 = min(tid * spt, N), i1 = min(i0 + spt, N);
     const int first = p.dev_base ? *p.dev_base : p.fixed_len;  // causal prompt queries
+    int* hist = S.hist[wave];
+    for (int k = lane; k <= kSelfKeys; k += kWave) hist[k] = 0;
     double tot = 0.0;
     int lmax = 0, nb = 0;
     for (int i = i0; i < i1; ++i) {
-        const int L = max(p.cur_len ? p.cur_len[i] : (p.causal ? first + i + 1 : p.fixed_len), 0);
+        const int L = max(lens ? lens[i] : (p.causal ? first + i + 1 : p.fixed_len), 0);
         S.len[i] = L;
         if (p.tab_off) S.to[i] = p.tab_off[i];
         tot += (double)max(L, 1);
@@ -146,9 +140,8 @@ __device__ void self_plan_setup(const DecodeParams& p, Lds& S) {
     if (lane == kWave - 1) {
         S.tot[wave] = tot;
         S.lmax[wave] = lmax;
-        S.part[0][wave] = nb_incl;
+        S.nb[wave] = nb_incl;
     }
-    if (tid < kSelfKeys) S.count[tid] = 0;
     __syncthreads();
     double tall = 0.0;
     int lall = 0, nb_pre = 0;
@@ -156,7 +149,7 @@ __device__ void self_plan_setup(const DecodeParams& p, Lds& S) {
     for (int w = 0; w < NW; ++w) {
         tall += S.tot[w];
         lall = max(lall, S.lmax[w]);
-        nb_pre += w < wave ? S.part[0][w] : 0;
+        nb_pre += w < wave ? S.nb[w] : 0;
     }
     // chunk target: the host planner's (make_plan, target 0) ...
     const long long tokens = (long long)tall;
@@ -170,11 +163,11 @@ __device__ void self_plan_setup(const DecodeParams& p, Lds& S) {
     long long fit = ceil_div_u(tokens, (long long)(p.sp_records - 1) * N);
     if (p.sp_nc_max) fit = max(fit, ((long long)lall + 62) / 63);
     fit = (fit + B - 1) >> bsh << bsh;
-    bool overflow = fit > p.sp_max_chunk;
+    const bool overflow = fit > p.sp_max_chunk;
     if (fit > T) T = min(fit, (long long)p.sp_max_chunk);
     const int Ti = uniform((int)T);
     int run = nb_pre + nb_incl - nb;  // packed tables: first entry of sequence i0
-    bool over = false;
+    int over = 0;
     for (int i = i0; i < i1; ++i) {
         const int L = S.len[i];
         if (p.causal) {
@@ -185,70 +178,85 @@ __device__ void self_plan_setup(const DecodeParams& p, Lds& S) {
         }
         int nc, chunk;
         self_split(p, L, Ti, bsh, nc, chunk);
-        over |= nc > kSelfMaxChunks || L > p.cap;
+        over += nc > kSelfMaxChunks || L > p.cap ? 1 : 0;
         const int ka = self_key(nc > 1, chunk, Ti);
         const int kb = self_key(nc > 1, nc > 1 ? L - (nc - 1) * chunk : L, Ti);
         S.cut[i] = min(nc, kSelfMaxChunks) | ((chunk >> bsh) << 16);
         S.keys[i] = ka | (kb << 8);
-        if (nc > 1) atomicAdd(&S.count[ka], hks * (nc - 1));
-        atomicAdd(&S.count[kb], hks);
+        if (nc > 1) atomicAdd(&hist[ka], hks * (nc - 1));
+        atomicAdd(&hist[kb], hks);
     }
-    overflow |= __syncthreads_or(over);
-    if (wave == 0) {
-        // descending keys: lane l holds keys 127 - 2l and 126 - 2l
-        const int ka = kSelfKeys - 1 - 2 * lane, kb = ka - 1;
-        const int ca = S.count[ka], cb = S.count[kb];
-        const int incl = wave_incl_scan(ca + cb);
-        S.base[ka] = incl - ca - cb;
-        S.base[kb] = incl - cb;
-        if (lane == kWave - 1) {
-            S.units = overflow ? N * hks : incl;
-            S.T = Ti;
-            S.overflow = overflow;
-        }
-    }
+    if (over) atomicAdd(&hist[kSelfKeys], over);
     __syncthreads();
+    // every wave adds the per-wave histograms and scans the keys in descending order
+    const int ka = kSelfKeys - 1 - 2 * lane, kb = ka - 1;
+    int ca = 0, cb = 0, ov = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+        ca += S.hist[w][ka];
+        cb += S.hist[w][kb];
+        ov += S.hist[w][kSelfKeys];
+    }
+    const int incl = wave_incl_scan(ca + cb);
+    SelfPlan sp;
+    sp.T = Ti;
+    sp.overflow = overflow || uniform(ov) > 0;
+    sp.units = sp.overflow ? N * hks : __builtin_amdgcn_readlane(incl, kWave - 1);
+    sp.base_a = incl - ca - cb;
+    sp.cnt_a = ca;
+    sp.base_b = incl - cb;
+    sp.cnt_b = cb;
+    return sp;
 }
 
-// The unit of rank r (r < S.units) as a planned-entry header.  Every thread of the
-// workgroup calls it with the same r.  Returns false (after writing NaN to the
+// The unit of rank r (r < sp.units) as a planned-entry header.  Every thread of the
+// workgroup calls it with the same r; each wave finds the unit on its own (lane
+// shuffles over the plan rows, no barrier).  Returns false (after writing NaN to the
 // unit's output rows) when the batch overflowed the plan's budget.
 template <typename E, int D, int NT, typename Lds>
-__device__ bool self_plan_unit(const DecodeParams& p, Lds& S, int r, int heads, int (&hdr)[8]) {
+__device__ bool self_plan_unit(const DecodeParams& p, const Lds& S, const SelfPlan& sp, int r, int heads,
+                               int (&hdr)[8]) {
     const int tid = threadIdx.x, lane = tid & (kWave - 1);
     const int N = p.N, hks = p.Hkv * p.nsub;
-    if (S.overflow) {
+    if (sp.overflow) {
         const int s = r / hks, h = r % hks;
         const int hq0 = (h / p.nsub) * p.group + (h % p.nsub) * heads;
         E* ob = static_cast<E*>(p.out) + ((size_t)s * p.Hq + hq0) * D;
         for (int e = tid; e < heads * D; e += NT) ob[e] = (E)__builtin_nanf("");
         return false;
     }
-    // the key holding rank r (every wave finds it; no barrier)
-    int key;
-    {
-        const int ka = 2 * lane, kb = ka + 1;
-        const bool ha = r >= S.base[ka] && r < S.base[ka] + S.count[ka];
-        const bool hb = r >= S.base[kb] && r < S.base[kb] + S.count[kb];
-        const unsigned long long ma = __ballot(ha), mb = __ballot(hb);
-        key = ma ? 2 * (__ffsll((long long)ma) - 1) : 2 * (__ffsll((long long)mb) - 1) + 1;
+    // the key holding rank r
+    const unsigned long long ma = __ballot(r >= sp.base_a && r < sp.base_a + sp.cnt_a);
+    const unsigned long long mb = __ballot(r >= sp.base_b && r < sp.base_b + sp.cnt_b);
+    if (!ma && !mb) return false;
+    int key, q;
+    if (ma) {
+        const int l = __ffsll((long long)ma) - 1;
+        key = kSelfKeys - 1 - 2 * l;
+        q = r - __builtin_amdgcn_readlane(sp.base_a, l);
+    } else {
+        const int l = __ffsll((long long)mb) - 1;
+        key = kSelfKeys - 2 - 2 * l;
+        q = r - __builtin_amdgcn_readlane(sp.base_b, l);
     }
-    const int q = r - S.base[key];
-    const int spt = (N + NT - 1) / NT;
-    const int i0 = min(tid * spt, N), i1 = min(i0 + spt, N);
-    int v[3] = {0, 0, 0};  // units in `key`, records, counters of this thread's sequences
+    // this lane's sequences, in order: units in `key`, records, counters
+    const int spl = (N + kWave - 1) / kWave;
+    const int i0 = min(lane * spl, N), i1 = min(i0 + spl, N);
+    int own = 0, nrec = 0, nctr = 0;
     for (int i = i0; i < i1; ++i) {
         const int nc = S.cut[i] & 0xFFFF;
         int ca, cb;
         self_runs(nc, S.keys[i], key, hks, ca, cb);
-        v[0] += ca + cb;
-        v[1] += nc > 1 ? nc : 0;
-        v[2] += nc > 1 ? 1 : 0;
+        own += ca + cb;
+        nrec += nc > 1 ? nc : 0;
+        nctr += nc > 1 ? 1 : 0;
     }
-    const int own = v[0];
-    block_excl_scan3<NT>(S, v);
-    if (q >= v[0] && q < v[0] + own) {  // exactly one thread
-        int base = v[0], rec = v[1], ctr = v[2];
+    int base = wave_incl_scan(own) - own;
+    int rec = wave_incl_scan(nrec) - nrec;
+    int ctr = wave_incl_scan(nctr) - nctr;
+    const bool mine = q >= base && q < base + own;  // exactly one lane
+    int h0 = 0, h1 = 0, h2 = 0, h3 = 0, h4 = 0, h5 = 0, h6 = 0, h7 = 0;
+    if (mine) {
         for (int i = i0; i < i1; ++i) {
             const int nc = S.cut[i] & 0xFFFF;
             int ca, cb;
@@ -266,14 +274,14 @@ __device__ bool self_plan_unit(const DecodeParams& p, Lds& S, int r, int heads, 
                 const int L = S.len[i];
                 const int cblk = S.cut[i] >> 16;
                 const int j0 = c * cblk * p.block;
-                S.hdr[0] = i;
-                S.hdr[1] = h | (c << 16);
-                S.hdr[2] = nc > 1 ? j0 : 0;
-                S.hdr[3] = nc > 1 ? min(j0 + cblk * p.block, L) : L;
-                S.hdr[4] = nc;
-                S.hdr[5] = nc > 1 ? hks * rec + h * nc : -1;
-                S.hdr[6] = nc > 1 ? hks * ctr + h : -1;
-                S.hdr[7] = S.to[i] + (nc > 1 ? c * cblk : 0);
+                h0 = i;
+                h1 = h | (c << 16);
+                h2 = nc > 1 ? j0 : 0;
+                h3 = nc > 1 ? min(j0 + cblk * p.block, L) : L;
+                h4 = nc;
+                h5 = nc > 1 ? hks * rec + h * nc : -1;
+                h6 = nc > 1 ? hks * ctr + h : -1;
+                h7 = S.to[i] + (nc > 1 ? c * cblk : 0);
                 break;
             }
             base += ca + cb;
@@ -281,9 +289,17 @@ __device__ bool self_plan_unit(const DecodeParams& p, Lds& S, int r, int heads, 
             ctr += nc > 1 ? 1 : 0;
         }
     }
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < 8; ++k) hdr[k] = uniform(S.hdr[k]);
+    const unsigned long long mm = __ballot(mine);
+    if (!mm) return false;
+    const int src = __ffsll((long long)mm) - 1;
+    hdr[0] = __builtin_amdgcn_readlane(h0, src);
+    hdr[1] = __builtin_amdgcn_readlane(h1, src);
+    hdr[2] = __builtin_amdgcn_readlane(h2, src);
+    hdr[3] = __builtin_amdgcn_readlane(h3, src);
+    hdr[4] = __builtin_amdgcn_readlane(h4, src);
+    hdr[5] = __builtin_amdgcn_readlane(h5, src);
+    hdr[6] = __builtin_amdgcn_readlane(h6, src);
+    hdr[7] = __builtin_amdgcn_readlane(h7, src);
     return true;
 }
 
