@@ -8,8 +8,9 @@
 // a synchronisation.  Instead every workgroup of a persistent grid derives the
 // host planner's work (kvc_decode_plan: the same chunk target, the same chunks,
 // the same partial-record and counter numbering) from the lengths, orders the units
-// as the planner does -- chunks of split sequences first, then by length, longest
-// first (64 length buckets relative to the chunk target) -- and serves ranks in
+// as the planner does (up to rounding at bucket edges) -- chunks of split sequences
+// first, then by length, longest first (64 length buckets relative to the chunk
+// target) -- and serves ranks in
 // rounds of gridDim.x (self_plan_rank).  Every workgroup computes the same order
 // from the same data, so each unit runs exactly once.  Per workgroup: one round of
 // loads (lengths, table offsets) into LDS, two reductions and a key histogram; per
@@ -43,7 +44,7 @@ struct SelfPlanLds {
     int cut[NMAX];             // chunks | chunk length in blocks << 16
     int keys[NMAX];            // key of chunks 0..nc-2 | key of the last chunk << 8
     int hist[NW][kSelfKeys + 1];  // per-wave units per order key; [kSelfKeys]: sequences past the limits
-    double tot[NW];            // per-wave sums of max(L, 1)
+    unsigned long long tot[NW];  // per-wave sums of max(L, 1)
     int lmax[NW];
     int nb[NW];                // per-wave blocks (packed tables)
 };
@@ -57,13 +58,28 @@ struct SelfPlan {
     int base_a, cnt_a, base_b, cnt_b;
 };
 
+// Inclusive prefix sum over the 64 lanes with DPP: shifts of 1, 2, 4, 8 within each
+// row of 16 lanes, then row 0's total into row 1 and row 2's into row 3 (row_bcast:15),
+// then the first two rows' total into rows 2 and 3 (row_bcast:31).  Out-of-row sources
+// and disabled rows contribute 0.
 __device__ __forceinline__ int wave_incl_scan(int x) {
-    const int lane = __lane_id();
-#pragma unroll
-    for (int o = 1; o < kWave; o <<= 1) {
-        const int y = __builtin_amdgcn_ds_bpermute((lane - o) << 2, x);
-        x += lane >= o ? y : 0;
-    }
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
+    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15, rows 1 and 3
+    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31, rows 2 and 3
+    return x;
+}
+
+// Running maximum over the lanes (the same pattern); values >= 0.
+__device__ __forceinline__ int wave_incl_max(int x) {
+    x = max(x, __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false));
+    x = max(x, __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false));
+    x = max(x, __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false));
+    x = max(x, __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false));
+    x = max(x, __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false));
+    x = max(x, __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false));
     return x;
 }
 
@@ -93,10 +109,13 @@ __device__ __forceinline__ void self_split(const DecodeParams& p, int L, int T, 
     }
 }
 
-// Order key of a unit of `len` tokens: split units above whole ones, longer above shorter.
-__device__ __forceinline__ int self_key(bool split, int len, int T) {
-    const unsigned b = min((unsigned)kSelfBuckets - 1, (unsigned)len * 42u / (unsigned)T);
-    return (split ? kSelfBuckets : 0) + (int)b;
+// Order key of a unit of `len` tokens: split units above whole ones, longer above
+// shorter; kscale = 42 / T.  The planner's bucket len * 42 / T, in float: the key
+// only orders the units (their chunks, records and counters do not depend on it),
+// so a unit at a bucket edge may sort one bucket away from the host plan's order.
+__device__ __forceinline__ int self_key(bool split, int len, float kscale) {
+    const int b = min(kSelfBuckets - 1, (int)((float)len * kscale));
+    return (split ? kSelfBuckets : 0) + b;
 }
 
 // Units of a sequence in key `key`: run A = chunks 0..nc-2 of every head (nc > 1),
@@ -121,29 +140,27 @@ __device__ SelfPlan self_plan_setup(const int* lens, const DecodeParams& p, Lds&
     const int first = p.dev_base ? *p.dev_base : p.fixed_len;  // causal prompt queries
     int* hist = S.hist[wave];
     for (int k = lane; k <= kSelfKeys; k += kWave) hist[k] = 0;
-    double tot = 0.0;
+    unsigned long long tot = 0;  // at most 4 sequences per thread (N <= 1024 <= 4 * NT): < 2^33
     int lmax = 0, nb = 0;
     for (int i = i0; i < i1; ++i) {
         const int L = max(lens ? lens[i] : (p.causal ? first + i + 1 : p.fixed_len), 0);
         S.len[i] = L;
         if (p.tab_off) S.to[i] = p.tab_off[i];
-        tot += (double)max(L, 1);
+        tot += (unsigned)max(L, 1);
         lmax = max(lmax, L);
         nb += (int)(((unsigned)L + B - 1) >> bsh);
     }
-#pragma unroll
-    for (int o = kWave / 2; o >= 1; o >>= 1) {
-        tot += __shfl_xor(tot, o);
-        lmax = max(lmax, __shfl_xor(lmax, o));
-    }
+    // wave totals: the 64-bit sum as two 32-bit scans of its low 20 and high bits
+    const int tlo = wave_incl_scan((int)(tot & 0xFFFFF)), thi = wave_incl_scan((int)(tot >> 20));
+    const int lmx = wave_incl_max(lmax);
     const int nb_incl = wave_incl_scan(nb);
     if (lane == kWave - 1) {
-        S.tot[wave] = tot;
-        S.lmax[wave] = lmax;
+        S.tot[wave] = ((unsigned long long)(unsigned)thi << 20) + (unsigned)tlo;
+        S.lmax[wave] = lmx;
         S.nb[wave] = nb_incl;
     }
     __syncthreads();
-    double tall = 0.0;
+    unsigned long long tall = 0;
     int lall = 0, nb_pre = 0;
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
@@ -166,6 +183,7 @@ __device__ SelfPlan self_plan_setup(const int* lens, const DecodeParams& p, Lds&
     const bool overflow = fit > p.sp_max_chunk;
     if (fit > T) T = min(fit, (long long)p.sp_max_chunk);
     const int Ti = uniform((int)T);
+    const float kscale = 42.0f / (float)Ti;
     int run = nb_pre + nb_incl - nb;  // packed tables: first entry of sequence i0
     int over = 0;
     for (int i = i0; i < i1; ++i) {
@@ -179,8 +197,8 @@ __device__ SelfPlan self_plan_setup(const int* lens, const DecodeParams& p, Lds&
         int nc, chunk;
         self_split(p, L, Ti, bsh, nc, chunk);
         over += nc > kSelfMaxChunks || L > p.cap ? 1 : 0;
-        const int ka = self_key(nc > 1, chunk, Ti);
-        const int kb = self_key(nc > 1, nc > 1 ? L - (nc - 1) * chunk : L, Ti);
+        const int ka = self_key(nc > 1, chunk, kscale);
+        const int kb = self_key(nc > 1, nc > 1 ? L - (nc - 1) * chunk : L, kscale);
         S.cut[i] = min(nc, kSelfMaxChunks) | ((chunk >> bsh) << 16);
         S.keys[i] = ka | (kb << 8);
         if (nc > 1) atomicAdd(&hist[ka], hks * (nc - 1));
