@@ -36,6 +36,7 @@ constexpr int kSelfMaxNMfma = 512;     // (keeps two matrix-core workgroups per 
 constexpr int kSelfBuckets = 64;       // length buckets per split flag
 constexpr int kSelfKeys = 2 * kSelfBuckets;
 constexpr int kSelfMaxChunks = 0xFFFF;  // chunks of one sequence (16-bit plan field)
+constexpr int kSelfSpt = 4;            // sequences per setup thread (kSelfMaxNValu / 256)
 
 template <int NMAX, int NW>
 struct SelfPlanLds {
@@ -140,15 +141,30 @@ __device__ SelfPlan self_plan_setup(const int* lens, const DecodeParams& p, Lds&
     const int first = p.dev_base ? *p.dev_base : p.fixed_len;  // causal prompt queries
     int* hist = S.hist[wave];
     for (int k = lane; k <= kSelfKeys; k += kWave) hist[k] = 0;
-    unsigned long long tot = 0;  // at most 4 sequences per thread (N <= 1024 <= 4 * NT): < 2^33
+    // the thread's lengths and table offsets, all loads issued before any is used
+    // (bounded buffer loads: indices past N read 0 and touch no memory)
+    static_assert(NT >= 256, "at most kSelfSpt sequences per thread");
+    const __amdgpu_buffer_rsrc_t lrs = tile_rsrc(lens, lens ? N * 4 : 0);
+    const __amdgpu_buffer_rsrc_t trs = tile_rsrc(p.tab_off, p.tab_off ? N * 4 : 0);
+    int lv[kSelfSpt], tv[kSelfSpt];
+#pragma unroll
+    for (int j = 0; j < kSelfSpt; ++j) {
+        lv[j] = (int)__builtin_amdgcn_raw_buffer_load_b32(lrs, (i0 + j) * 4, 0, 0);
+        tv[j] = (int)__builtin_amdgcn_raw_buffer_load_b32(trs, (i0 + j) * 4, 0, 0);
+    }
+    unsigned long long tot = 0;  // at most 4 sequences per thread: < 2^33
     int lmax = 0, nb = 0;
-    for (int i = i0; i < i1; ++i) {
-        const int L = max(lens ? lens[i] : (p.causal ? first + i + 1 : p.fixed_len), 0);
-        S.len[i] = L;
-        if (p.tab_off) S.to[i] = p.tab_off[i];
-        tot += (unsigned)max(L, 1);
-        lmax = max(lmax, L);
-        nb += (int)(((unsigned)L + B - 1) >> bsh);
+#pragma unroll
+    for (int j = 0; j < kSelfSpt; ++j) {
+        const int i = i0 + j;
+        if (i < i1) {
+            const int L = max(lens ? lv[j] : (p.causal ? first + i + 1 : p.fixed_len), 0);
+            S.len[i] = L;
+            S.to[i] = tv[j];
+            tot += (unsigned)max(L, 1);
+            lmax = max(lmax, L);
+            nb += (int)(((unsigned)L + B - 1) >> bsh);
+        }
     }
     // wave totals: the 64-bit sum as two 32-bit scans of its low 20 and high bits
     const int tlo = wave_incl_scan((int)(tot & 0xFFFFF)), thi = wave_incl_scan((int)(tot >> 20));

@@ -1,8 +1,11 @@
 // test_paged_flash.cpp -- the reference's tests/test_paged_flash.cu:12-65 setup
 // (3 sequences of 5/8/13 tokens, BLOCK 4, H 8, D 64, srand(7) data) through the
-// drop-in launchers: launch_batched_paged and launch_batched_paged_flash must
-// agree (reference bar 1e-4; here they are the same kernel, so bit-identical),
-// and launch_batched_decode on the contiguous copy must be bit-identical too.
+// drop-in launchers.  The check that counts: launch_batched_paged against a naive
+// softmax attention computed here in double precision (bar 1e-5, the fp32 path's).
+// launch_batched_decode on the contiguous copy must equal the paged result bit for
+// bit (different addressing, same chunks).  launch_batched_paged_flash is the same
+// entry point as launch_batched_paged here, so calling it only shows that the
+// reference's name compiles and runs.
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -61,13 +64,42 @@ int main() {
     OK(kvc_memcpy_d2h(r1.data(), o1, q.size() * 4, nullptr));
     OK(kvc_memcpy_d2h(r2.data(), o2, q.size() * 4, nullptr));
     OK(kvc_memcpy_d2h(r3.data(), o3, q.size() * 4, nullptr));
+    // naive attention per (sequence, head): scores over the sequence's tokens in
+    // table order, max-subtracted softmax, weighted sum of V, all in double
+    double dref = 0.0;
+    for (int s = 0; s < N; ++s)
+        for (int h = 0; h < H; ++h) {
+            const int L = cur_len[s];
+            std::vector<double> sc(L);
+            double mx = -1e300;
+            for (int t = 0; t < L; ++t) {
+                const int phys = table_all[tab_off[s] + t / BLOCK];
+                double dot = 0.0;
+                for (int d = 0; d < D; ++d)
+                    dot += (double)q[((size_t)s * H + h) * D + d] *
+                           (double)kp[(((size_t)phys * H + h) * BLOCK + t % BLOCK) * D + d];
+                sc[t] = dot * scale;
+                mx = std::fmax(mx, sc[t]);
+            }
+            double den = 0.0;
+            for (int t = 0; t < L; ++t) den += (sc[t] = std::exp(sc[t] - mx));
+            for (int d = 0; d < D; ++d) {
+                double num = 0.0;
+                for (int t = 0; t < L; ++t) {
+                    const int phys = table_all[tab_off[s] + t / BLOCK];
+                    num += sc[t] * (double)vp[(((size_t)phys * H + h) * BLOCK + t % BLOCK) * D + d];
+                }
+                dref = std::fmax(dref, std::fabs(num / den - (double)r1[((size_t)s * H + h) * D + d]));
+            }
+        }
     float d12 = 0.f, d13 = 0.f;
     for (size_t i = 0; i < q.size(); ++i) {
         d12 = std::fmax(d12, std::fabs(r1[i] - r2[i]));
         d13 = std::fmax(d13, std::fabs(r1[i] - r3[i]));
     }
-    const bool pass = d12 < 1e-4f && d13 == 0.f;
-    std::printf("max|flash - two-pass| = %.3e, max|paged - contiguous| = %.3e -> %s\n", d12, d13, pass ? "PASS" : "FAIL");
+    const bool pass = dref <= 1e-5 && d12 == 0.f && d13 == 0.f;
+    std::printf("max|paged - naive double| = %.3e, max|paged - contiguous| = %.3e, flash name %s -> %s\n", dref, d13,
+                d12 == 0.f ? "ran" : "DIFFERS", pass ? "PASS" : "FAIL");
     for (void* p : {dq, dkp, dvp, dkc, dvc, o1, o2, o3, dtab, dtoff, dlen}) kvc_free(p);
     return pass ? 0 : 1;
 }
