@@ -61,19 +61,24 @@ def _r16(a):
     return np.asarray(a, np.float32).astype(np.float16).astype(np.float32)
 
 
-def decoder_logits(W, cfg, tokens, logits_from=0):
+def decoder_logits(W, cfg, tokens, logits_from=0, round16=True):
     """Teacher-forced forward of one token sequence through the Qwen2-shaped decoder
     (qwen_serve.cu:97-121 for every position at once: causal attention over the
     prefix), returning float64 logits [T, vocab].  W maps names to fp16 arrays
     (kvcache_amd.model.QwenModel.tensor layout: [out, in] row-major); fp16 rounding is
     applied where the GPU stores a kernel's output, arithmetic is float32 (GEMMs) and
     float64 (norms, softmax).  Rows before `logits_from` are left out of the lm_head
-    (the returned array still has T rows; those are zero)."""
+    (the returned array still has T rows; those are zero).  round16=False runs the
+    same statements in float64 without the fp16 stores (the form compared with the
+    Hugging Face Qwen2 forward)."""
     H, Hq, Hkv, D = cfg.hidden, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim
     I, V = cfg.inter, cfg.vocab
     tok = np.asarray(tokens)
     T = len(tok)
-    f32 = lambda a: np.asarray(a, np.float32)
+    if round16:
+        f32, r16 = (lambda a: np.asarray(a, np.float32)), _r16
+    else:
+        f32 = r16 = lambda a: np.asarray(a, np.float64)
     embed = W["embed"].reshape(V, H)
     x = f32(embed[tok])
     pos = np.arange(T)
@@ -81,12 +86,12 @@ def decoder_logits(W, cfg, tokens, logits_from=0):
     g = Hq // Hkv
     for l in range(cfg.layers):
         w = lambda n, shape: f32(W[f"{n}.{l}"].reshape(shape))
-        n = _r16(rmsnorm(x, w("ln1", (H,)), cfg.eps))
-        q = _r16(_r16(n @ w("wq", (Hq * D, H)).T) + w("bq", (Hq * D,)))
-        k = _r16(_r16(n @ w("wk", (Hkv * D, H)).T) + w("bk", (Hkv * D,)))
-        v = _r16(_r16(n @ w("wv", (Hkv * D, H)).T) + w("bv", (Hkv * D,)))
-        q = _r16(rope(q.reshape(T, Hq, D), pos, D, cfg.theta))
-        k = _r16(rope(k.reshape(T, Hkv, D), pos, D, cfg.theta))
+        n = r16(rmsnorm(x, w("ln1", (H,)), cfg.eps))
+        q = r16(r16(n @ w("wq", (Hq * D, H)).T) + w("bq", (Hq * D,)))
+        k = r16(r16(n @ w("wk", (Hkv * D, H)).T) + w("bk", (Hkv * D,)))
+        v = r16(r16(n @ w("wv", (Hkv * D, H)).T) + w("bv", (Hkv * D,)))
+        q = r16(rope(q.reshape(T, Hq, D), pos, D, cfg.theta))
+        k = r16(rope(k.reshape(T, Hkv, D), pos, D, cfg.theta))
         v = v.reshape(T, Hkv, D).astype(np.float64)
         att = np.empty((T, Hq, D))
         for h in range(Hq):
@@ -94,13 +99,13 @@ def decoder_logits(W, cfg, tokens, logits_from=0):
             s[mask] = -np.inf
             s = np.exp(s - s.max(axis=1, keepdims=True))
             att[:, h] = (s / s.sum(axis=1, keepdims=True)) @ v[:, h // g]
-        att = _r16(att.reshape(T, Hq * D))
-        x = _r16(x + _r16(att @ w("wo", (H, Hq * D)).T))
-        n = _r16(rmsnorm(x, w("ln2", (H,)), cfg.eps))
-        a = _r16(silu_mul(_r16(n @ w("wg", (I, H)).T), _r16(n @ w("wu", (I, H)).T)))
-        x = _r16(x + _r16(a @ w("wd", (H, I)).T))
+        att = r16(att.reshape(T, Hq * D))
+        x = r16(x + r16(att @ w("wo", (H, Hq * D)).T))
+        n = r16(rmsnorm(x, w("ln2", (H,)), cfg.eps))
+        a = r16(silu_mul(r16(n @ w("wg", (I, H)).T), r16(n @ w("wu", (I, H)).T)))
+        x = r16(x + r16(a @ w("wd", (H, I)).T))
     out = np.zeros((T, V), np.float64)
-    n = _r16(rmsnorm(x[logits_from:], f32(W["norm"]), cfg.eps))
+    n = r16(rmsnorm(x[logits_from:], f32(W["norm"]), cfg.eps))
     out[logits_from:] = n @ f32(embed).T
     return out
 

@@ -1,6 +1,7 @@
 """The CPU restatement of the decoder-step operations (oracle/model.py), pinned by
 properties the mathematics fixes rather than by retyping its formulas."""
 import numpy as np
+import pytest
 
 from oracle import model as M
 
@@ -83,3 +84,53 @@ def test_decoder_grouped_query_equals_repeated_heads():
                 if len(shape) == 3 else np.repeat(W[f"{n}.{l}"].reshape(shape), 2, axis=0).ravel()
     tok = np.array([1, 2, 3, 4, 5])
     np.testing.assert_allclose(M.decoder_logits(W, cfg, tok), M.decoder_logits(Wm, cfg_m, tok), rtol=0, atol=0)
+
+
+def test_decoder_matches_hugging_face_qwen2():
+    """The decoder restatement (without its fp16 stores) against the Hugging Face
+    Qwen2 forward -- the library behind the reference's token oracle
+    (tools/ref_qwen.py) -- on the same random weights: biases on q/k/v only,
+    rotate-half RoPE with theta, RMSNorm, SwiGLU, grouped-query attention, tied
+    lm_head.  Built from a config offline (no download); the library computes its
+    norms and rotary tables in float32, hence the 1e-5 tolerance."""
+    torch = pytest.importorskip("torch")
+    tf = pytest.importorskip("transformers")
+    cfg, W = _tiny(layers=2, Hq=4, Hkv=2, D=8, H=16, I=24, V=50, seed=11)
+    for l in range(cfg.layers):  # non-trivial norm weights
+        rng = np.random.default_rng(100 + l)
+        W[f"ln1.{l}"] = (1 + 0.2 * rng.standard_normal(cfg.hidden)).astype(np.float16)
+        W[f"ln2.{l}"] = (1 + 0.2 * rng.standard_normal(cfg.hidden)).astype(np.float16)
+    hf_cfg = tf.Qwen2Config(vocab_size=cfg.vocab, hidden_size=cfg.hidden, intermediate_size=cfg.inter,
+                            num_hidden_layers=cfg.layers, num_attention_heads=cfg.n_heads,
+                            num_key_value_heads=cfg.n_kv_heads, head_dim=cfg.head_dim, rms_norm_eps=cfg.eps,
+                            tie_word_embeddings=True,
+                            rope_parameters={"rope_type": "default", "rope_theta": cfg.theta},
+                            attn_implementation="eager")
+    model = tf.Qwen2ForCausalLM(hf_cfg).to(torch.float64).eval()
+    t = lambda a, *shape: torch.from_numpy(np.asarray(a, np.float64).reshape(shape))
+    H, Hq, Hkv, D, I = cfg.hidden, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.inter
+    sd = {"model.embed_tokens.weight": t(W["embed"], cfg.vocab, H), "model.norm.weight": t(W["norm"], H)}
+    for l in range(cfg.layers):
+        pre = f"model.layers.{l}."
+        sd.update({pre + "self_attn.q_proj.weight": t(W[f"wq.{l}"], Hq * D, H),
+                   pre + "self_attn.q_proj.bias": t(W[f"bq.{l}"], Hq * D),
+                   pre + "self_attn.k_proj.weight": t(W[f"wk.{l}"], Hkv * D, H),
+                   pre + "self_attn.k_proj.bias": t(W[f"bk.{l}"], Hkv * D),
+                   pre + "self_attn.v_proj.weight": t(W[f"wv.{l}"], Hkv * D, H),
+                   pre + "self_attn.v_proj.bias": t(W[f"bv.{l}"], Hkv * D),
+                   pre + "self_attn.o_proj.weight": t(W[f"wo.{l}"], H, Hq * D),
+                   pre + "mlp.gate_proj.weight": t(W[f"wg.{l}"], I, H),
+                   pre + "mlp.up_proj.weight": t(W[f"wu.{l}"], I, H),
+                   pre + "mlp.down_proj.weight": t(W[f"wd.{l}"], H, I),
+                   pre + "input_layernorm.weight": t(W[f"ln1.{l}"], H),
+                   pre + "post_attention_layernorm.weight": t(W[f"ln2.{l}"], H)})
+    missing, unexpected = model.load_state_dict(sd, strict=False)
+    assert not unexpected and set(missing) <= {"lm_head.weight"}
+    tok = np.array([5, 9, 13, 2, 30, 11, 49, 0, 7])
+    with torch.no_grad():
+        ref = model(torch.from_numpy(tok)[None]).logits[0].numpy()
+    got = M.decoder_logits(W, cfg, tok, round16=False)
+    assert np.abs(ref).max() > 1.0
+    np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-5)
+    # the GPU-shaped form (fp16 stores) stays within fp16 rounding of it
+    np.testing.assert_allclose(M.decoder_logits(W, cfg, tok), ref, rtol=0, atol=0.05)
