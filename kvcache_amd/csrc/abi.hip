@@ -103,6 +103,7 @@ struct Plan {
     bool mfma = false;
     bool chunk_blocks_ok = true;  // the per-lane path stages at most 4096 block ids per chunk
     size_t acc_bytes = 0, ml_bytes = 0, ws_bytes = 0;
+    size_t n_ctr = 0;  // arrival counters
 };
 
 inline int ilog2_exact(int x) {  // log2 of a power of two, else -1
@@ -120,13 +121,14 @@ int choose_wpb(long long units) {
     return units < 1024 ? 8 : 4;
 }
 
-// Workspace: [part_acc | part_ml | arrival counters (one u64 per seq x KV head x subgroup)].
+// Workspace: [part_acc | part_ml | arrival counters (one per seq x KV head x subgroup, ctr_slot layout)].
 void size_workspace(Plan& pl, int N, int Hq, int Hkv, int D) {
     if (pl.max_chunks <= 1) return;
     const size_t recs = (size_t)N * pl.max_chunks * Hq;
     pl.acc_bytes = align_up(recs * D * sizeof(float), kAlign);
     pl.ml_bytes = align_up(recs * 2 * sizeof(float), kAlign);
-    pl.ws_bytes = pl.acc_bytes + pl.ml_bytes + align_up((size_t)N * Hkv * pl.nsub * sizeof(uint64_t), kAlign);
+    pl.n_ctr = (size_t)N * Hkv * pl.nsub;
+    pl.ws_bytes = pl.acc_bytes + pl.ml_bytes + align_up(ctr_region_bytes(pl.n_ctr), kAlign);
 }
 
 // Matrix-core path: all heads of the group per unit, 8 waves per unit, chunks of
@@ -244,6 +246,7 @@ int resolve_workspace(const Plan& pl, void* ws, size_t ws_bytes, DecodeParams& p
     p.part_acc = static_cast<float*>(ws);
     p.part_ml = reinterpret_cast<float*>(static_cast<char*>(ws) + pl.acc_bytes);
     p.counters = reinterpret_cast<unsigned long long*>(static_cast<char*>(ws) + pl.acc_bytes + pl.ml_bytes);
+    p.ctr_shift = ctr_shift_for(pl.n_ctr);
     p.epoch = next_epoch();
     const int t = tuning().fused_merge;
     p.merge_mode = t >= 0 ? t : (pl.max_chunks <= 8 ? kMergeAtomic : kMergeKernel);
@@ -492,7 +495,7 @@ size_t planned_workspace(int Hq, int Hkv, int D, int BLOCK, int dtype, int n_rec
     const size_t recs = (size_t)n_records * pl.G;
     pl.acc_bytes = align_up(recs * D * sizeof(float), kAlign);
     pl.ml_bytes = align_up(recs * 2 * sizeof(float), kAlign);
-    return pl.acc_bytes + pl.ml_bytes + align_up((size_t)n_records * sizeof(uint64_t), kAlign);
+    return pl.acc_bytes + pl.ml_bytes + align_up(ctr_region_bytes((size_t)n_records), kAlign);
 }
 
 template <class F>
@@ -605,6 +608,7 @@ int run_planned(const void* q, const void* k_new, const void* v_new, const int* 
             p.part_acc = static_cast<float*>(ws);
             p.part_ml = reinterpret_cast<float*>(static_cast<char*>(ws) + acc);
             p.counters = reinterpret_cast<unsigned long long*>(static_cast<char*>(ws) + acc + ml);
+            p.ctr_shift = ctr_shift_for((size_t)n_records);
         }
         p.epoch = next_epoch();
         p.merge_mode = tuning().fused_merge == kMergeFence ? kMergeFence : kMergeAtomic;  // planned: always fused
@@ -714,6 +718,7 @@ int run_self_planned(const void* q, const void* k, const void* v, const int* tab
     p.part_acc = static_cast<float*>(ws);
     p.part_ml = reinterpret_cast<float*>(static_cast<char*>(ws) + acc);
     p.counters = reinterpret_cast<unsigned long long*>(static_cast<char*>(ws) + acc + ml);
+    p.ctr_shift = ctr_shift_for(rall);
     p.epoch = next_epoch();
     p.merge_mode = kMergeAtomic;
     L.dtype = dtype; L.D = D; L.G = ps.G; L.mode = contig ? kSelfContig : kSelfPlanned; L.mfma = ps.mfma;

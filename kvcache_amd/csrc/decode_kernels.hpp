@@ -269,22 +269,46 @@ __device__ __forceinline__ void merge_head(const DecodeParams& p, size_t rec0, s
 }
 
 // Arrival count of a (sequence, KV head, head subgroup) before this unit, in a
-// 64-bit counter tagged with the call's epoch in the high word: a counter from
-// another call (or never initialised) counts as zero, and the last arriver
-// resets it to zero, so neither fresh nor replayed workspaces need clearing.
-// Only the first arrivals of a call see a stale tag and swap in (epoch, 1) with a
-// compare-and-swap; once the tag is current every arrival is one fetch-and-add,
-// so many chunks finishing together do not retry against each other.
+// 64-bit counter holding the call's epoch in the low word and the count in the high
+// word (counts never carry into the epoch): a counter from another call, reset, or
+// never initialised counts as zero, and the last arriver resets it to zero, so
+// neither fresh nor replayed workspaces need clearing.  An arrival is one
+// fetch-and-add; only when that returns another call's tag (the first arrivals of a
+// call) does the arriver adopt the counter with a compare-and-swap to (epoch, 1),
+// which discards the additions made to the stale value -- each of their arrivers
+// sees the stale tag too and comes through here.
 __device__ __forceinline__ unsigned arrive(unsigned long long* ctr, unsigned epoch) {
-    const unsigned long long tag = (unsigned long long)epoch << 32;
-    unsigned long long old = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    constexpr unsigned long long kOne = 1ull << 32;
+    unsigned long long old = __hip_atomic_fetch_add(ctr, kOne, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if ((unsigned)old == epoch) return (unsigned)(old >> 32);
+    old = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     for (;;) {
-        if ((old >> 32) == epoch)
-            return (unsigned)__hip_atomic_fetch_add(ctr, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (__hip_atomic_compare_exchange_strong(ctr, &old, tag | 1ull, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+        if ((unsigned)old == epoch)
+            return (unsigned)(__hip_atomic_fetch_add(ctr, kOne, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >> 32);
+        if (__hip_atomic_compare_exchange_strong(ctr, &old, kOne | epoch, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_AGENT))
             return 0u;
     }
+}
+
+// The parameter block of a decode kernel (its third argument, at byte 16 of the
+// kernarg segment after the work pointer and its int), read through a pointer the
+// compiler cannot prove loop-invariant.  A persistent loop would otherwise keep
+// every field it uses in scalar registers across all its iterations (some 60
+// registers, spilled into vector lanes); a fresh copy per unit lives only as long
+// as the unit that uses it.  The loads stay scalar (constant address space).
+constexpr int kParamsKernargOffset = 16;
+__device__ __forceinline__ DecodeParams fresh_params() {
+    static_assert(alignof(DecodeParams) == 8 && sizeof(const int*) == 8, "kernarg layout");
+#if defined(__HIP_DEVICE_COMPILE__)  // (the host pass only parses device functions)
+    typedef __attribute__((address_space(4))) const char* KArg;
+    typedef __attribute__((address_space(4))) const DecodeParams* KParams;
+    KArg ka = (KArg)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(ka));
+    return *(KParams)(ka + kParamsKernargOffset);
+#else
+    return DecodeParams{};
+#endif
 }
 
 // K/V registers of U wave-loads: the double-buffered unit of the inner loop.
@@ -418,7 +442,8 @@ constexpr int kMaxChunkBlocks = 4096;
 // writes either the normalised output (single-chunk sequence) or the chunk
 // partial, optionally followed by the fused cross-chunk merge.
 template <typename T, int D, int G, int MODE, int WPB, int U>
-__global__ __launch_bounds__(WPB * kWave) void split_kernel(const int* __restrict__ work, int work_ints, DecodeParams p) {
+__global__ __launch_bounds__(WPB * kWave) void split_kernel(const int* __restrict__ work, int work_ints, DecodeParams p_arg) {
+    const DecodeParams& p = p_arg;
     using Tr = Traits<T>;
     constexpr int EPL = Tr::EPL;
     constexpr int LPT = D / EPL;      // lanes per K/V row
@@ -441,8 +466,9 @@ __global__ __launch_bounds__(WPB * kWave) void split_kernel(const int* __restric
     // One unit, given its entry header (hdr) and, on the host-planned path, the
     // entry's block ids (ev: one int per lane after the 8-int header).
     auto run_unit = [&](const int (&hdr)[8], const int ev) {
-    // per-lane indices derived anew in every unit: in the persistent loop they would
-    // otherwise be hoisted out of it and held in registers across the whole loop
+    // self-planned (persistent) launches: the parameters and per-lane indices are
+    // derived anew in every unit, not hoisted out of the loop and held across it
+    const DecodeParams p = SELF ? fresh_params() : p_arg;
     int tid_u = threadIdx.x;
     if constexpr (SELF) asm volatile("" : "+v"(tid_u));
     const int lane = tid_u & (kWave - 1);
@@ -692,7 +718,7 @@ __global__ __launch_bounds__(WPB * kWave) void split_kernel(const int* __restric
     } else {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     }
-    unsigned long long* ctr = p.counters + ctr_idx;
+    unsigned long long* ctr = p.counters + ctr_slot(ctr_idx, p.ctr_shift);
     unsigned before = 0;
     if (lane == 0) before = arrive(ctr, p.epoch);
     before = (unsigned)uniform((int)before);
@@ -709,11 +735,7 @@ __global__ __launch_bounds__(WPB * kWave) void split_kernel(const int* __restric
 
     if constexpr (SELF) {
         // self-planned launches pass the device lengths as the (preloaded) first argument
-        const SelfPlan sp = self_plan_setup<WPB * kWave>(work, p, s_plan);
-        for (int k = 0, r = self_plan_rank(0); r < sp.units; r = self_plan_rank(++k)) {
-            int hdr[8];
-            if (self_plan_unit<T, D, WPB * kWave>(p, s_plan, sp, r, G, hdr)) run_unit(hdr, 0);
-        }
+        self_plan_loop<T, D, WPB * kWave>(work, work_ints, p, s_plan, G, [&](const int (&hdr)[8]) { run_unit(hdr, 0); });
     } else {
         // planned entries may carry the chunk's first block ids after the 8-int
         // header (one int per lane, read together with the header), so the first

@@ -55,7 +55,8 @@ __device__ __forceinline__ s16x4v ds_read_tr16(const char* p) {
 }
 
 template <int D, int MODE, int WPB>
-__global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(const int* __restrict__ work, int work_ints, DecodeParams p) {
+__global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(const int* __restrict__ work, int work_ints, DecodeParams p_arg) {
+    const DecodeParams& p = p_arg;
     static_assert(D == 64 || D == 128, "MFMA decode is built for head_dim 64 and 128");
     constexpr int ROW = D * 2;                 // bytes per fp16 K/V row
     constexpr int KJ = D / 32;                 // MFMA k-steps over the head dimension
@@ -86,8 +87,9 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(const int* __rest
     // One unit, given its entry header (hdr) and, on the host-planned path, the
     // entry's block ids (ev: one int per lane after the 8-int header).
     auto run_unit = [&](const int (&hdr)[8], const int ev) {
-    // per-lane indices derived anew in every unit (not hoisted out of the persistent
-    // loop and held across it)
+    // self-planned (persistent) launches: the parameters and per-lane indices are
+    // derived anew in every unit, not hoisted out of the loop and held across it
+    const DecodeParams p = SELF ? fresh_params() : p_arg;
     int tid_u = tid;
     if constexpr (SELF) asm volatile("" : "+v"(tid_u));
     const int lane = tid_u & (kWave - 1);
@@ -127,7 +129,9 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(const int* __rest
     // the new K/V in place of the pool's (this lane's slices of it, loaded here,
     // ahead of the table), and the unit of the first head subgroup stores the row
     // in the pool once the block ids are staged.
-    int wp = -1;
+    // The position is loaded here but resolved only after the first K/V tile is in
+    // flight (resolve_append): nothing before the first loads waits for it.
+    int wp = -1, w_raw = -1;
     u32x4 vnew = {0, 0, 0, 0}, kst = {0, 0, 0, 0};  // bytes (lane*16) % ROW of the new V and K rows
     if constexpr (PLANNED) {
         if (p.wpos != nullptr) {
@@ -135,8 +139,7 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(const int* __rest
             const char* vn = static_cast<const char*>(p.v_new) + ((size_t)s * p.Hkv + hk) * ROW;
             vnew = *reinterpret_cast<const u32x4*>(vn + (lane * 16) % ROW);
             kst = *reinterpret_cast<const u32x4*>(kn + (lane * 16) % ROW);
-            const int w = p.wpos[s];
-            wp = uniform((w >= j0 && w < j1) ? w : -1);
+            w_raw = p.wpos[s];
         }
     }
 
@@ -194,12 +197,21 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(const int* __rest
         if (inl) return __builtin_amdgcn_readlane(ev, 8 + min(rel, kWave - 9));
         return uniform(s_tab[min(rel, kMfmaMaxChunkBlocks - 1)]);
     };
-    if (PLANNED && wp >= 0 && u.sub == 0 && wave == 0 && lane < ROW / 16) {
-        const int phys = block_id(max((wp >> bsh) - b0, 0));
-        const size_t off = ((size_t)(phys * p.Hkv + hk) * p.block + (wp & bmask)) * ROW + lane * 16;
-        *reinterpret_cast<u32x4*>(const_cast<char*>(kb) + off) = kst;
-        *reinterpret_cast<u32x4*>(const_cast<char*>(vb) + off) = vnew;
-    }
+    // The step's new row: its position within this chunk (else -1), and its store into
+    // the pools by the first head subgroup.  No tile of this unit reads the pools'
+    // copy of that row (consume takes it from the inputs), so the store may land
+    // after the unit's loads.
+    auto resolve_append = [&]() {
+        if constexpr (PLANNED) {
+            if (p.wpos != nullptr) wp = uniform((w_raw >= j0 && w_raw < j1) ? w_raw : -1);
+        }
+        if (PLANNED && wp >= 0 && u.sub == 0 && wave == 0 && lane < ROW / 16) {
+            const int phys = block_id(max((wp >> bsh) - b0, 0));
+            const size_t off = ((size_t)(phys * p.Hkv + hk) * p.block + (wp & bmask)) * ROW + lane * 16;
+            *reinterpret_cast<u32x4*>(const_cast<char*>(kb) + off) = kst;
+            *reinterpret_cast<u32x4*>(const_cast<char*>(vb) + off) = vnew;
+        }
+    };
 
     struct Tile {
         u32x4 k[2][VL];   // both: 1 KiB of whole rows per wave load
@@ -348,6 +360,7 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(const int* __rest
     if (kmax > 0) {
         Tile A, B;
         issue(0, A);
+        resolve_append();
         for (int k = 0;; k += 2) {
             issue(k + 1, B);
             step(k, A);
@@ -356,6 +369,8 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(const int* __rest
             step(k + 1, B);
             if (k + 2 >= kmax) break;
         }
+    } else {
+        resolve_append();
     }
     l = sum_xor32(sum_xor16(l));
 
@@ -449,7 +464,7 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(const int* __rest
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     }
     __syncthreads();
-    unsigned long long* ctr = p.counters + u.ctr_idx;
+    unsigned long long* ctr = p.counters + ctr_slot(u.ctr_idx, p.ctr_shift);
     if (tid == 0) s_last = arrive(ctr, p.epoch) == (unsigned)(nc - 1);
     __syncthreads();
     if (!s_last) return;
@@ -509,11 +524,8 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(const int* __rest
 
     if constexpr (SELF) {
         // self-planned launches pass the device lengths as the (preloaded) first argument
-        const SelfPlan sp = self_plan_setup<WPB * kWave>(work, p, s_plan);
-        for (int k = 0, r = self_plan_rank(0); r < sp.units; r = self_plan_rank(++k)) {
-            int hdr[8];
-            if (self_plan_unit<_Float16, D, WPB * kWave>(p, s_plan, sp, r, heads, hdr)) run_unit(hdr, 0);
-        }
+        self_plan_loop<_Float16, D, WPB * kWave>(work, work_ints, p, s_plan, heads,
+                                                 [&](const int (&hdr)[8]) { run_unit(hdr, 0); });
     } else {
         // planned entries carry the unit's block ids after the 8-int header (one int
         // per lane): entry and header are read first, from the preloaded arguments

@@ -56,7 +56,9 @@ struct DecodeParams {
     const int* cur_len;       // device lengths (nullptr: use fixed_len)
     float* part_acc;          // [N*max_chunks*Hq, D] fp32 partial accumulators
     float* part_ml;           // [N*max_chunks*Hq, 2] (running max in log2 units, running sum)
-    unsigned long long* counters;  // [N*Hkv*nsub] arrival counters (fused merge), or nullptr
+    unsigned long long* counters;  // arrival counters (fused merge), or nullptr; counter i lives at
+                                   // ctr_slot(i, ctr_shift): consecutive counters on separate lines
+    int ctr_shift;            // log2 of the 128-byte lines of the counter region
     long long seq_stride;     // contiguous: elements between sequences
     long long head_stride;    // contiguous: elements between KV heads
     const int* work;          // planned units (work_ints ints each, see kvc_decode_plan), or nullptr
@@ -79,6 +81,27 @@ struct DecodeParams {
     int sp_records;           // partial records per (sequence, head) in the workspace
     const int* dev_base;
 };
+
+// Arrival counters.  Atomics that land on one 128-byte line serialise (about 10 ns
+// each on MI355X, whether or not they hit the same address), so counters that are
+// hot together must not share a line: counter i goes to line i mod L, word i / L
+// (L = 2^ctr_shift lines of 16 words).  L is at least min(count, 1024), so up to
+// 1024 counters each own a line.
+constexpr int kCtrWordsPerLine = 16;
+inline int ctr_shift_for(size_t count) {
+    size_t lines = count < 1024 ? count : 1024;
+    const size_t need = (count + kCtrWordsPerLine - 1) / kCtrWordsPerLine;
+    if (need > lines) lines = need;
+    int sh = 0;
+    while (((size_t)1 << sh) < lines) ++sh;
+    return sh;
+}
+inline size_t ctr_region_bytes(size_t count) {
+    return count ? ((size_t)kCtrWordsPerLine * sizeof(unsigned long long)) << ctr_shift_for(count) : 0;
+}
+__host__ __device__ inline size_t ctr_slot(size_t i, int shift) {
+    return ((i & (((size_t)1 << shift) - 1)) * kCtrWordsPerLine) + (i >> shift);
+}
 
 // How the chunk partials of a split sequence are combined.
 enum MergeMode {

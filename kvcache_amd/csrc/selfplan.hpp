@@ -7,16 +7,13 @@
 // qwen_kernels.cu:293-326), so the host cannot plan the launch without a copy and
 // a synchronisation.  Instead every workgroup of a persistent grid derives the
 // host planner's work (kvc_decode_plan: the same chunk target, the same chunks,
-// the same partial-record and counter numbering) from the lengths, orders the units
-// as the planner does (up to rounding at bucket edges) -- chunks of split sequences
-// first, then by length, longest first (64 length buckets relative to the chunk
-// target) -- and serves ranks in
-// rounds of gridDim.x (self_plan_rank).  Every workgroup computes the same order
-// from the same data, so each unit runs exactly once.  Per workgroup: one round of
-// loads (lengths, table offsets) into LDS, two reductions and a key histogram; per
-// rank, one wave-wide scan over the sequences.  Outputs equal the host-planned
-// launch's on the same lengths bit for bit (same chunks, same merge order); only the
-// order in which units run differs within a length bucket.
+// the same partial-record and counter numbering) from the lengths, puts the units in
+// one order -- eight buckets, chunks of split sequences first, then by length,
+// longest first; within a bucket by sequence -- and serves ranks in rounds of
+// gridDim.x (self_plan_rank).  Every workgroup computes the same order from the same
+// data, so each unit runs exactly once, and outputs equal the host-planned launch's
+// bit for bit (same chunks, same merge order); only the order in which units run
+// differs from the host plan's.
 //
 // Budget: every (sequence, KV head) may use up to p.sp_records partial records (64,
 // or more when the caller states a long bound), and on the matrix-core path a
@@ -25,38 +22,37 @@
 // even at the largest chunk, or with a length past its contiguous cache (p.cap),
 // gets NaN outputs: never a silent partial attention.
 //
-// Cost structure: the lengths pointer arrives as the kernel's first (preloaded)
-// argument, so their loads issue at wave start, beside the parameter block's; the
-// setup then needs two barriers.  Finding a rank's unit is wave-local: every wave
-// holds the key table in registers and scans the plan rows with lane shuffles, so
-// the persistent loop has no barrier and no LDS broadcast between units.
+// Cost structure.  A wave issues a dependent VALU instruction every ~6 cycles, so
+// the setup is written as short dependent chains: the lengths load at wave start
+// (their pointer is the kernel's preloaded first argument); one barrier publishes
+// the per-wave totals (tokens, longest length, table blocks), the chunk target is
+// integer arithmetic in 32 bits (the 64-bit forms only past 2^32 tokens); a second
+// barrier publishes the per-wave unit counts of the eight buckets and the record and
+// counter counts (wave scans); then each thread, knowing the first rank of each of
+// its sequences' runs, writes the headers of the ranks this workgroup serves in a
+// window of kSelfWindow rounds into LDS; a third barrier, and the persistent loop
+// only reads a header per unit.  Batches needing more rounds repeat the setup per
+// window.
 
-constexpr int kSelfMaxNValu = 1024;    // sequences per launch (their plan rows live in LDS)
-constexpr int kSelfMaxNMfma = 512;     // (keeps two matrix-core workgroups per CU)
-constexpr int kSelfBuckets = 64;       // length buckets per split flag
-constexpr int kSelfKeys = 2 * kSelfBuckets;
+constexpr int kSelfMaxNValu = 1024;   // sequences per launch (their plan rows live in LDS)
+constexpr int kSelfMaxNMfma = 512;    // (keeps the matrix-core kernel's LDS within two workgroups per CU)
+constexpr int kSelfSpt = 4;           // length loads in flight per lane of the planning wave
+constexpr int kSelfBuckets = 8;       // order buckets: 4 for chunks of split sequences, 4 for whole sequences
 constexpr int kSelfMaxChunks = 0xFFFF;  // chunks of one sequence (16-bit plan field)
-constexpr int kSelfSpt = 4;            // sequences per setup thread (kSelfMaxNValu / 256)
+constexpr int kSelfWindow = 16;       // rounds whose unit headers a workgroup resolves per setup
 
 template <int NMAX, int NW>
 struct SelfPlanLds {
     int len[NMAX];             // attended length of each sequence (>= 0)
     int to[NMAX];              // first table entry of each sequence
     int cut[NMAX];             // chunks | chunk length in blocks << 16
-    int keys[NMAX];            // key of chunks 0..nc-2 | key of the last chunk << 8
-    int hist[NW][kSelfKeys + 1];  // per-wave units per order key; [kSelfKeys]: sequences past the limits
-    unsigned long long tot[NW];  // per-wave sums of max(L, 1)
-    int lmax[NW];
-    int nb[NW];                // per-wave blocks (packed tables)
+    int bk[NMAX];              // bucket of run A | bucket of run B << 4
+    int plan[4];               // chunk target, units, overflow
+    int hdr[kSelfWindow][8];   // unit headers of this workgroup's ranks in the window (hdr[k][0] < 0: none)
 };
 
-// The plan as every wave holds it after self_plan_setup: the chunk target, the
-// number of ranks and, per lane, the first rank and the unit count of keys
-// kSelfKeys-1-2*lane (a) and kSelfKeys-2-2*lane (b); ranks run over the keys in
-// descending order.
 struct SelfPlan {
     int T, units, overflow;
-    int base_a, cnt_a, base_b, cnt_b;
 };
 
 // Inclusive prefix sum over the 64 lanes with DPP: shifts of 1, 2, 4, 8 within each
@@ -84,13 +80,19 @@ __device__ __forceinline__ int wave_incl_max(int x) {
     return x;
 }
 
-// ceil(a / b) for 0 <= a < 2^53, 0 < b < 2^31 (uniform operands: a double quotient
-// corrected to the exact integer, instead of a 64-bit integer division)
-__device__ __forceinline__ long long ceil_div_u(long long a, long long b) {
+// ceil(a / b), 64-bit, for the rare launches past 32-bit token counts (a < 2^53,
+// 0 < b < 2^53): a double quotient corrected to the exact integer.
+__device__ __forceinline__ long long ceil_div_u64(long long a, long long b) {
     long long q = (long long)((double)a / (double)b);
     while (q * b < a) ++q;
     while (q > 0 && (q - 1) * b >= a) --q;
     return q;
+}
+
+// ceil(a / b) in 32 bits (b > 0), without overflow near 2^32.
+__device__ __forceinline__ unsigned ceil_div_u32(unsigned a, unsigned b) {
+    const unsigned q = a / b;
+    return q + (q * b < a ? 1u : 0u);
 }
 
 // Chunks of a sequence of L tokens at chunk target T (make_plan in abi.hip), in
@@ -110,231 +112,12 @@ __device__ __forceinline__ void self_split(const DecodeParams& p, int L, int T, 
     }
 }
 
-// Order key of a unit of `len` tokens: split units above whole ones, longer above
-// shorter; kscale = 42 / T.  The planner's bucket len * 42 / T, in float: the key
-// only orders the units (their chunks, records and counters do not depend on it),
-// so a unit at a bucket edge may sort one bucket away from the host plan's order.
-__device__ __forceinline__ int self_key(bool split, int len, float kscale) {
-    const int b = min(kSelfBuckets - 1, (int)((float)len * kscale));
-    return (split ? kSelfBuckets : 0) + b;
-}
-
-// Units of a sequence in key `key`: run A = chunks 0..nc-2 of every head (nc > 1),
-// run B = the last chunk of every head.
-__device__ __forceinline__ void self_runs(int nc, int keys, int key, int hks, int& ca, int& cb) {
-    ca = nc > 1 && (keys & 0xFF) == key ? hks * (nc - 1) : 0;
-    cb = (keys >> 8) == key ? hks : 0;
-}
-
-// Reads the lengths (`lens`, device memory; NULL: causal prompt queries) and table
-// offsets, picks the chunk target, cuts every sequence into chunks and counts the
-// units per order key.  Every thread of the workgroup calls it; every wave returns
-// the same plan.
-template <int NT, typename Lds>
-__device__ SelfPlan self_plan_setup(const int* lens, const DecodeParams& p, Lds& S) {
-    constexpr int NW = NT / kWave;
-    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = uniform(tid >> 6);
-    const int N = p.N, B = p.block, hks = p.Hkv * p.nsub;
-    const int bsh = __builtin_ctz((unsigned)B);
-    const int spt = (N + NT - 1) / NT;  // consecutive sequences per thread
-    const int i0 = min(tid * spt, N), i1 = min(i0 + spt, N);
-    const int first = p.dev_base ? *p.dev_base : p.fixed_len;  // causal prompt queries
-    int* hist = S.hist[wave];
-    for (int k = lane; k <= kSelfKeys; k += kWave) hist[k] = 0;
-    // the thread's lengths and table offsets, all loads issued before any is used
-    // (bounded buffer loads: indices past N read 0 and touch no memory)
-    static_assert(NT >= 256, "at most kSelfSpt sequences per thread");
-    const __amdgpu_buffer_rsrc_t lrs = tile_rsrc(lens, lens ? N * 4 : 0);
-    const __amdgpu_buffer_rsrc_t trs = tile_rsrc(p.tab_off, p.tab_off ? N * 4 : 0);
-    int lv[kSelfSpt], tv[kSelfSpt];
-#pragma unroll
-    for (int j = 0; j < kSelfSpt; ++j) {
-        lv[j] = (int)__builtin_amdgcn_raw_buffer_load_b32(lrs, (i0 + j) * 4, 0, 0);
-        tv[j] = (int)__builtin_amdgcn_raw_buffer_load_b32(trs, (i0 + j) * 4, 0, 0);
-    }
-    unsigned long long tot = 0;  // at most 4 sequences per thread: < 2^33
-    int lmax = 0, nb = 0;
-#pragma unroll
-    for (int j = 0; j < kSelfSpt; ++j) {
-        const int i = i0 + j;
-        if (i < i1) {
-            const int L = max(lens ? lv[j] : (p.causal ? first + i + 1 : p.fixed_len), 0);
-            S.len[i] = L;
-            S.to[i] = tv[j];
-            tot += (unsigned)max(L, 1);
-            lmax = max(lmax, L);
-            nb += (int)(((unsigned)L + B - 1) >> bsh);
-        }
-    }
-    // wave totals: the 64-bit sum as two 32-bit scans of its low 20 and high bits
-    const int tlo = wave_incl_scan((int)(tot & 0xFFFFF)), thi = wave_incl_scan((int)(tot >> 20));
-    const int lmx = wave_incl_max(lmax);
-    const int nb_incl = wave_incl_scan(nb);
-    if (lane == kWave - 1) {
-        S.tot[wave] = ((unsigned long long)(unsigned)thi << 20) + (unsigned)tlo;
-        S.lmax[wave] = lmx;
-        S.nb[wave] = nb_incl;
-    }
-    __syncthreads();
-    unsigned long long tall = 0;
-    int lall = 0, nb_pre = 0;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) {
-        tall += S.tot[w];
-        lall = max(lall, S.lmax[w]);
-        nb_pre += w < wave ? S.nb[w] : 0;
-    }
-    // chunk target: the host planner's (make_plan, target 0) ...
-    const long long tokens = (long long)tall;
-    long long target = ceil_div_u(tokens * hks, p.sp_slots);
-    target = min(target, (long long)p.sp_target_cap);
-    target = min(target, (long long)(INT_MAX / 2));
-    long long T = max(target, (long long)p.sp_min_chunk);
-    T = (T + B - 1) >> bsh << bsh;
-    T = min(T, (long long)p.sp_max_chunk);
-    // ... raised to the record budget (and the 64-chunk merge of the matrix-core path)
-    long long fit = ceil_div_u(tokens, (long long)(p.sp_records - 1) * N);
-    if (p.sp_nc_max) fit = max(fit, ((long long)lall + 62) / 63);
-    fit = (fit + B - 1) >> bsh << bsh;
-    const bool overflow = fit > p.sp_max_chunk;
-    if (fit > T) T = min(fit, (long long)p.sp_max_chunk);
-    const int Ti = uniform((int)T);
-    const float kscale = 42.0f / (float)Ti;
-    int run = nb_pre + nb_incl - nb;  // packed tables: first entry of sequence i0
-    int over = 0;
-    for (int i = i0; i < i1; ++i) {
-        const int L = S.len[i];
-        if (p.causal) {
-            S.to[i] = 0;  // prompt queries: one shared table
-        } else if (!p.tab_off) {
-            S.to[i] = run;
-            run += (int)(((unsigned)L + B - 1) >> bsh);
-        }
-        int nc, chunk;
-        self_split(p, L, Ti, bsh, nc, chunk);
-        over += nc > kSelfMaxChunks || L > p.cap ? 1 : 0;
-        const int ka = self_key(nc > 1, chunk, kscale);
-        const int kb = self_key(nc > 1, nc > 1 ? L - (nc - 1) * chunk : L, kscale);
-        S.cut[i] = min(nc, kSelfMaxChunks) | ((chunk >> bsh) << 16);
-        S.keys[i] = ka | (kb << 8);
-        if (nc > 1) atomicAdd(&hist[ka], hks * (nc - 1));
-        atomicAdd(&hist[kb], hks);
-    }
-    if (over) atomicAdd(&hist[kSelfKeys], over);
-    __syncthreads();
-    // every wave adds the per-wave histograms and scans the keys in descending order
-    const int ka = kSelfKeys - 1 - 2 * lane, kb = ka - 1;
-    int ca = 0, cb = 0, ov = 0;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) {
-        ca += S.hist[w][ka];
-        cb += S.hist[w][kb];
-        ov += S.hist[w][kSelfKeys];
-    }
-    const int incl = wave_incl_scan(ca + cb);
-    SelfPlan sp;
-    sp.T = Ti;
-    sp.overflow = overflow || uniform(ov) > 0;
-    sp.units = sp.overflow ? N * hks : __builtin_amdgcn_readlane(incl, kWave - 1);
-    sp.base_a = incl - ca - cb;
-    sp.cnt_a = ca;
-    sp.base_b = incl - cb;
-    sp.cnt_b = cb;
-    return sp;
-}
-
-// The unit of rank r (r < sp.units) as a planned-entry header.  Every thread of the
-// workgroup calls it with the same r; each wave finds the unit on its own (lane
-// shuffles over the plan rows, no barrier).  Returns false (after writing NaN to the
-// unit's output rows) when the batch overflowed the plan's budget.
-template <typename E, int D, int NT, typename Lds>
-__device__ bool self_plan_unit(const DecodeParams& p, const Lds& S, const SelfPlan& sp, int r, int heads,
-                               int (&hdr)[8]) {
-    const int tid = threadIdx.x, lane = tid & (kWave - 1);
-    const int N = p.N, hks = p.Hkv * p.nsub;
-    if (sp.overflow) {
-        const int s = r / hks, h = r % hks;
-        const int hq0 = (h / p.nsub) * p.group + (h % p.nsub) * heads;
-        E* ob = static_cast<E*>(p.out) + ((size_t)s * p.Hq + hq0) * D;
-        for (int e = tid; e < heads * D; e += NT) ob[e] = (E)__builtin_nanf("");
-        return false;
-    }
-    // the key holding rank r
-    const unsigned long long ma = __ballot(r >= sp.base_a && r < sp.base_a + sp.cnt_a);
-    const unsigned long long mb = __ballot(r >= sp.base_b && r < sp.base_b + sp.cnt_b);
-    if (!ma && !mb) return false;
-    int key, q;
-    if (ma) {
-        const int l = __ffsll((long long)ma) - 1;
-        key = kSelfKeys - 1 - 2 * l;
-        q = r - __builtin_amdgcn_readlane(sp.base_a, l);
-    } else {
-        const int l = __ffsll((long long)mb) - 1;
-        key = kSelfKeys - 2 - 2 * l;
-        q = r - __builtin_amdgcn_readlane(sp.base_b, l);
-    }
-    // this lane's sequences, in order: units in `key`, records, counters
-    const int spl = (N + kWave - 1) / kWave;
-    const int i0 = min(lane * spl, N), i1 = min(i0 + spl, N);
-    int own = 0, nrec = 0, nctr = 0;
-    for (int i = i0; i < i1; ++i) {
-        const int nc = S.cut[i] & 0xFFFF;
-        int ca, cb;
-        self_runs(nc, S.keys[i], key, hks, ca, cb);
-        own += ca + cb;
-        nrec += nc > 1 ? nc : 0;
-        nctr += nc > 1 ? 1 : 0;
-    }
-    int base = wave_incl_scan(own) - own;
-    int rec = wave_incl_scan(nrec) - nrec;
-    int ctr = wave_incl_scan(nctr) - nctr;
-    const bool mine = q >= base && q < base + own;  // exactly one lane
-    int h0 = 0, h1 = 0, h2 = 0, h3 = 0, h4 = 0, h5 = 0, h6 = 0, h7 = 0;
-    if (mine) {
-        for (int i = i0; i < i1; ++i) {
-            const int nc = S.cut[i] & 0xFFFF;
-            int ca, cb;
-            self_runs(nc, S.keys[i], key, hks, ca, cb);
-            if (q < base + ca + cb) {
-                const int x = q - base;
-                int h, c;
-                if (x < ca) {
-                    h = x / (nc - 1);
-                    c = x - h * (nc - 1);
-                } else {
-                    h = x - ca;
-                    c = nc - 1;
-                }
-                const int L = S.len[i];
-                const int cblk = S.cut[i] >> 16;
-                const int j0 = c * cblk * p.block;
-                h0 = i;
-                h1 = h | (c << 16);
-                h2 = nc > 1 ? j0 : 0;
-                h3 = nc > 1 ? min(j0 + cblk * p.block, L) : L;
-                h4 = nc;
-                h5 = nc > 1 ? hks * rec + h * nc : -1;
-                h6 = nc > 1 ? hks * ctr + h : -1;
-                h7 = S.to[i] + (nc > 1 ? c * cblk : 0);
-                break;
-            }
-            base += ca + cb;
-            rec += nc > 1 ? nc : 0;
-            ctr += nc > 1 ? 1 : 0;
-        }
-    }
-    const unsigned long long mm = __ballot(mine);
-    if (!mm) return false;
-    const int src = __ffsll((long long)mm) - 1;
-    hdr[0] = __builtin_amdgcn_readlane(h0, src);
-    hdr[1] = __builtin_amdgcn_readlane(h1, src);
-    hdr[2] = __builtin_amdgcn_readlane(h2, src);
-    hdr[3] = __builtin_amdgcn_readlane(h3, src);
-    hdr[4] = __builtin_amdgcn_readlane(h4, src);
-    hdr[5] = __builtin_amdgcn_readlane(h5, src);
-    hdr[6] = __builtin_amdgcn_readlane(h6, src);
-    hdr[7] = __builtin_amdgcn_readlane(h7, src);
-    return true;
+// Order bucket of a run of units of `len` tokens each: chunks of split sequences
+// (4..7) above whole sequences (0..3), longer above shorter, in quarters of 3T/8
+// (kscale = 8 / 3T).  Buckets only order the units; chunks, records and counters do
+// not depend on them.
+__device__ __forceinline__ int self_bucket(bool split, int len, float kscale) {
+    return (split ? 4 : 0) + min(3, (int)((float)len * kscale));
 }
 
 // The k-th rank workgroup b serves: the grid walks the ranks in rounds of gridDim.x,
@@ -346,3 +129,242 @@ __device__ __forceinline__ int self_plan_rank(int k) {
     const int G = (int)gridDim.x, b = (int)blockIdx.x;
     return k * G + ((k & 1) ? G - 1 - b : b);
 }
+
+// Reads the lengths (`lens`, device memory; NULL: causal prompt queries) and table
+// offsets, picks the chunk target, cuts every sequence into chunks, orders the units
+// and writes the headers of this workgroup's ranks in rounds [kw, kw + kSelfWindow)
+// into S.hdr.  Wave 0 does all of it -- lane l owns the consecutive sequences
+// [l * spl, l * spl + spl), so every reduction and ordering is one wave scan -- while
+// the other waves wait at the closing barrier; every wave then returns the same plan.
+// Order: eight buckets (self_bucket), descending; within a bucket by sequence, and
+// within a sequence run A (chunks 0..nc-2 of every head) before run B (its last
+// chunk of every head).
+template <int NT, typename Lds>
+__device__ SelfPlan self_plan_setup(const int* lens, int n_seq, const DecodeParams& p, Lds& S, int kw) {
+    const int tid = threadIdx.x, lane = tid & (kWave - 1);
+    if (tid < kWave) {
+        // the lengths loads depend only on the preloaded arguments (lens, n_seq): they
+        // issue at wave start, beside the parameter block's
+        const int N = n_seq;
+        const int spl = (N + kWave - 1) / kWave;  // consecutive sequences per lane
+        const int i0 = min(lane * spl, N), i1 = min(i0 + spl, N);
+        const __amdgpu_buffer_rsrc_t lrs = tile_rsrc(lens, lens ? N * 4 : 0);
+        int lv0[kSelfSpt];
+#pragma unroll
+        for (int j = 0; j < kSelfSpt; ++j) lv0[j] = (int)__builtin_amdgcn_raw_buffer_load_b32(lrs, (i0 + j) * 4, 0, 0);
+        const int B = p.block, hks = p.Hkv * p.nsub;
+        const int bsh = __builtin_ctz((unsigned)B);
+        const int first = lens ? 0 : (p.dev_base ? *p.dev_base : p.fixed_len);  // causal prompt queries
+        if (lane < kSelfWindow) S.hdr[lane][0] = -1;
+        // this lane's lengths and table offsets, kSelfSpt loads in flight at a time
+        // (bounded buffer loads: indices past N read 0 and touch no memory)
+        const __amdgpu_buffer_rsrc_t trs = tile_rsrc(p.tab_off, p.tab_off ? N * 4 : 0);
+        unsigned tlo = 0, thi = 0;  // sum of max(L, 1): low 20 bits and the rest, apart
+        int lmax = 0, nb = 0;
+#pragma unroll 1
+        for (int ib = i0; ib < i1; ib += kSelfSpt) {
+            int lv[kSelfSpt], tv[kSelfSpt];
+#pragma unroll
+            for (int j = 0; j < kSelfSpt; ++j) {
+                lv[j] = ib == i0 ? lv0[j] : (int)__builtin_amdgcn_raw_buffer_load_b32(lrs, (ib + j) * 4, 0, 0);
+                tv[j] = (int)__builtin_amdgcn_raw_buffer_load_b32(trs, (ib + j) * 4, 0, 0);
+            }
+#pragma unroll
+            for (int j = 0; j < kSelfSpt; ++j) {
+                const int i = ib + j;
+                if (i < i1) {
+                    const int L = max(lens ? lv[j] : (p.causal ? first + i + 1 : p.fixed_len), 0);
+                    S.len[i] = L;
+                    S.to[i] = tv[j];
+                    const unsigned w = (unsigned)max(L, 1);
+                    tlo += w & 0xFFFFF;
+                    thi += w >> 20;
+                    lmax = max(lmax, L);
+                    nb += (int)(((unsigned)L + B - 1) >> bsh);
+                }
+            }
+        }
+        // the chunk target: the host planner's (make_plan with target 0) ...
+        const int slo = wave_incl_scan((int)tlo), shi = wave_incl_scan((int)thi);
+        const int lall = __builtin_amdgcn_readlane(wave_incl_max(lmax), kWave - 1);
+        nb = wave_incl_scan(nb) - nb;  // blocks of the sequences before this lane's (packed tables)
+        const unsigned long long tokens =
+            ((unsigned long long)(unsigned)__builtin_amdgcn_readlane(shi, kWave - 1) << 20) +
+            (unsigned)__builtin_amdgcn_readlane(slo, kWave - 1);
+        const int M = p.sp_max_chunk;  // a multiple of BLOCK; T never exceeds it
+        const unsigned long long prod = tokens * (unsigned)hks;
+        const unsigned long long pmax = (unsigned long long)(unsigned)p.sp_slots * (unsigned)M;
+        long long c;  // ceil(tokens * hks / slots), capped at M (the same T follows)
+        if (prod >= pmax) c = M;
+        else if (pmax <= 0xFFFFFFFFull) c = ceil_div_u32((unsigned)prod, (unsigned)p.sp_slots);
+        else c = ceil_div_u64((long long)prod, p.sp_slots);
+        long long T = min(c, (long long)p.sp_target_cap);
+        T = max(T, (long long)p.sp_min_chunk);
+        T = (T + B - 1) >> bsh << bsh;
+        T = min(T, (long long)M);
+        // ... raised to the record budget (and the 64-chunk merge of the matrix-core
+        // path): fit = ceil(tokens / ((sp_records - 1) * N)); past M only that matters
+        const unsigned long long den = (unsigned long long)(unsigned)(p.sp_records - 1) * (unsigned)N;
+        long long fit;
+        if (tokens > den * (unsigned)M) fit = (long long)M + B;
+        else if (tokens <= 0xFFFFFFFFull && den <= 0xFFFFFFFFull) fit = ceil_div_u32((unsigned)tokens, (unsigned)den);
+        else fit = ceil_div_u64((long long)tokens, (long long)den);
+        if (p.sp_nc_max) fit = max(fit, ((long long)lall + 62) / 63);
+        fit = (fit + B - 1) >> bsh << bsh;
+        const bool t_over = fit > M;
+        if (fit > T) T = min(fit, (long long)M);
+        const int Ti = uniform((int)T);
+        const float kscale = 8.0f / (3.0f * (float)Ti);
+        // this lane's sequences: chunks, and the buckets of their two runs
+        int cnt[kSelfBuckets];
+#pragma unroll
+        for (int b = 0; b < kSelfBuckets; ++b) cnt[b] = 0;
+        int nrec = 0, nctr = 0, over = 0;
+#pragma unroll 2
+        for (int i = i0; i < i1; ++i) {
+            const int L = S.len[i];
+            if (p.causal) {
+                S.to[i] = 0;  // prompt queries: one shared table
+            } else if (!p.tab_off) {
+                S.to[i] = nb;  // packed tables in sequence order
+                nb += (int)(((unsigned)L + B - 1) >> bsh);
+            }
+            int nc, chunk;
+            self_split(p, L, Ti, bsh, nc, chunk);
+            over |= nc > kSelfMaxChunks || L > p.cap;
+            nc = min(nc, kSelfMaxChunks);
+            const int ka = self_bucket(nc > 1, chunk, kscale);
+            const int kb = self_bucket(nc > 1, nc > 1 ? L - (nc - 1) * chunk : L, kscale);
+            S.cut[i] = nc | ((chunk >> bsh) << 16);
+            S.bk[i] = ka | (kb << 4);
+            const int ca = nc > 1 ? hks * (nc - 1) : 0;
+#pragma unroll
+            for (int b = 0; b < kSelfBuckets; ++b) cnt[b] += (b == ka ? ca : 0) + (b == kb ? hks : 0);
+            nrec += nc > 1 ? nc : 0;
+            nctr += nc > 1 ? 1 : 0;
+        }
+        // the order: buckets descending, sequences ascending within a bucket (run A
+        // before run B); first rank of this lane's units per bucket
+        int excl[kSelfBuckets];
+        int units = 0;
+#pragma unroll
+        for (int b = kSelfBuckets - 1; b >= 0; --b) {
+            const int inc = wave_incl_scan(cnt[b]);
+            excl[b] = units + inc - cnt[b];
+            units += __builtin_amdgcn_readlane(inc, kWave - 1);
+        }
+        const int rec0 = wave_incl_scan(nrec) - nrec, ctrb = wave_incl_scan(nctr) - nctr;
+        const bool overflow = t_over || __ballot(over) != 0;
+        units = overflow ? N * hks : units;
+        const int G = (int)gridDim.x;
+        const int kcount = overflow ? 0 : min(kSelfWindow, (units + G - 1) / G - kw);
+        if (lane == 0) {
+            S.plan[0] = Ti;
+            S.plan[1] = units;
+            S.plan[2] = overflow ? 1 : 0;
+        }
+        // the headers of this workgroup's ranks in the window: the lane holding a rank
+        // walks its sequences' runs in that bucket
+#pragma unroll 1
+        for (int k = 0; k < kcount; ++k) {
+            const int r = self_plan_rank(kw + k);
+            int bsel = -1, x = 0;
+#pragma unroll
+            for (int b = 0; b < kSelfBuckets; ++b) {
+                const bool in = (unsigned)(r - excl[b]) < (unsigned)cnt[b];
+                bsel = in ? b : bsel;
+                x = in ? r - excl[b] : x;
+            }
+            if (bsel < 0) continue;
+            int rec = rec0, ctr = ctrb;
+#pragma unroll 1
+            for (int i = i0; i < i1; ++i) {
+                const int cut = S.cut[i], bk = S.bk[i];
+                const int nc = cut & 0xFFFF, cblk = (unsigned)cut >> 16;
+                const int ka = bk & 15, kb = bk >> 4;
+                const int ca = ka == bsel && nc > 1 ? hks * (nc - 1) : 0;
+                const int cb = kb == bsel ? hks : 0;
+                if (x < ca + cb) {
+                    int h, cc;
+                    if (x < ca) {  // run A: chunks 0..nc-2 of every head
+                        h = x / (nc - 1);
+                        cc = x - h * (nc - 1);
+                    } else {       // run B: the last chunk of every head
+                        h = x - ca;
+                        cc = nc - 1;
+                    }
+                    const int L = S.len[i];
+                    const int j0 = nc > 1 ? cc * cblk * B : 0;
+                    int* e = S.hdr[k];
+                    e[1] = h | (cc << 16);
+                    e[2] = j0;
+                    e[3] = nc > 1 ? min(j0 + cblk * B, L) : L;
+                    e[4] = nc;
+                    e[5] = nc > 1 ? hks * rec + h * nc : -1;
+                    e[6] = nc > 1 ? hks * ctr + h : -1;
+                    e[7] = S.to[i] + (nc > 1 ? cc * cblk : 0);
+                    e[0] = i;
+                    break;
+                }
+                x -= ca + cb;
+                rec += nc > 1 ? nc : 0;
+                ctr += nc > 1 ? 1 : 0;
+            }
+        }
+    }
+    __syncthreads();
+    SelfPlan sp;
+    sp.T = uniform(S.plan[0]);
+    sp.units = uniform(S.plan[1]);
+    sp.overflow = uniform(S.plan[2]);
+    return sp;
+}
+
+// The unit of window slot k as a planned-entry header (read by every thread of the
+// workgroup from LDS); false when this workgroup has no unit in that round.
+template <typename Lds>
+__device__ __forceinline__ bool self_plan_header(const Lds& S, int k, int (&hdr)[8]) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) hdr[e] = uniform(S.hdr[k][e]);
+    return hdr[0] >= 0;
+}
+
+// A batch past the plan's budget: NaN in the output rows of every (sequence, KV
+// head subgroup), rank r = s * hks + h, ranks served as in the planned loop.
+template <typename E, int D, int NT>
+__device__ void self_plan_nan(const DecodeParams& p, int heads) {
+    const int hks = p.Hkv * p.nsub;
+    for (int k = 0, r = self_plan_rank(0); r < p.N * hks; r = self_plan_rank(++k)) {
+        const int s = r / hks, h = r % hks;
+        const int hq0 = (h / p.nsub) * p.group + (h % p.nsub) * heads;
+        E* ob = static_cast<E*>(p.out) + ((size_t)s * p.Hq + hq0) * D;
+        for (int e = threadIdx.x; e < heads * D; e += NT) ob[e] = (E)__builtin_nanf("");
+    }
+}
+
+// The persistent loop of a self-planned launch: windows of kSelfWindow rounds, each
+// planned by self_plan_setup, then its units (run(hdr)) in round order.  lens and
+// n_seq (= p.N) are the kernel's register-preloaded first two arguments.
+template <typename E, int D, int NT, typename Lds, typename Run>
+__device__ __forceinline__ void self_plan_loop(const int* lens, int n_seq, const DecodeParams& p, Lds& S, int heads,
+                                               Run&& run) {
+    const int G = (int)gridDim.x;
+    for (int kw = 0;; kw += kSelfWindow) {
+        const SelfPlan sp = self_plan_setup<NT>(lens, n_seq, p, S, kw);
+        if (sp.overflow) {
+            self_plan_nan<E, D, NT>(p, heads);
+            return;
+        }
+        const int rounds = (sp.units + G - 1) / G;
+        const int kend = min(rounds - kw, kSelfWindow);
+        for (int k = 0; k < kend; ++k) {
+            int hdr[8];
+            if (self_plan_header(S, k, hdr)) run(hdr);
+            // the unit's epilogue (one wave in the VALU kernel) still reads the other
+            // waves' partials in LDS: no wave starts the next unit before it is done
+            __syncthreads();
+        }
+        if (kw + kSelfWindow >= rounds) return;
+    }
+}
+
