@@ -268,6 +268,36 @@ def host_plan_cost(W, lens, Hq, Hkv, D, B, reps=500):
             "chunk_tokens": ops.decode_plan_chunk(lens, Hq, Hkv, D, B)}
 
 
+def host_plan_pipelined(W, lens, Hq, Hkv, D, B, steps, warmup, mode=0):
+    """The planned path as a serving loop runs it, in C++ over the C ABI
+    (tests/cpp/plan_pipeline.cpp, a child process): the host plans EVERY step
+    (kvc_decode_plan into a ring of 4 pinned buffers) and uploads the work list on a
+    copy stream while the GPU runs the previous step's kernel.  Returns the program's
+    JSON: compute-stream event time per step (host planning, uploads and kernels all
+    inside it) and the host's own time per step; the last step's output must equal a
+    plain planned launch's bit for bit."""
+    import json
+    import subprocess
+    import tempfile
+
+    exe = ROOT / "kvcache_amd" / "_build" / "bin" / "plan_pipeline"
+    if not exe.exists():
+        raise FileNotFoundError(f"{exe} (python -m kvcache_amd.build)")
+    lens = np.ascontiguousarray(lens, np.int32)
+    toff, tab = np.asarray(W["tab_off_host"], np.int32), np.asarray(W["table_host"], np.int32)
+    with tempfile.NamedTemporaryFile(suffix=".bin", delete=False) as f:
+        np.concatenate([np.array([len(lens), Hq, Hkv, D, B, len(tab)], np.int32), lens, toff, tab]).tofile(f)
+        path = f.name
+    try:
+        r = subprocess.run([str(exe), path, str(steps), str(warmup), str(mode)], stdout=subprocess.PIPE, stderr=subprocess.PIPE,
+                           text=True, timeout=120)
+    finally:
+        os.unlink(path)
+    if r.returncode != 0:
+        raise RuntimeError(f"plan_pipeline exit {r.returncode}: {r.stderr.strip()[-300:]}")
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
 def c2_variant(lens, steps, warmup, rotate):
     """A C2 batch of other lengths: planned and self-planned (device-lengths) paths."""
     N, Hq, Hkv, D, B = len(lens), 8, 8, 64, 16
@@ -638,6 +668,15 @@ def main() -> int:
     plan_cost["plan_plus_kernel_us"] = round(plan_cost["us_per_plan"] + t_launch * 1e3, 2)
     plan_cost["plan_plus_kernel_frac"] = round(total / ((plan_cost["us_per_plan"] + t_launch * 1e3) * 1e-6) / 1e9 /
                                                HBM_PEAK_GBS, 4)
+    try:
+        for mode, key in ((1, "pipelined"), (0, "pipelined_copy_stream")):
+            pp = host_plan_pipelined(W, lens, Hq, Hkv, D, B, a.steps, a.warmup, mode)
+            pp["what"] = ("C++ serving loop (tests/cpp/plan_pipeline.cpp): the host plans every step while the "
+                          "previous step's kernel runs; compute-stream events around the steps")
+            pp["frac_hbm_peak"] = round(total / (pp["us_per_step"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+            plan_cost[key] = pp
+    except Exception as e:  # noqa: BLE001 -- reported, not fatal to the headline
+        plan_cost["pipelined"] = {"error": repr(e)}
     log(f"host plan: {plan_cost}")
 
     extras = {}

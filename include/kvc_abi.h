@@ -94,6 +94,9 @@ int kvc_event_create(void** ev);
 int kvc_event_destroy(void* ev);
 int kvc_event_record(void* ev, kvc_stream_t stream);
 int kvc_event_synchronize(void* ev);
+/* work queued on `stream` after this call waits for `ev` (no host synchronisation): orders a copy
+ * stream and a compute stream */
+int kvc_stream_wait_event(kvc_stream_t stream, void* ev);
 int kvc_event_elapsed_ms(float* ms, void* start, void* stop); /* synchronizes on stop */
 /* HIP graphs (stream capture): the launches made on `stream` between begin and end
  * are recorded, not run; end instantiates them as one executable graph, launch

@@ -102,6 +102,7 @@ _SIGS = {
     "kvc_event_destroy": (i32, [vp]),
     "kvc_event_record": (i32, [vp, vp]),
     "kvc_event_synchronize": (i32, [vp]),
+    "kvc_stream_wait_event": (i32, [vp, vp]),
     "kvc_event_elapsed_ms": (i32, [C.POINTER(f32), vp, vp]),
     "kvc_step_upload": (i32, [vp, vp, sz, vp]),
     "kvc_fill_normal": (i32, [vp, sz, i32, u64, f32, vp]),

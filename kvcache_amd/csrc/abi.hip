@@ -879,6 +879,9 @@ int kvc_graph_destroy(void* exec) {
 int kvc_event_destroy(void* ev) { return ev ? hip_check(hipEventDestroy((hipEvent_t)ev), "hipEventDestroy") : KVC_OK; }
 int kvc_event_record(void* ev, kvc_stream_t st) { return hip_check(hipEventRecord((hipEvent_t)ev, S(st)), "hipEventRecord"); }
 int kvc_event_synchronize(void* ev) { return hip_check(hipEventSynchronize((hipEvent_t)ev), "hipEventSynchronize"); }
+int kvc_stream_wait_event(kvc_stream_t st, void* ev) {
+    return hip_check(hipStreamWaitEvent(S(st), (hipEvent_t)ev, 0), "hipStreamWaitEvent");
+}
 int kvc_event_elapsed_ms(float* ms, void* a, void* b) {
     if (!ms) return set_error(KVC_ERR_ARG, "null out pointer");
     int rc = hip_check(hipEventSynchronize((hipEvent_t)b), "hipEventSynchronize");

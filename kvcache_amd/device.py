@@ -126,6 +126,13 @@ class Event:
     def record(self, stream=None) -> None:
         check(lib().kvc_event_record(self.handle, stream))
 
+    def synchronize(self) -> None:
+        check(lib().kvc_event_synchronize(self.handle))
+
+    def wait_on(self, stream) -> None:
+        """Work queued on `stream` after this call waits for the event (no host wait)."""
+        check(lib().kvc_stream_wait_event(stream, self.handle))
+
     def elapsed_ms(self, later: "Event") -> float:
         ms = C.c_float()
         check(lib().kvc_event_elapsed_ms(C.byref(ms), self.handle, later.handle))
