@@ -63,7 +63,8 @@ struct RowsParams {
     int gpw;                 // column groups per workgroup (splits == 1)
     int groups;              // column groups in all
     float* part;             // [groups * splits][kRows][kCols] split partials
-    unsigned* ctr;           // [groups] arrival counters (zero between calls)
+    unsigned* ctr;           // arrival counters (zero between calls): group g's at ctr_word(g, ctr_shift)
+    int ctr_shift;           // log2 of the 128-byte lines the counters are spread over
     _Float16* out;           // store: y; residual: x (+=); swiglu: act; qkv: q
     const _Float16* bias;    // qkv: [q_cols + 2 kv_cols]
     _Float16* k_out;
@@ -78,6 +79,13 @@ struct RowsParams {
 };
 
 __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+// Atomics on one 128-byte line serialise (~10 ns each, whatever the address), so the
+// groups' counters are spread over lines: group g's at line g mod L, word g / L
+// (L = 2^shift lines of 32 words; one line per group up to 512 groups).
+__host__ __device__ inline unsigned ctr_word(int g, int shift) {
+    return ((unsigned)(g & ((1 << shift) - 1)) << 5) + ((unsigned)g >> shift);
+}
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
@@ -413,7 +421,7 @@ __global__ __launch_bounds__(WAVES * 64) void rows_kernel(RowsParams p) {
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
             __syncthreads();
             if (threadIdx.x == 0)
-                s_last = __hip_atomic_fetch_add(p.ctr + g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                s_last = __hip_atomic_fetch_add(p.ctr + ctr_word(g, p.ctr_shift), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                          (unsigned)(p.splits - 1);
             __syncthreads();
             if (!s_last) return false;
@@ -432,7 +440,7 @@ __global__ __launch_bounds__(WAVES * 64) void rows_kernel(RowsParams p) {
                     v[it][1] = a1;
                 }
             }
-            if (threadIdx.x == 0) __hip_atomic_store(p.ctr + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (threadIdx.x == 0) __hip_atomic_store(p.ctr + ctr_word(g, p.ctr_shift), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
 #pragma unroll
         for (int it = 0; it < kItems; ++it) {
@@ -561,7 +569,7 @@ int launch_rows(RowsParams p, const Shape& s, hipStream_t st) {
     return hip_check(hipGetLastError(), "rows linear launch");
 }
 
-// Workspace layout: [counters: 64 KiB][argmax candidates][split partials]
+// Workspace layout: [counters: 64 KiB = 512 lines of 32 counters][argmax candidates][split partials]
 constexpr size_t kCtrBytes = 64 << 10;
 
 int check_rows(int M, int K, const void* a, const void* w) {
@@ -623,6 +631,7 @@ int kvc_rows_linear(void* y, const void* x, const void* w, int M, int N, int K, 
         p.out = (_Float16*)y;
         p.dev_rows = dev_rows;
         p.ctr = (unsigned*)ws;
+        while ((1 << p.ctr_shift) < std::min(groups, (int)(kCtrBytes / 128))) ++p.ctr_shift;
         p.part = ws ? (float*)((char*)ws + kCtrBytes) : nullptr;
         const hipStream_t hs = (hipStream_t)st;
         if (norm_w) return residual ? launch_rows<kEpiResidual, true>(p, s, hs) : launch_rows<kEpiStore, true>(p, s, hs);
