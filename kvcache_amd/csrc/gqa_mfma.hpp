@@ -374,18 +374,24 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(const int* __rest
     }
     l = sum_xor32(sum_xor16(l));
 
-    // Combine the waves: per-wave (m, l) per head and O through LDS.
+    // Combine the waves: per-wave (m, l) per head and O through LDS.  Only the first
+    // nwa waves held tiles (they are dealt round-robin); the others hold (m, l, O) =
+    // (-FLT_MAX, 0, 0), whose weight exp2(-FLT_MAX - M) is 0, so leaving them out of
+    // the sums changes no bit of the result.
+    const int nwa = min(WPB, ntiles);
     __syncthreads();  // every wave is done with its V tile
     float* e_acc = reinterpret_cast<float*>(s_buf);                    // [WPB][16][D]
     float* e_ml = e_acc + WPB * kMfmaMaxHeads * D;                      // [WPB][16][2]
-    if (lane < 16) {
-        e_ml[(wave * kMfmaMaxHeads + lane) * 2] = m;
-        e_ml[(wave * kMfmaMaxHeads + lane) * 2 + 1] = l;
+    if (wave < nwa) {
+        if (lane < 16) {
+            e_ml[(wave * kMfmaMaxHeads + lane) * 2] = m;
+            e_ml[(wave * kMfmaMaxHeads + lane) * 2 + 1] = l;
+        }
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) e_acc[(wave * kMfmaMaxHeads + 4 * g4 + r) * D + n16 + 16 * nt] = O[nt][r];
     }
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) e_acc[(wave * kMfmaMaxHeads + 4 * g4 + r) * D + n16 + 16 * nt] = O[nt][r];
     __syncthreads();
 
     _Float16* ob = static_cast<_Float16*>(p.out) + ((size_t)s * p.Hq + hq0) * D;
@@ -400,10 +406,12 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(const int* __rest
             if (u.c >= ncq) continue;  // this chunk lies past the query's keys
             float M = -FLT_MAX;
 #pragma unroll
-            for (int w = 0; w < WPB; ++w) M = fmaxf(M, e_ml[(w * kMfmaMaxHeads + g) * 2]);
+            for (int w = 0; w < WPB; ++w)
+                if (w < nwa) M = fmaxf(M, e_ml[(w * kMfmaMaxHeads + g) * 2]);
             float lt = 0.f, at = 0.f;
 #pragma unroll
             for (int w = 0; w < WPB; ++w) {
+                if (w >= nwa) break;
                 const float wt = fast_exp2(e_ml[(w * kMfmaMaxHeads + g) * 2] - M);
                 lt = __builtin_fmaf(wt, e_ml[(w * kMfmaMaxHeads + g) * 2 + 1], lt);
                 at = __builtin_fmaf(wt, e_acc[(w * kMfmaMaxHeads + g) * D + d], at);
@@ -426,10 +434,12 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(const int* __rest
         const int g = idx / D, d = idx % D;
         float M = -FLT_MAX;
 #pragma unroll
-        for (int w = 0; w < WPB; ++w) M = fmaxf(M, e_ml[(w * kMfmaMaxHeads + g) * 2]);
+        for (int w = 0; w < WPB; ++w)
+            if (w < nwa) M = fmaxf(M, e_ml[(w * kMfmaMaxHeads + g) * 2]);
         float lt = 0.f, at = 0.f;
 #pragma unroll
         for (int w = 0; w < WPB; ++w) {
+            if (w >= nwa) break;
             const float wt = fast_exp2(e_ml[(w * kMfmaMaxHeads + g) * 2] - M);
             lt = __builtin_fmaf(wt, e_ml[(w * kMfmaMaxHeads + g) * 2 + 1], lt);
             at = __builtin_fmaf(wt, e_acc[(w * kMfmaMaxHeads + g) * D + d], at);
