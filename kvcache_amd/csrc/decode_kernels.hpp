@@ -366,7 +366,7 @@ __device__ __forceinline__ void read_seq(const DecodeParams& p, int (&h)[8]) {
     // the scalars load_unit needs come with the first fetch of the parameter block
     // (left to itself the compiler fetches them in a second round, after this one)
     asm volatile("" ::"s"(p.max_chunks), "s"(p.fixed_len), "s"(p.causal), "s"(p.cap), "s"(p.last_chunk_first));
-    const int s = (int)(blockIdx.x / (unsigned)(p.nsub * p.Hkv)) % p.N;
+    const int s = (int)(blockIdx.x / (unsigned)(p.max_chunks * p.nsub * p.Hkv));  // < N: load_unit's order
     h[0] = (int)__builtin_amdgcn_raw_buffer_load_b32(tile_rsrc(p.cur_len, p.cur_len ? p.N * 4 : 0), s * 4, 0, 0);
     h[1] = (int)__builtin_amdgcn_raw_buffer_load_b32(tile_rsrc(p.tab_off, PAGED && p.tab_off ? p.N * 4 : 0),
                                                      s * 4, 0, 0);
@@ -403,11 +403,16 @@ __device__ __forceinline__ bool load_unit(const DecodeParams& p, const int (&h)[
         if (u.s < 0 || u.s >= N || u.hk < 0 || u.hk >= p.Hkv || u.c < 0 || u.c >= u.nc) return false;
         return u.nc == 1 || (h[5] >= 0 && (long long)h[5] + u.nc <= n_records && h[6] >= 0 && h[6] < n_records);
     } else {
+        // chunk fastest: the hardware deals consecutive workgroups to the 8 XCDs in
+        // turn, so every sequence's chunks spread evenly over the XCDs (with the
+        // sequence fastest, blockIdx % 8 picked the (sequence, head) and an XCD holding
+        // the long sequences streamed twice its share through its fabric link)
         int unit = blockIdx.x;
+        const int cr = unit % p.max_chunks;  unit /= p.max_chunks;
         u.sub = unit % p.nsub;  unit /= p.nsub;
         u.hk = unit % p.Hkv;    unit /= p.Hkv;
-        u.s = unit % p.N;
-        u.c = p.last_chunk_first ? p.max_chunks - 1 - unit / p.N : unit / p.N;
+        u.s = unit;
+        u.c = p.last_chunk_first ? p.max_chunks - 1 - cr : cr;
         // length and table offset: read_seq (c >= max_chunks needs no test of its
         // own: nc <= max_chunks, so chunk_range_of rejects it)
         const int lu = uniform(h[0]);
