@@ -70,7 +70,11 @@ int         kvc_device_count(int* count);
  * "self_plan" (device-length decode with the automatic split: 1 = the kernel
  * derives the planner's units from the device lengths, 0 = a chunk x sequence x
  * head grid sized by cap), "self_grid" (self-planned launches: 0 = one workgroup
- * per resident slot, n = at most n workgroups, each then serving several units).
+ * per resident slot, n = at most n workgroups, each then serving several units),
+ * "self_prefetch_kib" (self-planned paged launches: about this many KiB of K and V,
+ * the first blocks of every sequence, are read ahead while the kernel plans;
+ * default 32768, 0 = none), "self_prefetch_min_len" (... of the sequences of at
+ * least this many tokens, default 256; at most a quarter of each is read ahead).
  * The matrix-core path takes fp16 K/V, head_dim 64 or 128, 3..16 query heads per
  * KV head and, paged, a power-of-two BLOCK >= 16; other shapes use the VALU
  * kernels. */

@@ -713,6 +713,12 @@ int run_self_planned(const void* q, const void* k, const void* v, const int* tab
     p.sp_slots = ps.slots; p.sp_min_chunk = ps.min_chunk; p.sp_max_chunk = ps.max_chunk;
     p.sp_target_cap = ps.target_cap; p.sp_nc_max = ps.mfma ? kMfmaMaxFusedChunks : 0;
     p.sp_records = self_plan_budget(ps, bound);
+    if (!contig && cur_len && tab_off && tuning().self_prefetch_kib > 0) {
+        // the first blocks of every sequence, about self_prefetch_kib KiB of K and V
+        const long long kvb = 2LL * Hkv * BLOCK * D * (dtype == KVC_F16 ? 2 : 4);
+        p.sp_pf_blocks = (int)std::min<long long>(((long long)tuning().self_prefetch_kib << 10) / ((long long)N * kvb), 4096);
+        p.sp_pf_min_len = std::max(tuning().self_prefetch_min_len, 1);
+    }
     const size_t rall = (size_t)recs;
     const size_t acc = align_up(rall * ps.G * D * sizeof(float), kAlign), ml = align_up(rall * ps.G * 2 * sizeof(float), kAlign);
     p.part_acc = static_cast<float*>(ws);
@@ -1237,6 +1243,8 @@ int kvc_set_tuning(const char* key, int value) {
     else if (k == "mfma_min_chunk" && value >= 16 && value <= 1 << 20) tuning().mfma_min_chunk = value;
     else if (k == "self_plan" && (value == 0 || value == 1)) tuning().self_plan = value;
     else if (k == "self_grid" && value >= 0) tuning().self_grid = value;
+    else if (k == "self_prefetch_kib" && value >= 0) tuning().self_prefetch_kib = value;
+    else if (k == "self_prefetch_min_len" && value >= 0) tuning().self_prefetch_min_len = value;
     else return set_error(KVC_ERR_ARG, "unknown tuning key or bad value: " + k);
     return KVC_OK;
 }
@@ -1256,6 +1264,8 @@ int kvc_get_tuning(const char* key, int* value) {
     else if (k == "mfma_min_chunk") *value = tuning().mfma_min_chunk;
     else if (k == "self_plan") *value = tuning().self_plan;
     else if (k == "self_grid") *value = tuning().self_grid;
+    else if (k == "self_prefetch_kib") *value = tuning().self_prefetch_kib;
+    else if (k == "self_prefetch_min_len") *value = tuning().self_prefetch_min_len;
     else return set_error(KVC_ERR_ARG, "unknown tuning key: " + k);
     return KVC_OK;
 }

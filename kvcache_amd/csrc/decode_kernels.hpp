@@ -740,7 +740,7 @@ __global__ __launch_bounds__(WPB * kWave) void split_kernel(const int* __restric
 
     if constexpr (SELF) {
         // self-planned launches pass the device lengths as the (preloaded) first argument
-        self_plan_loop<T, D, WPB * kWave>(work, work_ints, p, s_plan, G, [&](const int (&hdr)[8]) { run_unit(hdr, 0); });
+        self_plan_loop<T, D, WPB * kWave>(work, work_ints, s_plan, G, [&](const int (&hdr)[8]) { run_unit(hdr, 0); });
     } else {
         // planned entries may carry the chunk's first block ids after the 8-int
         // header (one int per lane, read together with the header), so the first

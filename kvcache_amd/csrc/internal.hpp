@@ -79,6 +79,8 @@ struct DecodeParams {
     int sp_slots, sp_min_chunk, sp_max_chunk, sp_target_cap;
     int sp_nc_max;            // chunks per sequence the merge can combine (0: any)
     int sp_records;           // partial records per (sequence, head) in the workspace
+    int sp_pf_blocks;         // blocks of every sequence read ahead while the plan is made (0: none)
+    int sp_pf_min_len;        // shortest sequence read ahead
     const int* dev_base;
 };
 
@@ -153,6 +155,9 @@ struct Tuning {
                                 // units (selfplan.hpp), 0 the chunk x sequence x head grid
     int self_grid = 0;          // self-planned launches: 0 automatic (resident workgroups), n: at most n
                                 // workgroups (each then serves several ranks, in rounds)
+    int self_prefetch_kib = 32768;  // self-planned paged launches: K+V bytes (KiB) read ahead while the
+                                    // kernel plans (the first blocks of every sequence; 0: none)
+    int self_prefetch_min_len = 256;  // ... of the sequences of at least this many tokens
 };
 // Dynamic LDS that caps decode workgroups per CU at wg_per_cu (0: none).
 size_t occupancy_lds(size_t static_lds, int wg_per_cu);

@@ -49,6 +49,7 @@ struct SelfPlanLds {
     int bk[NMAX];              // bucket of run A | bucket of run B << 4
     int plan[4];               // chunk target, units, overflow
     int hdr[kSelfWindow][8];   // unit headers of this workgroup's ranks in the window (hdr[k][0] < 0: none)
+    int sink[kWave];           // destination of the prefetch loads (never read)
 };
 
 struct SelfPlan {
@@ -139,43 +140,52 @@ __device__ __forceinline__ int self_plan_rank(int k) {
 // Order: eight buckets (self_bucket), descending; within a bucket by sequence, and
 // within a sequence run A (chunks 0..nc-2 of every head) before run B (its last
 // chunk of every head).
+// Wave 0's first kSelfSpt lengths (lane l: sequences l * spl ...), loaded before
+// anything else of the kernel: they depend only on the preloaded arguments.
+__device__ __forceinline__ void self_first_lengths(const int* lens, int N, int (&lv0)[kSelfSpt]) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int i0 = min(lane * ((N + kWave - 1) / kWave), N);
+    const __amdgpu_buffer_rsrc_t lrs = tile_rsrc(lens, lens ? N * 4 : 0);
+#pragma unroll
+    for (int j = 0; j < kSelfSpt; ++j) lv0[j] = (int)__builtin_amdgcn_raw_buffer_load_b32(lrs, (i0 + j) * 4, 0, 0);
+}
+
 template <int NT, typename Lds>
-__device__ SelfPlan self_plan_setup(const int* lens, int n_seq, const DecodeParams& p, Lds& S, int kw) {
+__device__ SelfPlan self_plan_setup(const int* lens, int n_seq, const DecodeParams& p, Lds& S, int kw,
+                                    const int (&lv0)[kSelfSpt]) {
     const int tid = threadIdx.x, lane = tid & (kWave - 1);
     if (tid < kWave) {
-        // the lengths loads depend only on the preloaded arguments (lens, n_seq): they
-        // issue at wave start, beside the parameter block's
         const int N = n_seq;
         const int spl = (N + kWave - 1) / kWave;  // consecutive sequences per lane
         const int i0 = min(lane * spl, N), i1 = min(i0 + spl, N);
         const __amdgpu_buffer_rsrc_t lrs = tile_rsrc(lens, lens ? N * 4 : 0);
-        int lv0[kSelfSpt];
-#pragma unroll
-        for (int j = 0; j < kSelfSpt; ++j) lv0[j] = (int)__builtin_amdgcn_raw_buffer_load_b32(lrs, (i0 + j) * 4, 0, 0);
         const int B = p.block, hks = p.Hkv * p.nsub;
         const int bsh = __builtin_ctz((unsigned)B);
         const int first = lens ? 0 : (p.dev_base ? *p.dev_base : p.fixed_len);  // causal prompt queries
         if (lane < kSelfWindow) S.hdr[lane][0] = -1;
-        // this lane's lengths and table offsets, kSelfSpt loads in flight at a time
-        // (bounded buffer loads: indices past N read 0 and touch no memory)
-        const __amdgpu_buffer_rsrc_t trs = tile_rsrc(p.tab_off, p.tab_off ? N * 4 : 0);
+        // this lane's table offsets: issued as soon as the parameter block is in, first
+        // used when the headers are written (bounded buffer loads: indices past N read
+        // 0 and touch no memory)
+        const bool offsets = p.tab_off && !p.causal;
+        const __amdgpu_buffer_rsrc_t trs = tile_rsrc(p.tab_off, offsets ? N * 4 : 0);
+        int tv0[kSelfSpt];
+#pragma unroll
+        for (int j = 0; j < kSelfSpt; ++j) tv0[j] = (int)__builtin_amdgcn_raw_buffer_load_b32(trs, (i0 + j) * 4, 0, 0);
+        // this lane's lengths, kSelfSpt loads in flight at a time
         unsigned tlo = 0, thi = 0;  // sum of max(L, 1): low 20 bits and the rest, apart
         int lmax = 0, nb = 0;
 #pragma unroll 1
         for (int ib = i0; ib < i1; ib += kSelfSpt) {
-            int lv[kSelfSpt], tv[kSelfSpt];
+            int lv[kSelfSpt];
 #pragma unroll
-            for (int j = 0; j < kSelfSpt; ++j) {
+            for (int j = 0; j < kSelfSpt; ++j)
                 lv[j] = ib == i0 ? lv0[j] : (int)__builtin_amdgcn_raw_buffer_load_b32(lrs, (ib + j) * 4, 0, 0);
-                tv[j] = (int)__builtin_amdgcn_raw_buffer_load_b32(trs, (ib + j) * 4, 0, 0);
-            }
 #pragma unroll
             for (int j = 0; j < kSelfSpt; ++j) {
                 const int i = ib + j;
                 if (i < i1) {
                     const int L = max(lens ? lv[j] : (p.causal ? first + i + 1 : p.fixed_len), 0);
                     S.len[i] = L;
-                    S.to[i] = tv[j];
                     const unsigned w = (unsigned)max(L, 1);
                     tlo += w & 0xFFFFF;
                     thi += w >> 20;
@@ -242,6 +252,18 @@ __device__ SelfPlan self_plan_setup(const int* lens, int n_seq, const DecodePara
             for (int b = 0; b < kSelfBuckets; ++b) cnt[b] += (b == ka ? ca : 0) + (b == kb ? hks : 0);
             nrec += nc > 1 ? nc : 0;
             nctr += nc > 1 ? 1 : 0;
+        }
+        if (offsets) {  // the table offsets, loaded at the start
+#pragma unroll 1
+            for (int ib = i0; ib < i1; ib += kSelfSpt) {
+                int tv[kSelfSpt];
+#pragma unroll
+                for (int j = 0; j < kSelfSpt; ++j)
+                    tv[j] = ib == i0 ? tv0[j] : (int)__builtin_amdgcn_raw_buffer_load_b32(trs, (ib + j) * 4, 0, 0);
+#pragma unroll
+                for (int j = 0; j < kSelfSpt; ++j)
+                    if (ib + j < i1) S.to[ib + j] = tv[j];
+            }
         }
         // the order: buckets descending, sequences ascending within a bucket (run A
         // before run B); first rank of this lane's units per bucket
@@ -342,18 +364,65 @@ __device__ void self_plan_nan(const DecodeParams& p, int heads) {
     }
 }
 
+// While wave 0 plans, no K/V bytes move: wave 1 of every workgroup reads the first
+// p.sp_pf_blocks blocks of every sequence, at most its first quarter (item
+// t = s + N * j: block j of sequence s;
+// workgroup b takes items b, b + G, ..., one per lane) so that they are on their way
+// from HBM into the memory-side cache while the plan is made, and the units that read
+// them later find them there.  Every block id is that of a block below the sequence's
+// length, read from its table as the units read it; each pool block is touched once
+// per 64 bytes by loads that write into an LDS sink (no registers held, nothing waits
+// for them before the units' own loads).
+template <typename E, int D, typename Lds>
+__device__ __forceinline__ void self_prefetch(const int* lens, int N, const DecodeParams& p, Lds& S) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const unsigned items = (unsigned)N * (unsigned)p.sp_pf_blocks;  // N <= kSelfMaxNValu, blocks <= 4096
+    const unsigned t = blockIdx.x + (unsigned)lane * gridDim.x;
+    const bool has = t < items;
+    const int s = has ? (int)(t % (unsigned)N) : 0, j = has ? (int)(t / (unsigned)N) : 0;
+    const __amdgpu_buffer_rsrc_t lrs = tile_rsrc(lens, N * 4), ors = tile_rsrc(p.tab_off, N * 4);
+    const int L = (int)__builtin_amdgcn_raw_buffer_load_b32(lrs, s * 4, 0, 0);
+    const int to = (int)__builtin_amdgcn_raw_buffer_load_b32(ors, s * 4, 0, 0);
+    // at most the first quarter of a sequence, and none of a short one: short units
+    // start streaming almost as soon as the plan is made, and reading them ahead as
+    // well only doubles their requests
+    const bool ok = has && L >= p.sp_pf_min_len && 4LL * j * p.block < (long long)L;
+    const int bid = ok ? p.table_all[to + j] : -1;
+    const int bytes = p.Hkv * p.block * D * (int)sizeof(E);  // one block of one pool, every KV head
+    const unsigned long long live = __ballot(ok);
+    auto* sink = (__attribute__((address_space(3))) void*)S.sink;
+#pragma unroll 1
+    for (int i = 0; i < kWave; ++i) {
+        if (!((live >> i) & 1ull)) continue;
+        const size_t base = (size_t)(unsigned)__builtin_amdgcn_readlane(bid, i) * (size_t)bytes;
+        const __amdgpu_buffer_rsrc_t kr = tile_rsrc(static_cast<const char*>(p.k) + base, bytes);
+        const __amdgpu_buffer_rsrc_t vr = tile_rsrc(static_cast<const char*>(p.v) + base, bytes);
+#pragma unroll 1
+        for (int x = lane * 64; x < bytes; x += kWave * 64) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, sink, 4, x, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, sink, 4, x, 0, 0, 0);
+        }
+    }
+}
+
 // The persistent loop of a self-planned launch: windows of kSelfWindow rounds, each
 // planned by self_plan_setup, then its units (run(hdr)) in round order.  lens and
-// n_seq (= p.N) are the kernel's register-preloaded first two arguments.
+// n_seq (= p.N) are the kernel's register-preloaded first two arguments.  Each window
+// reads its own copy of the parameter block (fresh_params): with the kernel argument
+// itself, the compiler hoists the planner's parameter arithmetic in front of the
+// loop -- ahead of the lengths loads, with its results spilled -- and keeps it live
+// across every unit.
 template <typename E, int D, int NT, typename Lds, typename Run>
-__device__ __forceinline__ void self_plan_loop(const int* lens, int n_seq, const DecodeParams& p, Lds& S, int heads,
-                                               Run&& run) {
+__device__ __forceinline__ void self_plan_loop(const int* lens, int n_seq, Lds& S, int heads, Run&& run) {
     const int G = (int)gridDim.x;
-    for (int kw = 0;; kw += kSelfWindow) {
-        const SelfPlan sp = self_plan_setup<NT>(lens, n_seq, p, S, kw);
+    // one window: plan it, run its units; false once every round is done
+    auto window = [&](int kw, int (&lv)[kSelfSpt]) -> bool {
+        const DecodeParams p = fresh_params();
+        if (kw == 0 && p.sp_pf_blocks > 0 && (threadIdx.x >> 6) == 1) self_prefetch<E, D>(lens, n_seq, p, S);
+        const SelfPlan sp = self_plan_setup<NT>(lens, n_seq, p, S, kw, lv);
         if (sp.overflow) {
             self_plan_nan<E, D, NT>(p, heads);
-            return;
+            return false;
         }
         const int rounds = (sp.units + G - 1) / G;
         const int kend = min(rounds - kw, kSelfWindow);
@@ -364,7 +433,18 @@ __device__ __forceinline__ void self_plan_loop(const int* lens, int n_seq, const
             // waves' partials in LDS: no wave starts the next unit before it is done
             __syncthreads();
         }
-        if (kw + kSelfWindow >= rounds) return;
+        return kw + kSelfWindow < rounds;
+    };
+    // the first window's lengths load before anything else (the later windows' load
+    // in their own iteration, so no lengths stay live across the units)
+    int lv0[kSelfSpt] = {};
+    if (threadIdx.x < kWave) self_first_lengths(lens, n_seq, lv0);
+    __builtin_amdgcn_sched_barrier(0);
+    if (!window(0, lv0)) return;
+    for (int kw = kSelfWindow;; kw += kSelfWindow) {
+        int lv[kSelfSpt] = {};
+        if (threadIdx.x < kWave) self_first_lengths(lens, n_seq, lv);
+        if (!window(kw, lv)) return;
     }
 }
 
