@@ -56,16 +56,43 @@ def measured_traffic():
 STATS_SUMMARY = ROOT / "profiles" / "split_kernel_planned_c2_stats.txt"
 
 
+def profile_values():
+    """The `key: number` lines of the committed rocprofv3 kernel-trace summary of the
+    default command (mean kernel durations in us of each workload's timed dispatches)."""
+    vals = {}
+    try:
+        for line in STATS_SUMMARY.read_text().splitlines():
+            k, sep, v = line.partition(":")
+            if sep and k and not k.startswith((" ", "#")) and " " not in k:
+                try:
+                    vals[k] = float(v)
+                except ValueError:
+                    pass
+    except OSError:
+        pass
+    return vals
+
+
 def profiled_launch_us():
     """Mean duration (us) of the headline kernel's timed dispatches in the committed
     rocprofv3 kernel-trace summary of the default command, or None."""
-    try:
-        for line in STATS_SUMMARY.read_text().splitlines():
-            if line.startswith("headline_timed_mean_us:"):
-                return float(line.split(":", 1)[1])
-    except (OSError, ValueError):
-        pass
-    return None
+    return profile_values().get("headline_timed_mean_us")
+
+
+def roofline_block(alg_bytes, us, kernel, profile_keys=()):
+    """An HBM roofline entry for an extra workload: algorithmic bytes over the measured
+    time, and the same over the profiled kernel time (sum of profile_keys) when the
+    committed summary has it."""
+    gbs = alg_bytes / (us * 1e-6) / 1e9
+    out = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+           "frac": round(gbs / HBM_PEAK_GBS, 4), "kernel": kernel, "algorithmic_bytes_per_launch": alg_bytes}
+    pv = profile_values()
+    if profile_keys and all(k in pv for k in profile_keys):
+        kus = sum(pv[k] for k in profile_keys)
+        out["profile"] = {"file": str(STATS_SUMMARY.relative_to(ROOT)), "kernel_us": round(kus, 3),
+                          "keys": list(profile_keys),
+                          "frac": round(alg_bytes / (kus * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    return out
 
 
 def log(msg: str) -> None:
@@ -353,7 +380,9 @@ def bench_c4_layer(steps, warmup):
     return {"workload": "config-4 layer step: 32 sequences of the BASELINE trace at prompt + gen/2 tokens "
                         f"(sum {int(lens.sum())}), planned grouped-query decode with fused append",
             "units": nu, "algorithmic_bytes": total, "us_per_launch": round(t * 1e3, 3),
-            "GBps": round(total / (t * 1e-3) / 1e9, 1), "frac_hbm_peak": round(total / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+            "GBps": round(total / (t * 1e-3) / 1e9, 1), "frac_hbm_peak": round(total / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "roofline": roofline_block(total, t * 1e3, "gqa_mfma_kernel<64, kPlannedUniform, 8> (one launch per "
+                                       "layer step; latency-bound: ~25k token-heads)", ("c4_layer_timed_mean_us",))}
 
 
 def bench_c3(steps, warmup, plan_sweep=()):
@@ -367,7 +396,10 @@ def bench_c3(steps, warmup, plan_sweep=()):
     res = {"workload": "C3 long-context split-K 14q/2kv D64 ctx {8k,16k,32k,32k} fp16 split 512",
            "us_per_step": round(t * 1e3, 2), "GBps": round(total / (t * 1e-3) / 1e9, 1),
            "frac_hbm_peak": round(total / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "kv_bytes": kv,
-           "algorithmic_bytes": total}
+           "algorithmic_bytes": total,
+           "roofline": roofline_block(total, t * 1e3, "gqa_mfma_kernel<64, kPagedUniform, 4> + merge_kernel<f16, 64> "
+                                      "(split 512; per step: both kernels and the gap between them)",
+                                      ("c3_split512_split_kernel_mean_us", "c3_split512_merge_kernel_mean_us"))}
     t2, _ = time_decode(W, lens, Hq, Hkv, D, B, 1024, steps, warmup)
     res["split_1024"] = {"us_per_step": round(t2 * 1e3, 2), "GBps": round(total / (t2 * 1e-3) / 1e9, 1),
                          "frac_hbm_peak": round(total / (t2 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
@@ -729,7 +761,8 @@ def main() -> int:
         "device_lengths_path": {"path": "self-planned (launch_batched_paged: the kernel plans from the device "
                                         "lengths, no host plan)" if split == 0 else f"split {split}",
                                 "us_per_step": round(t_raw * 1e3, 3), "GBps": round(raw, 1),
-                                "frac_hbm_peak": round(raw / HBM_PEAK_GBS, 4)},
+                                "frac_hbm_peak": round(raw / HBM_PEAK_GBS, 4),
+                                "profile_mean_launch_us": profile_values().get("device_lengths_timed_mean_us")},
         "host_plan": plan_cost,
         "pct_hbm_peak": round(100 * achieved / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
