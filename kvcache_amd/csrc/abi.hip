@@ -716,7 +716,8 @@ int run_self_planned(const void* q, const void* k, const void* v, const int* tab
     if (!contig && cur_len && tab_off && tuning().self_prefetch_kib > 0) {
         // the first blocks of every sequence, about self_prefetch_kib KiB of K and V
         const long long kvb = 2LL * Hkv * BLOCK * D * (dtype == KVC_F16 ? 2 : 4);
-        p.sp_pf_blocks = (int)std::min<long long>(((long long)tuning().self_prefetch_kib << 10) / ((long long)N * kvb), 4096);
+        if (kvb <= (4LL << 20))  // a block of both pools (every KV head) addressed with 32-bit offsets
+            p.sp_pf_blocks = (int)std::min<long long>(((long long)tuning().self_prefetch_kib << 10) / ((long long)N * kvb), 4096);
         p.sp_pf_min_len = std::max(tuning().self_prefetch_min_len, 1);
     }
     const size_t rall = (size_t)recs;

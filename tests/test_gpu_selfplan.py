@@ -211,3 +211,23 @@ def test_device_position_variants(orc):
     got = host(out, np.float16, q.shape).astype(np.float64)
     ref = orc.paged_causal(q, kp, vp, table, base, Hkv, B, 0.125)
     assert np.abs(got - ref).max() <= 2e-3
+
+
+@pytest.mark.parametrize("case", ["c2_reference", "gqa_mfma_long", "mha_fp32"])
+def test_read_ahead_changes_no_output(case):
+    """While the kernel plans, wave 1 of every workgroup reads the first blocks of every
+    sequence ahead into an LDS sink (self_prefetch): no output may change, bit for bit,
+    whatever the read-ahead budget -- none, the default, or one that covers whole
+    sequences -- and with the minimum length at 0 (short sequences read ahead too)."""
+    lens, Hq, Hkv, D, dtype = CASES[case]
+    say(f"self-planned read-ahead on/off: {case}")
+    B = 16
+    q, K, V = inputs(lens, Hq, Hkv, D, dtype, 340)
+    nb = sum((int(x) + B - 1) // B for x in lens)
+    kp, vp, table, tab_off = paged_layout(K, V, lens, B, np.random.default_rng(9).permutation(nb))
+    with tuning("self_prefetch_kib", 0):
+        ref = self_planned(q, kp, vp, table, tab_off, lens, Hkv, B, dtype)
+    for kib, min_len in ((32768, 256), (1 << 20, 0), (64, 1)):
+        with tuning("self_prefetch_kib", kib), tuning("self_prefetch_min_len", min_len):
+            got = self_planned(q, kp, vp, table, tab_off, lens, Hkv, B, dtype)
+        np.testing.assert_array_equal(got, ref)
