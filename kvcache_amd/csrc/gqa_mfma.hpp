@@ -71,8 +71,7 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(const int* __rest
     constexpr bool CAUSAL = MODE == kCausalTile;
     constexpr int kTileBytes = kMfmaTile * ROW;
     constexpr int kMainBytes = 2 * WPB * kTileBytes;   // per wave: V tile, then K tile
-    constexpr int kEpiBytes = WPB * kMfmaMaxHeads * (D + 2) * 4;
-    __shared__ __attribute__((aligned(16))) char s_buf[kMainBytes > kEpiBytes ? kMainBytes : kEpiBytes];
+    __shared__ __attribute__((aligned(16))) char s_buf[kMainBytes];
     __shared__ int s_tab[PAGED ? kMfmaMaxChunkBlocks : 1];
     __shared__ float s_w[kMfmaMaxHeads][kMaxFusedChunks];
     __shared__ float s_L[kMfmaMaxHeads];
@@ -379,18 +378,23 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(const int* __rest
     // (-FLT_MAX, 0, 0), whose weight exp2(-FLT_MAX - M) is 0, so leaving them out of
     // the sums changes no bit of the result.
     const int nwa = min(WPB, ntiles);
-    __syncthreads();  // every wave is done with its V tile
-    float* e_acc = reinterpret_cast<float*>(s_buf);                    // [WPB][16][D]
-    float* e_ml = e_acc + WPB * kMfmaMaxHeads * D;                      // [WPB][16][2]
+    // Each wave writes its partials over its own V tile (16 heads x D floats: exactly
+    // one tile) and K tile ((m, l) per head), which only it used, so one barrier
+    // (every wave's partials written) is enough.
+    static_assert(kMfmaMaxHeads * D * 4 == kTileBytes && kMfmaMaxHeads * 2 * 4 <= kTileBytes, "partials fit the tiles");
+    auto acc_of = [&](int w) { return reinterpret_cast<const float*>(s_buf + w * kTileBytes); };        // [16][D]
+    auto ml_of = [&](int w) { return reinterpret_cast<const float*>(s_buf + (WPB + w) * kTileBytes); };  // [16][2]
     if (wave < nwa) {
+        float* my_acc = reinterpret_cast<float*>(vt);
+        float* my_ml = reinterpret_cast<float*>(kt);
         if (lane < 16) {
-            e_ml[(wave * kMfmaMaxHeads + lane) * 2] = m;
-            e_ml[(wave * kMfmaMaxHeads + lane) * 2 + 1] = l;
+            my_ml[lane * 2] = m;
+            my_ml[lane * 2 + 1] = l;
         }
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) e_acc[(wave * kMfmaMaxHeads + 4 * g4 + r) * D + n16 + 16 * nt] = O[nt][r];
+            for (int r = 0; r < 4; ++r) my_acc[(4 * g4 + r) * D + n16 + 16 * nt] = O[nt][r];
     }
     __syncthreads();
 
@@ -407,14 +411,14 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(const int* __rest
             float M = -FLT_MAX;
 #pragma unroll
             for (int w = 0; w < WPB; ++w)
-                if (w < nwa) M = fmaxf(M, e_ml[(w * kMfmaMaxHeads + g) * 2]);
+                if (w < nwa) M = fmaxf(M, ml_of(w)[g * 2]);
             float lt = 0.f, at = 0.f;
 #pragma unroll
             for (int w = 0; w < WPB; ++w) {
                 if (w >= nwa) break;
-                const float wt = fast_exp2(e_ml[(w * kMfmaMaxHeads + g) * 2] - M);
-                lt = __builtin_fmaf(wt, e_ml[(w * kMfmaMaxHeads + g) * 2 + 1], lt);
-                at = __builtin_fmaf(wt, e_acc[(w * kMfmaMaxHeads + g) * D + d], at);
+                const float wt = fast_exp2(ml_of(w)[g * 2] - M);
+                lt = __builtin_fmaf(wt, ml_of(w)[g * 2 + 1], lt);
+                at = __builtin_fmaf(wt, acc_of(w)[g * D + d], at);
             }
             if (ncq == 1) {
                 static_cast<_Float16*>(p.out)[((size_t)q * p.Hq + qh) * D + d] =
@@ -435,14 +439,14 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(const int* __rest
         float M = -FLT_MAX;
 #pragma unroll
         for (int w = 0; w < WPB; ++w)
-            if (w < nwa) M = fmaxf(M, e_ml[(w * kMfmaMaxHeads + g) * 2]);
+            if (w < nwa) M = fmaxf(M, ml_of(w)[g * 2]);
         float lt = 0.f, at = 0.f;
 #pragma unroll
         for (int w = 0; w < WPB; ++w) {
             if (w >= nwa) break;
-            const float wt = fast_exp2(e_ml[(w * kMfmaMaxHeads + g) * 2] - M);
-            lt = __builtin_fmaf(wt, e_ml[(w * kMfmaMaxHeads + g) * 2 + 1], lt);
-            at = __builtin_fmaf(wt, e_acc[(w * kMfmaMaxHeads + g) * D + d], at);
+            const float wt = fast_exp2(ml_of(w)[g * 2] - M);
+            lt = __builtin_fmaf(wt, ml_of(w)[g * 2 + 1], lt);
+            at = __builtin_fmaf(wt, acc_of(w)[g * D + d], at);
         }
         if (nc == 1) {
             ob[(size_t)g * D + d] = (_Float16)(lt > 0.f ? at * (1.0f / lt) : 0.f);
