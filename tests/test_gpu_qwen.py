@@ -59,7 +59,8 @@ def test_small_prefill_logits_and_serving(small):
         total_exact += exact
         total += g
     print("exact", total_exact, "of", total)
-    assert total_exact >= 0.9 * total
+    # measured: 156 of 156; a near-tie may flip with the fp32 summation order, one is allowed
+    assert total_exact >= total - 1
 
 
 def test_graph_replay_matches_eager_steps():
@@ -108,7 +109,7 @@ def test_config5_shape_prefill_and_generation():
             print("exact", exact, "of", len(o), "bad", bad)
             assert not bad, bad
             total_exact += exact
-        assert total_exact >= 0.9 * sum(gens)
+        assert total_exact >= sum(gens) - 1  # measured: 24 of 24
     finally:
         m.close()
 
@@ -140,7 +141,7 @@ def test_config5_batch32_every_token_teacher_forced():
             total += len(o)
         print(f"config 5 batch 32: {total_exact} of {total} generated tokens exact; beyond-tie mismatches {worst}")
         assert not worst, worst
-        assert total_exact >= 0.97 * total
+        assert total_exact >= total - 2  # measured: 267 of 268 (one near-tie)
     finally:
         m.close()
 
