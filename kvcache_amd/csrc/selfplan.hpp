@@ -387,7 +387,9 @@ __device__ __forceinline__ void self_prefetch(const int* lens, int N, const Deco
     // start streaming almost as soon as the plan is made, and reading them ahead as
     // well only doubles their requests
     const bool ok = has && L >= p.sp_pf_min_len && 4LL * j * p.block < (long long)L;
-    const int bid = ok ? p.table_all[to + j] : -1;
+    // block id through a descriptor over the table (an offset past it reads 0), as the units read it
+    const __amdgpu_buffer_rsrc_t tbr = tile_rsrc(p.table_all, p.table_len * 4);
+    const int bid = ok ? (int)__builtin_amdgcn_raw_buffer_load_b32(tbr, (int)(((unsigned)to + (unsigned)j) * 4u), 0, 0) : -1;
     const int bytes = p.Hkv * p.block * D * (int)sizeof(E);  // one block of one pool, every KV head
     const unsigned long long live = __ballot(ok);
     auto* sink = (__attribute__((address_space(3))) void*)S.sink;
