@@ -365,14 +365,14 @@ __device__ void self_plan_nan(const DecodeParams& p, int heads) {
 }
 
 // While wave 0 plans, no K/V bytes move: wave 1 of every workgroup reads the first
-// p.sp_pf_blocks blocks of every sequence, at most its first quarter (item
-// t = s + N * j: block j of sequence s;
-// workgroup b takes items b, b + G, ..., one per lane) so that they are on their way
-// from HBM into the memory-side cache while the plan is made, and the units that read
-// them later find them there.  Every block id is that of a block below the sequence's
-// length, read from its table as the units read it; each pool block is touched once
-// per 64 bytes by loads that write into an LDS sink (no registers held, nothing waits
-// for them before the units' own loads).
+// p.sp_pf_blocks blocks of every sequence (at most its first quarter) so that they
+// are on their way from HBM into the memory-side cache while the plan is made, and
+// the units that read them later find them there.  Item t = s + N * j is block j of
+// sequence s; workgroup b takes items b, b + G, ..., one per lane.  Every block id is
+// that of a block below the sequence's length, read from its table as the units read
+// it; each pool block is touched once per 64 bytes by loads whose data land in an LDS
+// sink (no registers held; wave 1's first wait for its own unit's loads also covers
+// these, issued microseconds earlier).
 template <typename E, int D, typename Lds>
 __device__ __forceinline__ void self_prefetch(const int* lens, int N, const DecodeParams& p, Lds& S) {
     const int lane = threadIdx.x & (kWave - 1);
