@@ -260,3 +260,25 @@ def test_bench_memory_report_matches_readme(orc):
     assert r["seqs_in_4096mb_contiguous"] == pub("budget_4096mb_max_seqs_contiguous")
     assert r["seqs_in_4096mb_paged"] == pub("budget_4096mb_max_seqs_paged")
     assert m["fp16"]["used_mb"] * 2 == pytest.approx(r["used_mb"], abs=0.1)
+
+
+def test_bench_reads_the_committed_profiles():
+    """The bench line quotes the committed rocprofv3 summaries: every key it looks up is
+    there, the profiled kernel times are plausible, and the roofline blocks follow
+    from them (algorithmic bytes / time / 8 TB/s)."""
+    import sys
+    from pathlib import Path
+    sys.path.insert(0, str(Path(__file__).resolve().parent.parent))
+    import bench
+    pv = bench.profile_values()
+    for key in ("headline_timed_mean_us", "device_lengths_timed_mean_us", "c4_layer_timed_mean_us",
+                "c3_split512_split_kernel_mean_us", "c3_split512_merge_kernel_mean_us"):
+        assert 1.0 < pv[key] < 100.0, key
+    assert bench.profiled_launch_us() == pv["headline_timed_mean_us"]
+    rb = bench.roofline_block(46174244, 17.0, "k", ("c3_split512_split_kernel_mean_us", "c3_split512_merge_kernel_mean_us"))
+    us = pv["c3_split512_split_kernel_mean_us"] + pv["c3_split512_merge_kernel_mean_us"]
+    assert rb["profile"]["kernel_us"] == pytest.approx(us, abs=1e-3)
+    assert rb["profile"]["frac"] == pytest.approx(46174244 / (us * 1e-6) / 8e12, abs=1e-4)
+    assert rb["frac"] == pytest.approx(46174244 / 17e-6 / 8e12, abs=1e-4)
+    traffic, sym = bench.measured_traffic()
+    assert traffic and 1.0 < traffic / 170702384 < 1.02 and "split_kernel" in sym
