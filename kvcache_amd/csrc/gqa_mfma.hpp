@@ -100,7 +100,7 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(const int* __rest
         int unit = blockIdx.x;
         const int ntq = (p.N + 15) / 16;
         qh = unit % p.Hq;  unit /= p.Hq;
-        q0 = (unit % ntq) * 16;  unit /= ntq;
+        q0 = (ntq - 1 - unit % ntq) * 16;  unit /= ntq;  // longest prefixes first
         u.c = unit;
         u.s = 0;
         u.sub = 0;
