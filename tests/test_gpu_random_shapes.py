@@ -1,0 +1,70 @@
+"""Seeded random shapes through the three decode entry points, against the CPU oracle.
+
+Each case draws a batch of 1-24 sequences (lengths log-uniform up to 1500, with 0,
+1 and the block edges B-1, B, B+1, 2B mixed in), a head layout (Hkv in 1..8, query
+group 1..8), a head dimension (32, 64, 128), a block size (8, 16, 32, 48), a dtype
+and a split, then runs the device-lengths paged launch, the contiguous launch and
+the host-planned paged launch (reference entry points: launch_batched_paged,
+batched.cu:140-147, and launch_batched_paged_flash, batched.cu:199-208;
+launch_batched_decode, batched.cu:132-138).
+
+Bars: every path within the oracle tolerance (1e-5 fp32, 2e-3 fp16, max abs);
+paged == contiguous bit for bit when the block size is 16 or 32 (both launches
+then take the same kernel and the same chunks; at 8 or 48 the paged launch takes
+the VALU kernel, since the matrix-core kernel needs a power-of-two block of at
+least 16 tokens, or other chunks, and agrees with the contiguous one within
+tolerance only); a paged split that is not a multiple of the block size is refused
+with KVC_ERR_ARG.
+"""
+import numpy as np
+import pytest
+
+from kvcache_amd import KVC_F16, KVC_F32
+from kvcache_amd._native import KVC_ERR_ARG, KvcError
+
+from _helpers import normal, say, tol
+from test_gpu_decode import oracle_out, run_batched, run_planned
+
+pytestmark = pytest.mark.gpu
+
+
+def draw(seed):
+    r = np.random.default_rng(1000 + seed)
+    N = int(r.integers(1, 25))
+    Hkv = int(r.choice([1, 2, 4, 8]))
+    group = int(r.choice([1, 2, 3, 4, 7, 8]))
+    D = int(r.choice([32, 64, 128]))
+    B = int(r.choice([8, 16, 32, 48]))
+    dtype = KVC_F16 if r.random() < 0.6 else KVC_F32
+    edges = [0, 1, B - 1, B, B + 1, 2 * B]
+    lens = np.where(r.random(N) < 0.25, r.choice(edges, N), np.exp(r.uniform(0, np.log(1500), N)).astype(int))
+    split = int(r.choice([0, 0, B, 3 * B, 200, 512]))
+    return N, Hkv * group, Hkv, D, B, dtype, lens.astype(np.int32), split
+
+
+@pytest.mark.parametrize("seed", range(48))
+def test_random_shape_parity(orc, seed):
+    N, Hq, Hkv, D, B, dtype, lens, split = draw(seed)
+    nt = np.float16 if dtype == KVC_F16 else np.float32
+    say(f"random shape seed {seed}: N={N} Hq={Hq} Hkv={Hkv} D={D} B={B} "
+        f"{'f16' if dtype == KVC_F16 else 'f32'} split={split} max_len={int(lens.max())}")
+    S = max(int(lens.max()), 1)
+    q = normal((N, Hq, D), 3 * seed, nt)
+    K, V = normal((N, Hkv, S, D), 3 * seed + 1, nt), normal((N, Hkv, S, D), 3 * seed + 2, nt)
+    ref = oracle_out(orc, q, K, V, lens)
+    nb = sum((int(x) + B - 1) // B for x in lens)
+    perm = np.random.default_rng(seed).permutation(nb)
+
+    contig = run_batched(q, K, V, lens, Hkv, B, dtype, split=split, contiguous=True)
+    assert np.abs(contig - ref).max() <= tol(dtype)
+    planned = run_planned(q, K, V, lens, Hkv, B, dtype, perm=perm)
+    assert np.abs(planned - ref).max() <= tol(dtype)
+    if split % B:
+        with pytest.raises(KvcError) as ei:
+            run_batched(q, K, V, lens, Hkv, B, dtype, split=split, perm=perm)
+        assert ei.value.status == KVC_ERR_ARG
+        return
+    paged = run_batched(q, K, V, lens, Hkv, B, dtype, split=split, perm=perm)
+    assert np.abs(paged - ref).max() <= tol(dtype)
+    if B in (16, 32):
+        np.testing.assert_array_equal(paged, contig)
