@@ -292,7 +292,9 @@ size_t kvc_paged_causal_attn_workspace_size(int q_pos_base, int Nq, int Hq, int 
  * kvc_paged_causal_attn with the first query's position read from device memory
  * (*dev_q_pos_base), for captured graphs.  The kernel plans its own chunks from that
  * position (no host-side length); Nq <= 512 on the matrix-core path, 1024 otherwise,
- * and BLOCK a power of two. */
+ * and BLOCK a power of two whose block of one KV head holds at least 1 KiB
+ * (BLOCK * D * element size >= 1024: BLOCK >= 16 for fp16 D 32, >= 8 for fp16 D 64);
+ * other shapes are refused with KVC_ERR_UNSUPPORTED. */
 int kvc_paged_causal_attn_dev(const void* q, void* out, const void* k_pool, const void* v_pool,
                               const int* block_table, const int* dev_q_pos_base, int Nq, int Hq, int Hkv, int D,
                               int BLOCK, float scale, int dtype, void* workspace, size_t workspace_bytes,

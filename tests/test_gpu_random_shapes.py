@@ -19,10 +19,11 @@ with KVC_ERR_ARG.
 import numpy as np
 import pytest
 
-from kvcache_amd import KVC_F16, KVC_F32
-from kvcache_amd._native import KVC_ERR_ARG, KvcError
+from kvcache_amd import KVC_F16, KVC_F32, ops
+from kvcache_amd._native import KVC_ERR_ARG, KVC_ERR_UNSUPPORTED, KvcError
+from kvcache_amd.device import DeviceBuffer
 
-from _helpers import normal, say, tol
+from _helpers import dev, host, normal, say, tol
 from test_gpu_decode import oracle_out, run_batched, run_planned
 
 pytestmark = pytest.mark.gpu
@@ -68,3 +69,50 @@ def test_random_shape_parity(orc, seed):
     assert np.abs(paged - ref).max() <= tol(dtype)
     if B in (16, 32):
         np.testing.assert_array_equal(paged, contig)
+
+
+def draw_causal(seed):
+    r = np.random.default_rng(2000 + seed)
+    Hkv = int(r.choice([1, 2, 4]))
+    group = int(r.choice([1, 2, 4, 7]))
+    D = int(r.choice([32, 64, 128]))
+    B = int(r.choice([8, 16, 32, 64]))
+    dtype = KVC_F16 if r.random() < 0.6 else KVC_F32
+    base = 0 if r.random() < 0.4 else int(r.integers(1, 2000))
+    n = int(np.exp(r.uniform(0, np.log(500))))
+    return Hkv * group, Hkv, D, B, dtype, base, n
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_causal_parity(orc, seed):
+    """Prompt attention (qk_paged_causal_attn, qwen_kernels.h:19-21; the device-base
+    form qkcuda_paged_causal_attn, qwen_kernels.h:45-47) over seeded random shapes:
+    both forms within the oracle tolerance.  They need not agree bit for bit: the
+    host form chunks the prefix from the host position, the device form plans its
+    own chunks in the kernel."""
+    Hq, Hkv, D, B, dtype, base, n = draw_causal(seed)
+    nt = np.float16 if dtype == KVC_F16 else np.float32
+    say(f"random causal seed {seed}: Hq={Hq} Hkv={Hkv} D={D} B={B} {'f16' if dtype == KVC_F16 else 'f32'} "
+        f"base={base} n={n}")
+    nb = (base + n + B - 1) // B
+    table = np.random.default_rng(seed).permutation(nb + 5)[:nb].astype(np.int32)
+    NB = int(table.max()) + 1
+    kp, vp = normal((NB, Hkv, B, D), 5 * seed, nt), normal((NB, Hkv, B, D), 5 * seed + 1, nt)
+    q = normal((n, Hq, D), 5 * seed + 2, nt)
+    scale = float(1.0 / np.sqrt(D))
+    dq, dk, dv, dt = dev(q), dev(kp), dev(vp), dev(table)
+    out, out_dev = DeviceBuffer(q.nbytes), DeviceBuffer(q.nbytes)
+    ops.qk_paged_causal_attn(dq, out, dk, dv, dt, base, n, Hq, Hkv, D, B, scale, dtype=dtype)
+    got = host(out, nt, q.shape).astype(np.float64)
+    want = orc.paged_causal(q, kp, vp, table, base, Hkv, B, scale, nthreads=8)
+    assert np.abs(got - want).max() <= tol(dtype)
+    pos = dev(np.array([base], np.int32))
+    # the device-position form pages uniformly only: a power-of-two block of at least
+    # 1 KiB per KV head; other shapes are refused, never run partially
+    if B & (B - 1) or B * D * nt().itemsize < 1024:
+        with pytest.raises(KvcError) as ei:
+            ops.qkcuda_paged_causal_attn(dq, out_dev, dk, dv, dt, pos, n, Hq, Hkv, D, B, scale, dtype=dtype)
+        assert ei.value.status == KVC_ERR_UNSUPPORTED
+        return
+    ops.qkcuda_paged_causal_attn(dq, out_dev, dk, dv, dt, pos, n, Hq, Hkv, D, B, scale, dtype=dtype)
+    assert np.abs(host(out_dev, nt, q.shape).astype(np.float64) - want).max() <= tol(dtype)
