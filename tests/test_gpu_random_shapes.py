@@ -1,6 +1,7 @@
-"""Seeded random shapes through the three decode entry points, against the CPU oracle.
+"""Seeded random shapes through the decode, prompt-attention and K/V-write entry
+points, against the CPU oracle (attention) and numpy scatters (writes).
 
-Each case draws a batch of 1-24 sequences (lengths log-uniform up to 1500, with 0,
+Decode: each case draws a batch of 1-24 sequences (lengths log-uniform up to 1500, with 0,
 1 and the block edges B-1, B, B+1, 2B mixed in), a head layout (Hkv in 1..8, query
 group 1..8), a head dimension (32, 64, 128), a block size (8, 16, 32, 48), a dtype
 and a split, then runs the device-lengths paged launch, the contiguous launch and
@@ -116,3 +117,60 @@ def test_random_causal_parity(orc, seed):
         return
     ops.qkcuda_paged_causal_attn(dq, out_dev, dk, dv, dt, pos, n, Hq, Hkv, D, B, scale, dtype=dtype)
     assert np.abs(host(out_dev, nt, q.shape).astype(np.float64) - want).max() <= tol(dtype)
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_kv_writes(seed):
+    """K/V writes over seeded random shapes, bit-exact against numpy scatters of the
+    reference's addressing: a prompt's rows through its table (qk_write_kv,
+    qwen_kernels.cu:111-122), one row per sequence at its write position
+    (qk_batched_write_kv, qwen_kernels.cu:270-285; position -1 writes nothing) and
+    the same rows through a slot map; every other byte of the pools unchanged."""
+    r = np.random.default_rng(3000 + seed)
+    Hkv, D = int(r.choice([1, 2, 4, 8])), int(r.choice([32, 64, 128]))
+    B = int(r.choice([1, 8, 16, 32, 48]))
+    dtype = KVC_F16 if r.random() < 0.6 else KVC_F32
+    nt = np.float16 if dtype == KVC_F16 else np.float32
+    NB = int(r.integers(4, 80))
+    say(f"random writes seed {seed}: Hkv={Hkv} D={D} B={B} {'f16' if dtype == KVC_F16 else 'f32'} NB={NB}")
+    pool0 = normal((NB, Hkv, B, D), 7 * seed, nt)
+
+    # a prompt: L rows from start through a table of distinct blocks
+    cap = NB * B
+    start = int(r.integers(0, cap // 2 + 1))
+    L = int(r.integers(0, cap - start + 1))
+    table = r.permutation(NB).astype(np.int32)
+    k, v = normal((max(L, 1), Hkv, D), 7 * seed + 1, nt)[:L], normal((max(L, 1), Hkv, D), 7 * seed + 2, nt)[:L]
+    kp, vp = dev(pool0), dev(pool0)
+    ops.qk_write_kv(dev(k) if L else dev(np.zeros(1, nt)), dev(v) if L else dev(np.zeros(1, nt)), kp, vp,
+                    dev(table), start, L, Hkv, D, B, dtype=dtype)
+    ek, ev = pool0.copy(), pool0.copy()
+    for i in range(L):
+        pos = start + i
+        ek[table[pos // B], :, pos % B], ev[table[pos // B], :, pos % B] = k[i], v[i]
+    np.testing.assert_array_equal(host(kp, nt, pool0.shape), ek)
+    np.testing.assert_array_equal(host(vp, nt, pool0.shape), ev)
+
+    # one row per sequence: disjoint tables, a write position per row (or -1)
+    N = int(r.integers(1, min(NB, 32) + 1))
+    cuts = np.sort(r.choice(np.arange(1, NB), size=N - 1, replace=False)) if N > 1 else np.array([], int)
+    blocks = r.permutation(NB).astype(np.int32)
+    tables = np.split(blocks, cuts)
+    tab_off = np.concatenate([[0], np.cumsum([len(t) for t in tables])]).astype(np.int32)
+    wpos = np.array([int(r.integers(0, len(t) * B)) if r.random() < 0.85 else -1 for t in tables], np.int32)
+    k1, v1 = normal((N, Hkv, D), 7 * seed + 3, nt), normal((N, Hkv, D), 7 * seed + 4, nt)
+    kp, vp = dev(pool0), dev(pool0)
+    ops.qk_batched_write_kv(dev(k1), dev(v1), kp, vp, dev(blocks), dev(tab_off), dev(wpos), N, Hkv, D, B, dtype=dtype)
+    ek, ev = pool0.copy(), pool0.copy()
+    slots = np.full(N, -1, np.int32)
+    for i, t in enumerate(tables):
+        if wpos[i] >= 0:
+            phys, inb = t[wpos[i] // B], wpos[i] % B
+            ek[phys, :, inb], ev[phys, :, inb] = k1[i], v1[i]
+            slots[i] = phys * B + inb
+    np.testing.assert_array_equal(host(kp, nt, pool0.shape), ek)
+    np.testing.assert_array_equal(host(vp, nt, pool0.shape), ev)
+    kp, vp = dev(pool0), dev(pool0)
+    ops.write_kv_slots(dev(k1), dev(v1), kp, vp, dev(slots), N, Hkv, D, B, dtype=dtype)
+    np.testing.assert_array_equal(host(kp, nt, pool0.shape), ek)
+    np.testing.assert_array_equal(host(vp, nt, pool0.shape), ev)
