@@ -122,6 +122,41 @@ def test_engine_and_static_match_oracle(orc, trace, kv_write):
         _same(run_static(p, g, a, eng, 32), ref_s)
 
 
+def _random_trace(seed):
+    r = np.random.default_rng(4000 + seed)
+    n = int(r.integers(1, 121))
+    prompt = r.integers(1, int(r.choice([8, 64, 256, 1024])) + 1, size=n).astype(np.int32)
+    gmax = int(r.choice([4, 64, 512]))
+    if r.random() < 0.5:
+        gen = np.minimum(r.geometric(1.0 / max(gmax / 3, 1.5), size=n), gmax).astype(np.int32)
+    else:
+        gen = r.integers(1, gmax + 1, size=n).astype(np.int32)
+    rate = float(r.choice([0.0, 20.0, 400.0, 5000.0]))
+    arrival = np.cumsum(r.exponential(1e6 / rate, size=n)) if rate > 0 else np.zeros(n)
+    block = int(r.choice([1, 4, 16, 32]))
+    width = int(r.integers(1, 49))
+    need = max(blocks_needed(int(a + b), block) for a, b in zip(prompt, gen))
+    num_blocks = need + int(r.choice([0, 1, 3 * need, 100000]))
+    return prompt, gen, arrival.astype(np.float64), block, num_blocks, width, bool(r.random() < 0.5)
+
+
+@pytest.mark.parametrize("seed", range(20))
+def test_engine_random_traces_match_oracle(orc, seed):
+    """Seeded random traces (1-120 requests, prompts up to 1024, geometric or uniform
+    generation lengths, offline or Poisson arrivals at 20-5000 req/s, blocks of 1-32
+    tokens, widths 1-48, pools from the largest request's need up to roomy, with and
+    without K/V writes): the continuous engine and the static batcher make the
+    oracle's decisions step for step (engine.h:100-148, scheduler.h:182-238)."""
+    p, g, a, block, num_blocks, width, kv_write = _random_trace(seed)
+    eng = Engine(_cfg(block, num_blocks, width, kv_write))
+    rc, ref = orc.sim_engine(p, g, a, block, num_blocks, width, kv_write, COST)
+    assert rc == 0
+    _same(run_continuous(p, g, a, eng), ref)
+    rc, ref_s, _ = orc.sim_static(p, g, a, block, num_blocks, width, kv_write, COST)
+    assert rc == 0
+    _same(run_static(p, g, a, eng, width), ref_s)
+
+
 def test_engine_reference_known_answers():
     p, g, a = W.ref_trace()
     eng = Engine(_cfg(16, 32768, 32, False))
