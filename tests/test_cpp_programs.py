@@ -60,3 +60,29 @@ def test_paged_flash_device():
 @pytest.mark.gpu
 def test_runner_planned_and_device_length_paths_agree():
     assert run("test_runner_paths").returncode == 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("Hq,Hkv", [(8, 8), (14, 2)])
+@pytest.mark.parametrize("mode", [0, 1], ids=["copy_stream", "pinned_host_list"])
+def test_plan_pipeline_serving_loop_output(tmp_path, Hq, Hkv, mode):
+    """tests/cpp/plan_pipeline.cpp, the serving loop over the C ABI: the host plans every
+    step (kvc_decode_plan) while the previous step's kernel runs, the work list reaching
+    the kernel through a copy stream (mode 0) or from pinned host memory (mode 1); the
+    last step's output equals a plain planned launch's bit for bit."""
+    import json
+
+    import numpy as np
+    rng = np.random.default_rng(17 + mode + Hq)
+    N, D, B = 48, 64, 16
+    lens = rng.integers(1, 1500, N).astype(np.int32)
+    nb = (lens + B - 1) // B
+    tab_off = np.concatenate([[0], np.cumsum(nb)]).astype(np.int32)
+    table = rng.permutation(int(tab_off[-1]) + 7)[: tab_off[-1]].astype(np.int32)
+    path = tmp_path / "batch.bin"
+    np.concatenate([np.array([N, Hq, Hkv, D, B, len(table)], np.int32), lens, tab_off, table]).tofile(path)
+    r = run("plan_pipeline", str(path), "8", "2", str(mode))
+    assert r.returncode == 0
+    res = json.loads(r.stdout.strip().splitlines()[-1])
+    assert res["units"] > 0 and res["steps"] == 8
+    assert res["output_equals_plain_planned_launch"] is True
