@@ -8,9 +8,9 @@
 //     failure message is kvc_last_error();
 //   * launch_batched_paged and launch_batched_paged_flash are one entry point: the
 //     online fp32 softmax with split-K is the only implementation; the kernel plans
-//     its chunks from the device lengths, so `cap` is not needed there (shapes
-//     without that path give a sequence longer than `cap` NaN outputs, never a
-//     partial attention);
+//     its chunks from the device lengths, so `cap` only raises its planning budget
+//     (shapes without that path give a sequence longer than `cap` NaN outputs, never
+//     a partial attention, and a report kvc_check_device_errors returns);
 //   * launch_flash_decode allocates nothing per call: its partials live in a
 //     grow-only library workspace (pass your own through kvc_flash_decode).
 // Optional trailing arguments select a stream (hipStream_t as void*).
@@ -80,12 +80,17 @@ inline int qk_paged_causal_attn(const half* q, half* out, const half* k_pool, co
                                  KVC_F16, nullptr, 0, stream);
 }
 
-// As the reference, no length bound: the kernel plans its own chunks from the
-// device lengths (cap 0 = unknown), so every sequence is attended over its whole
-// length.
+// As the reference, any N and BLOCK and no length bound: the kernel plans its own
+// chunks from the device lengths (cap 0 = unknown; a batch of more sequences than one
+// launch plans runs as consecutive launches, a shape without that path reads the
+// longest length from the device).  With cap 0 the planning budget holds a mean length
+// of up to 63 of the largest chunks (64 blocks for one- or two-head units, 1024 blocks
+// on the matrix cores); past it the rows are NaN and kvc_check_device_errors reports
+// it.  `cap`, after the stream, states a longer bound.
 inline int qk_batched_paged_decode_attn(const half* q, half* out, const half* k_pool, const half* v_pool,
                                         const int* table_all, const int* tab_off, const int* cur_len, int N, int Hq,
-                                        int Hkv, int D, int BLOCK, float scale, kvc_stream_t stream = nullptr) {
-    return kvc_batched_paged_decode(q, k_pool, v_pool, table_all, tab_off, cur_len, out, N, Hq, Hkv, D, BLOCK, 0,
+                                        int Hkv, int D, int BLOCK, float scale, kvc_stream_t stream = nullptr,
+                                        int cap = 0) {
+    return kvc_batched_paged_decode(q, k_pool, v_pool, table_all, tab_off, cur_len, out, N, Hq, Hkv, D, BLOCK, cap,
                                     scale, KVC_F16, nullptr, 0, stream);
 }

@@ -75,12 +75,22 @@ inline int qkcuda_write_kv(const half* k, const half* v, half* k_pool, half* v_p
 }
 
 // qwen_kernels.h:45-47 -- qk_paged_causal_attn with the first query at *q_pos_base
-// (device memory); the kernel plans its chunks from that position.  The reference
-// calls it under graph capture, so it takes the allocation-free entry point (its
-// partials live in a static device array; calls overlapping on one GPU race).
+// (device memory); the kernel plans its chunks from that position.  Outside stream
+// capture the partials go to the library's per-stream workspace (up to 512 queries at
+// the matrix-core shapes, 1024 otherwise).  The reference captures this call in a graph
+// (qwen_infer.cu:145-162, one query per step); under capture nothing may be allocated,
+// so it takes the allocation-free entry point, whose partials live in a 4 MiB static
+// device array per GPU: about 17 queries of the 14q/2kv D 64 shape at most (larger calls
+// are refused with KVC_ERR_UNSUPPORTED), and captured calls that overlap on one GPU race.
 inline int qkcuda_paged_causal_attn(const half* q, half* out, const half* k_pool, const half* v_pool,
                                     const int* block_table_dev, int* q_pos_base, int Nq, int Hq, int Hkv, int D,
                                     int BLOCK, float scale, kvc_stream_t stream = nullptr) {
-    return kvc_paged_causal_attn_dev_noalloc(q, out, k_pool, v_pool, block_table_dev, q_pos_base, Nq, Hq, Hkv, D,
-                                             BLOCK, scale, KVC_F16, stream);
+    int capturing = 0;
+    const int rc = kvc_stream_is_capturing(stream, &capturing);
+    if (rc) return rc;
+    if (capturing)
+        return kvc_paged_causal_attn_dev_noalloc(q, out, k_pool, v_pool, block_table_dev, q_pos_base, Nq, Hq, Hkv, D,
+                                                 BLOCK, scale, KVC_F16, stream);
+    return kvc_paged_causal_attn_dev(q, out, k_pool, v_pool, block_table_dev, q_pos_base, Nq, Hq, Hkv, D, BLOCK,
+                                     scale, KVC_F16, nullptr, 0, stream);
 }

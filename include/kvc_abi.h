@@ -108,6 +108,19 @@ int kvc_event_elapsed_ms(float* ms, void* start, void* stop); /* synchronizes on
  * qwen_infer.cu:135-214).  Only graph-safe entry points may be captured: those that
  * allocate nothing and take per-step counts from device memory (the *_dev and
  * dev_rows forms below). */
+/* 1 in *capturing when `stream` is being captured into a graph (0 for the null stream). */
+int kvc_stream_is_capturing(kvc_stream_t stream, int* capturing);
+/* Device-side failure reports.  A device-length decode launch that cannot attend a
+ * sequence whole -- a length past the stated cap on the explicit-split grid, a batch past
+ * the self-planned record budget, a contiguous length past MAXS -- writes NaN in that
+ * sequence's output rows (never a partial attention) and stores a report in a per-device
+ * word of pinned host memory.  kvc_check_device_errors synchronizes `stream` and returns
+ * KVC_ERR_ARG (message in kvc_last_error) when such a report is pending, KVC_OK otherwise;
+ * it clears the report.  The next device-length decode call on the device
+ * (kvc_batched_decode*, kvc_batched_paged_decode*, kvc_paged_causal_attn_dev) also returns
+ * a report that has reached the host by then, without launching, and clears it.  No
+ * counterpart in the reference, whose launchers return void (kv_cache.h:2-34). */
+int kvc_check_device_errors(kvc_stream_t stream);
 int kvc_graph_begin(kvc_stream_t stream);
 int kvc_graph_end(kvc_stream_t stream, void** graph_exec);
 int kvc_graph_launch(void* graph_exec, kvc_stream_t stream);
@@ -164,7 +177,9 @@ int kvc_paged_decode(const void* q, const void* k_pool, const void* v_pool,
                      int H, int D, int BLOCK, float scale, int dtype, kvc_stream_t stream);
 
 /* launch_batched_decode (kv_cache.h:15-17, batched.cu:49-88,132-138): caches
- * [N,Hkv,MAXS,D], lengths cur_len[N] (device), cap = max length (host). */
+ * [N,Hkv,MAXS,D], lengths cur_len[N] (device), cap = max length (host; 0: MAXS bounds
+ * every length).  A length past MAXS gets NaN rows and a device error report
+ * (kvc_check_device_errors). */
 int kvc_batched_decode(const void* q, const void* k_cache, const void* v_cache,
                        const int* cur_len, void* out, int N, int Hq, int Hkv, int D,
                        int MAXS, int cap, float scale, int dtype,
@@ -173,13 +188,19 @@ int kvc_batched_decode(const void* q, const void* k_cache, const void* v_cache,
 /* launch_batched_paged / launch_batched_paged_flash (kv_cache.h:20-27,
  * batched.cu:97-147,157-207) and qk_batched_paged_decode_attn (qwen_kernels.h:35-37,
  * qwen_kernels.cu:293-335): one query per sequence over its pages [0,cur_len[s]).
- * Bit-identical to kvc_batched_decode on the same logical data.
- * cap: the caller's bound on every cur_len.  Shapes with a self-planned path
- * (tuning "self_plan", at most 1024 sequences, 512 on the matrix cores; a
- * power-of-two BLOCK of at least 1024 / (D * element bytes) tokens) plan from the
- * device lengths and ignore it (0 allowed): every sequence is
- * attended over its whole length.  Other shapes need cap > 0 and give a sequence
- * longer than cap NaN outputs: never a silent partial attention. */
+ * Bit-identical to kvc_batched_decode on the same logical data (at BLOCK 16 or 32).
+ * cap: the caller's bound on every cur_len, or 0 (unknown).
+ *  - Shapes with a self-planned path (tuning "self_plan"; a power-of-two BLOCK of at
+ *    least 1024 / (D * element bytes) tokens) plan from the device lengths; cap only
+ *    raises the planning budget.  Batches of more than 1024 sequences (512 on the matrix
+ *    cores) run as consecutive launches of that many.  The budget holds 64 partial
+ *    records per (sequence, head): a batch whose mean length passes 63 x the largest
+ *    chunk (64,512 tokens for one- or two-head units at BLOCK 16) with cap 0 gets NaN
+ *    rows and a device error report (kvc_check_device_errors); stating cap avoids it.
+ *  - Other shapes with cap 0 read the longest length from the device (one
+ *    synchronisation; refused with KVC_ERR_STATE under stream capture); with cap > 0 a
+ *    sequence longer than cap gets NaN rows and a device error report -- never a
+ *    silent partial attention. */
 int kvc_batched_paged_decode(const void* q, const void* k_pool, const void* v_pool,
                              const int* table_all, const int* tab_off, const int* cur_len,
                              void* out, int N, int Hq, int Hkv, int D, int BLOCK, int cap,

@@ -232,6 +232,62 @@ int default_workspace(size_t bytes, hipStream_t st, void** out) {
     return KVC_OK;
 }
 
+bool stream_capturing(hipStream_t st) {
+    if (st == nullptr) return false;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+}
+
+// Device-side failure reports.  A launch that cannot attend a sequence whole (a length
+// past its stated cap or its contiguous cache, a batch past the self-planned budget)
+// writes NaN rows and stores a DeviceError code into this per-device word of pinned
+// host memory (kernels store with system scope; the host reads it without a device
+// synchronisation).  The word is made on the first decode call on a device that may
+// allocate (never under stream capture, never by the allocation-free entry point,
+// which then reports through NaN rows only) and lives until the process ends.
+std::mutex g_err_mu;
+std::vector<int*> g_err_words;
+
+int* device_error_word(hipStream_t st, bool may_alloc) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+    std::lock_guard<std::mutex> lk(g_err_mu);
+    if ((int)g_err_words.size() <= dev) g_err_words.resize(dev + 1, nullptr);
+    if (!g_err_words[dev] && may_alloc && !stream_capturing(st)) {
+        void* w = nullptr;
+        if (hipHostMalloc(&w, 64, hipHostMallocDefault) == hipSuccess) {
+            __atomic_store_n(static_cast<int*>(w), 0, __ATOMIC_RELAXED);
+            g_err_words[dev] = static_cast<int*>(w);
+        }
+    }
+    return g_err_words[dev];
+}
+
+// Takes (reads and clears) the current device's reported code; 0 when none.
+int take_device_error() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    std::lock_guard<std::mutex> lk(g_err_mu);
+    if ((int)g_err_words.size() <= dev || !g_err_words[dev]) return 0;
+    return __atomic_exchange_n(g_err_words[dev], 0, __ATOMIC_ACQ_REL);
+}
+
+int device_error_status(int code) {
+    switch (code) {
+        case kDevErrNone: return KVC_OK;
+        case kDevErrCap:
+            return set_error(KVC_ERR_ARG, "an earlier decode launch on this device had a sequence longer than its "
+                                          "stated cap; its rows were written as NaN");
+        default:
+            return set_error(KVC_ERR_ARG, "an earlier decode launch on this device had a batch past its planning "
+                                          "budget or a length past its contiguous cache; its rows were written as NaN");
+    }
+}
+
+// Entry check of the device-length decode calls: an earlier launch's report (as far as
+// it has reached the host) fails this call before it launches, and is cleared.
+int pending_device_error() { return device_error_status(take_device_error()); }
+
 int resolve_workspace(const Plan& pl, void* ws, size_t ws_bytes, DecodeParams& p, hipStream_t st) {
     if (pl.max_chunks <= 1) return KVC_OK;
     if (!ws) {
@@ -294,6 +350,7 @@ int run_batched(const void* q, const void* k, const void* v, const int* table_al
     p.group = Hq / Hkv; p.nsub = pl.nsub;
     p.chunk_tokens = pl.chunk; p.num_splits = 0; p.max_chunks = pl.max_chunks;
     p.scale_log2 = scale * 1.4426950408889634f;
+    p.err_word = device_error_word(st, true);
     rc = resolve_workspace(pl, ws, ws_bytes, p, st);
     if (rc) return rc;
     p.lpb_shift = pl.lpb_shift;
@@ -663,6 +720,16 @@ size_t self_plan_workspace(int N, int Hq, int Hkv, int D, int BLOCK, int dtype, 
     return planned_workspace(Hq, Hkv, D, BLOCK, dtype, (int)self_plan_records(N, Hq, Hkv, D, BLOCK, dtype, bound));
 }
 
+// Sequences per launch when a batch has more than one self-planned launch plans (it
+// then runs as consecutive groups); 0 when the shape has no self-planned path at all.
+int self_plan_group(int N, int Hq, int Hkv, int D, int BLOCK, int dtype, long long bound = 0) {
+    if (N <= 0 || !self_plan_ok(1, Hq, Hkv, D, BLOCK, dtype, bound)) return 0;
+    const PlanShape ps = plan_shape(Hq, Hkv, D, BLOCK, dtype);
+    int g = std::min(N, ps.mfma ? kSelfMaxNMfmaHost : kSelfMaxNValuHost);
+    while (g > 1 && !self_plan_ok(g, Hq, Hkv, D, BLOCK, dtype, bound)) g /= 2;
+    return g;
+}
+
 // Contiguous caches are planned with chunks cut at this granularity, the paged
 // path's usual block, so a paged batch with 16-token blocks and the same batch in
 // contiguous caches run the same chunks (bit-identical outputs).
@@ -675,7 +742,7 @@ constexpr int kSelfContigBlock = 16;
 int run_self_planned(const void* q, const void* k, const void* v, const int* table_all, const int* tab_off,
                      const int* cur_len, const int* dev_base, void* out, int N, int Hq, int Hkv, int D, int BLOCK,
                      int cap, float scale, int dtype, void* ws, size_t ws_bytes, hipStream_t st, bool contig = false,
-                     long long seq_stride = 0, long long head_stride = 0) {
+                     long long seq_stride = 0, long long head_stride = 0, bool no_alloc = false) {
     int rc = check_common(N, Hq, Hkv, D, dtype, q, k, v, out);
     if (rc || N == 0) return rc;
     if (contig) BLOCK = kSelfContigBlock;
@@ -719,6 +786,7 @@ int run_self_planned(const void* q, const void* k, const void* v, const int* tab
         if (kvb <= (4LL << 20))  // a block of both pools (every KV head) addressed with 32-bit offsets
             p.sp_pf_blocks = (int)std::min<long long>(((long long)tuning().self_prefetch_kib << 10) / ((long long)N * kvb), 4096);
         p.sp_pf_min_len = std::max(tuning().self_prefetch_min_len, 1);
+        p.sp_pf_xcd = tuning().self_prefetch_xcd != 0 && ps.nsub == 1 && Hkv % 8 == 0;
     }
     const size_t rall = (size_t)recs;
     const size_t acc = align_up(rall * ps.G * D * sizeof(float), kAlign), ml = align_up(rall * ps.G * 2 * sizeof(float), kAlign);
@@ -728,6 +796,7 @@ int run_self_planned(const void* q, const void* k, const void* v, const int* tab
     p.ctr_shift = ctr_shift_for(rall);
     p.epoch = next_epoch();
     p.merge_mode = kMergeAtomic;
+    p.err_word = device_error_word(st, !no_alloc);
     L.dtype = dtype; L.D = D; L.G = ps.G; L.mode = contig ? kSelfContig : kSelfPlanned; L.mfma = ps.mfma;
     L.wg_per_cu = tuning().wg_per_cu >= 0 ? tuning().wg_per_cu : (!ps.mfma && ps.G <= 2 ? 6 : 0);
     L.wpb = tuning().waves_per_block ? tuning().waves_per_block : ps.wpb;
@@ -860,6 +929,24 @@ int kvc_event_create(void** ev) {
     int rc = hip_check(hipEventCreate(&e), "hipEventCreate");
     *ev = e;
     return rc;
+}
+int kvc_stream_is_capturing(kvc_stream_t st, int* capturing) {
+    if (!capturing) return set_error(KVC_ERR_ARG, "null out pointer");
+    *capturing = 0;
+    if (st == nullptr) return KVC_OK;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    int rc = hip_check(hipStreamIsCapturing(S(st), &cs), "hipStreamIsCapturing");
+    if (rc == KVC_OK) *capturing = cs != hipStreamCaptureStatusNone ? 1 : 0;
+    return rc;
+}
+int kvc_check_device_errors(kvc_stream_t st) {
+    return guarded([&]() -> int {
+        if (stream_capturing(S(st)))
+            return set_error(KVC_ERR_STATE, "kvc_check_device_errors synchronizes: not under stream capture");
+        int rc = hip_check(hipStreamSynchronize(S(st)), "hipStreamSynchronize");
+        if (rc) return rc;
+        return device_error_status(take_device_error());
+    });
 }
 int kvc_graph_begin(kvc_stream_t st) {
     return hip_check(hipStreamBeginCapture(S(st), hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
@@ -1008,15 +1095,20 @@ int kvc_batched_decode_split(const void* q, const void* k_cache, const void* v_c
     return guarded([&]() -> int {
         if (MAXS < 0 || cap < 0 || cap > MAXS) return set_error(KVC_ERR_ARG, "cap must be in [0, MAXS]");
         if (N > 0 && !cur_len) return set_error(KVC_ERR_ARG, "null cur_len");
+        int rc = check_common(N, Hq, Hkv, D, dtype, q, k_cache, v_cache, out);
+        if (rc || N == 0) return rc;
+        rc = pending_device_error();
+        if (rc) return rc;
         // automatic split: the kernel plans from the device lengths, with the chunks of
         // the paged path (so paged and contiguous batches agree bit for bit)
         if (split == 0 && tuning().self_plan != 0 && self_plan_ok(N, Hq, Hkv, D, kSelfContigBlock, dtype, cap))
             return run_self_planned(q, k_cache, v_cache, nullptr, nullptr, cur_len, nullptr, out, N, Hq, Hkv, D, 0,
                                     cap, scale, dtype, ws, ws_bytes, S(st), true, (long long)Hkv * MAXS * D,
                                     (long long)MAXS * D);
+        // every length is at most MAXS (the cache's extent): cap 0 means that bound
         return run_batched(q, k_cache, v_cache, nullptr, nullptr, cur_len, 0, out, N, Hq, Hkv, D, 0,
-                           (long long)Hkv * MAXS * D, (long long)MAXS * D, cap, scale, dtype, split, false, ws,
-                           ws_bytes, S(st));
+                           (long long)Hkv * MAXS * D, (long long)MAXS * D, cap > 0 ? cap : MAXS, scale, dtype, split,
+                           false, ws, ws_bytes, S(st));
     });
 }
 
@@ -1034,12 +1126,45 @@ int kvc_batched_paged_decode_split(const void* q, const void* k_pool, const void
     return guarded([&]() -> int {
         if (N > 0 && (!tab_off || !cur_len)) return set_error(KVC_ERR_ARG, "null tab_off / cur_len");
         if (cap < 0) return set_error(KVC_ERR_ARG, "cap must be >= 0");
-        // automatic split: the kernel plans from the device lengths (cap only a hint)
-        if (split == 0 && tuning().self_plan != 0 && self_plan_ok(N, Hq, Hkv, D, BLOCK, dtype, cap))
-            return run_self_planned(q, k_pool, v_pool, table_all, tab_off, cur_len, nullptr, out, N, Hq, Hkv, D,
-                                    BLOCK, cap, scale, dtype, ws, ws_bytes, S(st));
-        if (cap == 0 && N > 0)
-            return set_error(KVC_ERR_ARG, "this shape needs cap, the longest length (no self-planned path for it)");
+        int rc = check_common(N, Hq, Hkv, D, dtype, q, k_pool, v_pool, out);
+        if (rc || N == 0) return rc;
+        if (BLOCK <= 0 || !table_all) return set_error(KVC_ERR_ARG, "paged decode needs BLOCK > 0 and a block table");
+        rc = pending_device_error();
+        if (rc) return rc;
+        if (split == 0 && tuning().self_plan != 0) {
+            // automatic split: the kernel plans from the device lengths (cap only a hint)
+            if (self_plan_ok(N, Hq, Hkv, D, BLOCK, dtype, cap))
+                return run_self_planned(q, k_pool, v_pool, table_all, tab_off, cur_len, nullptr, out, N, Hq, Hkv, D,
+                                        BLOCK, cap, scale, dtype, ws, ws_bytes, S(st));
+            // more sequences than one self-planned launch plans: consecutive groups of
+            // them, one launch each (the launches share the workspace in stream order)
+            const int group = self_plan_group(N, Hq, Hkv, D, BLOCK, dtype, cap);
+            if (group > 0) {
+                const size_t qrow = (size_t)Hq * D * esize(dtype);
+                for (int g0 = 0; g0 < N; g0 += group) {
+                    const int n = std::min(group, N - g0);
+                    rc = run_self_planned(static_cast<const char*>(q) + g0 * qrow, k_pool, v_pool, table_all,
+                                          tab_off + g0, cur_len + g0, nullptr, static_cast<char*>(out) + g0 * qrow, n,
+                                          Hq, Hkv, D, BLOCK, cap, scale, dtype, ws, ws_bytes, S(st));
+                    if (rc) return rc;
+                }
+                return KVC_OK;
+            }
+        }
+        if (cap == 0 && N > 0) {
+            // no self-planned path and no bound stated: the longest length is read from the
+            // device (a synchronisation; refused under stream capture) and sizes the grid
+            if (stream_capturing(S(st)))
+                return set_error(KVC_ERR_STATE, "this shape has no self-planned path: under stream capture it needs "
+                                                "cap, the longest length");
+            std::vector<int> h(N);
+            rc = hip_check(hipMemcpyAsync(h.data(), cur_len, (size_t)N * sizeof(int), hipMemcpyDeviceToHost, S(st)),
+                           "hipMemcpyAsync (lengths)");
+            if (rc) return rc;
+            rc = hip_check(hipStreamSynchronize(S(st)), "hipStreamSynchronize (lengths)");
+            if (rc) return rc;
+            cap = std::max(1, *std::max_element(h.begin(), h.end()));
+        }
         return run_batched(q, k_pool, v_pool, table_all, tab_off, cur_len, 0, out, N, Hq, Hkv, D, BLOCK, 0, 0, cap,
                            scale, dtype, split, true, ws, ws_bytes, S(st));
     });
@@ -1066,6 +1191,8 @@ int kvc_paged_causal_attn_dev(const void* q, void* out, const void* k_pool, cons
     return guarded([&]() -> int {
         if (Nq < 0) return set_error(KVC_ERR_ARG, "Nq must be >= 0");
         if (Nq > 0 && !dev_q_pos_base) return set_error(KVC_ERR_ARG, "null q_pos_base pointer");
+        int rc = pending_device_error();
+        if (rc) return rc;
         if (Nq > 0 && !self_plan_ok(Nq, Hq, Hkv, D, BLOCK, dtype))
             return set_error(KVC_ERR_UNSUPPORTED, "device-position prompt attention needs a power-of-two BLOCK the "
                                                   "kernels page uniformly and at most 512 queries");
@@ -1099,7 +1226,7 @@ int kvc_paged_causal_attn_dev_noalloc(const void* q, void* out, const void* k_po
         int rc = scratch_address(&ws);
         if (rc) return rc;
         return run_self_planned(q, k_pool, v_pool, block_table, nullptr, nullptr, dev_q_pos_base, out, Nq, Hq, Hkv,
-                                D, BLOCK, 0, scale, dtype, ws, kScratchBytes, S(st));
+                                D, BLOCK, 0, scale, dtype, ws, kScratchBytes, S(st), false, 0, 0, true);
     });
 }
 
@@ -1212,6 +1339,9 @@ size_t kvc_decode_workspace_size(int N, int Hq, int Hkv, int D, int BLOCK, int c
     if (split == 0 && tuning().self_plan != 0) {
         const int b = BLOCK > 0 ? BLOCK : kSelfContigBlock;
         if (self_plan_ok(N, Hq, Hkv, D, b, dtype, cap)) return self_plan_workspace(N, Hq, Hkv, D, b, dtype, cap);
+        // paged batches larger than one self-planned launch: consecutive groups
+        const int g = BLOCK > 0 ? self_plan_group(N, Hq, Hkv, D, b, dtype, cap) : 0;
+        if (g > 0) return self_plan_workspace(g, Hq, Hkv, D, b, dtype, cap);
     }
     return plan_batched(N, Hq, Hkv, D, BLOCK, cap, dtype, split, BLOCK > 0).ws_bytes;
 }
@@ -1246,6 +1376,7 @@ int kvc_set_tuning(const char* key, int value) {
     else if (k == "self_grid" && value >= 0) tuning().self_grid = value;
     else if (k == "self_prefetch_kib" && value >= 0) tuning().self_prefetch_kib = value;
     else if (k == "self_prefetch_min_len" && value >= 0) tuning().self_prefetch_min_len = value;
+    else if (k == "self_prefetch_xcd" && (value == 0 || value == 1)) tuning().self_prefetch_xcd = value;
     else return set_error(KVC_ERR_ARG, "unknown tuning key or bad value: " + k);
     return KVC_OK;
 }
@@ -1267,6 +1398,7 @@ int kvc_get_tuning(const char* key, int* value) {
     else if (k == "self_grid") *value = tuning().self_grid;
     else if (k == "self_prefetch_kib") *value = tuning().self_prefetch_kib;
     else if (k == "self_prefetch_min_len") *value = tuning().self_prefetch_min_len;
+    else if (k == "self_prefetch_xcd") *value = tuning().self_prefetch_xcd;
     else return set_error(KVC_ERR_ARG, "unknown tuning key: " + k);
     return KVC_OK;
 }

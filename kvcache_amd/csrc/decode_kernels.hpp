@@ -340,10 +340,19 @@ struct Unit {
 // NaN in the output rows of `heads` query heads from hq0 of sequence s: what a
 // sequence longer than the launch's stated cap gets instead of a silently
 // truncated attention.
+// The failure is also reported to the host: thread 0 stores `code` into the launch's
+// error word (pinned host memory, a system-scope store), which the library returns as a
+// status from kvc_check_device_errors and from the next device-length decode call.
+__device__ __forceinline__ void report_device_error(const DecodeParams& p, int code) {
+    if (p.err_word != nullptr && threadIdx.x == 0)
+        __hip_atomic_store(p.err_word, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 template <typename T, int D, int NT>
 __device__ void nan_rows(const DecodeParams& p, int s, int hq0, int heads) {
     T* ob = static_cast<T*>(p.out) + ((size_t)s * p.Hq + hq0) * D;
     for (int e = threadIdx.x; e < heads * D; e += NT) ob[e] = (T)__builtin_nanf("");
+    report_device_error(p, kDevErrCap);
 }
 
 // The 8-int header of this workgroup's planned entry.  The kernels take the work

@@ -81,7 +81,19 @@ struct DecodeParams {
     int sp_records;           // partial records per (sequence, head) in the workspace
     int sp_pf_blocks;         // blocks of every sequence read ahead while the plan is made (0: none)
     int sp_pf_min_len;        // shortest sequence read ahead
+    int sp_pf_xcd;            // 1: each KV head's slice is read ahead on the XCD of its units (self_prefetch)
     const int* dev_base;
+    // where a launch reports a length it could not attend (the rows get NaN as well):
+    // a pinned host word per device (device_error_word in abi.hip), or nullptr
+    int* err_word;
+};
+
+// Codes the kernels store into DecodeParams::err_word.
+enum DeviceError {
+    kDevErrNone = 0,
+    kDevErrCap = 1,      // a sequence longer than the launch's stated cap (explicit-split grid)
+    kDevErrBudget = 2    // a self-planned batch past its planning budget, or a contiguous
+                         // length past its cache (MAXS)
 };
 
 // Arrival counters.  Atomics that land on one 128-byte line serialise (about 10 ns
@@ -158,6 +170,8 @@ struct Tuning {
     int self_prefetch_kib = 32768;  // self-planned paged launches: K+V bytes (KiB) read ahead while the
                                     // kernel plans (the first blocks of every sequence; 0: none)
     int self_prefetch_min_len = 256;  // ... of the sequences of at least this many tokens
+    int self_prefetch_xcd = 1;  // 1: read each KV head's slice ahead on the XCD whose units use it
+                                // (whole-KV-head units and a multiple of 8 KV heads only)
 };
 // Dynamic LDS that caps decode workgroups per CU at wg_per_cu (0: none).
 size_t occupancy_lds(size_t static_lds, int wg_per_cu);

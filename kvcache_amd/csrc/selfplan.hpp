@@ -138,8 +138,11 @@ __device__ __forceinline__ int self_plan_rank(int k) {
 // [l * spl, l * spl + spl), so every reduction and ordering is one wave scan -- while
 // the other waves wait at the closing barrier; every wave then returns the same plan.
 // Order: eight buckets (self_bucket), descending; within a bucket by sequence, and
-// within a sequence run A (chunks 0..nc-2 of every head) before run B (its last
-// chunk of every head).
+// within a sequence run A (chunks 0..nc-2, the hks heads of each chunk in turn)
+// before run B (its last chunk of every head).  Every run holds a multiple of hks
+// units, so a unit's rank is congruent to its head modulo hks: with hks a multiple of
+// 8, the unit of head h at rank r < gridDim.x runs on workgroup r, which the hardware
+// places on XCD r mod 8 = h mod 8 (self_prefetch relies on this).
 // Wave 0's first kSelfSpt lengths (lane l: sequences l * spl ...), loaded before
 // anything else of the kernel: they depend only on the preloaded arguments.
 __device__ __forceinline__ void self_first_lengths(const int* lens, int N, int (&lv0)[kSelfSpt]) {
@@ -308,9 +311,9 @@ __device__ SelfPlan self_plan_setup(const int* lens, int n_seq, const DecodePara
                 const int cb = kb == bsel ? hks : 0;
                 if (x < ca + cb) {
                     int h, cc;
-                    if (x < ca) {  // run A: chunks 0..nc-2 of every head
-                        h = x / (nc - 1);
-                        cc = x - h * (nc - 1);
+                    if (x < ca) {  // run A: chunks 0..nc-2, every head of a chunk in turn
+                        cc = x / hks;
+                        h = x - cc * hks;
                     } else {       // run B: the last chunk of every head
                         h = x - ca;
                         cc = nc - 1;
@@ -355,6 +358,7 @@ __device__ __forceinline__ bool self_plan_header(const Lds& S, int k, int (&hdr)
 // head subgroup), rank r = s * hks + h, ranks served as in the planned loop.
 template <typename E, int D, int NT>
 __device__ void self_plan_nan(const DecodeParams& p, int heads) {
+    report_device_error(p, kDevErrBudget);
     const int hks = p.Hkv * p.nsub;
     for (int k = 0, r = self_plan_rank(0); r < p.N * hks; r = self_plan_rank(++k)) {
         const int s = r / hks, h = r % hks;
@@ -373,9 +377,52 @@ __device__ void self_plan_nan(const DecodeParams& p, int heads) {
 // it; each pool block is touched once per 64 bytes by loads whose data land in an LDS
 // sink (no registers held; wave 1's first wait for its own unit's loads also covers
 // these, issued microseconds earlier).
+//
+// Targeted form (p.sp_pf_xcd, set when every unit covers one whole KV head and Hkv is
+// a multiple of 8): the unit of KV head h at rank r < gridDim.x runs on XCD h mod 8
+// (self_plan_setup's order), so the read-ahead of head h's slice of a block is made
+// by a workgroup of that XCD (workgroup b sits on XCD b mod 8) and lands in the L2
+// that the unit reads through: the unit finds the bytes there instead of requesting
+// them again from the memory-side cache.  Item t = s + N * (j + pf * hh) is block j
+// of sequence s, KV head x + 8 * hh of this workgroup's XCD x; workgroup 8 * q + x
+// takes items q, q + Q, ... (Q = gridDim.x / 8 workgroups per XCD), one per lane.
 template <typename E, int D, typename Lds>
 __device__ __forceinline__ void self_prefetch(const int* lens, int N, const DecodeParams& p, Lds& S) {
     const int lane = threadIdx.x & (kWave - 1);
+    if (p.sp_pf_xcd) {
+        const unsigned Q = gridDim.x >> 3, xcd = blockIdx.x & 7u, q = blockIdx.x >> 3;
+        const unsigned per_head = (unsigned)N * (unsigned)p.sp_pf_blocks;  // N <= kSelfMaxNValu, blocks <= 4096
+        const unsigned items = per_head * (unsigned)(p.Hkv >> 3);
+        const unsigned t = q + (unsigned)lane * Q;
+        const bool has = q < Q && t < items;
+        const unsigned hh = has ? t / per_head : 0, r = has ? t - hh * per_head : 0;
+        const int s = (int)(r % (unsigned)N), j = (int)(r / (unsigned)N);
+        const int h = (int)(xcd + 8 * hh);
+        const __amdgpu_buffer_rsrc_t lrs = tile_rsrc(lens, N * 4), ors = tile_rsrc(p.tab_off, N * 4);
+        const int L = (int)__builtin_amdgcn_raw_buffer_load_b32(lrs, s * 4, 0, 0);
+        const int to = (int)__builtin_amdgcn_raw_buffer_load_b32(ors, s * 4, 0, 0);
+        const bool ok = has && L >= p.sp_pf_min_len && 4LL * j * p.block < (long long)L;
+        const __amdgpu_buffer_rsrc_t tbr = tile_rsrc(p.table_all, p.table_len * 4);
+        const int bid = ok ? (int)__builtin_amdgcn_raw_buffer_load_b32(tbr, (int)(((unsigned)to + (unsigned)j) * 4u), 0, 0) : -1;
+        const int bytes = p.block * D * (int)sizeof(E);  // one block of one KV head, one pool
+        unsigned long long live = __ballot(ok);
+        auto* sink = (__attribute__((address_space(3))) void*)S.sink;
+#pragma unroll 1
+        while (live) {
+            const int i = __builtin_ctzll(live);
+            live &= live - 1;
+            const size_t base = ((size_t)(unsigned)__builtin_amdgcn_readlane(bid, i) * (unsigned)p.Hkv +
+                                 (unsigned)__builtin_amdgcn_readlane(h, i)) * (size_t)bytes;
+            const __amdgpu_buffer_rsrc_t kr = tile_rsrc(static_cast<const char*>(p.k) + base, bytes);
+            const __amdgpu_buffer_rsrc_t vr = tile_rsrc(static_cast<const char*>(p.v) + base, bytes);
+#pragma unroll 1
+            for (int x = lane * 64; x < bytes; x += kWave * 64) {
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, sink, 4, x, 0, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, sink, 4, x, 0, 0, 0);
+            }
+        }
+        return;
+    }
     const unsigned items = (unsigned)N * (unsigned)p.sp_pf_blocks;  // N <= kSelfMaxNValu, blocks <= 4096
     const unsigned t = blockIdx.x + (unsigned)lane * gridDim.x;
     const bool has = t < items;

@@ -19,7 +19,7 @@ __all__ = [
     "qk_batched_paged_decode_attn", "write_kv_slots", "decode_workspace_size", "decode_auto_split",
     "decode_plan", "planned_workspace_size", "launch_batched_paged_planned", "launch_batched_paged_append_planned",
     "flash_decode_workspace_size", "qk_paged_causal_attn", "qkcuda_paged_causal_attn", "qkcuda_write_kv",
-    "qkcuda_rope", "KVC_F16", "KVC_F32",
+    "qkcuda_rope", "check_device_errors", "stream_is_capturing", "KVC_F16", "KVC_F32",
 ]
 
 
@@ -93,7 +93,9 @@ def qk_batched_write_kv(k, v, k_pool, v_pool, table_all, tab_off, wpos, N, Hkv, 
 def qk_batched_paged_decode_attn(q, out, k_pool, v_pool, table_all, tab_off, cur_len, N, Hq, Hkv, D, BLOCK, scale,
                                  *, cap=0, dtype=KVC_F16, split=0, workspace=None, stream=None):
     """qwen_kernels.h:35-37: no length bound is needed (cap = 0: the kernel plans its
-    own chunks from the device lengths); a cap > 0 only sizes the launch."""
+    own chunks from the device lengths; larger batches run as consecutive launches;
+    shapes without a self-planned path read the longest length from the device); a
+    cap > 0 raises the planning budget."""
     ws, wsb = _ws(workspace)
     check(lib().kvc_batched_paged_decode_split(_p(q), _p(k_pool), _p(v_pool), _p(table_all), _p(tab_off),
                                                _p(cur_len), _p(out), N, Hq, Hkv, D, BLOCK, cap, scale, dtype, split,
@@ -280,3 +282,17 @@ def decode_auto_split(N, Hq, Hkv, D, BLOCK, cap, dtype=KVC_F16) -> int:
 
 def flash_decode_workspace_size(H, D, num_splits) -> int:
     return int(lib().kvc_flash_decode_workspace_size(H, D, num_splits))
+
+
+def check_device_errors(stream=None) -> None:
+    """kvc_check_device_errors: synchronizes `stream`; raises KvcError (KVC_ERR_ARG)
+    when an earlier device-length decode launch on this device reported a sequence it
+    could not attend whole (its rows were written as NaN), and clears the report."""
+    check(lib().kvc_check_device_errors(stream))
+
+
+def stream_is_capturing(stream) -> bool:
+    import ctypes as C
+    flag = C.c_int(0)
+    check(lib().kvc_stream_is_capturing(stream, C.byref(flag)))
+    return bool(flag.value)

@@ -91,6 +91,9 @@ int main(int argc, char** argv) {
     const size_t ws_bytes = std::max<size_t>(kvc_decode_planned_workspace_size(Hq, Hkv, D, B, KVC_F16, cap_units), 256);
     void* ws;
     CK(kvc_malloc(&ws, ws_bytes));
+    // the fills and the table upload ran on the null stream, which the non-blocking
+    // compute and copy streams do not wait for: finish them before the first step
+    CK(kvc_device_synchronize());
     kvc_stream_t compute, copy;
     CK(kvc_stream_create(&compute));
     CK(kvc_stream_create(&copy));

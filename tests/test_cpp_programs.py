@@ -58,6 +58,12 @@ def test_paged_flash_device():
 
 
 @pytest.mark.gpu
+def test_dropin_device_position_causal_attention_in_and_out_of_capture():
+    r = run("test_dropin_causal")
+    assert r.returncode == 0 and "PASS" in r.stdout
+
+
+@pytest.mark.gpu
 def test_runner_planned_and_device_length_paths_agree():
     assert run("test_runner_paths").returncode == 0
 

@@ -14,6 +14,7 @@ import pytest
 
 from kvcache_amd import KVC_F16, KVC_F32, ops
 from kvcache_amd import workloads as W
+from kvcache_amd._native import KVC_ERR_ARG, KvcError
 from kvcache_amd.device import DeviceBuffer
 
 from _helpers import as_np, dev, host, normal, paged_layout, say, tol, tuning
@@ -152,6 +153,7 @@ def test_long_mean_context_within_the_stated_cap(orc):
     assert np.abs(got - oracle(orc, q, K, V, lens)).max() <= 2e-3
     unbounded = self_planned(q, kp, vp, table, tab_off, lens, Hkv, 16, KVC_F16, cap=0)
     assert np.all(np.isnan(unbounded))
+    expect_device_error()
 
 
 def test_explicit_split_past_cap_gives_nan_rows(orc):
@@ -169,6 +171,7 @@ def test_explicit_split_past_cap_gives_nan_rows(orc):
     assert np.all(np.isnan(got[1]))
     ref = oracle(orc, q, K, V, lens)
     assert np.abs(got[[0, 2]] - ref[[0, 2]]).max() <= 2e-3
+    expect_device_error(b"longer than its stated cap")
 
 
 def test_contiguous_length_past_its_cache_gives_nan():
@@ -179,6 +182,77 @@ def test_contiguous_length_past_its_cache_gives_nan():
     out = DeviceBuffer(q.nbytes)
     ops.launch_batched_decode(dev(q), dev(K), dev(V), dev(lens), out, 2, Hq, D, S, S, 0.125, Hkv=Hkv, dtype=KVC_F16)
     assert np.all(np.isnan(host(out, np.float16, q.shape).astype(np.float64)))
+    expect_device_error()
+
+
+def expect_device_error(text=b"NaN"):
+    """The launch that wrote NaN rows also reported it: kvc_check_device_errors returns
+    KVC_ERR_ARG once, then the report is cleared."""
+    from kvcache_amd._native import lib
+    with pytest.raises(KvcError) as e:
+        ops.check_device_errors()
+    assert e.value.status == KVC_ERR_ARG
+    assert text in lib().kvc_last_error()
+    ops.check_device_errors()
+
+
+def test_device_error_fails_the_next_device_length_call(orc):
+    """Without an explicit check, the next device-length decode call returns the report
+    (KVC_ERR_ARG, nothing launched) and clears it; the call after that runs normally."""
+    say("device error report surfaces at the next call")
+    lens = np.array([50, 500, 80], np.int32)
+    Hq, Hkv, D = 8, 8, 64
+    q, K, V = inputs(lens, Hq, Hkv, D, KVC_F16, 341)
+    kp, vp, table, tab_off = paged_layout(K, V, lens, 16)
+    args = (dev(q), dev(kp), dev(vp), dev(table), dev(tab_off), dev(lens))
+    out = DeviceBuffer(q.nbytes)
+    ops.launch_batched_paged(*args, out, 3, Hq, D, 16, 100, float(1.0 / np.sqrt(D)), dtype=KVC_F16, split=64)
+    host(out, np.float16, q.shape)  # the launch has finished: its report is in host memory
+    with pytest.raises(KvcError) as e:
+        ops.launch_batched_paged(*args, out, 3, Hq, D, 16, 0, float(1.0 / np.sqrt(D)), dtype=KVC_F16)
+    assert e.value.status == KVC_ERR_ARG
+    ops.launch_batched_paged(*args, out, 3, Hq, D, 16, 0, float(1.0 / np.sqrt(D)), dtype=KVC_F16)
+    got = host(out, np.float16, q.shape).astype(np.float64)
+    assert np.abs(got - oracle(orc, q, K, V, lens)).max() <= 2e-3
+    ops.check_device_errors()
+
+
+@pytest.mark.parametrize("case", ["gqa_mfma_600", "mha_valu_1100"])
+def test_dropin_batches_past_one_launch(orc, case):
+    """qk_batched_paged_decode_attn takes any N (a grid of N x Hq in the reference,
+    qwen_kernels.cu:326-334) and no cap: more sequences than one self-planned launch plans
+    (512 on the matrix cores, 1024 otherwise) run as consecutive launches, each attended
+    whole."""
+    rng = np.random.default_rng(370)
+    N, Hq, Hkv, D, hi = (600, 14, 2, 64, 700) if case == "gqa_mfma_600" else (1100, 2, 2, 64, 200)
+    say(f"drop-in batch of {N} sequences, {Hq}q/{Hkv}kv D{D}, cap 0")
+    lens = rng.integers(0, hi, N).astype(np.int32)
+    q, K, V = inputs(lens, Hq, Hkv, D, KVC_F16, 371)
+    kp, vp, table, tab_off = paged_layout(K, V, lens, 16)
+    out = DeviceBuffer(q.nbytes)
+    ops.qk_batched_paged_decode_attn(dev(q), out, dev(kp), dev(vp), dev(table), dev(tab_off), dev(lens), N, Hq, Hkv,
+                                     D, 16, float(1.0 / np.sqrt(D)))
+    got = host(out, np.float16, q.shape).astype(np.float64)
+    assert np.abs(got - oracle(orc, q, K, V, lens)).max() <= 2e-3
+    ops.check_device_errors()
+
+
+@pytest.mark.parametrize("B", [48, 4])
+def test_dropin_block_without_self_plan_needs_no_cap(orc, B):
+    """A BLOCK the self-planned kernel does not page (not a power of two, or smaller than a
+    wave-load) with cap 0: the longest length is read from the device and sizes the grid,
+    so every sequence is attended whole, as in the reference."""
+    say(f"drop-in BLOCK {B}, cap 0")
+    lens = np.array([1, 47, 48, 49, 1000, 3000, 0, 333], np.int32)
+    Hq, Hkv, D = 14, 2, 64
+    q, K, V = inputs(lens, Hq, Hkv, D, KVC_F16, 380 + B)
+    kp, vp, table, tab_off = paged_layout(K, V, lens, B)
+    out = DeviceBuffer(q.nbytes)
+    ops.qk_batched_paged_decode_attn(dev(q), out, dev(kp), dev(vp), dev(table), dev(tab_off), dev(lens), len(lens),
+                                     Hq, Hkv, D, B, float(1.0 / np.sqrt(D)))
+    got = host(out, np.float16, q.shape).astype(np.float64)
+    assert np.abs(got - oracle(orc, q, K, V, lens)).max() <= 2e-3
+    ops.check_device_errors()
 
 
 def test_device_position_variants(orc):

@@ -49,9 +49,16 @@ def test_noalloc_equals_workspace_entry_on_two_calls(orc):
 
 
 def test_noalloc_refuses_sizes_past_its_scratch():
+    """A call whose partials would not fit the static array is refused.  Every buffer is
+    real and large enough for the call, so even a refusal that came too late could not
+    make the kernel read outside them."""
     say("no-alloc prompt attention: oversized call refused")
     L = lib()
-    p = C.c_void_p(256)  # never dereferenced: the size check comes first
-    rc = L.kvc_paged_causal_attn_dev_noalloc(p, p, p, p, p, p, 300, Hq, Hkv, D, B, C.c_float(0.125), KVC_F16, None)
+    rng = np.random.default_rng(78)
+    q, kp, vp, table = _case(rng, 0, 300)
+    dq, dk, dv, dt, pos = dev(q), dev(kp), dev(vp), dev(table), dev(np.array([0], np.int32))
+    out = DeviceBuffer(q.nbytes)
+    rc = L.kvc_paged_causal_attn_dev_noalloc(dq.ptr, out.ptr, dk.ptr, dv.ptr, dt.ptr, pos.ptr, 300, Hq, Hkv, D, B,
+                                             C.c_float(0.125), KVC_F16, None)
     assert rc == KVC_ERR_UNSUPPORTED
     assert b"static scratch" in L.kvc_last_error()
