@@ -104,12 +104,14 @@ def set_tuning(key: str, value: int) -> None:
     check(lib().kvc_set_tuning(key.encode(), int(value)))
 
 
-def build_c2(lens, Hq, Hkv, D, B, rotate, seed, shuffle=True):
+def build_c2(lens, Hq, Hkv, D, B, rotate, seed, shuffle=True, dtype=None):
     from kvcache_amd import KVC_F16
     from kvcache_amd.device import DeviceBuffer, fill_normal
     from kvcache_amd.engine import BlockAllocator
     from kvcache_amd.workloads import build_tables
 
+    dtype = KVC_F16 if dtype is None else dtype
+    esz = 2 if dtype == KVC_F16 else 4
     nb = int(sum((int(x) + B - 1) // B for x in lens))
     alloc = BlockAllocator(nb)           # pool sized to actual use
     if shuffle:
@@ -119,15 +121,15 @@ def build_c2(lens, Hq, Hkv, D, B, rotate, seed, shuffle=True):
     elems = nb * Hkv * B * D
     pools = []
     for r in range(rotate):
-        k, v = DeviceBuffer(elems * 2), DeviceBuffer(elems * 2)
-        fill_normal(k, elems, KVC_F16, seed * 1000 + 2 * r + 1)
-        fill_normal(v, elems, KVC_F16, seed * 1000 + 2 * r + 2)
+        k, v = DeviceBuffer(elems * esz), DeviceBuffer(elems * esz)
+        fill_normal(k, elems, dtype, seed * 1000 + 2 * r + 1)
+        fill_normal(v, elems, dtype, seed * 1000 + 2 * r + 2)
         pools.append((k, v))
-    q = DeviceBuffer(N * Hq * D * 2)
-    fill_normal(q, N * Hq * D, KVC_F16, seed * 1000 + 999)
+    q = DeviceBuffer(N * Hq * D * esz)
+    fill_normal(q, N * Hq * D, dtype, seed * 1000 + 999)
     meta = dict(table=DeviceBuffer.from_numpy(table), tab_off=DeviceBuffer.from_numpy(tab_off),
-                lens=DeviceBuffer.from_numpy(np.asarray(lens, np.int32)), out=DeviceBuffer(N * Hq * D * 2))
-    return dict(nb=nb, table_host=table, tab_off_host=tab_off, pools=pools, q=q, **meta)
+                lens=DeviceBuffer.from_numpy(np.asarray(lens, np.int32)), out=DeviceBuffer(N * Hq * D * esz))
+    return dict(nb=nb, table_host=table, tab_off_host=tab_off, pools=pools, q=q, dtype=dtype, **meta)
 
 
 def alg_bytes(lens, Hq, Hkv, D, B, esz=2):
@@ -151,7 +153,7 @@ def time_decode(W, lens, Hq, Hkv, D, B, split, steps, warmup, stream=None, per_l
     def launch(i):
         k, v = W["pools"][i % len(W["pools"])]
         ops.launch_batched_paged(W["q"], k, v, W["table"], W["tab_off"], W["lens"], W["out"], N, Hq, D, B, cap,
-                                 scale, Hkv=Hkv, dtype=KVC_F16, split=split, stream=stream)
+                                 scale, Hkv=Hkv, dtype=W.get("dtype", KVC_F16), split=split, stream=stream)
 
     for i in range(warmup):
         launch(i)
@@ -201,6 +203,148 @@ def time_planned(W, lens, Hq, Hkv, D, B, steps, warmup, target=0, rotate=None):
     e1.record()
     synchronize()
     return e0.elapsed_ms(e1) / steps, nu, nr, launch
+
+
+def practical_ceiling(W, lens, Hq, Hkv, D, B, steps, warmup, target=0):
+    """The read-only probe (kvc_read_probe_planned) over the planned decode's own work list:
+    the same units in the same grid order, the same loads, the same rotating pools, and no
+    arithmetic.  Its time is the floor of the access pattern.  Returns (us per launch, units)."""
+    from kvcache_amd import KVC_F16, ops
+    from kvcache_amd._native import check, lib
+    from kvcache_amd.device import DeviceBuffer, Event, synchronize
+
+    dtype = W.get("dtype", KVC_F16)
+    work, nu, _ = ops.decode_plan(lens, Hq, Hkv, D, B, tab_off=W["tab_off_host"], table=W["table_host"],
+                                  dtype=dtype, target_tokens=target)
+    wdev = DeviceBuffer.from_numpy(work)
+    sink = DeviceBuffer(max(nu, 1) * 4)
+    tl = len(W["table_host"])
+
+    def launch(i):
+        k, v = W["pools"][i % len(W["pools"])]
+        check(lib().kvc_read_probe_planned(k.ptr, v.ptr, W["table"].ptr, tl, wdev.ptr, nu, Hq, Hkv, D, B, dtype,
+                                           sink.ptr, None))
+
+    for i in range(warmup):
+        launch(i)
+    synchronize()
+    e0, e1 = Event(), Event()
+    e0.record()
+    for i in range(steps):
+        launch(i)
+    e1.record()
+    synchronize()
+    return e0.elapsed_ms(e1) / steps * 1e3, nu
+
+
+def bench_c2_contiguous(steps, warmup, rotate):
+    """The reference's bench_throughput comparison (bench_throughput.cu:120-132): the config-2 batch
+    (reference lengths) as contiguous caches [N, H, LMAX=2048, D] (launch_batched_decode) and as the
+    paged pool (launch_batched_paged), both from device lengths, in fp16 (config 2) and in the
+    reference's fp32.  The reference publishes 1340 us contiguous / 1454 us paged in fp32 on its GPU
+    (README.md:76-77)."""
+    from kvcache_amd import KVC_F16, KVC_F32, ops
+    from kvcache_amd import workloads as Wl
+    from kvcache_amd.device import DeviceBuffer, Event, fill_normal, synchronize
+
+    lens = Wl.ref_lengths()
+    N, H, D, B, LMAX = 128, 8, 64, 16, 2048
+    scale = float(1.0 / np.sqrt(D))
+    res = {"workload": "C2 batch (reference lengths, N=128, H=8, D=64): contiguous [N,H,2048,D] caches vs the "
+                       "paged pool (BLOCK 16, shuffled free list), device-lengths path, rotating copies",
+           "reference_published_us": {"contiguous": 1340.0, "paged": 1454.0, "dtype": "f32",
+                                      "source": "README.md:76-77"}}
+    for dtype, name in ((KVC_F16, "f16"), (KVC_F32, "f32")):
+        esz = 2 if dtype == KVC_F16 else 4
+        _, total = alg_bytes(lens, H, H, D, B, esz)
+        W = build_c2(lens, H, H, D, B, rotate, seed=12345, dtype=dtype)
+        t_paged, _ = time_decode(W, lens, H, H, D, B, 0, steps, warmup)
+        del W["pools"]
+        elems = N * H * LMAX * D
+        caches = []
+        for r in range(rotate):
+            k, v = DeviceBuffer(elems * esz), DeviceBuffer(elems * esz)
+            fill_normal(k, elems, dtype, 4242 + 2 * r)
+            fill_normal(v, elems, dtype, 4243 + 2 * r)
+            caches.append((k, v))
+        cap = int(max(lens))
+
+        def launch(i):
+            k, v = caches[i % len(caches)]
+            ops.launch_batched_decode(W["q"], k, v, W["lens"], W["out"], N, H, D, LMAX, cap, scale, Hkv=H,
+                                      dtype=dtype)
+
+        for i in range(warmup):
+            launch(i)
+        synchronize()
+        e0, e1 = Event(), Event()
+        e0.record()
+        for i in range(steps):
+            launch(i)
+        e1.record()
+        synchronize()
+        t_contig = e0.elapsed_ms(e1) / steps
+        del caches
+        res[name] = {"contiguous_us": round(t_contig * 1e3, 3), "paged_us": round(t_paged * 1e3, 3),
+                     "paged_over_contiguous": round(t_paged / t_contig, 4),
+                     "contiguous_GBps": round(total / (t_contig * 1e-3) / 1e9, 1),
+                     "paged_GBps": round(total / (t_paged * 1e-3) / 1e9, 1), "algorithmic_bytes": total}
+    res["reference_paged_over_contiguous"] = round(1454.0 / 1340.0, 4)
+    return res
+
+
+def bench_single_seq(iters=300, warmup=30):
+    """The reference's single-sequence latency sweep (bench_paged.cu:40-108): H=8, D=64, fp32, one query,
+    S = 128 ... 4096, contiguous [H,S,D] (launch_decode) vs paged [NB,H,16,D] with the identity block table
+    (launch_paged); back-to-back launches between two events; the two outputs must agree bit for bit.
+    The reference publishes 21.9/27.2, 139.6/222.3 and 507.6/881.1 us at S = 128, 1024, 4096
+    (README.md:62-66) on its GPU."""
+    from kvcache_amd import KVC_F32, ops
+    from kvcache_amd.device import DeviceBuffer, Event, synchronize
+
+    H, D, B = 8, 64, 16
+    scale = float(1.0 / np.sqrt(D))
+    published = {128: (21.9, 27.2), 1024: (139.6, 222.3), 4096: (507.6, 881.1)}
+    rng = np.random.default_rng(64)
+    rows = []
+    for S in (128, 256, 512, 1024, 2048, 4096):
+        q = rng.standard_normal((H, D)).astype(np.float32)
+        K = rng.standard_normal((H, S, D)).astype(np.float32)
+        V = rng.standard_normal((H, S, D)).astype(np.float32)
+        nb = (S + B - 1) // B
+        kp = np.zeros((nb, H, B, D), np.float32)
+        vp = np.zeros_like(kp)
+        for b in range(nb):                      # identity table: logical block b is physical block b
+            t1 = min((b + 1) * B, S)
+            kp[b, :, : t1 - b * B] = K[:, b * B:t1]
+            vp[b, :, : t1 - b * B] = V[:, b * B:t1]
+        dq, dK, dV = (DeviceBuffer.from_numpy(x) for x in (q, K, V))
+        dkp, dvp = DeviceBuffer.from_numpy(kp), DeviceBuffer.from_numpy(vp)
+        dtab = DeviceBuffer.from_numpy(np.arange(nb, dtype=np.int32))
+        oc, op = DeviceBuffer(H * D * 4), DeviceBuffer(H * D * 4)
+        runs = {"contiguous": lambda: ops.launch_decode(dq, dK, dV, oc, S, H, D, S, scale, dtype=KVC_F32),
+                "paged": lambda: ops.launch_paged(dq, dkp, dvp, dtab, op, S, H, D, B, scale, dtype=KVC_F32)}
+        t = {}
+        for name, run in runs.items():
+            for _ in range(warmup):
+                run()
+            synchronize()
+            e0, e1 = Event(), Event()
+            e0.record()
+            for _ in range(iters):
+                run()
+            e1.record()
+            synchronize()
+            t[name] = e0.elapsed_ms(e1) / iters * 1e3
+        diff = float(np.abs(oc.to_numpy(np.float32, (H, D)) - op.to_numpy(np.float32, (H, D))).max())
+        row = {"S": S, "contiguous_us": round(t["contiguous"], 2), "paged_us": round(t["paged"], 2),
+               "paged_overhead_pct": round(100 * (t["paged"] / t["contiguous"] - 1), 1),
+               "max_abs_diff": diff}
+        if S in published:
+            row["reference_us"] = {"contiguous": published[S][0], "paged": published[S][1]}
+        rows.append(row)
+    return {"workload": "single sequence, H=8, D=64, fp32, one query; identity block table, BLOCK 16",
+            "rows": rows, "source": "bench_paged.cu:40-108, README.md:62-66"}
 
 
 def check_c2(W, lens, Hq, Hkv, D, B, split):
@@ -333,7 +477,10 @@ def c2_variant(lens, steps, warmup, rotate):
     kv, total = alg_bytes(lens, Hq, Hkv, D, B)
     t_self, _ = time_decode(W, lens, Hq, Hkv, D, B, 0, steps, warmup)
     t_plan, nu, _, launch = time_planned(W, lens, Hq, Hkv, D, B, steps, warmup)
+    t_probe, _ = practical_ceiling(W, lens, Hq, Hkv, D, B, steps, warmup)
     return {"sum_len": int(np.sum(lens)), "algorithmic_bytes": total, "parity_max_abs_err": err,
+            "practical_ceiling_us": round(t_probe, 3),
+            "practical_ceiling_frac": round(total / (t_probe * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "planned": {"us_per_step": round(t_plan * 1e3, 3), "GBps": round(total / (t_plan * 1e-3) / 1e9, 1),
                         "frac_hbm_peak": round(total / (t_plan * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "units": nu},
             "device_lengths_self_planned": {"us_per_step": round(t_self * 1e3, 3),
@@ -400,6 +547,18 @@ def bench_c3(steps, warmup, plan_sweep=()):
            "roofline": roofline_block(total, t * 1e3, "gqa_mfma_kernel<64, kPagedUniform, 4> + merge_kernel<f16, 64> "
                                       "(split 512; per step: both kernels and the gap between them)",
                                       ("c3_split512_split_kernel_mean_us", "c3_split512_merge_kernel_mean_us"))}
+    # the read-only probe over 512-token units of every (sequence, KV head): the same bytes in
+    # the split kernel's units (a host plan cut at 512 tokens)
+    set_tuning("mfma_min_chunk", 512)
+    try:
+        t_probe, nu_probe = practical_ceiling(W, lens, Hq, Hkv, D, B, steps, warmup, target=512)
+    finally:
+        set_tuning("mfma_min_chunk", 1024)
+    res["roofline"]["practical_ceiling_us"] = round(t_probe, 3)
+    res["roofline"]["practical_ceiling"] = {
+        "what": "kvc_read_probe_planned over 512-token units of every (sequence, KV head): the split kernel's "
+                "bytes and units, no arithmetic, one launch", "units": nu_probe, "us": round(t_probe, 3),
+        "frac": round(total / (t_probe * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
     t2, _ = time_decode(W, lens, Hq, Hkv, D, B, 1024, steps, warmup)
     res["split_1024"] = {"us_per_step": round(t2 * 1e3, 2), "GBps": round(total / (t2 * 1e-3) / 1e9, 1),
                          "frac_hbm_peak": round(total / (t2 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
@@ -467,8 +626,27 @@ def bench_c5(n_req=64, gen=64, seed=5, graph=False):
         out, st = m.serve(prompts, [gen] * n_req)
     finally:
         m.close()
+    # algorithmic bytes of the decode steps: each step reads every layer's weights and the (tied)
+    # lm_head once for the whole batch, and each running sequence's K/V once per layer; a
+    # sequence's decode step t = 1 .. gen-1 attends over its prompt + t keys
+    L, H, I, V, Hq, Hkv, Dh = cfg.layers, cfg.hidden, cfg.inter, cfg.vocab, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim
+    qkv = (Hq + 2 * Hkv) * Dh
+    layer_w = 2 * (H * qkv + qkv + Hq * Dh * H + H * 2 * I + I * H + 2 * H)
+    head_w = 2 * (V * H + H)
+    kv_keys = sum(len(p) * (gen - 1) + gen * (gen - 1) // 2 for p in prompts)
+    kv_bytes = kv_keys * L * 2 * Hkv * Dh * 2
+    step_bytes = st["steps"] * (L * layer_w + head_w) + kv_bytes
+    dec_s = st["decode_us"] * 1e-6
+    roof = {"bound": "hbm", "achieved": round(step_bytes / dec_s / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(step_bytes / dec_s / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "whole decode step: 24 x (q|k|v rows kernel, attention with fused append, o_proj, gate|up, "
+                      "down) + lm_head + argmax",
+            "algorithmic_bytes_per_step": round(step_bytes / max(st["steps"], 1)),
+            "weights_bytes_per_step": L * layer_w + head_w, "kv_bytes_all_steps": kv_bytes,
+            "floor_us_per_step": round(step_bytes / max(st["steps"], 1) / (HBM_PEAK_GBS * 1e9) * 1e6, 1)}
     return {"workload": f"C5 Qwen2-shaped decoder, {n_req} requests, prompts 16-256 tokens, {gen} generated each, "
                         "greedy, continuous batching width 32, random fp16 weights",
+            "roofline": roof,
             "graph_replay": bool(graph), "graph_steps": st["graph_steps"],
             "tokens": st["tokens"], "prompt_tokens": st["prompt_tokens"], "steps": st["steps"],
             "tokens_per_s": round(st["tokens"] / (st["wall_us"] * 1e-6), 1),
@@ -684,6 +862,8 @@ def main() -> int:
         print(json.dumps({"metric": METRIC, "error": f"planned parity failure: max abs err {err_planned}"}))
         return 1
     ms_per_step = t_launch
+    t_probe, _ = practical_ceiling(W, lens, Hq, Hkv, D, B, a.steps, a.warmup, target=a.plan_target)
+    log(f"C2 read-only probe over the same plan: {t_probe:.2f} us/launch")
     traffic, sym = measured_traffic()
     prof_us = profiled_launch_us()
     traffic_src = (f"rocprofv3 --pmc FETCH_SIZE x2.0 + WRITE_SIZE x1.0 per dispatch of {sym} "
@@ -719,6 +899,16 @@ def main() -> int:
             log(f"C2 log-uniform: {extras['c2_loguniform']}")
         except Exception as e:  # noqa: BLE001 -- extras never hide the headline
             extras["c2_loguniform"] = {"error": repr(e)}
+        try:
+            extras["c2_contiguous_vs_paged"] = bench_c2_contiguous(a.steps, a.warmup, a.rotate)
+            log(f"C2 contiguous vs paged: {extras['c2_contiguous_vs_paged']}")
+        except Exception as e:  # noqa: BLE001 -- extras never hide the headline
+            extras["c2_contiguous_vs_paged"] = {"error": repr(e)}
+        try:
+            extras["single_seq"] = bench_single_seq()
+            log(f"single sequence sweep: {extras['single_seq']}")
+        except Exception as e:  # noqa: BLE001
+            extras["single_seq"] = {"error": repr(e)}
         try:
             extras["c4_layer"] = bench_c4_layer(a.steps, a.warmup)
             log(f"C4 layer kernel: {extras['c4_layer']}")
@@ -772,6 +962,13 @@ def main() -> int:
                                "fused LSE merge)",
                      "algorithmic_bytes_per_launch": total, "kv_bytes_per_launch": kv,
                      "mean_launch_us": round(t_launch * 1e3, 3),
+                     "practical_ceiling_us": round(t_probe, 3),
+                     "practical_ceiling": {"what": "kvc_read_probe_planned: the same work list, grid order, loads "
+                                                   "and rotating pools, no arithmetic (the access pattern's floor)",
+                                           "us": round(t_probe, 3),
+                                           "GBps": round(total / (t_probe * 1e-6) / 1e9, 1),
+                                           "frac": round(total / (t_probe * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                                           "decode_over_probe": round(t_launch * 1e3 / t_probe, 4)},
                      "profile": ({"file": str(STATS_SUMMARY.relative_to(ROOT)), "mean_launch_us": prof_us,
                                   "frac": round(total / (prof_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                                   "note": "rocprofv3 kernel trace of the default command on an earlier box; "

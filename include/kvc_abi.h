@@ -108,6 +108,17 @@ int kvc_event_elapsed_ms(float* ms, void* start, void* stop); /* synchronizes on
  * qwen_infer.cu:135-214).  Only graph-safe entry points may be captured: those that
  * allocate nothing and take per-step counts from device memory (the *_dev and
  * dev_rows forms below). */
+/* No counterpart in the reference; a measurement aid for the practical ceiling of the
+ * decode's access pattern.  Reads the K/V bytes that kvc_batched_paged_decode_planned
+ * reads for the same work list (kvc_decode_plan for Hq/Hkv/D/BLOCK/dtype), unit by unit in
+ * the same grid order, with the same 16-byte-per-lane loads and buffer descriptors, and
+ * computes nothing from them (sink: n_units ints, written only in the unlikely event
+ * that a unit's xor of its bytes equals a fixed constant).  The chunks of the plan must
+ * span at most 64 blocks (every plan of the one/two-head shapes does); BLOCK must hold a
+ * power-of-two number of 1 KiB loads per KV head. */
+int kvc_read_probe_planned(const void* k_pool, const void* v_pool, const int* table_all, int table_len,
+                           const int* work, int n_units, int Hq, int Hkv, int D, int BLOCK, int dtype, int* sink,
+                           kvc_stream_t stream);
 /* 1 in *capturing when `stream` is being captured into a graph (0 for the null stream). */
 int kvc_stream_is_capturing(kvc_stream_t stream, int* capturing);
 /* Device-side failure reports.  A device-length decode launch that cannot attend a

@@ -930,6 +930,29 @@ int kvc_event_create(void** ev) {
     *ev = e;
     return rc;
 }
+int kvc_read_probe_planned(const void* k_pool, const void* v_pool, const int* table_all, int table_len,
+                           const int* work, int n_units, int Hq, int Hkv, int D, int BLOCK, int dtype, int* sink,
+                           kvc_stream_t st) {
+    return guarded([&]() -> int {
+        if (n_units < 0 || table_len < 0) return set_error(KVC_ERR_ARG, "n_units and table_len must be >= 0");
+        if (n_units == 0) return KVC_OK;
+        if (!k_pool || !v_pool || !table_all || !work || !sink) return set_error(KVC_ERR_ARG, "null pointer");
+        if (Hq <= 0 || Hkv <= 0 || Hq % Hkv || BLOCK <= 0 || !d_ok(D) || !dtype_ok(dtype))
+            return set_error(KVC_ERR_ARG, "bad shape");
+        const PlanShape ps = plan_shape(Hq, Hkv, D, BLOCK, dtype);
+        const int row = D * esize(dtype);
+        const int tpw = 1024 / row;
+        const int lpb = BLOCK % tpw == 0 ? ilog2_exact(BLOCK / tpw) : -1;
+        if (row > 1024 || lpb < 0 || ilog2_exact(tpw) < 0)
+            return set_error(KVC_ERR_UNSUPPORTED, "the read probe needs blocks of a power-of-two number of 1 KiB loads");
+        if (!aligned16(k_pool) || !aligned16(v_pool)) return set_error(KVC_ERR_ARG, "pools must be 16-byte aligned");
+        ProbeParams p{};
+        p.k = k_pool; p.v = v_pool; p.table_all = table_all; p.table_len = table_len;
+        p.Hkv = Hkv; p.block = BLOCK; p.nsub = ps.mfma ? 1 : ps.nsub;
+        p.row_bytes = row; p.tpw_shift = ilog2_exact(tpw); p.lpb_shift = lpb; p.sink = sink;
+        return launch_read_probe(p, work, ps.entry_ints, n_units, S(st));
+    });
+}
 int kvc_stream_is_capturing(kvc_stream_t st, int* capturing) {
     if (!capturing) return set_error(KVC_ERR_ARG, "null out pointer");
     *capturing = 0;

@@ -197,4 +197,18 @@ int launch_write(const WriteParams& p, int dtype, hipStream_t stream);
 // Deterministic N(0,1) fill (Box-Muller over a counter hash), fp32 or fp16.
 int launch_fill_normal(void* dst, size_t n, int dtype, uint64_t seed, float stddev, hipStream_t stream);
 
+// Read-only pass over the K/V bytes of a planned decode work list (probe.hip).
+struct ProbeParams {
+    const void* k;
+    const void* v;
+    const int* table_all;
+    int table_len;
+    int Hkv, block, nsub;
+    int row_bytes;    // D * element size (at most 1024)
+    int tpw_shift;    // log2(rows per 1 KiB wave-load)
+    int lpb_shift;    // log2(wave-loads per block)
+    int* sink;        // [n_units]; written only when a unit's xor equals a fixed value
+};
+int launch_read_probe(const ProbeParams& p, const int* work, int work_ints, int n_units, hipStream_t stream);
+
 }  // namespace kvc

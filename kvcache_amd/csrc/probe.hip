@@ -1,0 +1,95 @@
+// probe.hip -- a read-only pass over exactly the K/V bytes a planned decode reads.
+//
+// Measurement aid (no counterpart in the reference).  The kernel takes the planned
+// decode's own work list (kvc_decode_plan) and, unit by unit in the same grid order,
+// streams each unit's K and V tiles with the decode kernel's loads -- 16 bytes per lane,
+// one wave-load = the rows one 1 KiB load covers, dealt round-robin to 4 waves, two
+// batches of 4 wave-loads in flight per wave, rows past the chunk cut off by the
+// buffer descriptor -- and does nothing with them but fold them into an xor that is
+// stored only when it equals a fixed constant (so the loads stay; random inputs almost
+// never produce it, and the store costs nothing otherwise).  Its time is the floor of the
+// access pattern alone (no scores, no softmax, no partials), so
+// decode time / probe time says how much of a launch is spent beyond moving its bytes.
+#include "internal.hpp"
+#include "kvc_abi.h"
+
+namespace kvc {
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+constexpr int kProbeWaves = 4;
+constexpr int kProbeU = 4;
+constexpr int kProbeMagic = 0x5eed1e55;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t probe_rsrc(const void* base, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
+
+__global__ __launch_bounds__(kProbeWaves * 64) void read_probe_kernel(const int* __restrict__ work, int work_ints,
+                                                                      ProbeParams p) {
+    const int* w = work + (size_t)blockIdx.x * work_ints;
+    const int s = __builtin_amdgcn_readfirstlane(w[0]);
+    const int hks = __builtin_amdgcn_readfirstlane(w[1]) & 0xFFFF;
+    const int j0 = __builtin_amdgcn_readfirstlane(w[2]);
+    const int j1 = __builtin_amdgcn_readfirstlane(w[3]);
+    const int tab = __builtin_amdgcn_readfirstlane(w[7]);
+    // head subgroups of one KV head read the same bytes: the first subgroup reads them
+    if (s < 0 || hks % p.nsub != 0 || hks / p.nsub >= p.Hkv || j1 <= j0 || tab < 0) return;
+    const int hk = hks / p.nsub;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int row = p.row_bytes, tsh = p.tpw_shift, tpw = 1 << tsh;  // rows per 1 KiB wave-load
+    const int nwl = (j1 - j0 + tpw - 1) >> tsh;
+    const int kmax = wave < nwl ? (nwl - wave + kProbeWaves - 1) >> 2 : 0;
+    static_assert(kProbeWaves == 4, "kmax uses a shift by 2");
+    // the chunk's block ids, one per lane, through a descriptor bounded by the table
+    const int tbl = (int)__builtin_amdgcn_raw_buffer_load_b32(probe_rsrc(p.table_all, p.table_len * 4),
+                                                              (tab + lane) * 4, 0, 0);
+    const char* kb = static_cast<const char*>(p.k);
+    const char* vb = static_cast<const char*>(p.v);
+    u32x4 acc = {0u, 0u, 0u, 0u};
+    u32x4 ka[kProbeU], va[kProbeU], kb2[kProbeU], vb2[kProbeU];
+    auto issue = [&](int k0, u32x4 (&K)[kProbeU], u32x4 (&V)[kProbeU]) {
+#pragma unroll
+        for (int u = 0; u < kProbeU; ++u) {
+            const int i = wave + kProbeWaves * (k0 + u);
+            const int t0 = j0 + (i << tsh);
+            int rows = max(j1 - t0, 0);
+            asm("" : "+s"(rows));
+            rows = min(rows, tpw);
+            const int rel = min(i >> p.lpb_shift, 63);
+            const int phys = __builtin_amdgcn_readlane(tbl, rel);
+            const int in = (i & ((1 << p.lpb_shift) - 1)) << tsh;
+            const size_t tile = ((size_t)(phys * p.Hkv + hk) * p.block + in) * row;
+            K[u] = __builtin_amdgcn_raw_buffer_load_b128(probe_rsrc(kb + tile, rows * row), lane * 16, 0, 0);
+            V[u] = __builtin_amdgcn_raw_buffer_load_b128(probe_rsrc(vb + tile, rows * row), lane * 16, 0, 0);
+        }
+    };
+    auto consume = [&](const u32x4 (&K)[kProbeU], const u32x4 (&V)[kProbeU]) {
+#pragma unroll
+        for (int u = 0; u < kProbeU; ++u) acc ^= K[u] ^ V[u];
+    };
+    if (kmax > 0) {
+        issue(0, ka, va);
+        for (int k = 0;; k += 2 * kProbeU) {
+            issue(k + kProbeU, kb2, vb2);
+            consume(ka, va);
+            if (k + kProbeU >= kmax) break;
+            issue(k + 2 * kProbeU, ka, va);
+            consume(kb2, vb2);
+            if (k + 2 * kProbeU >= kmax) break;
+        }
+    }
+    const unsigned x = acc.x ^ acc.y ^ acc.z ^ acc.w;
+    if (x == (unsigned)kProbeMagic) p.sink[blockIdx.x] = (int)x;  // keeps the loads; (almost) never taken
+}
+
+}  // namespace
+
+int launch_read_probe(const ProbeParams& p, const int* work, int work_ints, int n_units, hipStream_t st) {
+    if (n_units <= 0) return KVC_OK;
+    hipLaunchKernelGGL(read_probe_kernel, dim3((unsigned)n_units), dim3(kProbeWaves * 64), 0, st, work, work_ints, p);
+    return hip_check(hipGetLastError(), "read probe launch");
+}
+
+}  // namespace kvc
