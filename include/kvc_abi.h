@@ -529,6 +529,14 @@ int  kvc_engine_add_request(kvc_engine* e, int prompt_len, int max_new_tokens, d
 int  kvc_engine_step(kvc_engine* e, int* more);
 int  kvc_engine_run(kvc_engine* e, kvc_engine_stats* out);
 int  kvc_engine_stats_get(const kvc_engine* e, kvc_engine_stats* out);
+/* No counterpart in the reference: what the last decode step ran, for checking it from
+ * outside.  n = its batch; lens[n], tab_off[n+1] and table[] (table_cap ints at least)
+ * are the packed metadata it uploaded (model_runner.h:61-69 order); wpos/slots (may be
+ * NULL) each row's write position and pool slot (-1: none); dev[6] = the runner's
+ * q [L][max_batch][Hq][D], new K and V [L][max_batch][Hkv][D] and out [max_batch][Hq][D]
+ * (the last layer's) buffers and the K and V pools [L][num_blocks][Hkv][BLOCK][D]. */
+int  kvc_engine_last_step(const kvc_engine* e, int* n, int* lens, int* tab_off, int* table, int table_cap,
+                          int* wpos, int* slots, void** dev);
 /* run_static (scheduler.h:33-89) over the engine's pool and runner. */
 int  kvc_run_static(kvc_engine* e, const kvc_request* reqs, int n, int max_batch, kvc_engine_stats* out);
 

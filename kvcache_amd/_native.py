@@ -184,6 +184,7 @@ _SIGS = {
     "kvc_engine_step": (i32, [vp, ip]),
     "kvc_engine_run": (i32, [vp, C.POINTER(EngineStatsC)]),
     "kvc_engine_stats_get": (i32, [vp, C.POINTER(EngineStatsC)]),
+    "kvc_engine_last_step": (i32, [vp, ip, ip, ip, ip, i32, ip, ip, C.POINTER(vp)]),
     "kvc_run_static": (i32, [vp, C.POINTER(RequestC), i32, i32, C.POINTER(EngineStatsC)]),
 }
 

@@ -140,6 +140,32 @@ int kvc_engine_run(kvc_engine* e, kvc_engine_stats* out) {
         return KVC_OK;
     });
 }
+int kvc_engine_last_step(const kvc_engine* e, int* n, int* lens, int* tab_off, int* table, int table_cap,
+                         int* wpos, int* slots, void** dev) {
+    if (!e || !n) return kvc::set_error(KVC_ERR_ARG, "null engine / out pointer");
+    return guard([&]() -> int {
+        const ModelRunner& r = e->e.runner;
+        const int m = (int)r.h_len.size();
+        *n = m;
+        if (m == 0) return KVC_OK;
+        const int T = (int)r.h_tab.size();
+        if (!lens || !tab_off || !table || !dev) return kvc::set_error(KVC_ERR_ARG, "null output array");
+        if (table_cap < T) return kvc::set_error(KVC_ERR_ARG, "table_cap < " + std::to_string(T));
+        std::copy(r.h_len.begin(), r.h_len.end(), lens);
+        std::copy(r.h_off.begin(), r.h_off.end(), tab_off);
+        std::copy(r.h_tab.begin(), r.h_tab.end(), table);
+        if (wpos && slots) {
+            for (int i = 0; i < m; ++i) {
+                wpos[i] = i < (int)r.h_wpos.size() ? r.h_wpos[i] : -1;
+                slots[i] = i < (int)r.h_slot.size() ? r.h_slot[i] : -1;
+            }
+        }
+        const KVCacheManager& kvm = e->e.kvm;
+        dev[0] = r.dq; dev[1] = r.dk; dev[2] = r.dv; dev[3] = r.dout;
+        dev[4] = kvm.k_layer(0); dev[5] = kvm.v_layer(0);
+        return KVC_OK;
+    });
+}
 int kvc_engine_stats_get(const kvc_engine* e, kvc_engine_stats* out) {
     if (!e || !out) return kvc::set_error(KVC_ERR_ARG, "null engine / out pointer");
     to_c(e->e.stats, out);

@@ -140,6 +140,27 @@ class Engine:
         check(lib().kvc_engine_run(self._h, C.byref(s)))
         return EngineStats.from_c("continuous", s)
 
+    def last_step(self) -> dict:
+        """The last decode step's batch (kvc_engine_last_step): lens, tab_off, table, wpos,
+        slots (host arrays) and the device addresses of the runner's q / new K / new V /
+        out buffers and of the K / V pools."""
+        import numpy as np
+        n = C.c_int(0)
+        cap = 1 << 16
+        lens, off = np.zeros(cap, np.int32), np.zeros(cap + 1, np.int32)
+        table, wpos, slots = np.zeros(cap, np.int32), np.zeros(cap, np.int32), np.zeros(cap, np.int32)
+        dev = (C.c_void_p * 6)()
+        check(lib().kvc_engine_last_step(self._h, C.byref(n), lens.ctypes.data_as(C.POINTER(C.c_int)),
+                                         off.ctypes.data_as(C.POINTER(C.c_int)),
+                                         table.ctypes.data_as(C.POINTER(C.c_int)), cap,
+                                         wpos.ctypes.data_as(C.POINTER(C.c_int)),
+                                         slots.ctypes.data_as(C.POINTER(C.c_int)), dev))
+        m = n.value
+        T = int(off[m]) if m else 0
+        return {"n": m, "lens": lens[:m].copy(), "tab_off": off[:m + 1].copy(), "table": table[:T].copy(),
+                "wpos": wpos[:m].copy(), "slots": slots[:m].copy(),
+                "dev": {k: dev[i] for i, k in enumerate(["q", "k_new", "v_new", "out", "k_pool", "v_pool"])}}
+
     def stats(self) -> EngineStats:
         s = EngineStatsC()
         check(lib().kvc_engine_stats_get(self._h, C.byref(s)))
