@@ -54,23 +54,31 @@ def measured_traffic():
 
 
 STATS_SUMMARY = ROOT / "profiles" / "split_kernel_planned_c2_stats.txt"
+PROFILES = ROOT / "profiles"
 
 
-def profile_values():
-    """The `key: number` lines of the committed rocprofv3 kernel-trace summary of the
-    default command (mean kernel durations in us of each workload's timed dispatches)."""
-    vals = {}
-    try:
-        for line in STATS_SUMMARY.read_text().splitlines():
+def profile_sources():
+    """key -> (value, file) for the `key: number` lines of the committed rocprofv3
+    summaries under profiles/ (mean kernel durations in us of each workload's timed
+    dispatches; each summary names the command that made it)."""
+    out = {}
+    for f in sorted(PROFILES.glob("*.txt")):
+        try:
+            text = f.read_text()
+        except OSError:
+            continue
+        for line in text.splitlines():
             k, sep, v = line.partition(":")
             if sep and k and not k.startswith((" ", "#")) and " " not in k:
                 try:
-                    vals[k] = float(v)
+                    out[k] = (float(v), f)
                 except ValueError:
                     pass
-    except OSError:
-        pass
-    return vals
+    return out
+
+
+def profile_values():
+    return {k: v for k, (v, _) in profile_sources().items()}
 
 
 def profiled_launch_us():
@@ -86,10 +94,10 @@ def roofline_block(alg_bytes, us, kernel, profile_keys=()):
     gbs = alg_bytes / (us * 1e-6) / 1e9
     out = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
            "frac": round(gbs / HBM_PEAK_GBS, 4), "kernel": kernel, "algorithmic_bytes_per_launch": alg_bytes}
-    pv = profile_values()
-    if profile_keys and all(k in pv for k in profile_keys):
-        kus = sum(pv[k] for k in profile_keys)
-        out["profile"] = {"file": str(STATS_SUMMARY.relative_to(ROOT)), "kernel_us": round(kus, 3),
+    src = profile_sources()
+    if profile_keys and all(k in src for k in profile_keys):
+        kus = sum(src[k][0] for k in profile_keys)
+        out["profile"] = {"file": str(src[profile_keys[0]][1].relative_to(ROOT)), "kernel_us": round(kus, 3),
                           "keys": list(profile_keys),
                           "frac": round(alg_bytes / (kus * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
     return out
@@ -754,6 +762,75 @@ def copy_calibration(mib: int) -> int:
     return 0
 
 
+def summarize_rocprof(root: Path, patterns) -> None:
+    """Summary of rocprofv3 CSV output (what profiles/*.txt hold): the kernel stats table;
+    for kernels whose name contains one of `patterns`, the runs of consecutive dispatches
+    (dispatch-id gaps of at most 8) with their mean duration and the mean of their last
+    50 dispatches (a timed loop's); for --pmc output, each counter's mean per dispatch
+    over the same runs."""
+    import csv
+    import glob
+    import re
+    from collections import defaultdict
+
+    def short(name):
+        n = re.sub(r"_ZN3kvc12_GLOBAL__N_112split_kernelIDF16_Li(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)EEEvPKiiNS_12DecodeParamsE",
+                   r"split_kernel<f16, D\1, G\2, mode\3, WPB\4, U\5>", name)
+        n = re.sub(r"_ZN3kvc12_GLOBAL__N_115gqa_mfma_kernelILi(\d+)ELi(\d+)ELi(\d+)EEEvPKiiNS_12DecodeParamsE",
+                   r"gqa_mfma_kernel<D\1, mode\2, WPB\3>", n)
+        n = re.sub(r"_ZN3kvc12_GLOBAL__N_112merge_kernelIDF16_Li(\d+)EEEvNS_12DecodeParamsE", r"merge_kernel<f16, D\1>", n)
+        n = re.sub(r"_ZN3kvc12_GLOBAL__N_117read_probe_kernelEPKiiNS_11ProbeParamsE", "read_probe_kernel", n)
+        return n[:72]
+
+    def runs_of(rows):
+        rows.sort()
+        out, cur = [], [rows[0]]
+        for r in rows[1:]:
+            if r[0] - cur[-1][0] > 8:
+                out.append(cur)
+                cur = []
+            cur.append(r)
+        out.append(cur)
+        return out
+
+    for f in sorted(glob.glob(str(root / "**" / "*kernel_stats.csv"), recursive=True)):
+        rows = sorted(csv.DictReader(open(f)), key=lambda r: -float(r["TotalDurationNs"]))
+        print(f"# {Path(f).name}: kernels by total time")
+        print(f"{'kernel':72s} {'calls':>8s} {'avg_us':>9s} {'min_us':>9s} {'max_us':>9s} {'pct':>6s}")
+        for r in rows[:24]:
+            print(f"{short(r['Name']):72s} {int(r['Calls']):8d} {float(r['AverageNs']) / 1e3:9.3f} "
+                  f"{float(r['MinNs']) / 1e3:9.3f} {float(r['MaxNs']) / 1e3:9.3f} {float(r['Percentage']):6.2f}")
+    for f in sorted(glob.glob(str(root / "**" / "*kernel_trace.csv"), recursive=True)):
+        by = defaultdict(list)
+        with open(f) as fh:
+            for r in csv.DictReader(fh):
+                if any(pt in r["Kernel_Name"] for pt in patterns):
+                    by[r["Kernel_Name"]].append((int(r["Dispatch_Id"]), int(r["Start_Timestamp"]),
+                                                 int(r["End_Timestamp"])))
+        print(f"# {Path(f).name}: runs of consecutive dispatches (us)")
+        for name, rows in sorted(by.items(), key=lambda kv: min(x[0] for x in kv[1])):
+            print(short(name))
+            for i, run in enumerate(runs_of(rows)):
+                dur = [(e - s) / 1e3 for _, s, e in run]
+                last = dur[-50:]
+                print(f"  run {i:3d} dispatches {run[0][0]:>8d}-{run[-1][0]:<8d} n={len(run):6d} "
+                      f"mean {sum(dur) / len(dur):9.3f} last50 {sum(last) / len(last):9.3f}")
+    for f in sorted(glob.glob(str(root / "**" / "*counter_collection.csv"), recursive=True)):
+        by = defaultdict(lambda: defaultdict(list))
+        with open(f) as fh:
+            for r in csv.DictReader(fh):
+                if any(pt in r["Kernel_Name"] for pt in patterns):
+                    by[r["Kernel_Name"]][r["Counter_Name"]].append((int(r["Dispatch_Id"]), float(r["Counter_Value"])))
+        print(f"# {Path(f).name}: counters per dispatch")
+        for name, ctrs in by.items():
+            print(short(name))
+            for c, rows in ctrs.items():
+                for i, run in enumerate(runs_of([(d, v, 0) for d, v in rows])):
+                    vals = [v for _, v, _ in run][-50:]
+                    print(f"  {c:22s} run {i:3d} n={len(run):5d} last50 mean {sum(vals) / len(vals):14.1f} "
+                          f"min {min(vals):14.1f} max {max(vals):14.1f}")
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -775,8 +852,13 @@ def main() -> int:
     ap.add_argument("--plan-sweep", type=str, default="", help="comma list of planned targets to time")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="only run 10 device-to-device copies of MIB MiB (HBM counter calibration) and exit")
-    ap.add_argument("--only", choices=["c3", "c4", "c5", "prefill"], default=None,
-                    help="run only config 3 or config 4 and print its result (profiling)")
+    ap.add_argument("--only", choices=["c3", "c4", "c4_layer", "c5", "prefill"], default=None,
+                    help="run only one extra workload and print its result (profiling)")
+    ap.add_argument("--summarize-rocprof", metavar="DIR", default=None,
+                    help="print a summary of the rocprofv3 CSV output under DIR (kernel stats, runs of "
+                         "consecutive dispatches per kernel, --pmc counter means) and exit")
+    ap.add_argument("--kernels", default="split_kernel,gqa_mfma_kernel,merge_kernel,read_probe_kernel",
+                    help="with --summarize-rocprof: comma list of kernel-name substrings whose runs are listed")
     ap.add_argument("--warm", action="store_true",
                     help="also time the planned path on one pool copy (Infinity-Cache resident)")
     ap.add_argument("--graph", action="store_true",
@@ -786,6 +868,9 @@ def main() -> int:
     ap.add_argument("--fused", type=int, default=-1,
                     help="merge mode: -1 automatic, 0 merge kernel, 1 fused with fences, 2 fused coherent")
     a = ap.parse_args()
+    if a.summarize_rocprof:  # host-only: reads rocprofv3's CSV files
+        summarize_rocprof(Path(a.summarize_rocprof), [k for k in a.kernels.split(",") if k])
+        return 0
     if a.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {a.gpus} is not supported (the path shards by "
               "sequence with no exchange, so a single GPU's share at its real shape is what is measured)",
@@ -811,6 +896,7 @@ def main() -> int:
     if a.only:
         res = (bench_c3(a.steps, a.warmup, sweep_targets) if a.only == "c3" else
                bench_prefill(a.steps, a.warmup) if a.only == "prefill" else
+               bench_c4_layer(a.steps, a.warmup) if a.only == "c4_layer" else
                bench_c5(graph=a.graph) if a.only == "c5" else bench_c4(graph=a.graph))
         print(json.dumps(res), flush=True)
         return 0
@@ -971,8 +1057,11 @@ def main() -> int:
                                            "decode_over_probe": round(t_launch * 1e3 / t_probe, 4)},
                      "profile": ({"file": str(STATS_SUMMARY.relative_to(ROOT)), "mean_launch_us": prof_us,
                                   "frac": round(total / (prof_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-                                  "note": "rocprofv3 kernel trace of the default command on an earlier box; "
-                                          "achieved/frac above come from this run's HIP events"}
+                                  "note": "rocprofv3 kernel trace of the headline command (bench.py --no-extras "
+                                          "--no-cpu-baseline) on an earlier box; achieved/frac above come from "
+                                          "this run's HIP events",
+                                  "across_boxes_us": "33.2-34.4 (HIP events of the planned step on the boxes "
+                                                     "measured; the profile is one of them)"}
                                  if prof_us else None)},
         "warm_GBps": warm,
         "memory": memory_accounting(lens, Hkv, D, B),
