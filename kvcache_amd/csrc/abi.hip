@@ -788,6 +788,11 @@ int run_self_planned(const void* q, const void* k, const void* v, const int* tab
         p.sp_pf_min_len = std::max(tuning().self_prefetch_min_len, 1);
         p.sp_pf_xcd = tuning().self_prefetch_xcd != 0 && ps.nsub == 1 && Hkv % 8 == 0;
     }
+    // short sequences attended while the kernel plans the others (VALU decodes whose
+    // table offsets, if paged, are given; at most the largest chunk: a chunk's block
+    // ids are one per lane)
+    if (!ps.mfma && cur_len && (contig || tab_off) && tuning().self_lead_tokens > 0)
+        p.sp_lead = std::min(tuning().self_lead_tokens, ps.max_chunk);
     const size_t rall = (size_t)recs;
     const size_t acc = align_up(rall * ps.G * D * sizeof(float), kAlign), ml = align_up(rall * ps.G * 2 * sizeof(float), kAlign);
     p.part_acc = static_cast<float*>(ws);
@@ -1400,6 +1405,7 @@ int kvc_set_tuning(const char* key, int value) {
     else if (k == "self_prefetch_kib" && value >= 0) tuning().self_prefetch_kib = value;
     else if (k == "self_prefetch_min_len" && value >= 0) tuning().self_prefetch_min_len = value;
     else if (k == "self_prefetch_xcd" && (value == 0 || value == 1)) tuning().self_prefetch_xcd = value;
+    else if (k == "self_lead_tokens" && value >= 0) tuning().self_lead_tokens = value;
     else return set_error(KVC_ERR_ARG, "unknown tuning key or bad value: " + k);
     return KVC_OK;
 }
@@ -1422,6 +1428,7 @@ int kvc_get_tuning(const char* key, int* value) {
     else if (k == "self_prefetch_kib") *value = tuning().self_prefetch_kib;
     else if (k == "self_prefetch_min_len") *value = tuning().self_prefetch_min_len;
     else if (k == "self_prefetch_xcd") *value = tuning().self_prefetch_xcd;
+    else if (k == "self_lead_tokens") *value = tuning().self_lead_tokens;
     else return set_error(KVC_ERR_ARG, "unknown tuning key: " + k);
     return KVC_OK;
 }

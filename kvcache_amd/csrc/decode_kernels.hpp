@@ -472,14 +472,23 @@ __global__ __launch_bounds__(WPB * kWave) void split_kernel(const int* __restric
     __shared__ float s_acc[WPB][G][D];
     __shared__ float s_m[WPB][G], s_l[WPB][G];
     __shared__ int s_tab[PER_LANE ? kMaxChunkBlocks : 1];
-    __shared__ std::conditional_t<SELF, SelfPlanLds<kSelfMaxNValu, WPB>, char> s_plan;
+    __shared__ std::conditional_t<SELF, SelfPlanLds<kSelfMaxNValu, WPB, true>, char> s_plan;
+    // self-planned short sequences: the partials of waves 1 .. WPB-1, kept until lead_finish
+    constexpr int LW = SELF ? WPB - 1 : 1;
+    __shared__ float s_lacc[LW][G][D];
+    __shared__ float s_lm[LW][G], s_ll[LW][G];
 
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = uniform(threadIdx.x >> 6);
 
     // One unit, given its entry header (hdr) and, on the host-planned path, the
-    // entry's block ids (ev: one int per lane after the 8-int header).
-    auto run_unit = [&](const int (&hdr)[8], const int ev) {
+    // entry's block ids (ev: one int per lane after the 8-int header).  LEAD: a short
+    // sequence of a self-planned launch, whole, on waves 1 .. WPB-1 while wave 0 plans
+    // (hdr = {sequence, head subgroup, length, first table entry}); its partials stay
+    // in LDS (s_lacc) for lead_finish.
+    auto body = [&](auto lead_tag, const int (&hdr)[8], const int ev) {
+    constexpr bool LEAD = decltype(lead_tag)::value;
+    constexpr int NW = LEAD ? WPB - 1 : WPB;  // waves that share the unit's wave-loads
     // self-planned (persistent) launches: the parameters and per-lane indices are
     // derived anew in every unit, not hoisted out of the loop and held across it
     const DecodeParams p = SELF ? fresh_params() : p_arg;
@@ -488,8 +497,19 @@ __global__ __launch_bounds__(WPB * kWave) void split_kernel(const int* __restric
     const int lane = tid_u & (kWave - 1);
     const int tslot = lane / LPT;
     const int dl = lane % LPT;
+    const int wv = LEAD ? wave - 1 : wave;
     Unit u;
-    if (!load_unit<PLANNED, !CONTIG>(p, hdr, G, u)) {
+    if constexpr (LEAD) {
+        u.s = hdr[0];
+        u.hk = hdr[1] / p.nsub;
+        u.sub = hdr[1] - u.hk * p.nsub;
+        u.c = 0;
+        u.nc = 1;
+        u.j0 = 0;
+        u.j1 = min(max(hdr[2], 0), p.cap);  // (a length past the cap fails the plan: NaN rows)
+        u.tab_start = hdr[3];
+        u.rec0 = u.cstride = u.ctr_idx = 0;
+    } else if (!load_unit<PLANNED, !CONTIG>(p, hdr, G, u)) {
         if (u.over_cap) nan_rows<T, D, WPB * kWave>(p, u.s, u.hk * p.group + u.sub * G, G);
         return;
     }
@@ -499,7 +519,7 @@ __global__ __launch_bounds__(WPB * kWave) void split_kernel(const int* __restric
     const size_t rec0 = u.rec0, cstride = u.cstride, ctr_idx = u.ctr_idx;
     const int hq0 = hk * p.group + sub * G;
     const int nwl = (j1 - j0 + TPW - 1) / TPW;                          // wave-loads in the chunk
-    const int kmax = wave < nwl ? (nwl - wave + WPB - 1) / WPB : 0;     // this wave's share
+    const int kmax = wv < nwl ? (nwl - wv + NW - 1) / NW : 0;           // this wave's share
 
     u32x4 qv[G];
     {
@@ -525,7 +545,7 @@ __global__ __launch_bounds__(WPB * kWave) void split_kernel(const int* __restric
     // when the chunk holds its position (loads issued without waiting for wpos)
     int wp = -1;
     u32x4 knew = {0, 0, 0, 0}, vnew = {0, 0, 0, 0};
-    if constexpr (PLANNED) {
+    if constexpr (PLANNED && !LEAD) {
         if (p.wpos != nullptr) {
             const size_t row = ((size_t)s * p.Hkv + hk) * ROW + dl * 16;
             knew = *reinterpret_cast<const u32x4*>(static_cast<const char*>(p.k_new) + row);
@@ -543,10 +563,12 @@ __global__ __launch_bounds__(WPB * kWave) void split_kernel(const int* __restric
         // The block ids are read through a descriptor: on the planned path the
         // descriptor spans table_all (table_len ints), so any plan reads inside it;
         // otherwise it spans this chunk's nblk entries.
+        // (a short sequence of a self-planned launch: its own entries)
+        constexpr bool WHOLE_TABLE = PLANNED && !LEAD;
         const int first = tab_start + (PLANNED ? 0 : b0);
         const __amdgpu_buffer_rsrc_t trs =
-            PLANNED ? tile_rsrc(p.table_all, p.table_len * 4) : tile_rsrc(p.table_all + first, nblk * 4);
-        const int tb = PLANNED ? first * 4 : 0;  // byte offset of the chunk's first entry
+            WHOLE_TABLE ? tile_rsrc(p.table_all, p.table_len * 4) : tile_rsrc(p.table_all + first, nblk * 4);
+        const int tb = WHOLE_TABLE ? first * 4 : 0;  // byte offset of the chunk's first entry
         if constexpr (UNIFORM) {
             // unconditional: lanes past the chunk's blocks read a neighbour's id or 0 and
             // are never selected by the readlane below
@@ -572,7 +594,7 @@ __global__ __launch_bounds__(WPB * kWave) void split_kernel(const int* __restric
         b.k0 = k0;
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int i = wave + WPB * (k0 + u);   // wave-load index within the chunk
+            const int i = wv + NW * (k0 + u);      // wave-load index within the chunk
             const int t0 = j0 + i * TPW;
             if constexpr (PER_LANE) {
                 int tt = t0 + tslot;
@@ -616,7 +638,7 @@ __global__ __launch_bounds__(WPB * kWave) void split_kernel(const int* __restric
         u32x4 kq[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int tok = j0 + (wave + WPB * (b.k0 + u)) * TPW + tslot;
+            const int tok = j0 + (wv + NW * (b.k0 + u)) * TPW + tslot;
             valid[u] = tok < j1;
             kq[u] = tok == wp ? knew : b.k[u];
             Tr::to_float(tok == wp ? vnew : b.v[u], vf[u]);
@@ -675,6 +697,22 @@ __global__ __launch_bounds__(WPB * kWave) void split_kernel(const int* __restric
             for (int e = 0; e < EPL; ++e) acc[g][e] = acc[g][e] * ws + shfl_xor(acc[g][e], msk) * wo;
             m[g] = mx;
         }
+    }
+    if constexpr (LEAD) {  // lead_finish combines the waves' partials
+        if (tslot == 0) {
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) s_lacc[wv][g][dl * EPL + e] = acc[g][e];
+        }
+        if (lane == 0) {
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                s_lm[wv][g] = m[g];
+                s_ll[wv][g] = l[g];
+            }
+        }
+        return;
     }
     if (tslot == 0) {
 #pragma unroll
@@ -745,11 +783,51 @@ __global__ __launch_bounds__(WPB * kWave) void split_kernel(const int* __restric
         for (int g = 0; g < G; ++g) merge_head<T, D, false>(p, first + g, cstride, nc, ob + (size_t)g * D, lane);
     }
     if (lane == 0) __hip_atomic_store(ctr, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    };  // run_unit
+    };  // body
+    auto run_unit = [&](const int (&hdr)[8], const int ev) { body(std::false_type{}, hdr, ev); };
 
     if constexpr (SELF) {
+        // waves 1 ..: sequence b / hks, head subgroup b % hks, when it is short
+        auto lead = [&]() -> bool {
+            const DecodeParams p = fresh_params();
+            const int hks = p.Hkv * p.nsub, b = (int)blockIdx.x;
+            if (b >= p.N * hks) return false;
+            const int s = b / hks;
+            const int L = p.cur_len[s];
+            if (L > p.sp_lead) return false;
+            const int hdr[8] = {s, b - s * hks, L, p.tab_off ? p.tab_off[s] : 0, 0, 0, 0, 0};
+            body(std::true_type{}, hdr, 0);
+            return true;
+        };
+        // wave 1, once the plan (and the lengths) are in LDS: the output of that short
+        // sequence from the lead waves' partials
+        auto lead_finish = [&]() {
+            if (wave != 1) return;
+            const DecodeParams p = fresh_params();
+            const int hks = p.Hkv * p.nsub, b = (int)blockIdx.x;
+            if (b >= p.N * hks) return;
+            const int s = b / hks, hh = b - s * hks;
+            if (uniform(s_plan.len[s]) > p.sp_lead) return;
+            const int hk = hh / p.nsub, sub = hh - hk * p.nsub;
+            T* ob = static_cast<T*>(p.out) + ((size_t)s * p.Hq + hk * p.group + sub * G) * D;
+            for (int idx = lane; idx < G * D; idx += kWave) {
+                const int g = idx / D, d = idx % D;
+                float M = -FLT_MAX;
+#pragma unroll
+                for (int w = 0; w < LW; ++w) M = fmaxf(M, s_lm[w][g]);
+                float lt = 0.f, at = 0.f;
+#pragma unroll
+                for (int w = 0; w < LW; ++w) {
+                    const float wt = fast_exp2(s_lm[w][g] - M);
+                    lt = __builtin_fmaf(wt, s_ll[w][g], lt);
+                    at = __builtin_fmaf(wt, s_lacc[w][g][d], at);
+                }
+                ob[(size_t)g * D + d] = (T)(lt > 0.f ? at * (1.0f / lt) : 0.f);
+            }
+        };
         // self-planned launches pass the device lengths as the (preloaded) first argument
-        self_plan_loop<T, D, WPB * kWave>(work, work_ints, s_plan, G, [&](const int (&hdr)[8]) { run_unit(hdr, 0); });
+        self_plan_loop<T, D, WPB * kWave>(work, work_ints, s_plan, G, [&](const int (&hdr)[8]) { run_unit(hdr, 0); },
+                                          lead, lead_finish);
     } else {
         // planned entries may carry the chunk's first block ids after the 8-int
         // header (one int per lane, read together with the header), so the first
@@ -903,10 +981,14 @@ inline long long resident_blocks_for(const void* kernel, int block, unsigned lds
 
 // Grid of a self-planned launch: at most the units it can have, at most one
 // workgroup per resident slot.
+// Short sequences attended while the kernel plans need a workgroup per (sequence,
+// head subgroup): with fewer, the launch plans every sequence.
 template <typename K>
-dim3 self_grid(K kernel, int block, unsigned lds, dim3 upper) {
+dim3 self_grid(K kernel, int block, unsigned lds, dim3 upper, DecodeParams& p) {
     const long long r = resident_blocks_for(reinterpret_cast<const void*>(kernel), block, lds);
-    return dim3((unsigned)std::max(1LL, std::min((long long)upper.x, r)));
+    const dim3 g((unsigned)std::max(1LL, std::min((long long)upper.x, r)));
+    if (p.sp_lead > 0 && (long long)p.N * p.Hkv * p.nsub > (long long)g.x) p.sp_lead = 0;
+    return g;
 }
 
 template <typename T, int D, int G, int WPB, int U>
@@ -920,15 +1002,15 @@ int launch_split_mode(DecodeLaunch L, dim3 grid, hipStream_t st) {
         case kPlannedPerLane: L.lds_pad = lds_pad(split_kernel<T, D, G, kPlannedPerLane, WPB, U>, L.wg_per_cu); hipLaunchKernelGGL((split_kernel<T, D, G, kPlannedPerLane, WPB, U>), grid, block, L.lds_pad, st, L.p.work, L.p.work_ints, L.p); break;
         case kSelfPlanned:
             L.lds_pad = lds_pad(split_kernel<T, D, G, kSelfPlanned, WPB, U>, L.wg_per_cu);
-            hipLaunchKernelGGL((split_kernel<T, D, G, kSelfPlanned, WPB, U>),
-                               self_grid(split_kernel<T, D, G, kSelfPlanned, WPB, U>, block.x, L.lds_pad, grid), block,
-                               L.lds_pad, st, L.p.cur_len, L.p.N, L.p);
+            grid = self_grid(split_kernel<T, D, G, kSelfPlanned, WPB, U>, block.x, L.lds_pad, grid, L.p);
+            hipLaunchKernelGGL((split_kernel<T, D, G, kSelfPlanned, WPB, U>), grid, block, L.lds_pad, st, L.p.cur_len,
+                               L.p.N, L.p);
             break;
         case kSelfContig:
             L.lds_pad = lds_pad(split_kernel<T, D, G, kSelfContig, WPB, U>, L.wg_per_cu);
-            hipLaunchKernelGGL((split_kernel<T, D, G, kSelfContig, WPB, U>),
-                               self_grid(split_kernel<T, D, G, kSelfContig, WPB, U>, block.x, L.lds_pad, grid), block,
-                               L.lds_pad, st, L.p.cur_len, L.p.N, L.p);
+            grid = self_grid(split_kernel<T, D, G, kSelfContig, WPB, U>, block.x, L.lds_pad, grid, L.p);
+            hipLaunchKernelGGL((split_kernel<T, D, G, kSelfContig, WPB, U>), grid, block, L.lds_pad, st, L.p.cur_len,
+                               L.p.N, L.p);
             break;
         default: return set_error(KVC_ERR_ARG, "unknown decode mode");
     }
@@ -984,15 +1066,15 @@ int launch_gqa_mode(DecodeLaunch L, dim3 grid, hipStream_t st) {
         case kCausalTile:     hipLaunchKernelGGL((gqa_mfma_kernel<D, kCausalTile, WPB>), grid, block, 0, st, L.p.work, L.p.work_ints, L.p); break;
         case kSelfPlanned:
             L.lds_pad = lds_pad(gqa_mfma_kernel<D, kSelfPlanned, WPB>, L.wg_per_cu);
-            hipLaunchKernelGGL((gqa_mfma_kernel<D, kSelfPlanned, WPB>),
-                               self_grid(gqa_mfma_kernel<D, kSelfPlanned, WPB>, block.x, L.lds_pad, grid), block,
-                               L.lds_pad, st, L.p.cur_len, L.p.N, L.p);
+            grid = self_grid(gqa_mfma_kernel<D, kSelfPlanned, WPB>, block.x, L.lds_pad, grid, L.p);
+            hipLaunchKernelGGL((gqa_mfma_kernel<D, kSelfPlanned, WPB>), grid, block, L.lds_pad, st, L.p.cur_len, L.p.N,
+                               L.p);
             break;
         case kSelfContig:
             L.lds_pad = lds_pad(gqa_mfma_kernel<D, kSelfContig, WPB>, L.wg_per_cu);
-            hipLaunchKernelGGL((gqa_mfma_kernel<D, kSelfContig, WPB>),
-                               self_grid(gqa_mfma_kernel<D, kSelfContig, WPB>, block.x, L.lds_pad, grid), block,
-                               L.lds_pad, st, L.p.cur_len, L.p.N, L.p);
+            grid = self_grid(gqa_mfma_kernel<D, kSelfContig, WPB>, block.x, L.lds_pad, grid, L.p);
+            hipLaunchKernelGGL((gqa_mfma_kernel<D, kSelfContig, WPB>), grid, block, L.lds_pad, st, L.p.cur_len, L.p.N,
+                               L.p);
             break;
         default: return set_error(KVC_ERR_ARG, "matrix-core decode: unsupported addressing mode");
     }

@@ -539,7 +539,8 @@ __global__ __launch_bounds__(WPB * kWave) void gqa_mfma_kernel(const int* __rest
     if constexpr (SELF) {
         // self-planned launches pass the device lengths as the (preloaded) first argument
         self_plan_loop<_Float16, D, WPB * kWave>(work, work_ints, s_plan, heads,
-                                                 [&](const int (&hdr)[8]) { run_unit(hdr, 0); });
+                                                 [&](const int (&hdr)[8]) { run_unit(hdr, 0); },
+                                                 [] { return false; }, [] {});
     } else {
         // planned entries carry the unit's block ids after the 8-int header (one int
         // per lane): entry and header are read first, from the preloaded arguments

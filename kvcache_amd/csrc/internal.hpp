@@ -82,6 +82,10 @@ struct DecodeParams {
     int sp_pf_blocks;         // blocks of every sequence read ahead while the plan is made (0: none)
     int sp_pf_min_len;        // shortest sequence read ahead
     int sp_pf_xcd;            // 1: each KV head's slice is read ahead on the XCD of its units (self_prefetch)
+    // short sequences (VALU self-planned decode): a sequence of at most sp_lead tokens
+    // is attended whole, while wave 0 plans, by waves 1.. of workgroup s * hks + h (one
+    // per head subgroup h); the plan leaves it out (0: none; a multiple of the block)
+    int sp_lead;
     const int* dev_base;
     // where a launch reports a length it could not attend (the rows get NaN as well):
     // a pinned host word per device (device_error_word in abi.hip), or nullptr
@@ -172,6 +176,8 @@ struct Tuning {
     int self_prefetch_min_len = 256;  // ... of the sequences of at least this many tokens
     int self_prefetch_xcd = 1;  // 1: read each KV head's slice ahead on the XCD whose units use it
                                 // (whole-KV-head units and a multiple of 8 KV heads only)
+    int self_lead_tokens = 320; // self-planned VALU decode: sequences of at most this many tokens are
+                                // attended while the kernel plans the others (0: none)
 };
 // Dynamic LDS that caps decode workgroups per CU at wg_per_cu (0: none).
 size_t occupancy_lds(size_t static_lds, int wg_per_cu);

@@ -41,8 +41,9 @@ constexpr int kSelfBuckets = 8;       // order buckets: 4 for chunks of split se
 constexpr int kSelfMaxChunks = 0xFFFF;  // chunks of one sequence (16-bit plan field)
 constexpr int kSelfWindow = 16;       // rounds whose unit headers a workgroup resolves per setup
 
-template <int NMAX, int NW>
+template <int NMAX, int NW, bool LEAD = false>
 struct SelfPlanLds {
+    static constexpr bool kLead = LEAD;  // the kernel attends short sequences while it plans (sp_lead)
     int len[NMAX];             // attended length of each sequence (>= 0)
     int to[NMAX];              // first table entry of each sequence
     int cut[NMAX];             // chunks | chunk length in blocks << 16
@@ -165,6 +166,7 @@ __device__ SelfPlan self_plan_setup(const int* lens, int n_seq, const DecodePara
         const int B = p.block, hks = p.Hkv * p.nsub;
         const int bsh = __builtin_ctz((unsigned)B);
         const int first = lens ? 0 : (p.dev_base ? *p.dev_base : p.fixed_len);  // causal prompt queries
+        const int P = Lds::kLead ? p.sp_lead : 0;  // sequences of at most P tokens are not planned
         if (lane < kSelfWindow) S.hdr[lane][0] = -1;
         // this lane's table offsets: issued as soon as the parameter block is in, first
         // used when the headers are written (bounded buffer loads: indices past N read
@@ -242,6 +244,12 @@ __device__ SelfPlan self_plan_setup(const int* lens, int n_seq, const DecodePara
                 S.to[i] = nb;  // packed tables in sequence order
                 nb += (int)(((unsigned)L + B - 1) >> bsh);
             }
+            if (P > 0 && L <= P) {  // attended while the plan is made: no units, no records
+                over |= L > p.cap;
+                S.cut[i] = 0;
+                S.bk[i] = 0;
+                continue;
+            }
             int nc, chunk;
             self_split(p, L, Ti, bsh, nc, chunk);
             over |= nc > kSelfMaxChunks || L > p.cap;
@@ -308,7 +316,7 @@ __device__ SelfPlan self_plan_setup(const int* lens, int n_seq, const DecodePara
                 const int nc = cut & 0xFFFF, cblk = (unsigned)cut >> 16;
                 const int ka = bk & 15, kb = bk >> 4;
                 const int ca = ka == bsel && nc > 1 ? hks * (nc - 1) : 0;
-                const int cb = kb == bsel ? hks : 0;
+                const int cb = kb == bsel && nc > 0 ? hks : 0;
                 if (x < ca + cb) {
                     int h, cc;
                     if (x < ca) {  // run A: chunks 0..nc-2, every head of a chunk in turn
@@ -461,13 +469,24 @@ __device__ __forceinline__ void self_prefetch(const int* lens, int N, const Deco
 // itself, the compiler hoists the planner's parameter arithmetic in front of the
 // loop -- ahead of the lengths loads, with its results spilled -- and keeps it live
 // across every unit.
-template <typename E, int D, int NT, typename Lds, typename Run>
-__device__ __forceinline__ void self_plan_loop(const int* lens, int n_seq, Lds& S, int heads, Run&& run) {
+//
+// Short sequences (Lds::kLead and p.sp_lead > 0): while wave 0 plans the first window,
+// the other waves run lead() -- a sequence of at most p.sp_lead tokens whole, for this
+// workgroup's (sequence, head subgroup), its partials left in LDS; false when there is
+// none, and wave 1 then reads ahead -- and after the window's first unit (whose
+// epilogue runs on wave 0 alone) wave 1 writes its output (lead_finish).
+template <typename E, int D, int NT, typename Lds, typename Run, typename Lead, typename LeadFinish>
+__device__ __forceinline__ void self_plan_loop(const int* lens, int n_seq, Lds& S, int heads, Run&& run, Lead&& lead,
+                                               LeadFinish&& lead_finish) {
     const int G = (int)gridDim.x;
     // one window: plan it, run its units; false once every round is done
     auto window = [&](int kw, int (&lv)[kSelfSpt]) -> bool {
         const DecodeParams p = fresh_params();
-        if (kw == 0 && p.sp_pf_blocks > 0 && (threadIdx.x >> 6) == 1) self_prefetch<E, D>(lens, n_seq, p, S);
+        const bool leads = Lds::kLead && kw == 0 && p.sp_lead > 0;
+        const int w = threadIdx.x >> 6;
+        bool led = false;
+        if (leads && w != 0) led = lead();
+        if (kw == 0 && p.sp_pf_blocks > 0 && w == 1 && !led) self_prefetch<E, D>(lens, n_seq, p, S);
         const SelfPlan sp = self_plan_setup<NT>(lens, n_seq, p, S, kw, lv);
         if (sp.overflow) {
             self_plan_nan<E, D, NT>(p, heads);
@@ -478,10 +497,12 @@ __device__ __forceinline__ void self_plan_loop(const int* lens, int n_seq, Lds& 
         for (int k = 0; k < kend; ++k) {
             int hdr[8];
             if (self_plan_header(S, k, hdr)) run(hdr);
+            if (leads && k == 0) lead_finish();
             // the unit's epilogue (one wave in the VALU kernel) still reads the other
             // waves' partials in LDS: no wave starts the next unit before it is done
             __syncthreads();
         }
+        if (leads && kend <= 0) lead_finish();
         return kw + kSelfWindow < rounds;
     };
     // the first window's lengths load before anything else (the later windows' load

@@ -5,7 +5,11 @@ qwen_kernels.cu:293-326).
 Every workgroup derives the host planner's units from the device lengths, so the
 outputs must equal the host-planned launch's bit for bit (same chunks, same merge
 order), whatever order the units run in and however many workgroups serve them; and
-they must match the CPU oracle within the path's tolerance.  No length is truncated:
+they must match the CPU oracle within the path's tolerance.  On the VALU kernel,
+sequences of at most self_lead_tokens tokens are attended whole by the waves that
+wait while wave 0 plans, and the plan leaves them out: the other sequences still
+equal the host plan bit for bit, the short ones match the oracle, and paged equals
+contiguous bit for bit.  No length is truncated:
 a stated cap only sizes the launch, and the explicit-split path (whose grid is sized
 by the cap) gives NaN rows, never a partial attention, for a sequence longer than it.
 """
@@ -59,6 +63,8 @@ CASES = {
     "mha_fp32": (np.array([1, 17, 640, 961, 2000, 3000, 0, 64], np.int32), 8, 8, 64, KVC_F32),
     "gqa_valu_fp32": (np.array([1000, 15, 16, 17, 3000, 1], np.int32), 14, 2, 64, KVC_F32),
     "group2_fp16": (np.array([2048, 1024, 333, 5000, 7], np.int32), 8, 4, 64, KVC_F16),
+    # every length within the largest short-sequence threshold: the plan has no units at all
+    "short_mha": (np.array([1, 0, 700, 1024, 33, 64, 65, 1000], np.int32), 8, 8, 64, KVC_F16),
 }
 
 
@@ -70,11 +76,18 @@ def test_self_planned_equals_host_planned(orc, case):
     q, K, V = inputs(lens, Hq, Hkv, D, dtype, 300)
     nb = sum((int(x) + B - 1) // B for x in lens)
     kp, vp, table, tab_off = paged_layout(K, V, lens, B, np.random.default_rng(8).permutation(nb))
-    got = self_planned(q, kp, vp, table, tab_off, lens, Hkv, B, dtype, cap=int(max(lens)))
+    with tuning("self_lead_tokens", 0):
+        got = self_planned(q, kp, vp, table, tab_off, lens, Hkv, B, dtype, cap=int(max(lens)))
     ref = host_planned(q, kp, vp, table, tab_off, lens, Hkv, B, dtype)
     np.testing.assert_array_equal(got, ref)
-    assert np.abs(got - oracle(orc, q, K, V, lens)).max() <= tol(dtype)
+    want = oracle(orc, q, K, V, lens)
+    assert np.abs(got - want).max() <= tol(dtype)
     assert np.all(got[np.asarray(lens) == 0] == 0)
+    lead = self_planned(q, kp, vp, table, tab_off, lens, Hkv, B, dtype, cap=int(max(lens)))  # short ones while planning
+    assert np.abs(lead - want).max() <= tol(dtype)
+    assert np.all(lead[np.asarray(lens) == 0] == 0)
+    planned = np.asarray(lens) > 320  # (the default threshold; matrix-core shapes plan every sequence)
+    np.testing.assert_array_equal(lead[planned], ref[planned])
 
 
 @pytest.mark.parametrize("grid", [1, 7, 100])
@@ -88,7 +101,8 @@ def test_small_grids_serve_every_rank_once(orc, grid):
     kp, vp, table, tab_off = paged_layout(K, V, lens, 16)
     ws = DeviceBuffer(ops.decode_workspace_size(len(lens), Hq, Hkv, D, 16, 0, 0, dtype))
     ws.upload(np.random.default_rng(1).integers(0, 256, ws.nbytes, dtype=np.uint8))
-    ref = self_planned(q, kp, vp, table, tab_off, lens, Hkv, 16, dtype)
+    with tuning("self_lead_tokens", 0):  # (small grids run without lead chunks)
+        ref = self_planned(q, kp, vp, table, tab_off, lens, Hkv, 16, dtype)
     with tuning("self_grid", grid):
         a = self_planned(q, kp, vp, table, tab_off, lens, Hkv, 16, dtype, workspace=ws)
         b = self_planned(q, kp, vp, table, tab_off, lens, Hkv, 16, dtype, workspace=ws)
@@ -299,9 +313,46 @@ def test_read_ahead_changes_no_output(case):
     q, K, V = inputs(lens, Hq, Hkv, D, dtype, 340)
     nb = sum((int(x) + B - 1) // B for x in lens)
     kp, vp, table, tab_off = paged_layout(K, V, lens, B, np.random.default_rng(9).permutation(nb))
-    with tuning("self_prefetch_kib", 0):
-        ref = self_planned(q, kp, vp, table, tab_off, lens, Hkv, B, dtype)
-    for kib, min_len in ((32768, 256), (1 << 20, 0), (64, 1)):
-        with tuning("self_prefetch_kib", kib), tuning("self_prefetch_min_len", min_len):
-            got = self_planned(q, kp, vp, table, tab_off, lens, Hkv, B, dtype)
-        np.testing.assert_array_equal(got, ref)
+    with tuning("self_lead_tokens", 0):  # (the read-ahead runs when there are no lead chunks)
+        with tuning("self_prefetch_kib", 0):
+            ref = self_planned(q, kp, vp, table, tab_off, lens, Hkv, B, dtype)
+        for kib, min_len in ((32768, 256), (1 << 20, 0), (64, 1)):
+            with tuning("self_prefetch_kib", kib), tuning("self_prefetch_min_len", min_len):
+                got = self_planned(q, kp, vp, table, tab_off, lens, Hkv, B, dtype)
+            np.testing.assert_array_equal(got, ref)
+
+
+LEAD_CASES = ["c2_reference", "c2_loguniform", "mha_fp32", "gqa_valu_fp32", "group2_fp16", "short_mha"]
+
+
+@pytest.mark.parametrize("case", LEAD_CASES)
+def test_short_sequences_while_planning(orc, case):
+    """Short-sequence thresholds -- one block, the default, more than most sequences,
+    and the largest (a chunk's 64 blocks; larger requests are cut to it) -- against the
+    oracle, on a first and a second launch over one never-cleared workspace; and paged
+    against contiguous caches bit for bit (both cut the same chunks)."""
+    lens, Hq, Hkv, D, dtype = CASES[case]
+    say(f"self-planned, short sequences while planning: {case}")
+    B = 16
+    lens = np.asarray(lens, np.int32)
+    N = len(lens)
+    q, K, V = inputs(lens, Hq, Hkv, D, dtype, 350)
+    nb = sum((int(x) + B - 1) // B for x in lens)
+    kp, vp, table, tab_off = paged_layout(K, V, lens, B, np.random.default_rng(10).permutation(nb + 7))
+    want = oracle(orc, q, K, V, lens)
+    ws = DeviceBuffer(ops.decode_workspace_size(N, Hq, Hkv, D, B, 0, 0, dtype))
+    ws.upload(np.random.default_rng(11).integers(0, 256, ws.nbytes, dtype=np.uint8))
+    for lead in (16, 64, 1000, 1 << 20):
+        with tuning("self_lead_tokens", lead):
+            a = self_planned(q, kp, vp, table, tab_off, lens, Hkv, B, dtype, workspace=ws)
+            b = self_planned(q, kp, vp, table, tab_off, lens, Hkv, B, dtype, workspace=ws)
+            out = DeviceBuffer(q.nbytes)
+            ops.launch_batched_decode(dev(q), dev(K), dev(V), dev(lens), out, N, Hq, D, K.shape[2], 0,
+                                      float(1.0 / np.sqrt(D)), Hkv=Hkv, dtype=dtype)
+            contig = host(out, q.dtype, q.shape).astype(np.float64)
+        err = np.abs(a - want).max()
+        say(f"  threshold {lead}: max |err| {err:.2e}")
+        assert err <= tol(dtype)
+        np.testing.assert_array_equal(a, b)
+        np.testing.assert_array_equal(a, contig)
+        assert np.all(a[lens == 0] == 0)
