@@ -30,6 +30,9 @@ from pathlib import Path
 
 import numpy as np
 
+# kernel arguments in device memory (also for the C++ child process): see kvcache_amd/_native.py
+os.environ.setdefault("HIP_FORCE_DEV_KERNARG", "1")
+
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 

@@ -6,6 +6,7 @@ import of any op fails loudly: there is no CPU fallback for the hot path.
 from __future__ import annotations
 
 import ctypes as C
+import os
 import threading
 from pathlib import Path
 
@@ -202,6 +203,13 @@ def lib() -> C.CDLL:
                     raise RuntimeError(
                         f"{LIB_PATH} is missing: build it with `python -m kvcache_amd.build` "
                         "(there is no CPU fallback for the decode path)")
+                # kernel arguments in device memory (unless the caller chose otherwise): every
+                # decode workgroup reads its parameter block from the kernel-argument segment,
+                # and where the HIP runtime's default puts that segment in host memory each
+                # read crosses PCIe (MI355X, same box: config 2 37.4 vs 33.5 us per launch,
+                # one config-4 layer 8.0 vs 6.0 us).  HIP reads it when it initialises, which
+                # the library's first call does.
+                os.environ.setdefault("HIP_FORCE_DEV_KERNARG", "1")
                 L = C.CDLL(str(LIB_PATH))
                 for name, (res, args) in _SIGS.items():
                     fn = getattr(L, name)

@@ -13,6 +13,9 @@ import pytest
 ROOT = Path(__file__).resolve().parents[1]
 if str(ROOT) not in sys.path:
     sys.path.insert(0, str(ROOT))
+# kernel arguments in device memory, as the Python binding sets it, also for the C++
+# test programs started before the library is loaded here
+os.environ.setdefault("HIP_FORCE_DEV_KERNARG", "1")
 
 
 def pytest_configure(config):
