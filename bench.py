@@ -978,6 +978,8 @@ def main() -> int:
             plan_cost[key] = pp
     except Exception as e:  # noqa: BLE001 -- reported, not fatal to the headline
         plan_cost["pipelined"] = {"error": repr(e)}
+    plan_cost["per_step_on_device"] = ("a serving loop that re-plans every step can instead pass the lengths in "
+                                       "device memory: device_lengths_path plans each launch on the GPU")
     log(f"host plan: {plan_cost}")
 
     extras = {}
