@@ -80,7 +80,11 @@ int         kvc_device_count(int* count);
  * "self_prefetch_kib" (self-planned paged launches: about this many KiB of K and V,
  * the first blocks of every sequence, are read ahead while the kernel plans;
  * default 32768, 0 = none), "self_prefetch_min_len" (... of the sequences of at
- * least this many tokens, default 256; at most a quarter of each is read ahead).
+ * least this many tokens, default 256; at most a quarter of each is read ahead),
+ * "self_prefetch_xcd" (1: each KV head's slice is read ahead on the XCD whose
+ * units read it), "self_lead_tokens" (self-planned launches on the VALU kernel: a
+ * sequence of at most this many tokens is attended whole while the kernel plans the
+ * others, default 320, 0 = none; at most the largest chunk).
  * The matrix-core path takes fp16 K/V, head_dim 64 or 128, 3..16 query heads per
  * KV head and, paged, a power-of-two BLOCK >= 16; other shapes use the VALU
  * kernels. */

@@ -147,9 +147,12 @@ def test_planned_and_prefill_argument_errors():
 def test_tuning_round_trip_and_rejects():
     L = N.lib()
     v = C.c_int(0)
-    for key in (b"mfma", b"wg_per_cu", b"split_first", b"fused_merge", b"waves_per_block"):
+    for key in (b"mfma", b"wg_per_cu", b"split_first", b"fused_merge", b"waves_per_block", b"self_prefetch_xcd",
+                b"self_lead_tokens"):
         assert L.kvc_get_tuning(key, C.byref(v)) == N.KVC_OK
         old = v.value
         assert L.kvc_set_tuning(key, old) == N.KVC_OK
     assert L.kvc_set_tuning(b"mfma", 7) == N.KVC_ERR_ARG
     assert L.kvc_set_tuning(b"no_such_knob", 1) == N.KVC_ERR_ARG
+    assert L.kvc_set_tuning(b"self_lead_tokens", -1) == N.KVC_ERR_ARG
+    assert L.kvc_get_tuning(b"self_lead_tokens", C.byref(v)) == N.KVC_OK and v.value == 320
