@@ -13,7 +13,10 @@
 // gridDim.x (self_plan_rank).  Every workgroup computes the same order from the same
 // data, so each unit runs exactly once, and outputs equal the host-planned launch's
 // bit for bit (same chunks, same merge order); only the order in which units run
-// differs from the host plan's.
+// differs from the host plan's.  On the VALU kernel a sequence of at most p.sp_lead
+// tokens is attended instead by waves 1.. of workgroup s * hks + h while wave 0 plans
+// (self_plan_loop), and the plan leaves it out: the other sequences' units are the
+// host plan's, the short ones differ from it only in rounding (three waves share them).
 //
 // Budget: every (sequence, KV head) may use up to p.sp_records partial records (64,
 // or more when the caller states a long bound), and on the matrix-core path a
@@ -22,17 +25,16 @@
 // even at the largest chunk, or with a length past its contiguous cache (p.cap),
 // gets NaN outputs: never a silent partial attention.
 //
-// Cost structure.  A wave issues a dependent VALU instruction every ~6 cycles, so
-// the setup is written as short dependent chains: the lengths load at wave start
-// (their pointer is the kernel's preloaded first argument); one barrier publishes
-// the per-wave totals (tokens, longest length, table blocks), the chunk target is
-// integer arithmetic in 32 bits (the 64-bit forms only past 2^32 tokens); a second
-// barrier publishes the per-wave unit counts of the eight buckets and the record and
-// counter counts (wave scans); then each thread, knowing the first rank of each of
-// its sequences' runs, writes the headers of the ranks this workgroup serves in a
-// window of kSelfWindow rounds into LDS; a third barrier, and the persistent loop
-// only reads a header per unit.  Batches needing more rounds repeat the setup per
-// window.
+// Cost structure.  A lone wave issues a dependent VALU instruction every ~6 cycles,
+// so the setup is one wave of short dependent chains: the lengths load at wave start
+// (their pointer is the kernel's preloaded first argument); wave scans give the
+// totals (tokens, longest length, table blocks) and the chunk target, in 32-bit
+// integer arithmetic (the 64-bit forms only past 2^32 tokens); each lane splits its
+// sequences and counts their units per bucket; eight wave scans give every lane the
+// first rank of its runs in each bucket; then the lane holding each of this
+// workgroup's ranks in a window of kSelfWindow rounds writes its header into LDS; one
+// barrier, and the persistent loop only reads a header per unit.  Batches needing
+// more rounds repeat the setup per window.
 
 constexpr int kSelfMaxNValu = 1024;   // sequences per launch (their plan rows live in LDS)
 constexpr int kSelfMaxNMfma = 512;    // (keeps the matrix-core kernel's LDS within two workgroups per CU)
