@@ -248,6 +248,26 @@ def practical_ceiling(W, lens, Hq, Hkv, D, B, steps, warmup, target=0):
     return e0.elapsed_ms(e1) / steps * 1e3, nu
 
 
+def launch_floor(steps, warmup):
+    """us per launch of an empty kernel (kvc_empty_launch) back to back, with 1 and with 1024
+    one-wave workgroups: the cost every decode launch pays before any work."""
+    from kvcache_amd._native import check, lib
+    from kvcache_amd.device import Event, synchronize
+    out = {}
+    for blocks in (1, 1024):
+        for _ in range(warmup):
+            check(lib().kvc_empty_launch(blocks, None))
+        synchronize()
+        e0, e1 = Event(), Event()
+        e0.record()
+        for _ in range(steps):
+            check(lib().kvc_empty_launch(blocks, None))
+        e1.record()
+        synchronize()
+        out[f"{blocks}_workgroups_us"] = round(e0.elapsed_ms(e1) / steps * 1e3, 3)
+    return out
+
+
 def bench_c2_contiguous(steps, warmup, rotate):
     """The reference's bench_throughput comparison (bench_throughput.cu:120-132): the config-2 batch
     (reference lengths) as contiguous caches [N, H, LMAX=2048, D] (launch_batched_decode) and as the
@@ -953,6 +973,8 @@ def main() -> int:
     ms_per_step = t_launch
     t_probe, _ = practical_ceiling(W, lens, Hq, Hkv, D, B, a.steps, a.warmup, target=a.plan_target)
     log(f"C2 read-only probe over the same plan: {t_probe:.2f} us/launch")
+    floor = launch_floor(200, 20)
+    log(f"launch floor (empty kernels back to back): {floor}")
     traffic, sym = measured_traffic()
     prof_us = profiled_launch_us()
     traffic_src = (f"rocprofv3 --pmc FETCH_SIZE x2.0 + WRITE_SIZE x1.0 per dispatch of {sym} "
@@ -1060,6 +1082,8 @@ def main() -> int:
                                            "GBps": round(total / (t_probe * 1e-6) / 1e9, 1),
                                            "frac": round(total / (t_probe * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                                            "decode_over_probe": round(t_launch * 1e3 / t_probe, 4)},
+                     "launch_floor": dict(floor, what="kvc_empty_launch back to back: the per-launch cost before "
+                                                      "any work"),
                      "profile": ({"file": str(STATS_SUMMARY.relative_to(ROOT)), "mean_launch_us": prof_us,
                                   "frac": round(total / (prof_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                                   "note": "rocprofv3 kernel trace of the headline command (bench.py --no-extras "

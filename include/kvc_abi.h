@@ -129,6 +129,10 @@ int kvc_event_elapsed_ms(float* ms, void* start, void* stop); /* synchronizes on
 int kvc_read_probe_planned(const void* k_pool, const void* v_pool, const int* table_all, int table_len,
                            const int* work, int n_units, int Hq, int Hkv, int D, int BLOCK, int dtype, int* sink,
                            kvc_stream_t stream);
+/* No counterpart in the reference; a measurement aid: one launch of an empty kernel of
+ * `blocks` (1..65535) one-wave workgroups on `stream`.  Timed back to back it gives the
+ * launch floor that every decode launch pays. */
+int kvc_empty_launch(int blocks, kvc_stream_t stream);
 /* 1 in *capturing when `stream` is being captured into a graph (0 for the null stream). */
 int kvc_stream_is_capturing(kvc_stream_t stream, int* capturing);
 /* Device-side failure reports.  A device-length decode launch that cannot attend a

@@ -153,6 +153,7 @@ _SIGS = {
     "kvc_decode_plan_capacity": (i32, [i32, C.c_longlong, i32, i32, i32, i32, i32, ip]),
     "kvc_decode_plan_chunk": (i32, [vp, i32, i32, i32, i32, i32, i32, i32, ip]),
     "kvc_read_probe_planned": (i32, [vp, vp, vp, i32, vp, i32, i32, i32, i32, i32, i32, vp, vp]),
+    "kvc_empty_launch": (i32, [i32, vp]),
     "kvc_stream_is_capturing": (i32, [vp, ip]),
     "kvc_check_device_errors": (i32, [vp]),
     "kvc_graph_begin": (i32, [vp]),

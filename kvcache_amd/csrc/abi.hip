@@ -958,6 +958,10 @@ int kvc_read_probe_planned(const void* k_pool, const void* v_pool, const int* ta
         return launch_read_probe(p, work, ps.entry_ints, n_units, S(st));
     });
 }
+int kvc_empty_launch(int blocks, kvc_stream_t st) {
+    if (blocks < 1 || blocks > 65535) return set_error(KVC_ERR_ARG, "blocks must be in 1..65535");
+    return launch_empty(blocks, S(st));
+}
 int kvc_stream_is_capturing(kvc_stream_t st, int* capturing) {
     if (!capturing) return set_error(KVC_ERR_ARG, "null out pointer");
     *capturing = 0;

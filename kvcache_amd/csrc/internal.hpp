@@ -216,5 +216,7 @@ struct ProbeParams {
     int* sink;        // [n_units]; written only when a unit's xor equals a fixed value
 };
 int launch_read_probe(const ProbeParams& p, const int* work, int work_ints, int n_units, hipStream_t stream);
+// One launch of an empty kernel of `blocks` one-wave workgroups (probe.hip).
+int launch_empty(int blocks, hipStream_t stream);
 
 }  // namespace kvc

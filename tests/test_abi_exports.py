@@ -155,4 +155,5 @@ def test_tuning_round_trip_and_rejects():
     assert L.kvc_set_tuning(b"mfma", 7) == N.KVC_ERR_ARG
     assert L.kvc_set_tuning(b"no_such_knob", 1) == N.KVC_ERR_ARG
     assert L.kvc_set_tuning(b"self_lead_tokens", -1) == N.KVC_ERR_ARG
+    assert L.kvc_empty_launch(0, None) == N.KVC_ERR_ARG and L.kvc_empty_launch(65536, None) == N.KVC_ERR_ARG
     assert L.kvc_get_tuning(b"self_lead_tokens", C.byref(v)) == N.KVC_OK and v.value == 320

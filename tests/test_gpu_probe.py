@@ -38,3 +38,13 @@ def test_probe_runs_over_planner_work_lists(case):
                                        sink.ptr, None))
     assert nu > 0
     assert not host(sink, np.int32, (max(nu, 1),)).any()
+
+
+def test_empty_launch_runs():
+    """kvc_empty_launch (the launch-floor measurement) launches and completes for 1 and
+    1024 workgroups."""
+    from kvcache_amd.device import synchronize
+    say("empty launches")
+    for blocks in (1, 1024):
+        check(lib().kvc_empty_launch(blocks, None))
+    synchronize()
