@@ -642,14 +642,15 @@ def bench_prefill(steps, warmup):
     return res
 
 
-def bench_c5(n_req=64, gen=64, seed=5, graph=False):
+def bench_c5(n_req=64, gen=64, seed=5, graph=False, chain=0):
     """Config 5: the Qwen2-shaped decoder (24 layers, hidden 896, 14q/2kv, D 64, SwiGLU 4864, vocab 151936,
     random N(0, 0.02) fp16 weights) serving n_req requests greedily with continuous batching at batch 32;
     prompts of 16..256 random tokens, gen tokens each.  Throughput on the host clock around the whole run
-    (each step ends with the sampled tokens on the host, as serving needs them)."""
+    (each step ends with the sampled tokens on the host, as serving needs them).  chain=1: the linear layers
+    between two attention launches as one launch (kvc_rows_chain)."""
     from kvcache_amd.model import QwenConfig, QwenModel
     rng = np.random.default_rng(seed)
-    cfg = QwenConfig(max_batch=32, max_rows=256, seed=seed, graph=int(graph))
+    cfg = QwenConfig(max_batch=32, max_rows=256, seed=seed, graph=int(graph), chain=int(chain))
     m = QwenModel(cfg)
     try:
         prompts = [rng.integers(0, cfg.vocab, int(n)) for n in rng.integers(16, 257, n_req)]
@@ -679,6 +680,7 @@ def bench_c5(n_req=64, gen=64, seed=5, graph=False):
                         "greedy, continuous batching width 32, random fp16 weights",
             "roofline": roof,
             "graph_replay": bool(graph), "graph_steps": st["graph_steps"],
+            "layer_chain": bool(chain), "chain_launches": st["chain_launches"],
             "tokens": st["tokens"], "prompt_tokens": st["prompt_tokens"], "steps": st["steps"],
             "tokens_per_s": round(st["tokens"] / (st["wall_us"] * 1e-6), 1),
             "wall_ms": round(st["wall_us"] / 1e3, 2), "prefill_ms": round(st["prefill_us"] / 1e3, 2),
@@ -875,6 +877,8 @@ def main() -> int:
     ap.add_argument("--plan-sweep", type=str, default="", help="comma list of planned targets to time")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="only run 10 device-to-device copies of MIB MiB (HBM counter calibration) and exit")
+    ap.add_argument("--chain", type=int, default=0, choices=[0, 1],
+                    help="--only c5: 1 runs the linear layers between two attention launches as one launch")
     ap.add_argument("--only", choices=["c3", "c4", "c4_layer", "c5", "prefill"], default=None,
                     help="run only one extra workload and print its result (profiling)")
     ap.add_argument("--summarize-rocprof", metavar="DIR", default=None,
@@ -920,7 +924,7 @@ def main() -> int:
         res = (bench_c3(a.steps, a.warmup, sweep_targets) if a.only == "c3" else
                bench_prefill(a.steps, a.warmup) if a.only == "prefill" else
                bench_c4_layer(a.steps, a.warmup) if a.only == "c4_layer" else
-               bench_c5(graph=a.graph) if a.only == "c5" else bench_c4(graph=a.graph))
+               bench_c5(graph=a.graph, chain=a.chain) if a.only == "c5" else bench_c4(graph=a.graph))
         print(json.dumps(res), flush=True)
         return 0
     if a.lengths == "reference":
@@ -1040,6 +1044,10 @@ def main() -> int:
         try:
             extras["c5"] = bench_c5(graph=a.graph)
             log(f"C5: {extras['c5']}")
+            ch = bench_c5(chain=1)
+            extras["c5"]["with_layer_chain"] = {k: ch[k] for k in ("ms_per_decode_step", "tokens_per_s", "decode_ms",
+                                                                    "chain_launches")}
+            log(f"C5 with the layer chain: {extras['c5']['with_layer_chain']}")
         except Exception as e:  # noqa: BLE001
             extras["c5"] = {"error": repr(e)}
         try:

@@ -46,6 +46,9 @@ struct QwenConfig {
     int step_path = 0;  // 0: fused kernels for steps of <= 32 rows; 1: one kernel per op
     int graph = 0;      // 1: fused steps replay one captured HIP graph (measured no faster than eager)
     int prefill_rows = 4096;  // prompt rows stacked into one prefill forward (a longer prompt runs alone)
+    int chain = 0;  // eager fused steps: 1 runs the linear layers between two attention launches as one
+                    // persistent launch (kvc_rows_chain) where the device and shapes allow; 0 one launch each
+                    // (the default: measured no faster per step, and it holds a grid barrier)
 };
 
 struct QwenModel {
@@ -75,6 +78,10 @@ struct QwenModel {
     void* rws = nullptr;  // fused kernels' workspace (zero between calls)
     size_t rws_bytes = 0;
     bool rows_ok = false;
+    void* cws = nullptr;  // layer chain's workspace (its own: barrier counters persist between launches)
+    size_t cws_bytes = 0;
+    bool chain_ok = false;
+    long long chain_launches = 0;
     // graph-replayed steps: metadata at fixed places,
     // [n, units, records, 0 | ids B | pos B | work cap_units*ipu | table cap_tab]
     void* gexec = nullptr;
@@ -137,6 +144,12 @@ struct QwenModel {
                                   kvc_rows_workspace_size(c.vocab, H)});
             rws = alloc(rws_bytes);
             kvc::check(kvc_memset(rws, 0, rws_bytes, stream), "rows workspace");
+            cws_bytes = c.chain == 1 ? kvc_rows_chain_workspace_size(H, I) : 0;
+            if (cws_bytes) {
+                cws = alloc(cws_bytes);
+                kvc::check(kvc_memset(cws, 0, cws_bytes, stream), "chain workspace");
+                chain_ok = true;
+            }
         }
         kvc::check(kvc_stream_synchronize(stream), "init");
     }
@@ -225,6 +238,7 @@ struct QwenModel {
         const int* d_rows = d_counts;
         const int H = c.hidden, QD = c.n_heads * c.head_dim, I = c.inter;
         const float scale = 1.0f / __builtin_sqrtf((float)c.head_dim);
+        if (chain_ok && !d_counts && chain_layers(M, d_pos, d_table, T, d_work, nu, nr, scale)) return;
         for (int l = 0; l < c.layers; ++l) {
             const Layer& w = L[l];
             kvc::check(kvc_rows_qkv(q, k, v, x, w.ln1, c.eps, w.wq, w.bq, d_pos, M, H, c.n_heads, c.n_kv_heads,
@@ -249,6 +263,44 @@ struct QwenModel {
             kvc::check(kvc_rows_linear(x, gate, w.wd, M, H, I, nullptr, 0.f, 1, d_rows, rws, rws_bytes, stream),
                        "down_proj + residual");
         }
+    }
+
+    // The same layers with the linear layers between two attention launches as one
+    // launch (kvc_rows_chain): the head of layer 0, then per layer the attention and
+    // one launch with that layer's tail and the next layer's head.  Returns false (and
+    // turns the chain off) when the device or shapes do not allow it; it then launched
+    // nothing.
+    bool chain_layers(int M, const int* d_pos, const int* d_table, int T, const int* d_work, int nu, int nr,
+                      float scale) {
+        kvc_layer_chain ch{};
+        ch.M = M; ch.H = c.hidden; ch.Hq = c.n_heads; ch.Hkv = c.n_kv_heads; ch.D = c.head_dim; ch.I = c.inter;
+        ch.eps = c.eps; ch.theta = c.theta;
+        ch.x = x; ch.att = att; ch.act = gate; ch.q = q; ch.k = k; ch.v = v; ch.pos = d_pos;
+        auto set_head = [&](int l) {
+            ch.ln1 = l < c.layers ? L[l].ln1 : nullptr;
+            ch.w_qkv = l < c.layers ? L[l].wq : nullptr;
+            ch.b_qkv = l < c.layers ? L[l].bq : nullptr;
+        };
+        set_head(0);
+        const int rc = kvc_rows_chain(&ch, cws, cws_bytes, stream);
+        if (rc == KVC_ERR_UNSUPPORTED) {
+            chain_ok = false;
+            return false;
+        }
+        kvc::check(rc, "layer chain");
+        ++chain_launches;
+        for (int l = 0; l < c.layers; ++l) {
+            kvc::check(kvc_batched_paged_append_decode_planned(q, k, v, d_pos, kl(l), vl(l), d_table, T, att, M,
+                                                               c.n_heads, c.n_kv_heads, c.head_dim, c.block_size,
+                                                               scale, KVC_F16, d_work, nu, nr, ws, ws_bytes, stream),
+                       "decode attention");
+            const Layer& w = L[l];
+            ch.w_o = w.wo; ch.ln2 = w.ln2; ch.w_gate_up = w.wg; ch.w_down = w.wd;
+            set_head(l + 1);
+            kvc::check(kvc_rows_chain(&ch, cws, cws_bytes, stream), "layer chain");
+            ++chain_launches;
+        }
+        return true;
     }
 
     // Final norm of `rows` rows starting at x row `first` (consecutive), fp32 logits
@@ -657,7 +709,7 @@ struct QwenModel {
     };
     struct ServeStats {
         int steps = 0, finished = 0;
-        long long tokens = 0, prompt_tokens = 0, graph_steps = 0, graph_captures = 0;
+        long long tokens = 0, prompt_tokens = 0, graph_steps = 0, graph_captures = 0, chain_launches = 0;
         double wall_us = 0, prefill_us = 0, decode_us = 0;
     };
 
@@ -665,7 +717,7 @@ struct QwenModel {
     ServeStats serve(const std::vector<Request>& reqs, std::vector<std::vector<int>>& out) {
         using clk = std::chrono::steady_clock;
         ServeStats st;
-        const long long graph_steps0 = graph_steps, graph_captures0 = graph_captures;
+        const long long graph_steps0 = graph_steps, graph_captures0 = graph_captures, chain0 = chain_launches;
         kvm.reset();
         out.assign(reqs.size(), {});
         std::vector<Sequence> seqs(reqs.size());
@@ -756,6 +808,7 @@ struct QwenModel {
         st.wall_us = std::chrono::duration<double, std::micro>(clk::now() - t0).count();
         st.graph_steps = graph_steps - graph_steps0;
         st.graph_captures = graph_captures - graph_captures0;
+        st.chain_launches = chain_launches - chain0;
         return st;
     }
 };

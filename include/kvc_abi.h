@@ -423,6 +423,42 @@ int kvc_rows_lm_head(float* logits, int* tokens, const void* x, const void* norm
                      kvc_stream_t stream);
 int kvc_rows_set_tuning(int splits, int groups_per_wg, int shape);
 
+/* The linear layers between two attention launches of a decode step as ONE launch:
+ * the tail of layer l -- x += att W_o^T; act = silu(n W_g^T) * (n W_u^T) with
+ * n = RMSNorm(x) * ln2; x += act W_d^T -- then the head of layer l + 1 -- q|k|v =
+ * rotary(RMSNorm(x) * ln1 [wq;wk;wv]^T + b) at positions pos -- in the fused kernels'
+ * shapes and rounding, phases separated by grid barriers inside the launch
+ * (qwen_serve.cu:127-175 runs them as GEMMs plus one kernel per elementwise op; no
+ * single counterpart in the reference).  Results equal kvc_rows_linear (o_proj,
+ * residual), kvc_rows_swiglu, kvc_rows_linear (down_proj, residual) and kvc_rows_qkv
+ * run in order, bit for bit.  The tail is skipped when w_o is NULL, the head when
+ * w_qkv is NULL.  Layouts: x [M,H], att [M,Hq*D], act [M,I] (scratch), w_o [H,Hq*D],
+ * w_gate_up [2I,H], w_down [H,I], w_qkv [(Hq+2Hkv)D,H], b_qkv [(Hq+2Hkv)D], q/k/v as
+ * kvc_rows_qkv; fp16; M <= 32; H a multiple of 32 (<= 1024), I of 32, D of 32.
+ * workspace (tail): kvc_rows_chain_workspace_size(H, I) bytes, 256-byte aligned,
+ * ZERO-FILLED before first use and then used by kvc_rows_chain calls of one stream
+ * only (the launches keep their barrier counters consistent from one to the next, not
+ * zero: do not share it with the other kvc_rows_* calls).  The grid (at most one workgroup per CU) must be resident at once:
+ * KVC_ERR_UNSUPPORTED when the device is too small or a shape falls outside the
+ * kernel's.  A barrier wait that gives up (workgroups not all resident, e.g. another
+ * stream's kernels holding CUs) ends the launch without finishing it and reports
+ * through the device error word: the next kvc_rows_chain call with a tail, or
+ * kvc_check_device_errors, returns KVC_ERR_STATE (and the call clears the counters).
+ * Not graph-safe in the sense of the *_dev entry points (M is fixed at capture). */
+typedef struct kvc_layer_chain {
+    int M, H, Hq, Hkv, D, I;
+    float eps, theta;
+    void* x;
+    const void *att, *w_o, *ln2, *w_gate_up;
+    void* act;
+    const void* w_down;
+    void *q, *k, *v;
+    const void *ln1, *w_qkv, *b_qkv;
+    const int* pos;
+} kvc_layer_chain;
+size_t kvc_rows_chain_workspace_size(int H, int I);
+int kvc_rows_chain(const kvc_layer_chain* chain, void* workspace, size_t workspace_bytes, kvc_stream_t stream);
+
 /* ---- Qwen2-shaped decoder served with continuous batching (include/kvc/qwen_model.h;
  * the model track of the reference, qwen_serve.cu:60-210) ----
  * Random N(0, init_std) fp16 weights from `seed` (norm weights 1, lm_head tied to the
@@ -435,6 +471,8 @@ typedef struct kvc_qwen_config {
     int step_path;  /* 0: fused decode-step kernels when a step has <= 32 rows; 1: one kernel per op */
     int graph;      /* 1: fused steps replay one captured HIP graph (0: eager launches) */
     int prefill_rows;  /* prompt rows stacked into one prefill forward (0: 4096) */
+    int chain;      /* 1: eager fused steps run the linear layers between two attention launches as one
+                       launch (kvc_rows_chain) where the device and shapes allow; 0: one launch each */
 } kvc_qwen_config;
 typedef struct kvc_qwen_stats {
     int steps, finished;
@@ -442,6 +480,7 @@ typedef struct kvc_qwen_stats {
     double wall_us, prefill_us, decode_us;   /* host clock around the whole run / prefills / decode steps */
     long long graph_steps;                   /* decode steps that replayed the captured graph */
     long long graph_captures;                /* step graphs captured (again after a workspace growth) */
+    long long chain_launches;                /* layer-chain launches (kvc_rows_chain) of the decode steps */
 } kvc_qwen_stats;
 typedef struct kvc_qwen kvc_qwen;
 int  kvc_qwen_create(const kvc_qwen_config* cfg, kvc_qwen** out);

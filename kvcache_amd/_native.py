@@ -54,7 +54,7 @@ class QwenConfigC(C.Structure):
         ("layers", i32), ("hidden", i32), ("n_heads", i32), ("n_kv_heads", i32), ("head_dim", i32),
         ("inter", i32), ("vocab", i32), ("eps", C.c_float), ("theta", C.c_float), ("init_std", C.c_float),
         ("block_size", i32), ("num_blocks", i32), ("max_batch", i32), ("max_rows", i32), ("seed", u64),
-        ("step_path", i32), ("graph", i32), ("prefill_rows", i32),
+        ("step_path", i32), ("graph", i32), ("prefill_rows", i32), ("chain", i32),
     ]
 
 
@@ -62,7 +62,18 @@ class QwenStatsC(C.Structure):
     _fields_ = [
         ("steps", i32), ("finished", i32), ("tokens", C.c_longlong), ("prompt_tokens", C.c_longlong),
         ("wall_us", f64), ("prefill_us", f64), ("decode_us", f64), ("graph_steps", C.c_longlong),
-        ("graph_captures", C.c_longlong),
+        ("graph_captures", C.c_longlong), ("chain_launches", C.c_longlong),
+    ]
+
+
+class LayerChainC(C.Structure):
+    """kvc_layer_chain (include/kvc_abi.h)."""
+    _fields_ = [
+        ("M", i32), ("H", i32), ("Hq", i32), ("Hkv", i32), ("D", i32), ("I", i32), ("eps", C.c_float),
+        ("theta", C.c_float), ("x", C.c_void_p), ("att", C.c_void_p), ("w_o", C.c_void_p), ("ln2", C.c_void_p),
+        ("w_gate_up", C.c_void_p), ("act", C.c_void_p), ("w_down", C.c_void_p), ("q", C.c_void_p),
+        ("k", C.c_void_p), ("v", C.c_void_p), ("ln1", C.c_void_p), ("w_qkv", C.c_void_p), ("b_qkv", C.c_void_p),
+        ("pos", C.c_void_p),
     ]
 
 
@@ -161,6 +172,8 @@ _SIGS = {
     "kvc_graph_launch": (i32, [vp, vp]),
     "kvc_graph_destroy": (i32, [vp]),
     "kvc_rows_set_tuning": (i32, [i32, i32, i32]),
+    "kvc_rows_chain_workspace_size": (sz, [i32, i32]),
+    "kvc_rows_chain": (i32, [vp, vp, sz, vp]),
     "kvc_flash_decode": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, f32, i32, i32, vp, sz, vp]),
     "kvc_flash_decode_workspace_size": (sz, [i32, i32, i32]),
     "kvc_block_allocator_create": (i32, [i32, C.POINTER(vp)]),

@@ -248,6 +248,8 @@ bool stream_capturing(hipStream_t st) {
 std::mutex g_err_mu;
 std::vector<int*> g_err_words;
 
+}  // namespace
+
 int* device_error_word(hipStream_t st, bool may_alloc) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return nullptr;
@@ -272,12 +274,25 @@ int take_device_error() {
     return __atomic_exchange_n(g_err_words[dev], 0, __ATOMIC_ACQ_REL);
 }
 
+bool take_device_error_code(int code) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return false;
+    std::lock_guard<std::mutex> lk(g_err_mu);
+    if ((int)g_err_words.size() <= dev || !g_err_words[dev]) return false;
+    int expected = code;
+    return __atomic_compare_exchange_n(g_err_words[dev], &expected, 0, false, __ATOMIC_ACQ_REL, __ATOMIC_ACQUIRE);
+}
+
 int device_error_status(int code) {
     switch (code) {
         case kDevErrNone: return KVC_OK;
         case kDevErrCap:
             return set_error(KVC_ERR_ARG, "an earlier decode launch on this device had a sequence longer than its "
                                           "stated cap; its rows were written as NaN");
+        case kDevErrBarrier:
+            return set_error(KVC_ERR_STATE, "an earlier layer-chain launch on this device gave up waiting at a grid "
+                                            "barrier (its workgroups were not all resident); its outputs are "
+                                            "incomplete");
         default:
             return set_error(KVC_ERR_ARG, "an earlier decode launch on this device had a batch past its planning "
                                           "budget or a length past its contiguous cache; its rows were written as NaN");
@@ -287,6 +302,8 @@ int device_error_status(int code) {
 // Entry check of the device-length decode calls: an earlier launch's report (as far as
 // it has reached the host) fails this call before it launches, and is cleared.
 int pending_device_error() { return device_error_status(take_device_error()); }
+
+namespace {
 
 int resolve_workspace(const Plan& pl, void* ws, size_t ws_bytes, DecodeParams& p, hipStream_t st) {
     if (pl.max_chunks <= 1) return KVC_OK;
@@ -1410,6 +1427,7 @@ int kvc_set_tuning(const char* key, int value) {
     else if (k == "self_prefetch_min_len" && value >= 0) tuning().self_prefetch_min_len = value;
     else if (k == "self_prefetch_xcd" && (value == 0 || value == 1)) tuning().self_prefetch_xcd = value;
     else if (k == "self_lead_tokens" && value >= 0) tuning().self_lead_tokens = value;
+    else if (k == "chain_spin" && value >= 0) tuning().chain_spin = value;
     else return set_error(KVC_ERR_ARG, "unknown tuning key or bad value: " + k);
     return KVC_OK;
 }
@@ -1433,6 +1451,7 @@ int kvc_get_tuning(const char* key, int* value) {
     else if (k == "self_prefetch_min_len") *value = tuning().self_prefetch_min_len;
     else if (k == "self_prefetch_xcd") *value = tuning().self_prefetch_xcd;
     else if (k == "self_lead_tokens") *value = tuning().self_lead_tokens;
+    else if (k == "chain_spin") *value = tuning().chain_spin;
     else return set_error(KVC_ERR_ARG, "unknown tuning key: " + k);
     return KVC_OK;
 }

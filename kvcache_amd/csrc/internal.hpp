@@ -96,9 +96,18 @@ struct DecodeParams {
 enum DeviceError {
     kDevErrNone = 0,
     kDevErrCap = 1,      // a sequence longer than the launch's stated cap (explicit-split grid)
-    kDevErrBudget = 2    // a self-planned batch past its planning budget, or a contiguous
+    kDevErrBudget = 2,   // a self-planned batch past its planning budget, or a contiguous
                          // length past its cache (MAXS)
+    kDevErrBarrier = 3   // a layer-chain launch gave up waiting at a grid barrier
 };
+
+// Device-side failure reports (abi.hip): the per-device pinned host word the kernels
+// store a DeviceError into (made on first use when may_alloc, never under capture;
+// nullptr if none); take_device_error_code clears the word if it holds `code` and says
+// whether it did; device_error_status turns a code into a status + message.
+int* device_error_word(hipStream_t st, bool may_alloc);
+bool take_device_error_code(int code);
+int device_error_status(int code);
 
 // Arrival counters.  Atomics that land on one 128-byte line serialise (about 10 ns
 // each on MI355X, whether or not they hit the same address), so counters that are
@@ -178,6 +187,8 @@ struct Tuning {
                                 // (whole-KV-head units and a multiple of 8 KV heads only)
     int self_lead_tokens = 320; // self-planned VALU decode: sequences of at most this many tokens are
                                 // attended while the kernel plans the others (0: none)
+    int chain_spin = 1 << 20;   // layer chain (kvc_rows_chain): polls before a grid-barrier wait gives
+                                // up and reports kDevErrBarrier (about a second at the default)
 };
 // Dynamic LDS that caps decode workgroups per CU at wg_per_cu (0: none).
 size_t occupancy_lds(size_t static_lds, int wg_per_cu);

@@ -49,6 +49,8 @@ int kvc_qwen_create(const kvc_qwen_config* cfg, kvc_qwen** out) {
         c.graph = cfg->graph;
         if (cfg->prefill_rows < 0) return kvc::set_error(KVC_ERR_ARG, "qwen config: prefill_rows >= 0");
         if (cfg->prefill_rows > 0) c.prefill_rows = cfg->prefill_rows;
+        if (cfg->chain != 0 && cfg->chain != 1) return kvc::set_error(KVC_ERR_ARG, "qwen config: chain 0 or 1");
+        c.chain = cfg->chain;
         if (c.layers <= 0 || c.hidden <= 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 || c.head_dim <= 0 || c.inter <= 0 ||
             c.vocab <= 0 || c.block_size <= 0 || c.num_blocks <= 0 || c.max_batch <= 0 || c.max_rows <= 0)
             return kvc::set_error(KVC_ERR_ARG, "qwen config: sizes must be positive");
@@ -107,6 +109,7 @@ int kvc_qwen_serve(kvc_qwen* h, int n_req, const int* prompt_off, const int* pro
             stats->decode_us = st.decode_us;
             stats->graph_steps = st.graph_steps;
             stats->graph_captures = st.graph_captures;
+            stats->chain_launches = st.chain_launches;
         }
         return KVC_OK;
     });

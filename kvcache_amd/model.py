@@ -31,12 +31,13 @@ class QwenConfig:
     step_path: int = 0  # 0: fused decode-step kernels for steps of <= 32 rows; 1: one kernel per op
     graph: int = 0  # 1: fused decode steps replay one captured HIP graph
     prefill_rows: int = 4096  # prompt rows stacked into one prefill forward
+    chain: int = 0  # 1: linear layers between two attention launches as one launch (where allowed); 0: off
 
     def to_c(self) -> QwenConfigC:
         return QwenConfigC(self.layers, self.hidden, self.n_heads, self.n_kv_heads, self.head_dim, self.inter,
                            self.vocab, self.eps, self.theta, self.init_std, self.block_size, self.num_blocks,
                            self.max_batch, self.max_rows, self.seed, self.step_path, self.graph,
-                           self.prefill_rows)
+                           self.prefill_rows, self.chain)
 
 
 class QwenModel:
@@ -98,4 +99,4 @@ class QwenModel:
         return res, {"steps": st.steps, "finished": st.finished, "tokens": st.tokens,
                      "prompt_tokens": st.prompt_tokens, "wall_us": st.wall_us, "prefill_us": st.prefill_us,
                      "decode_us": st.decode_us, "graph_steps": st.graph_steps,
-                     "graph_captures": st.graph_captures}
+                     "graph_captures": st.graph_captures, "chain_launches": st.chain_launches}

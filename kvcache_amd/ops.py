@@ -262,6 +262,27 @@ def rows_lm_head(logits, tokens, x, w, M, V, H, *, norm_w=None, eps=1e-6, dev_ro
                                  wsb, stream))
 
 
+def rows_chain_workspace_size(H, I) -> int:
+    return int(lib().kvc_rows_chain_workspace_size(H, I))
+
+
+def rows_chain(x, M, H, Hq, Hkv, D, I, *, eps=1e-6, theta=1e6, tail=None, head=None, workspace=None, stream=None):
+    """The linear layers between two attention launches as one launch (kvc_rows_chain).
+    tail: dict(att, w_o, ln2, w_gate_up, act, w_down) -- o_proj + residual, norm + gate|up
+    + SwiGLU, down_proj + residual; head: dict(q, k, v, ln1, w_qkv, b_qkv, pos) -- norm +
+    q|k|v + bias + rotary.  Returns the status (KVC_ERR_UNSUPPORTED / KVC_ERR_STATE are
+    returned, not raised)."""
+    import ctypes as C
+
+    from ._native import LayerChainC
+    t, h = tail or {}, head or {}
+    c = LayerChainC(M, H, Hq, Hkv, D, I, eps, theta, _p(x), _p(t.get("att")), _p(t.get("w_o")), _p(t.get("ln2")),
+                    _p(t.get("w_gate_up")), _p(t.get("act")), _p(t.get("w_down")), _p(h.get("q")), _p(h.get("k")),
+                    _p(h.get("v")), _p(h.get("ln1")), _p(h.get("w_qkv")), _p(h.get("b_qkv")), _p(h.get("pos")))
+    ws, wsb = _ws(workspace)
+    return int(lib().kvc_rows_chain(C.byref(c), ws, wsb, stream))
+
+
 def rows_set_tuning(splits: int = -1, groups_per_wg: int = -1, shape: int = -1) -> None:
     """Overrides of the rows kernels' launch shape (-1: automatic)."""
     check(lib().kvc_rows_set_tuning(int(splits), int(groups_per_wg), int(shape)))
@@ -285,9 +306,10 @@ def flash_decode_workspace_size(H, D, num_splits) -> int:
 
 
 def check_device_errors(stream=None) -> None:
-    """kvc_check_device_errors: synchronizes `stream`; raises KvcError (KVC_ERR_ARG)
-    when an earlier device-length decode launch on this device reported a sequence it
-    could not attend whole (its rows were written as NaN), and clears the report."""
+    """kvc_check_device_errors: synchronizes `stream`; raises KvcError when an earlier
+    launch on this device reported a failure, and clears the report: KVC_ERR_ARG for a
+    device-length decode launch with a sequence it could not attend whole (its rows were
+    written as NaN), KVC_ERR_STATE for a layer-chain launch whose grid barrier gave up."""
     check(lib().kvc_check_device_errors(stream))
 
 

@@ -148,7 +148,7 @@ def test_tuning_round_trip_and_rejects():
     L = N.lib()
     v = C.c_int(0)
     for key in (b"mfma", b"wg_per_cu", b"split_first", b"fused_merge", b"waves_per_block", b"self_prefetch_xcd",
-                b"self_lead_tokens"):
+                b"self_lead_tokens", b"chain_spin"):
         assert L.kvc_get_tuning(key, C.byref(v)) == N.KVC_OK
         old = v.value
         assert L.kvc_set_tuning(key, old) == N.KVC_OK
@@ -156,4 +156,10 @@ def test_tuning_round_trip_and_rejects():
     assert L.kvc_set_tuning(b"no_such_knob", 1) == N.KVC_ERR_ARG
     assert L.kvc_set_tuning(b"self_lead_tokens", -1) == N.KVC_ERR_ARG
     assert L.kvc_empty_launch(0, None) == N.KVC_ERR_ARG and L.kvc_empty_launch(65536, None) == N.KVC_ERR_ARG
+    # the layer chain: argument checks before any device call
+    assert L.kvc_rows_chain(None, None, 0, None) == N.KVC_ERR_ARG
+    assert L.kvc_rows_chain_workspace_size(896, 4864) > L.kvc_rows_workspace_size(896, 4864) > 0
+    assert L.kvc_rows_chain_workspace_size(896, 100) == 0
     assert L.kvc_get_tuning(b"self_lead_tokens", C.byref(v)) == N.KVC_OK and v.value == 320
+    assert L.kvc_get_tuning(b"chain_spin", C.byref(v)) == N.KVC_OK and v.value == 1 << 20
+    assert L.kvc_set_tuning(b"chain_spin", -1) == N.KVC_ERR_ARG

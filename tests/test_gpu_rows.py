@@ -220,3 +220,159 @@ def test_rows_dev_rows_equal_plain_calls(n):
     p_, g_ = both((cap,), np.int32, lambda o, M_, d: ops.rows_lm_head(
         None, o, dev(x), dev(wl), M_, V, H, norm_w=dev(nw), eps=EPS, dev_rows=d, workspace=ws))
     np.testing.assert_array_equal(g_[:n], p_[:n])
+
+
+# ---- layer chain (kvc_rows_chain): the linear layers between two attention launches as
+# one launch with grid barriers; must equal the separate launches bit for bit ----------
+H_, HQ, HKV, D_, I_ = 896, 14, 2, 64, 4864
+QD, KD = HQ * D_, HKV * D_
+
+
+def chain_weights(seed):
+    w = {
+        "w_o": (0.03 * normal((H_, QD), seed)).astype(np.float16),
+        "ln2": (1 + 0.1 * normal((H_,), seed + 1)).astype(np.float16),
+        "w_gate_up": (0.03 * normal((2 * I_, H_), seed + 2)).astype(np.float16),
+        "w_down": (0.015 * normal((H_, I_), seed + 3)).astype(np.float16),
+        "ln1": (1 + 0.1 * normal((H_,), seed + 4)).astype(np.float16),
+        "w_qkv": (0.03 * normal((QD + 2 * KD, H_), seed + 5)).astype(np.float16),
+        "b_qkv": (0.1 * normal((QD + 2 * KD,), seed + 6)).astype(np.float16),
+    }
+    return {k: dev(v) for k, v in w.items()}
+
+
+def chain_separate(W, x, att, pos, M_, tail, head, rws):
+    """The same layers as the separate fused launches (kvc_rows_linear / swiglu / qkv)."""
+    act = DeviceBuffer(M_ * I_ * 2)
+    q, k, v = DeviceBuffer(M_ * QD * 2), DeviceBuffer(M_ * KD * 2), DeviceBuffer(M_ * KD * 2)
+    if tail:
+        ops.rows_linear(x, att, W["w_o"], M_, H_, QD, residual=True, workspace=rws)
+        ops.rows_swiglu(act, x, W["w_gate_up"], M_, I_, H_, norm_w=W["ln2"], eps=EPS)
+        ops.rows_linear(x, act, W["w_down"], M_, H_, I_, residual=True, workspace=rws)
+    if head:
+        ops.rows_qkv(q, k, v, x, W["w_qkv"], W["b_qkv"], pos, M_, H_, HQ, HKV, D_, 1e6, norm_w=W["ln1"], eps=EPS)
+    return act, q, k, v
+
+
+def chain_run(W, x, att, pos, M_, tail, head, cws):
+    act = DeviceBuffer(M_ * I_ * 2)
+    q, k, v = DeviceBuffer(M_ * QD * 2), DeviceBuffer(M_ * KD * 2), DeviceBuffer(M_ * KD * 2)
+    t = dict(att=att, w_o=W["w_o"], ln2=W["ln2"], w_gate_up=W["w_gate_up"], act=act, w_down=W["w_down"]) if tail else None
+    h = dict(q=q, k=k, v=v, ln1=W["ln1"], w_qkv=W["w_qkv"], b_qkv=W["b_qkv"], pos=pos) if head else None
+    rc = ops.rows_chain(x, M_, H_, HQ, HKV, D_, I_, eps=EPS, theta=1e6, tail=t, head=h, workspace=cws)
+    return rc, act, q, k, v
+
+
+def chain_workspace():
+    cws = DeviceBuffer(ops.rows_chain_workspace_size(H_, I_))
+    cws.zero()
+    return cws
+
+
+def test_chain_workspace_size():
+    assert ops.rows_chain_workspace_size(H_, I_) > ops.rows_workspace_size(H_, I_)
+    assert ops.rows_chain_workspace_size(H_, 100) == 0 and ops.rows_chain_workspace_size(0, I_) == 0
+
+
+@pytest.mark.parametrize("parts", ["tail+head", "tail", "head"])
+def test_chain_equals_separate_launches(parts):
+    """Several calls in a row on one workspace (the barrier counters carry over), rows
+    from 32 down to 1 (one and two 16-row tiles), each bit-exact with the separate
+    launches on the same inputs."""
+    from kvcache_amd._native import KVC_OK
+    tail, head = "tail" in parts, "head" in parts
+    W = chain_weights(700)
+    rws = workspace(H_, I_)
+    cws = chain_workspace()
+    for M_ in (32, 17, 16, 5, 1, 32):
+        say(f"layer chain {parts} M={M_}")
+        x0 = normal((M_, H_), 710 + M_, np.float16)
+        att = dev(normal((M_, QD), 720 + M_, np.float16))
+        pos = dev(np.random.default_rng(730 + M_).integers(0, 4000, M_).astype(np.int32))
+        xa, xb = dev(x0), dev(x0)
+        ra = chain_separate(W, xa, att, pos, M_, tail, head, rws)
+        rc, *rb = chain_run(W, xb, att, pos, M_, tail, head, cws)
+        assert rc == KVC_OK
+        assert np.array_equal(host(xa, np.uint16, (M_, H_)), host(xb, np.uint16, (M_, H_)))
+        if tail:
+            assert np.array_equal(host(ra[0], np.uint16, (M_, I_)), host(rb[0], np.uint16, (M_, I_)))
+        if head:
+            for a, b, n in zip(ra[1:], rb[1:], (QD, KD, KD)):
+                assert np.array_equal(host(a, np.uint16, (M_, n)), host(b, np.uint16, (M_, n)))
+    ops.check_device_errors()
+
+
+def test_chain_against_oracle():
+    """One tail + head at 9 rows against the CPU restatement with the op-by-op rounding
+    points (the separate launches are pinned the same way elsewhere)."""
+    from kvcache_amd._native import KVC_OK
+    M_ = 9
+    rng = np.random.default_rng(750)
+    hw = {
+        "w_o": (0.03 * normal((H_, QD), 751)).astype(np.float16),
+        "ln2": (1 + 0.1 * normal((H_,), 752)).astype(np.float16),
+        "w_gate_up": (0.03 * normal((2 * I_, H_), 753)).astype(np.float16),
+        "w_down": (0.015 * normal((H_, I_), 754)).astype(np.float16),
+        "ln1": (1 + 0.1 * normal((H_,), 755)).astype(np.float16),
+        "w_qkv": (0.03 * normal((QD + 2 * KD, H_), 756)).astype(np.float16),
+        "b_qkv": (0.1 * normal((QD + 2 * KD,), 757)).astype(np.float16),
+    }
+    W = {k: dev(v) for k, v in hw.items()}
+    x0 = normal((M_, H_), 758, np.float16)
+    att0 = normal((M_, QD), 759, np.float16)
+    pos0 = rng.integers(0, 4000, M_).astype(np.int32)
+    x = dev(x0)
+    rc, act, q, k, v = chain_run(W, x, dev(att0), dev(pos0), M_, True, True, chain_workspace())
+    assert rc == KVC_OK
+    # CPU: the op-by-op rounding points of the decode step
+    xr = _r16(x0.astype(np.float32) + _r16(M.linear(att0.astype(np.float32), hw["w_o"])))
+    n2 = _r16(M.rmsnorm(xr, hw["ln2"], EPS))
+    g = _r16(M.linear(n2, hw["w_gate_up"][:I_]))
+    u = _r16(M.linear(n2, hw["w_gate_up"][I_:]))
+    actr = _r16(g / (1 + np.exp(-g)) * u)
+    xr2 = _r16(xr + _r16(M.linear(actr, hw["w_down"])))
+    close(host(act, np.float16, (M_, I_)), actr)
+    close(host(x, np.float16, (M_, H_)), xr2, rel=8e-3)
+    n1 = _r16(M.rmsnorm(xr2, hw["ln1"], EPS))
+    qkv = _r16(_r16(M.linear(n1, hw["w_qkv"])) + hw["b_qkv"].astype(np.float32))
+    vr = qkv[:, QD + KD:]
+    close(host(v, np.float16, (M_, KD)), vr, rel=8e-3)
+
+
+def test_chain_barrier_give_up_reports_error():
+    """A barrier wait that gives up (forced from the host with a spin limit of 0 polls:
+    every wait ends at once, every wave exits normally) is reported through the device
+    error word: kvc_check_device_errors and the next chain call say KVC_ERR_STATE, the
+    call clears the counters, and the chain then works again."""
+    from kvcache_amd._native import KVC_ERR_STATE, KVC_OK, KvcError
+    from _helpers import tuning
+    W = chain_weights(760)
+    M_ = 8
+    x0 = normal((M_, H_), 761, np.float16)
+    att = dev(normal((M_, QD), 762, np.float16))
+    pos = dev(np.arange(M_, dtype=np.int32))
+    cws = chain_workspace()
+    say("layer chain with a zero spin limit")
+    with tuning("chain_spin", 0):
+        rc, *_ = chain_run(W, dev(x0), att, pos, M_, True, True, cws)
+        assert rc == KVC_OK  # the launch itself is fine; its barrier gives up on the device
+        with pytest.raises(KvcError) as e:
+            ops.check_device_errors()
+        assert e.value.status == KVC_ERR_STATE
+        # the report was taken by check_device_errors; give up again and let the next
+        # chain call find it
+        rc, *_ = chain_run(W, dev(x0), att, pos, M_, True, True, cws)
+        assert rc == KVC_OK
+        from kvcache_amd.device import synchronize
+        synchronize()
+        rc, *_ = chain_run(W, dev(x0), att, pos, M_, True, True, cws)
+        assert rc == KVC_ERR_STATE
+    say("layer chain after the reset")
+    rws = workspace(H_, I_)
+    xa, xb = dev(x0), dev(x0)
+    ra = chain_separate(W, xa, att, pos, M_, True, True, rws)
+    rc, *rb = chain_run(W, xb, att, pos, M_, True, True, cws)
+    assert rc == KVC_OK
+    assert np.array_equal(host(xa, np.uint16, (M_, H_)), host(xb, np.uint16, (M_, H_)))
+    assert np.array_equal(host(ra[1], np.uint16, (M_, QD)), host(rb[1], np.uint16, (M_, QD)))
+    ops.check_device_errors()
