@@ -212,6 +212,14 @@ __device__ __forceinline__ void epilogue(const RowsParams& p, int M, int g, int 
     }
 }
 
+// ---- building blocks of the layer chain's phases (further below) ------------------
+// The steps of rows_kernel's unit of work as functions, in the same order and
+// arithmetic, so a chain phase computes exactly what the standalone kernel does.
+// (rows_kernel keeps its own inline copy of these steps: written through these
+// functions, the compiler gave its 4-wave shapes ~45 more VGPRs -- lm_head at 286
+// instead of 236, one wave per SIMD instead of two -- so the standalone kernel is left
+// as measured; the chain tests compare the two paths bit for bit.)
+//
 // LDS of a rows workgroup: per wave two 16-row x 128-byte staging blocks (a step
 // pair of two A tiles or of the two weight tiles; 16-byte chunk c of row r at chunk
 // c ^ (r & 7)), the double-buffered cross-wave reduction, the per-wave sums of
@@ -241,8 +249,8 @@ struct RowsLane {
     // whole-line loads: step pair pp, half h = rows 8h .. 8h+7 of a 16-row tile; lane l
     // reads row 8h + l/8, 16-byte chunk l%8 of the 128 bytes at k step first + 2pp
     // (chunks 0-3 belong to the pair's first step, 4-7 to its second)
-    // (the offset goes through an empty asm so the compiler keeps one load per offset
-    // instead of splitting it into branches with constant-offset copies of the load)
+    // (the offset goes through an empty asm: with the chain's run-time validity flags
+    // the compiler otherwise splits the load into branches with constant-offset copies)
     __device__ __forceinline__ int pair_ofs(int pp, int h, bool ok) const {
         int o = ok && 2 * pp + (lch >> 2) < nsteps ? (8 * h + lrow) * kbytes + (first + 2 * pp) * 64 + lch * 16 : kOob;
         asm("" : "+v"(o));
@@ -505,42 +513,266 @@ __global__ __launch_bounds__(WAVES * 64) void rows_kernel(RowsParams p) {
     // the rows of this call (graph-safe launches read them from device memory);
     // p itself is never copied: a modified copy of the parameters ends up in scratch
     const int M = uniform(p.dev_rows ? min(max(*p.dev_rows, 0), p.M) : p.M);
-    constexpr int kItems = kRows * 16 / (WAVES * 64);  // (row, column pair) items per thread
-    __shared__ RowsLds<WAVES> L;
-    using Lane = RowsLane<WAVES, S>;
-    constexpr int NP = Lane::NP;
+    constexpr int kThreads = WAVES * 64;
+    constexpr int kItems = kRows * 16 / kThreads;  // (row, column pair) items per thread
+    __shared__ float s_red[2][WAVES][kRows][kCols + 1];
+    __shared__ float s_ss[WAVES][kRows];
+    __shared__ unsigned s_last;
+    // per wave: two 16-row x 128-byte blocks (a step pair of two A tiles or of the
+    // two weight tiles), 16-byte chunk c of row r at chunk c ^ (r & 7)
+    __shared__ __attribute__((aligned(16))) char s_stage[WAVES][2][16 * 128];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = uniform(threadIdx.x >> 6);
     const int unit = uniform(blockIdx.x / p.splits), sp = uniform(blockIdx.x % p.splits);
     const int g0 = unit * p.gpw;
     const int ng = min(p.gpw, p.groups - g0);
-    const Lane ln(p, sp);
+    const int ksteps = p.K / 32;
+    const int first = (sp * WAVES + wave) * S;
+    const int nsteps = max(0, min(S, ksteps - first));
+    const int r16 = lane & 15, q4 = lane >> 4;
+    const int kbytes = p.K * 2;
+    // whole-line loads: step pair pp, half h = rows 8h .. 8h+7 of a 16-row tile; lane l
+    // reads row 8h + l/8, 16-byte chunk l%8 of the 128 bytes at k step first + 2pp
+    // (chunks 0-3 belong to the pair's first step, 4-7 to its second)
+    constexpr int NP = (S + 1) / 2;
+    const int lrow = lane >> 3, lch = lane & 7;
+    auto pair_ofs = [&](int pp, int h, bool ok) {
+        return ok && 2 * pp + (lch >> 2) < nsteps ? (8 * h + lrow) * kbytes + (first + 2 * pp) * 64 + lch * 16 : kOob;
+    };
+    char(*stg)[16 * 128] = s_stage[wave];
+    auto swz = [](int r, int c) { return r * 128 + ((c ^ (r & 7)) << 4); };
+    // block b (0/1) of the wave's area <- the lane's two whole-line chunks
+    auto stage = [&](int b, u4 lo, u4 hi) {
+        *reinterpret_cast<u4*>(stg[b] + swz(lrow, lch)) = lo;
+        *reinterpret_cast<u4*>(stg[b] + swz(8 + lrow, lch)) = hi;
+    };
+    // operand fragment of step j (0/1) of the pair in block b: row r16, chunk 4j + q4
+    auto unstage = [&](int b, int j) { return *reinterpret_cast<const u4*>(stg[b] + swz(r16, 4 * j + q4)); };
+    auto lds_fence = []() {
+        __builtin_amdgcn_wave_barrier();
+        asm volatile("" ::: "memory");
+    };
 
+    // A rows of this wave's k range (rows >= M and steps past K read as zero), loaded
+    // as whole lines
+    const auto ar = rsrc(p.a, M * kbytes);
     u4 al[NP][MT][2];
-    load_a<0>(ln, p, M, al);
     u4 nw[NORM ? S : 1];
-    if constexpr (NORM) load_norm_w(ln, p, nw);
+#pragma unroll
+    for (int pp = 0; pp < NP; ++pp)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int o = pair_ofs(pp, h, true);
+                al[pp][mt][h] = __builtin_amdgcn_raw_buffer_load_b128(ar, o == kOob ? kOob : mt * 16 * kbytes + o, 0, 0);
+            }
+    if constexpr (NORM) {
+#pragma unroll
+        for (int i = 0; i < S; ++i) {
+            const int kofs = (first + i) * 64 + q4 * 16;  // byte offset of the lane's 8 k values
+            nw[i] = __builtin_amdgcn_raw_buffer_load_b128(rsrc(p.norm_w, kbytes), i < nsteps ? kofs : kOob, 0, 0);
+        }
+    }
+    // Weight tiles of group g: two 16-row tiles, S steps each.  Always issued (a
+    // group past the end reads zeros without touching memory), so the instruction
+    // stream has no branches and the compiler's load counters stay exact: the waits
+    // for one group leave the next group's loads in flight.
+    auto load_b = [&](u4 (&b)[NP][2][2], EpiIn (&e)[kItems], int g, bool valid) {
+#pragma unroll
+        for (int it = 0; it < kItems; ++it) {
+            const int item = threadIdx.x + it * kThreads;
+            e[it] = epi_load<EPI, 0>(p, M, valid ? g : g0, item / 16, item % 16, valid);
+        }
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const auto br = rsrc(p.w + (size_t)tile_row<EPI>(p, valid ? g : g0, t) * p.K, 16 * kbytes);
+#pragma unroll
+            for (int pp = 0; pp < NP; ++pp)
+#pragma unroll
+                for (int h = 0; h < 2; ++h) b[pp][t][h] = __builtin_amdgcn_raw_buffer_load_b128(br, pair_ofs(pp, h, valid), 0, 0);
+        }
+    };
     u4 b0[NP][2][2], b1[NP][2][2];
     EpiIn e0[kItems], e1[kItems];
-    load_e<EPI, 0, WAVES>(p, M, g0, g0, true, e0);
-    load_w<EPI>(ln, p, g0, true, b0);
+    load_b(b0, e0, g0, true);
+
+    // A into the operand layout, a step pair at a time through the wave's LDS area
     u4 af[S][MT];
-    prologue<NORM, MT, S>(ln, p, al, nw, af, L);
+#pragma unroll
+    for (int pp = 0; pp < NP; ++pp) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) stage(mt, al[pp][mt][0], al[pp][mt][1]);
+        lds_fence();
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            if (2 * pp + j < S) {
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) af[2 * pp + j][mt] = unstage(mt, j);
+            }
+        lds_fence();
+    }
+
+    if constexpr (NORM) {
+        // RMSNorm of the rows (qwen_kernels.cu:24-40): sum of squares over this wave's
+        // k range, summed over the waves in LDS, then A = fp16(x * inv_rms * w).
+        float ss[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            ss[mt] = 0.f;
+#pragma unroll
+            for (int i = 0; i < S; ++i) {
+                const h8 x = as_h8(af[i][mt]);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) ss[mt] = __builtin_fmaf((float)x[e], (float)x[e], ss[mt]);
+            }
+            ss[mt] += __shfl_xor(ss[mt], 16);
+            ss[mt] += __shfl_xor(ss[mt], 32);
+            s_ss[wave][mt * 16 + r16] = ss[mt];  // (the four lanes of a row write the same value)
+        }
+        __syncthreads();
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            float tot = 0.f;
+#pragma unroll
+            for (int w = 0; w < WAVES; ++w) tot += s_ss[w][mt * 16 + r16];
+            const float inv = 1.0f / sqrtf(tot / (float)p.K + p.eps);
+#pragma unroll
+            for (int i = 0; i < S; ++i) {
+                const h8 x = as_h8(af[i][mt]), wv = as_h8(nw[i]);
+                h8 y;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) y[e] = (_Float16)((float)x[e] * inv * (float)wv[e]);
+                af[i][mt] = __builtin_bit_cast(u4, y);
+            }
+        }
+    }
+
+    // One column group: MFMAs over this wave's k range, sum over the waves, epilogue.
+    // `ok` false (a group past the end) runs the same code with every store dropped.
+    // Returns false when this workgroup is not the last of a split group (it is done).
+    auto run_group = [&](const u4 (&b)[NP][2][2], const EpiIn (&e)[kItems], int j, bool ok) -> bool {
+        const int g = g0 + j;
+        f4 acc[MT][2];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int t = 0; t < 2; ++t) acc[mt][t] = f4{0.f, 0.f, 0.f, 0.f};
+        // (steps past this wave's range hold zeros: no guard, no branch); the weight
+        // tiles go to the operand layout a step pair at a time through the LDS area
+#pragma unroll
+        for (int pp = 0; pp < NP; ++pp) {
+#pragma unroll
+            for (int t = 0; t < 2; ++t) stage(t, b[pp][t][0], b[pp][t][1]);
+            lds_fence();
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj)
+                if (2 * pp + jj < S) {
+                    const int i = 2 * pp + jj;
+                    u4 bw[2];
+#pragma unroll
+                    for (int t = 0; t < 2; ++t) bw[t] = unstage(t, jj);
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                        for (int t = 0; t < 2; ++t)
+                            acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(af[i][mt]), as_h8(bw[t]),
+                                                                                acc[mt][t], 0, 0, 0);
+                }
+            lds_fence();
+        }
+        // C lane layout: rows 4*(l/16) + r of the 16-row tile, column l%16.
+        float(*red)[kRows][kCols + 1] = s_red[j & 1];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) red[wave][mt * 16 + 4 * q4 + r][t * 16 + r16] = acc[mt][t][r];
+        __syncthreads();
+        float v[kItems][2];
+#pragma unroll
+        for (int it = 0; it < kItems; ++it) {
+            const int item = threadIdx.x + it * kThreads, m = item / 16, c = item % 16;
+            const int mr = m < MT * 16 ? m : 0;  // rows of an unused tile: the sum is never stored
+            v[it][0] = v[it][1] = 0.f;
+#pragma unroll
+            for (int w = 0; w < WAVES; ++w) {
+                v[it][0] += red[w][mr][c];
+                v[it][1] += red[w][mr][c + 16];
+            }
+        }
+        if constexpr (SPLIT) {  // one group per workgroup
+            float* mine = p.part + ((size_t)g * p.splits + sp) * kRows * kCols;
+#pragma unroll
+            for (int it = 0; it < kItems; ++it) {
+                const int item = threadIdx.x + it * kThreads, m = item / 16, c = item % 16;
+                if (m < M) {
+                    __hip_atomic_store(mine + m * kCols + c, v[it][0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(mine + m * kCols + c + 16, v[it][1], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+            // every store of this workgroup has completed before the arrival is counted
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            __builtin_amdgcn_s_waitcnt(0);
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            __syncthreads();
+            if (threadIdx.x == 0)
+                s_last = __hip_atomic_fetch_add(p.ctr + ctr_word(g, p.ctr_shift), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                         (unsigned)(p.splits - 1);
+            __syncthreads();
+            if (!s_last) return false;
+            const float* all = p.part + (size_t)g * p.splits * kRows * kCols;
+            auto ld = [](const float* a) { return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+#pragma unroll
+            for (int it = 0; it < kItems; ++it) {
+                const int item = threadIdx.x + it * kThreads, m = item / 16, c = item % 16;
+                if (m < M) {
+                    float a0 = 0.f, a1 = 0.f;
+                    for (int s2 = 0; s2 < p.splits; ++s2) {
+                        a0 += ld(all + (size_t)s2 * kRows * kCols + m * kCols + c);
+                        a1 += ld(all + (size_t)s2 * kRows * kCols + m * kCols + c + 16);
+                    }
+                    v[it][0] = a0;
+                    v[it][1] = a1;
+                }
+            }
+            if (threadIdx.x == 0) __hip_atomic_store(p.ctr + ctr_word(g, p.ctr_shift), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+#pragma unroll
+        for (int it = 0; it < kItems; ++it) {
+            const int item = threadIdx.x + it * kThreads, m = item / 16, c = item % 16;
+            float bv = -FLT_MAX;
+            int bi = INT_MAX;
+            epilogue<EPI, 0>(p, M, ok ? g : g0, m, c, v[it][0], v[it][1], ok, e[it], bv, bi);
+            if constexpr (EPI == kEpiLogits) {
+                // the 16 column pairs of row m sit in 16 consecutive lanes
+#pragma unroll
+                for (int o = 1; o < 16; o <<= 1) {
+                    const float ov = __shfl_xor(bv, o);
+                    const int oi = __shfl_xor(bi, o);
+                    better(bv, bi, ov, oi);
+                }
+                // one lane per row stores the group's candidate (rows >= M are never read)
+                const int o = ok && c == 0 ? (g * kRows + m) * 4 : kOob;
+                st_f<0>(rsrc(p.best_v, p.groups * kRows * 4), o, bv);
+                __builtin_amdgcn_raw_buffer_store_b32((unsigned)bi, rsrc(p.best_i, p.groups * kRows * 4), o, 0, 0);
+            }
+        }
+        return true;
+    };
 
     if constexpr (SPLIT) {
-        run_group<EPI, 0, true>(ln, p, M, g0, 0, true, sp, af, b0, e0, L);
+        run_group(b0, e0, 0, true);
     } else {
         // two groups per iteration so the buffers swap roles without register copies
-        // (the scheduling barriers keep each group's loads issued ahead of the work on
-        // the previous group: left alone, the scheduler may start that work first and
-        // wait for its loads before issuing the next ones)
         for (int j = 0; j < ng; j += 2) {
-            load_e<EPI, 0, WAVES>(p, M, g0 + j + 1, g0, j + 1 < ng, e1);
-            load_w<EPI>(ln, p, j + 1 < ng ? g0 + j + 1 : g0, j + 1 < ng, b1);
-            __builtin_amdgcn_sched_barrier(0);
-            run_group<EPI, 0, false>(ln, p, M, g0, j, true, sp, af, b0, e0, L);
-            load_e<EPI, 0, WAVES>(p, M, g0 + j + 2, g0, j + 2 < ng, e0);
-            load_w<EPI>(ln, p, j + 2 < ng ? g0 + j + 2 : g0, j + 2 < ng, b0);
-            __builtin_amdgcn_sched_barrier(0);
-            run_group<EPI, 0, false>(ln, p, M, g0, j + 1, j + 1 < ng, sp, af, b1, e1, L);
+            load_b(b1, e1, g0 + j + 1, j + 1 < ng);
+            run_group(b0, e0, j, true);
+            load_b(b0, e0, g0 + j + 2, j + 2 < ng);
+            run_group(b1, e1, j + 1, j + 1 < ng);
         }
     }
 }
