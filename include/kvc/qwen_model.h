@@ -48,7 +48,7 @@ struct QwenConfig {
     int prefill_rows = 4096;  // prompt rows stacked into one prefill forward (a longer prompt runs alone)
     int chain = 0;  // eager fused steps: 1 runs the linear layers between two attention launches as one
                     // persistent launch (kvc_rows_chain) where the device and shapes allow; 0 one launch each
-                    // (the default: measured no faster per step, and it holds a grid barrier)
+                    // (the default: ~1% faster per step measured, and it holds a grid barrier)
 };
 
 struct QwenModel {
