@@ -17,7 +17,9 @@
 //     (bench_throughput.cu:50-57 lengths, bench_continuous.cu:38-50 trace).  The
 //     other harness generators (hval, the fill and shuffle of bench_paged.cu /
 //     main_paged.cu, the demo trace) are plain input generators in
-//     kvcache_amd/workloads.py: no parity check depends on their values.
+//     kvcache_amd/workloads.py: no parity check depends on their values (hval and
+//     the shuffle are still compared with the reference's own code, compiled by
+//     oracle/Makefile into _ref/ref_gen_driver).
 //
 // Pinning (what checks each function independently of this text) is listed in
 // tests/test_oracle_*.py; the header comment of every exported function names

@@ -97,6 +97,43 @@ def test_shuffle_perm_is_a_permutation():
         assert nb < 64 or perm.tolist() != list(range(nb))
 
 
+REF_GEN = Path(__file__).resolve().parents[1] / "oracle" / "_ref" / "ref_gen_driver"
+_no_ref_gen = pytest.mark.skipif(not REF_GEN.exists(), reason="oracle/_ref/ref_gen_driver is built only where the "
+                                                             "reference tree is present (oracle/Makefile, target ref)")
+
+
+def _ref_gen(what):
+    import subprocess
+    return subprocess.run([str(REF_GEN), what], check=True, capture_output=True, text=True).stdout.splitlines()
+
+
+@_no_ref_gen
+def test_hval_equals_reference_generator():
+    """workloads.hval against the reference's own hval (bench_throughput.cu:21-25,
+    compiled from the reference tree into oracle/_ref): 864 argument tuples, large
+    ones included (the hash wraps in uint32), bit for bit."""
+    from kvcache_amd import workloads as W
+    rows = [ln.split() for ln in _ref_gen("hval")]
+    assert len(rows) == 864
+    args = np.array([[int(x) for x in r[:5]] for r in rows], dtype=np.uint64)
+    want = np.array([np.float32(float(r[5])) for r in rows], dtype=np.float32)
+    got = np.array([W.hval(*a) for a in args], dtype=np.float32)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@_no_ref_gen
+def test_shuffle_perm_equals_reference_generator():
+    """workloads.shuffle_perm against the reference's table-shuffle loop (main_paged.cu:
+    28-37, seed 42, compiled from the reference tree into oracle/_ref), element for
+    element, for 1 .. 1000 blocks."""
+    from kvcache_amd import workloads as W
+    lines = _ref_gen("shuffle")
+    assert len(lines) == 6
+    for ln in lines:
+        v = [int(x) for x in ln.split()]
+        np.testing.assert_array_equal(W.shuffle_perm(v[0], 42), v[1:])
+
+
 # ---- allocator / manager ---------------------------------------------------------
 def test_kv_manager_known_answers(orc):
     # test_kv_manager.cu:13-55: 8 blocks x 4 tokens, Hkv 2, D 8
