@@ -1260,9 +1260,11 @@ int kvc_rows_chain(const kvc_layer_chain* c, void* ws, size_t ws_bytes, kvc_stre
         if (tail) {
             if (!ws || ((uintptr_t)ws & 255) || ws_bytes < chain_ws_bytes(H, I))
                 return set_error(KVC_ERR_ARG, "rows chain: workspace too small (kvc_rows_chain_workspace_size)");
-            // a barrier that gave up left its counters part-way: clear them, report once
+            // a barrier that gave up left its counters part-way -- the barriers' and the
+            // down_proj split's (workgroups past the barrier may have counted in without
+            // the one that gave up): clear both, report once
             if (take_device_error_code(kDevErrBarrier)) {
-                if (!capturing) (void)hipMemsetAsync(ws, 0, kChainHdrBytes, hs);
+                if (!capturing) (void)hipMemsetAsync(ws, 0, kChainHdrBytes + kCtrBytes, hs);
                 return device_error_status(kDevErrBarrier);
             }
         }
