@@ -376,3 +376,51 @@ def test_chain_barrier_give_up_reports_error():
     assert np.array_equal(host(xa, np.uint16, (M_, H_)), host(xb, np.uint16, (M_, H_)))
     assert np.array_equal(host(ra[1], np.uint16, (M_, QD)), host(rb[1], np.uint16, (M_, QD)))
     ops.check_device_errors()
+
+
+def test_chain_other_shape_and_refusal():
+    """The chain at another decoder shape (hidden 512, 8q/2kv, SwiGLU 1536, 13 rows) equals
+    the separate launches bit for bit; a shape outside its kernel shapes (SwiGLU 8960:
+    three column groups per workgroup in the gate|up layer) is refused with
+    KVC_ERR_UNSUPPORTED before anything is launched, and the separate launches still run it."""
+    from kvcache_amd._native import KVC_ERR_UNSUPPORTED, KVC_OK
+    H, Hq, Hkv, D = 512, 8, 2, 64
+    qd, kd = Hq * D, Hkv * D
+    for I, M_, expect in ((1536, 13, KVC_OK), (8960, 9, KVC_ERR_UNSUPPORTED)):
+        say(f"layer chain H={H} I={I} M={M_}")
+        w = {
+            "w_o": dev((0.03 * normal((H, qd), 800)).astype(np.float16)),
+            "ln2": dev((1 + 0.1 * normal((H,), 801)).astype(np.float16)),
+            "w_gate_up": dev((0.03 * normal((2 * I, H), 802)).astype(np.float16)),
+            "w_down": dev((0.015 * normal((H, I), 803)).astype(np.float16)),
+            "ln1": dev((1 + 0.1 * normal((H,), 804)).astype(np.float16)),
+            "w_qkv": dev((0.03 * normal((qd + 2 * kd, H), 805)).astype(np.float16)),
+            "b_qkv": dev((0.1 * normal((qd + 2 * kd,), 806)).astype(np.float16)),
+        }
+        x0 = normal((M_, H), 807, np.float16)
+        att = dev(normal((M_, qd), 808, np.float16))
+        pos = dev(np.arange(M_, dtype=np.int32) * 37)
+        xa, xb = dev(x0), dev(x0)
+        rws = DeviceBuffer(max(ops.rows_workspace_size(H, I), 1 << 20))
+        rws.zero()
+        acta, actb = DeviceBuffer(M_ * I * 2), DeviceBuffer(M_ * I * 2)
+        qa, ka, va = DeviceBuffer(M_ * qd * 2), DeviceBuffer(M_ * kd * 2), DeviceBuffer(M_ * kd * 2)
+        qb, kb, vb = DeviceBuffer(M_ * qd * 2), DeviceBuffer(M_ * kd * 2), DeviceBuffer(M_ * kd * 2)
+        ops.rows_linear(xa, att, w["w_o"], M_, H, qd, residual=True, workspace=rws)
+        ops.rows_swiglu(acta, xa, w["w_gate_up"], M_, I, H, norm_w=w["ln2"], eps=EPS)
+        ops.rows_linear(xa, acta, w["w_down"], M_, H, I, residual=True, workspace=rws)
+        ops.rows_qkv(qa, ka, va, xa, w["w_qkv"], w["b_qkv"], pos, M_, H, Hq, Hkv, D, 1e6, norm_w=w["ln1"], eps=EPS)
+        cws = DeviceBuffer(ops.rows_chain_workspace_size(H, I))
+        cws.zero()
+        rc = ops.rows_chain(xb, M_, H, Hq, Hkv, D, I, eps=EPS, theta=1e6, workspace=cws,
+                            tail=dict(att=att, w_o=w["w_o"], ln2=w["ln2"], w_gate_up=w["w_gate_up"], act=actb,
+                                      w_down=w["w_down"]),
+                            head=dict(q=qb, k=kb, v=vb, ln1=w["ln1"], w_qkv=w["w_qkv"], b_qkv=w["b_qkv"], pos=pos))
+        assert rc == expect
+        if expect != KVC_OK:
+            assert np.array_equal(host(xb, np.uint16, (M_, H)), x0.view(np.uint16))  # nothing ran
+            continue
+        assert np.array_equal(host(xa, np.uint16, (M_, H)), host(xb, np.uint16, (M_, H)))
+        assert np.array_equal(host(acta, np.uint16, (M_, I)), host(actb, np.uint16, (M_, I)))
+        for a, b, n in ((qa, qb, qd), (ka, kb, kd), (va, vb, kd)):
+            assert np.array_equal(host(a, np.uint16, (M_, n)), host(b, np.uint16, (M_, n)))
